@@ -1,0 +1,145 @@
+/*
+ * libsparkfp8 -- C ABI of the MI355X (gfx950) FP8 SwiGLU MLP kernels.
+ *
+ * Drop-in boundary for the FP8 MLP sub-block of N8python/spark-gpt
+ * (``_FP8MLPBlock``, train.py:1193-1252).  Each entry point replaces one
+ * kernel launch (or torch-op sequence) of the reference, cited per function.
+ *
+ * Conventions
+ *  - All pointers are device pointers (hipMalloc / torch CUDA tensors) except
+ *    where noted; sizes are elements unless named *_bytes.
+ *  - bf16 tensors are passed as `const void*` (uint16 storage), FP8 tensors as
+ *    `void*` (one byte per element: OCP e4m3fn or e5m2, as torch.float8_*).
+ *  - `scale` points at the 5 delayed per-tensor scales of one block, `amax`
+ *    at its 5 amax slots (slot map: 0 = x, 1 = gu, 2 = h (e4m3); 3 = d_gu,
+ *    4 = dy (e5m2); train.py:916-919).  Kernels read `scale` on the device and
+ *    max-accumulate into `amax`; nothing is read back to the host.
+ *  - `wscale` points at the 2 just-in-time weight scales [q_gu, q_d]
+ *    (train.py:1213).
+ *  - Token-contiguous ("transposed") FP8 copies have leading dimension
+ *    `ldt` = T rounded up to a multiple of 256; producers write zeros in
+ *    columns T..ldt-1 so weight-gradient GEMMs reduce over ldt tokens.
+ *  - `stream` is a hipStream_t; every call is asynchronous on it, never
+ *    synchronises the device and never allocates device memory.  Callers
+ *    provide every output and workspace buffer.
+ *  - Return value: 0 on success; a negative SFP8_ERR_* code for invalid
+ *    arguments (nothing is launched); a positive hipError_t from the launch.
+ *  - Calls are re-entrant: the library has no mutable global state.
+ */
+#ifndef SPARKFP8_H
+#define SPARKFP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFP8_OK 0
+#define SFP8_ERR_NULL_POINTER (-1)
+#define SFP8_ERR_BAD_SHAPE (-2)
+#define SFP8_ERR_BAD_ALIGNMENT (-3)
+#define SFP8_ERR_WORKSPACE_TOO_SMALL (-4)
+
+/* ---- quantizers -------------------------------------------------------- */
+
+/* Standalone quantizer: x8 = e4m3(clamp(x * scale[0], +-448)) row-major
+ * [rows, cols], x8t = x8^T with leading dimension ldt (>= rows; columns
+ * rows..ldt-1 zero), amax[0] = max(amax[0], max|x|).
+ * The norm-free core of _fp8_norm_quant_kernel (train.py:966-972).
+ * cols % 128 == 0; x, x8 16-byte aligned. */
+int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const float* scale, float* amax,
+                           void* x8, void* x8t, int64_t ldt, void* stream);
+
+/* Norm-fused quantizer, replaces _fp8_norm_quant_kernel (train.py:955-972,
+ * launched at train.py:1208-1210).  h [T, D] bf16, norm_w [D] fp32 ->
+ * x8 [T, D] e4m3, x8t [D, ldt] e4m3, rstd [T] fp32; amax[0] max-accumulated.
+ * D in {128, 256, 512, 1024, 2048, 4096}; ldt = T rounded up to 256. */
+int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
+                    const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
+                    void* stream);
+
+/* Just-in-time weight quantization, replaces _fp8_quantize_weight
+ * (train.py:949-952, called at train.py:1211-1212) and the transposed copies
+ * the reference saves for backward (w8.t().contiguous(), train.py:1225) plus a
+ * transposed bf16 copy of the master (the down-proj dgrad operand; the
+ * reference saves w_down.to(bf16), train.py:1224).
+ * w [rows, cols] fp32 -> q_out[0] = exp2(floor(log2(448/max(amax,1e-30)))),
+ * w8 [rows, cols] e4m3 (optional), w8t [cols, rows] e4m3 (optional),
+ * wbf16t [cols, rows] bf16 (optional).  partials: device workspace of
+ * nparts_cap >= 512 floats.  cols % 4 == 0. */
+int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partials, int64_t nparts_cap,
+                      float* q_out, void* w8, void* w8t, void* wbf16t, void* stream);
+
+/* Delayed-scale roll, replaces fp8_update_scales' tensor ops
+ * (train.py:937-946): for each of nsets contiguous 5-slot sets, every slot
+ * with amax > 0 gets scale = exp2(floor(log2(fmax/amax)) - 1); amax = 0. */
+int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
+
+/* ---- GEMMs -------------------------------------------------------------- */
+
+/* gate/up forward + SwiGLU epilogue, replaces _fp8_swiglu_fwd_kernel
+ * (train.py:975-1016, launched at train.py:1216-1218).
+ * x8 [T, D] e4m3, w8 [2I, D] e4m3 -> gu8 [T, 2I] e4m3, h8 [T, I] e4m3,
+ * h8t [I, ldt] e4m3 (token-contiguous copy of h8 for the down wgrad);
+ * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0. */
+int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
+                                const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
+                                void* h8t, int64_t ldt, void* stream);
+
+/* down forward + residual, replaces _fp8_down_fwd_kernel (train.py:1019-1046,
+ * launched at train.py:1220-1222).  h8 [T, I] e4m3, wd8 [D, I] e4m3,
+ * res [T, D] bf16 -> y [T, D] bf16.  I % 128 == 0. */
+int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
+                       const float* scale, const float* wscale, void* y, void* stream);
+
+/* bf16 down dgrad + SwiGLU backward, replaces _fp8_down_dgrad_swiglu_kernel
+ * (train.py:1049-1094, launched at train.py:1236-1238).  dy [T, D] bf16,
+ * wdt [I, D] bf16 (= w_down^T), gu8 [T, 2I] e4m3 -> dgu8 [T, 2I] e5m2,
+ * dgu8t [2I, ldt] e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is
+ * recorded by sfp8_norm_bwd.)  D % 64 == 0. */
+int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
+                                int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
+                                int64_t ldt, void* stream);
+
+/* gate/up dgrad, replaces torch._scaled_mm (train.py:1239-1241):
+ * dxn = bf16((dgu8 @ w8) / (scale[3] * wscale[0])), dgu8 [T, 2I] e5m2,
+ * w8t [D, 2I] e4m3 -> dxn [T, D] bf16. */
+int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
+                           const float* scale, const float* wscale, void* dxn, void* stream);
+
+/* Weight gradient reduced over tokens, replaces _fp8_wgrad / _fp8_wgrad_kernel
+ * (train.py:1150-1187, call at train.py:1247) and _fp8_mm_kernel with A read
+ * transposed (train.py:1097-1127, call at train.py:1249-1251):
+ * out[m, n] = sum_t at[m, t] * bt[n, t] / (sa[0] * sb[0]), fp32 [M, N].
+ * at [M, ldt] e5m2 (fmt_a = 1), bt [N, ldt] e4m3 (fmt_b = 0).
+ * ws: fp32 workspace of sfp8_wgrad_workspace_floats(M, N, ldt) floats (may be
+ * NULL when that is 0).  Deterministic (split-K partials summed in order). */
+int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
+                    const float* sa, const float* sb, float* out, float* ws, int64_t ws_floats, void* stream);
+int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt);
+int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt);
+
+/* Split-K partial sum: out = (sum_s ws[s]) / (sa[0] * sb[0]), s ascending. */
+int sfp8_splitk_reduce(const float* ws, int64_t splits, int64_t M, int64_t N, const float* sa,
+                       const float* sb, float* out, void* stream);
+
+/* ---- norm backward ------------------------------------------------------ */
+
+/* RMSNorm backward + residual, replaces _fp8_norm_bwd_kernel
+ * (train.py:1130-1147, launched at train.py:1243-1246) and the dnw sum
+ * (train.py:1252).  h, dxn, dy [T, D] bf16, rstd [T] -> dh [T, D] bf16,
+ * dnw [D] fp32; also dy8t [D, ldt] = e5m2(dy * scale[4])^T (the down wgrad
+ * operand quantized in registers at train.py:1171-1172) and amax[4] = max|dy|
+ * (train.py:1074-1081).  partials: fp32 workspace of
+ * sfp8_norm_bwd_partials(D, ldt) * D floats. */
+int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                  int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
+                  float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream);
+int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARKFP8_H */

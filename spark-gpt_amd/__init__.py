@@ -1,0 +1,13 @@
+"""MI355X-native FP8 SwiGLU MLP block for spark-gpt (gfx950 HIP kernels behind a C ABI).
+
+Import as ``spark_gpt_amd`` (the repository-root module of that name loads
+this directory as the package).
+"""
+from .mlp import (FP8_HEADROOM_BINADES, FP8_MLP, FP8_SITE_MAX, MAX_HIDDEN, MLP, _FP8MLPBlock,
+                  _use_fp8_mlp, fp8_mlp_block, fp8_update_scales)
+from . import ops
+
+__all__ = [
+    "FP8_HEADROOM_BINADES", "FP8_MLP", "FP8_SITE_MAX", "MAX_HIDDEN", "MLP", "_FP8MLPBlock",
+    "_use_fp8_mlp", "fp8_mlp_block", "fp8_update_scales", "ops",
+]

@@ -1,0 +1,147 @@
+// Shared device helpers for the gfx950 FP8 MLP kernels.
+//
+// Conventions used by every kernel in this library:
+//  * FP8 is OCP e4m3fn / e5m2 (gfx950 hardware formats), bit-identical to
+//    torch.float8_e4m3fn / torch.float8_e5m2.
+//  * Every cast clamps first (to +-448 or +-57344) and keeps NaN, as the
+//    reference does before each .to(fp8) (spark-gpt train.py:952, 968, 1013-1014,
+//    1091-1092, 1172); the hardware converter then rounds to nearest even.
+//  * amax slots are fp32 and are max-accumulated with an unsigned atomic max on
+//    the bit pattern of |x| (exact and order independent for x >= 0).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SFP8_DEV __device__ __forceinline__
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int intx2 __attribute__((ext_vector_type(2)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+namespace sfp8 {
+
+constexpr float kE4M3Max = 448.0f;
+constexpr float kE5M2Max = 57344.0f;
+
+// Library status codes (hipError_t values are passed through unchanged and are
+// all positive; ours are negative).
+enum Status : int {
+  kOk = 0,
+  kErrNullPointer = -1,
+  kErrBadShape = -2,
+  kErrBadAlignment = -3,
+  kErrWorkspaceTooSmall = -4,
+};
+
+SFP8_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet (torch semantics).
+SFP8_DEV uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+SFP8_DEV float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+
+// clamp that keeps NaN (comparisons with NaN are false)
+SFP8_DEV float clamp_keep_nan(float x, float m) {
+  x = (x > m) ? m : x;
+  x = (x < -m) ? -m : x;
+  return x;
+}
+
+// Four fp32 -> four e4m3 bytes packed little-endian (a = lowest byte).
+SFP8_DEV uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  int v = 0;
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_keep_nan(a, kE4M3Max), clamp_keep_nan(b, kE4M3Max), v, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_keep_nan(c, kE4M3Max), clamp_keep_nan(d, kE4M3Max), v, true);
+  return (uint32_t)v;
+}
+
+SFP8_DEV uint32_t pack4_e5m2(float a, float b, float c, float d) {
+  int v = 0;
+  v = __builtin_amdgcn_cvt_pk_bf8_f32(clamp_keep_nan(a, kE5M2Max), clamp_keep_nan(b, kE5M2Max), v, false);
+  v = __builtin_amdgcn_cvt_pk_bf8_f32(clamp_keep_nan(c, kE5M2Max), clamp_keep_nan(d, kE5M2Max), v, true);
+  return (uint32_t)v;
+}
+
+// fp8 byte -> fp32 (exact).  Hardware converter on gfx950.
+SFP8_DEV float e4m3_to_f32(uint32_t word, int byte) {
+  switch (byte) {
+    case 0: return __builtin_amdgcn_cvt_f32_fp8(word, 0);
+    case 1: return __builtin_amdgcn_cvt_f32_fp8(word, 1);
+    case 2: return __builtin_amdgcn_cvt_f32_fp8(word, 2);
+    default: return __builtin_amdgcn_cvt_f32_fp8(word, 3);
+  }
+}
+
+SFP8_DEV float e5m2_to_f32(uint32_t word, int byte) {
+  switch (byte) {
+    case 0: return __builtin_amdgcn_cvt_f32_bf8(word, 0);
+    case 1: return __builtin_amdgcn_cvt_f32_bf8(word, 1);
+    case 2: return __builtin_amdgcn_cvt_f32_bf8(word, 2);
+    default: return __builtin_amdgcn_cvt_f32_bf8(word, 3);
+  }
+}
+
+SFP8_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+SFP8_DEV double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+SFP8_DEV float wave_sum_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// |x| is non-negative, so the unsigned order of its bits is the float order
+// (NaN patterns sort above +inf, so a NaN amax sticks, as torch.amax would).
+SFP8_DEV void atomic_max_nonneg(float* addr, float v) {
+  atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
+}
+
+// Work-group max of a non-negative value; one atomic per work-group.
+// `red` must hold one float per wave.
+template <int NWAVES>
+SFP8_DEV void block_amax_atomic(float v, float* red, float* dst) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < NWAVES; ++i) m = fmaxf(m, red[i]);
+    atomic_max_nonneg(dst, m);
+  }
+}
+
+// 4x4 byte transpose across four dwords: in[r] holds bytes (r,0..3) of a
+// row-major 4x4 byte block; out[c] holds bytes (0..3,c).
+SFP8_DEV void transpose4x4_bytes(const uint32_t in[4], uint32_t out[4]) {
+  // stage 1: interleave bytes of row pairs
+  uint32_t a01lo = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // r0c0 r1c0 r0c1 r1c1
+  uint32_t a01hi = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // r0c2 r1c2 r0c3 r1c3
+  uint32_t a23lo = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+  uint32_t a23hi = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+  // stage 2: combine half-words
+  out[0] = __builtin_amdgcn_perm(a23lo, a01lo, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(a23lo, a01lo, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(a23hi, a01hi, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(a23hi, a01hi, 0x07060302u);
+}
+
+}  // namespace sfp8

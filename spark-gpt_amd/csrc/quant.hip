@@ -1,0 +1,592 @@
+// HBM-bound kernels of the FP8 MLP block (gfx950):
+//   quant_rowcol    standalone bf16 -> e4m3 row-major + transposed, amax
+//   norm_quant      RMSNorm -> e4m3 row-major + transposed, rstd, amax slot 0
+//   weight_quant    just-in-time per-tensor pow2 e4m3 copy of an fp32 master
+//   update_scales   delayed-scale roll of the 5 recipe slots
+//   norm_bwd        RMSNorm backward + residual, dnw partials, e5m2 dy^T, amax slot 4
+//   reductions      dnw partial sum, split-K sum
+//
+// Byte transposes go through an LDS tile: the row-major pass writes the fp8
+// tile into LDS, then each thread gathers a 16(row) x 4(col) byte block with
+// dword reads, transposes it in registers (v_perm) and writes 16-byte runs of
+// the transposed output.
+#include "common.h"
+#include "scale.h"
+
+namespace sfp8 {
+
+// --------------------------------------------------------------------------
+// Transposed write-out of an fp8 tile held in LDS.
+//   lds:      tile of `rows` rows x `cols` bytes, row stride `stride` bytes
+//   out:      destination, out[c * ldo + r0 + r] = tile[r][c]
+//   rows_valid: rows >= rows_valid are written as zero bytes
+// rows % 16 == 0, cols % 4 == 0, (r0 % 16 == 0 and ldo % 16 == 0) for the
+// vector path.  `nthreads` threads cooperate.
+template <int NTHREADS>
+SFP8_DEV void lds_tile_store_transposed(const uint8_t* lds, int rows, int cols, int stride,
+                                        uint8_t* out, int64_t ldo, int64_t r0, int rows_valid,
+                                        int64_t rows_total) {
+  const int nb_c = cols >> 2;
+  const int nblocks = (rows >> 4) * nb_c;
+  for (int idx = threadIdx.x; idx < nblocks; idx += NTHREADS) {
+    const int b = idx % nb_c;  // column block (4 bytes)
+    const int a = idx / nb_c;  // row block (16 rows)
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = a * 16 + i;
+      w[i] = (r < rows_valid) ? *reinterpret_cast<const uint32_t*>(lds + r * stride + b * 4) : 0u;
+    }
+    uint32_t t[4][4];  // t[c][q]: column (4b+c), rows 4q..4q+3 of the block
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t o[4];
+      transpose4x4_bytes(&w[4 * q], o);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) t[c][q] = o[c];
+    }
+    const int64_t rbase = r0 + a * 16;
+    if (rbase >= rows_total) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint8_t* dst = out + (int64_t)(b * 4 + c) * ldo + rbase;
+      if (rbase + 16 <= rows_total && ((((uintptr_t)dst) & 15u) == 0)) {
+        *reinterpret_cast<intx4*>(dst) = intx4{(int)t[c][0], (int)t[c][1], (int)t[c][2], (int)t[c][3]};
+      } else {
+        const int nv = (int)((rows_total - rbase) < 16 ? (rows_total - rbase) : 16);
+        for (int k = 0; k < nv; ++k) dst[k] = (uint8_t)(t[c][k >> 2] >> (8 * (k & 3)));
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// Standalone quantizer: x8 = e4m3(x * s), x8t = x8^T, amax = max|x|.
+// Tile 128 rows x 128 cols, 256 threads.
+constexpr int QR_TILE = 128;
+constexpr int QR_STRIDE = QR_TILE + 8;
+
+__global__ __launch_bounds__(256) void quant_rowcol_kernel(
+    const uint16_t* __restrict__ x, int64_t R, int64_t C, const float* __restrict__ scale,
+    float* __restrict__ amax, uint8_t* __restrict__ x8, uint8_t* __restrict__ x8t, int64_t ldt) {
+  __shared__ __align__(16) uint8_t tile[QR_TILE * QR_STRIDE];
+  __shared__ float red[4];
+  const int64_t r0 = (int64_t)blockIdx.x * QR_TILE;
+  const int64_t c0 = (int64_t)blockIdx.y * QR_TILE;
+  const float s = scale[0];
+  float m = 0.0f;
+  const int c8 = threadIdx.x & 15;  // 8-element chunk within the tile row
+#pragma unroll 4
+  for (int i = 0; i < 8; ++i) {
+    const int r = (threadIdx.x >> 4) + 16 * i;
+    const int64_t gr = r0 + r;
+    uint32_t lo = 0u, hi = 0u;
+    if (gr < R) {
+      const intx4 v = *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8);
+      float f[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t u = (uint32_t)v[j];
+        f[2 * j] = bf16_bits_to_f32(u & 0xffffu);
+        f[2 * j + 1] = bf16_bits_to_f32(u >> 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(f[j]));
+      lo = pack4_e4m3(f[0] * s, f[1] * s, f[2] * s, f[3] * s);
+      hi = pack4_e4m3(f[4] * s, f[5] * s, f[6] * s, f[7] * s);
+      *reinterpret_cast<intx2*>(x8 + gr * C + c0 + c8 * 8) = intx2{(int)lo, (int)hi};
+    }
+    *reinterpret_cast<intx2*>(tile + r * QR_STRIDE + c8 * 8) = intx2{(int)lo, (int)hi};
+  }
+  __syncthreads();
+  const int rows_valid = (int)((R - r0) < QR_TILE ? (R - r0) : QR_TILE);
+  lds_tile_store_transposed<256>(tile, QR_TILE, QR_TILE, QR_STRIDE, x8t + c0 * ldt, ldt, r0,
+                                 rows_valid, ldt);
+  block_amax_atomic<4>(m, red, amax);
+}
+
+// --------------------------------------------------------------------------
+// Norm-fused quantizer (spark-gpt train.py:955-972).
+//   rstd[t] = fl32(1/sqrt(fl64(fl32(sum h^2)/D + eps)))   (sum exact in fp64)
+//   n = (h * rstd) * w;  x8 = e4m3(n * s0);  amax0 = max |n|
+// x8t has leading dimension ldt (>= T, multiple of 16); columns T..ldt-1 of
+// every x8t row are written as zeros so a GEMM can reduce over ldt tokens.
+// Each work-group owns RT rows; a row is split over LPR lanes holding CPL
+// 8-element chunks each.
+template <int D>
+struct NormCfg {
+  static constexpr int LPR = (D / 8) < 64 ? (D / 8) : 64;  // lanes per row
+  static constexpr int RPW = 64 / LPR;                       // rows per wave pass
+  static constexpr int CPL = D / (8 * LPR);                  // chunks per lane
+  static constexpr int RT = (65536 / D) < 64 ? (65536 / D) : 64;  // rows per WG
+  static constexpr int STRIDE = D + 8;                             // LDS row stride
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void norm_quant_kernel(
+    const uint16_t* __restrict__ h, const float* __restrict__ nw, int64_t T, float eps,
+    const float* __restrict__ scale, float* __restrict__ amax, uint8_t* __restrict__ x8,
+    uint8_t* __restrict__ x8t, int64_t ldt, float* __restrict__ rstd) {
+  using Cfg = NormCfg<D>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[4];
+  uint8_t* tile = smem;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
+  const int64_t t0 = (int64_t)blockIdx.x * Cfg::RT;
+  const float s0 = scale[0];
+  float m = 0.0f;
+  // norm weight for this lane's chunks
+  float w[Cfg::CPL][8];
+#pragma unroll
+  for (int c = 0; c < Cfg::CPL; ++c) {
+    const int d = (c * Cfg::LPR + li) * 8;
+    const floatx4 a = *reinterpret_cast<const floatx4*>(nw + d);
+    const floatx4 b = *reinterpret_cast<const floatx4*>(nw + d + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; }
+  }
+  for (int rr = wid * Cfg::RPW; rr < Cfg::RT; rr += 4 * Cfg::RPW) {
+    const int r = rr + sr;
+    const int64_t t = t0 + r;
+    const bool valid = t < T;
+    intx4 v[Cfg::CPL];
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c) {
+      const int d = (c * Cfg::LPR + li) * 8;
+      v[c] = valid ? *reinterpret_cast<const intx4*>(h + t * D + d) : intx4{0, 0, 0, 0};
+    }
+    double ss = 0.0;
+    float f[Cfg::CPL][8];
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t u = (uint32_t)v[c][j];
+        f[c][2 * j] = bf16_bits_to_f32(u & 0xffffu);
+        f[c][2 * j + 1] = bf16_bits_to_f32(u >> 16);
+        // squares of bf16 values are exact in fp64
+        ss = __builtin_fma((double)f[c][2 * j], (double)f[c][2 * j], ss);
+        ss = __builtin_fma((double)f[c][2 * j + 1], (double)f[c][2 * j + 1], ss);
+      }
+#pragma unroll
+    for (int o = Cfg::LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float var = (float)ss / (float)D + eps;
+    const float r_ = (float)(1.0 / __builtin_sqrt((double)var));
+    if (valid && li == 0) rstd[t] = r_;
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c) {
+      const int d = (c * Cfg::LPR + li) * 8;
+      float n[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        n[j] = (f[c][j] * r_) * w[c][j];
+        if (valid) m = fmaxf(m, fabsf(n[j]));
+      }
+      uint32_t lo = 0u, hi = 0u;
+      if (valid) {
+        lo = pack4_e4m3(n[0] * s0, n[1] * s0, n[2] * s0, n[3] * s0);
+        hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
+        *reinterpret_cast<intx2*>(x8 + t * D + d) = intx2{(int)lo, (int)hi};
+      }
+      *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
+    }
+  }
+  __syncthreads();
+  const int rows_valid = (int)((T - t0) < Cfg::RT ? (T - t0) : Cfg::RT);
+  lds_tile_store_transposed<256>(tile, Cfg::RT, D, Cfg::STRIDE, x8t, ldt, t0, rows_valid, ldt);
+  block_amax_atomic<4>(m, red, amax);
+}
+
+// --------------------------------------------------------------------------
+// Weight quantization (spark-gpt train.py:949-952), two launches:
+//   weight_amax_kernel:  per-block max|w| partials (no zero-init needed)
+//   weight_quant_kernel: every block folds the partials into amax and
+//     q = exp2(floor(log2(448 / max(amax, 1e-30)))), then writes its tile of
+//     w8 = e4m3(w * q) row-major and/or transposed, and optionally a
+//     transposed bf16 copy of w.  Block 0 stores q.
+constexpr int WQ_PARTS = 512;
+
+__global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restrict__ w, int64_t n,
+                                                           float* __restrict__ partials) {
+  __shared__ float red[4];
+  float m = 0.0f;
+  const int64_t n4 = n >> 2;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const floatx4 v = reinterpret_cast<const floatx4*>(w)[i];
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  if (blockIdx.x == 0)
+    for (int64_t i = (n4 << 2) + threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(w[i]));
+  m = wave_max(m);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) partials[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+constexpr int WQ_TILE = 64;
+
+__global__ __launch_bounds__(256) void weight_quant_kernel(
+    const float* __restrict__ w, int64_t R, int64_t C, const float* __restrict__ partials, int nparts,
+    float* __restrict__ q_out, uint8_t* __restrict__ w8, uint8_t* __restrict__ w8t,
+    uint16_t* __restrict__ wbt) {
+  __shared__ float red[4];
+  __shared__ float qs;
+  __shared__ __align__(16) uint8_t t8[WQ_TILE * (WQ_TILE + 8)];
+  __shared__ __align__(16) uint16_t t16[WQ_TILE * (WQ_TILE + 2)];
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < nparts; i += 256) m = fmaxf(m, partials[i]);
+  m = wave_max(m);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float q = pow2_scale(a, kE4M3Max, 0);
+    qs = q;
+    if (blockIdx.x == 0 && blockIdx.y == 0) *q_out = q;
+  }
+  __syncthreads();
+  const float q = qs;
+  const int64_t r0 = (int64_t)blockIdx.x * WQ_TILE, c0 = (int64_t)blockIdx.y * WQ_TILE;
+  // each thread: 4 consecutive columns of 4 rows (64x64 tile = 1024 quads)
+  for (int idx = threadIdx.x; idx < WQ_TILE * WQ_TILE / 4; idx += 256) {
+    const int r = idx / (WQ_TILE / 4), c4 = idx % (WQ_TILE / 4);
+    const int64_t gr = r0 + r, gc = c0 + c4 * 4;
+    floatx4 v = {0.f, 0.f, 0.f, 0.f};
+    if (gr < R && gc < C) v = *reinterpret_cast<const floatx4*>(w + gr * C + gc);
+    const uint32_t p = pack4_e4m3(v[0] * q, v[1] * q, v[2] * q, v[3] * q);
+    if (gr < R && gc < C) {
+      if (w8) *reinterpret_cast<uint32_t*>(w8 + gr * C + gc) = p;
+    }
+    *reinterpret_cast<uint32_t*>(t8 + r * (WQ_TILE + 8) + c4 * 4) = p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t16[(c4 * 4 + j) * (WQ_TILE + 2) + r] = (uint16_t)f32_to_bf16_bits(v[j]);
+  }
+  __syncthreads();
+  if (w8t) {
+    const int rows_valid = (int)((R - r0) < WQ_TILE ? (R - r0) : WQ_TILE);
+    const int cols = (int)((C - c0) < WQ_TILE ? (C - c0) : WQ_TILE);
+    lds_tile_store_transposed<256>(t8, WQ_TILE, cols, WQ_TILE + 8, w8t + c0 * R, R, r0, rows_valid, R);
+  }
+  if (wbt) {
+    for (int idx = threadIdx.x; idx < WQ_TILE * WQ_TILE; idx += 256) {
+      const int c = idx / WQ_TILE, r = idx % WQ_TILE;
+      if (r0 + r < R && c0 + c < C) wbt[(c0 + c) * R + r0 + r] = t16[c * (WQ_TILE + 2) + r];
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// Delayed-scale roll (spark-gpt train.py:937-946): for each slot with amax > 0,
+// scale = exp2(floor(log2(fmax / amax)) - 1); amax = 0.
+__global__ void update_scales_kernel(float* __restrict__ scale, float* __restrict__ amax, int nsets,
+                                     int headroom) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nsets * 5) return;
+  const int slot = i % 5;
+  const float fmax = slot < 3 ? kE4M3Max : kE5M2Max;
+  const float a = amax[i];
+  if (a > 0.0f) scale[i] = pow2_scale(a, fmax, headroom);
+  amax[i] = 0.0f;
+}
+
+// --------------------------------------------------------------------------
+// RMSNorm backward + residual (spark-gpt train.py:1130-1147):
+//   g = dxn, gw = g*w, S = sum_d gw*h
+//   dh = bf16(gw*r - h*(S*r*r*r*(1/D)) + dy)
+//   dnw_part[block][d] = sum over the block's rows of g*(h*r)
+// plus, for the down-proj weight gradient, dy8t = e5m2(dy * s4)^T with zero
+// columns T..ldt-1, and amax slot 4 = max|dy| (recorded at train.py:1074-1081).
+template <int D>
+__global__ __launch_bounds__(256) void norm_bwd_kernel(
+    const uint16_t* __restrict__ h, const float* __restrict__ rstd, const uint16_t* __restrict__ dxn,
+    const uint16_t* __restrict__ dy, const float* __restrict__ nw, int64_t T,
+    const float* __restrict__ scale, float* __restrict__ amax, uint16_t* __restrict__ dh,
+    float* __restrict__ dnw_part, uint8_t* __restrict__ dy8t, int64_t ldt) {
+  using Cfg = NormCfg<D>;
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[4];
+  uint8_t* tile = smem;
+  float* dnw_red = reinterpret_cast<float*>(smem + Cfg::RT * Cfg::STRIDE);  // [4 waves][D]
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
+  const int64_t t0 = (int64_t)blockIdx.x * Cfg::RT;
+  const float s4 = scale[4];
+  float m = 0.0f;
+  float w[Cfg::CPL][8], acc[Cfg::CPL][8];
+#pragma unroll
+  for (int c = 0; c < Cfg::CPL; ++c) {
+    const int d = (c * Cfg::LPR + li) * 8;
+    const floatx4 a = *reinterpret_cast<const floatx4*>(nw + d);
+    const floatx4 b = *reinterpret_cast<const floatx4*>(nw + d + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; acc[c][j] = 0.f; acc[c][4 + j] = 0.f; }
+  }
+  for (int rr = wid * Cfg::RPW; rr < Cfg::RT; rr += 4 * Cfg::RPW) {
+    const int r = rr + sr;
+    const int64_t t = t0 + r;
+    const bool valid = t < T;
+    intx4 vh[Cfg::CPL], vg[Cfg::CPL], vd[Cfg::CPL];
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c) {
+      const int d = (c * Cfg::LPR + li) * 8;
+      const intx4 z = {0, 0, 0, 0};
+      vh[c] = valid ? *reinterpret_cast<const intx4*>(h + t * D + d) : z;
+      vg[c] = valid ? *reinterpret_cast<const intx4*>(dxn + t * D + d) : z;
+      vd[c] = valid ? *reinterpret_cast<const intx4*>(dy + t * D + d) : z;
+    }
+    const float rs = valid ? rstd[t] : 0.0f;
+    float S = 0.0f;
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t uh = (uint32_t)vh[c][j >> 1], ug = (uint32_t)vg[c][j >> 1];
+        const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
+        const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
+        S += (g * w[c][j]) * hf;
+      }
+#pragma unroll
+    for (int o = Cfg::LPR / 2; o > 0; o >>= 1) S += __shfl_xor(S, o, 64);
+    const float coef = S * rs * rs * rs * (1.0f / (float)D);
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c) {
+      const int d = (c * Cfg::LPR + li) * 8;
+      float o[8], dyf[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t uh = (uint32_t)vh[c][j >> 1], ug = (uint32_t)vg[c][j >> 1];
+        const uint32_t ud = (uint32_t)vd[c][j >> 1];
+        const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
+        const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
+        dyf[j] = bf16_bits_to_f32((j & 1) ? (ud >> 16) : (ud & 0xffffu));
+        const float gw = g * w[c][j];
+        o[j] = (gw * rs - hf * coef) + dyf[j];
+        acc[c][j] += g * (hf * rs);
+        m = fmaxf(m, fabsf(dyf[j]));
+      }
+      uint32_t lo = 0u, hi = 0u;
+      if (valid) {
+        intx4 ov;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          ov[j] = (int)(f32_to_bf16_bits(o[2 * j]) | (f32_to_bf16_bits(o[2 * j + 1]) << 16));
+        *reinterpret_cast<intx4*>(dh + t * D + d) = ov;
+        lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
+        hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
+      }
+      *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
+    }
+  }
+  // fold this lane's dnw accumulators over the rows sharing its columns
+#pragma unroll
+  for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v = acc[c][j];
+      for (int o = Cfg::LPR; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+      acc[c][j] = v;
+    }
+  if (sr == 0) {
+#pragma unroll
+    for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dnw_red[wid * D + (c * Cfg::LPR + li) * 8 + j] = acc[c][j];
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256)
+    dnw_part[(int64_t)blockIdx.x * D + d] =
+        ((dnw_red[d] + dnw_red[D + d]) + dnw_red[2 * D + d]) + dnw_red[3 * D + d];
+  const int rows_valid = (int)((T - t0) < Cfg::RT ? (T - t0) : Cfg::RT);
+  lds_tile_store_transposed<256>(tile, Cfg::RT, D, Cfg::STRIDE, dy8t, ldt, t0, rows_valid, ldt);
+  block_amax_atomic<4>(m, red, amax + 4);
+}
+
+// Fixed-order column sums: out[d] = sum_b part[b][d] (b ascending).
+__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, int64_t nb,
+                                                     int64_t D, float* __restrict__ out) {
+  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (d >= D) return;
+  float s = 0.0f;
+  for (int64_t b = 0; b < nb; ++b) s += part[b * D + d];
+  out[d] = s;
+}
+
+// Split-K reduction: out = (sum_s ws[s]) * (1 / (sa * sb)), s ascending.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits,
+                                                            int64_t n4, const float* __restrict__ sa,
+                                                            const float* __restrict__ sb,
+                                                            float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float deq = 1.0f / (sa[0] * sb[0]);
+  floatx4 acc = reinterpret_cast<const floatx4*>(ws)[i];
+  for (int s = 1; s < splits; ++s) acc += reinterpret_cast<const floatx4*>(ws)[(int64_t)s * n4 + i];
+  reinterpret_cast<floatx4*>(out)[i] = acc * deq;
+}
+
+}  // namespace sfp8
+
+// ============================================================================
+// C ABI
+// ============================================================================
+using namespace sfp8;
+
+static inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? kOk : (int)e;
+}
+
+static inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
+
+template <typename K>
+static int allow_lds(K kernel, size_t bytes) {
+  // dynamic LDS above 64 KiB must be opted into per kernel
+  if (bytes <= 65536) return kOk;
+  const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)bytes);
+  return e == hipSuccess ? kOk : (int)e;
+}
+
+template <int D>
+static int launch_norm_quant(const void* h, const float* nw, int64_t T, float eps, const float* scale,
+                             float* amax, void* x8, void* x8t, int64_t ldt, float* rstd, hipStream_t st) {
+  using Cfg = NormCfg<D>;
+  const size_t lds = (size_t)Cfg::RT * Cfg::STRIDE;
+  const unsigned nblk = (unsigned)(ldt / Cfg::RT);
+  const int rc = allow_lds(norm_quant_kernel<D>, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(norm_quant_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, nw, T,
+                     eps, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt, rstd);
+  return launch_status();
+}
+
+template <int D>
+static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy,
+                           const float* nw, int64_t T, const float* scale, float* amax, void* dh,
+                           float* dnw, float* part, void* dy8t, int64_t ldt, hipStream_t st) {
+  using Cfg = NormCfg<D>;
+  const size_t lds = (size_t)Cfg::RT * Cfg::STRIDE + 4 * D * sizeof(float);
+  const unsigned nblk = (unsigned)(ldt / Cfg::RT);
+  const int rc = allow_lds(norm_bwd_kernel<D>, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, rstd,
+                     (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, scale, amax, (uint16_t*)dh, part,
+                     (uint8_t*)dy8t, ldt);
+  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, part,
+                     (int64_t)nblk, (int64_t)D, dnw);
+  return launch_status();
+}
+
+extern "C" {
+
+int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const float* scale, float* amax,
+                           void* x8, void* x8t, int64_t ldt, void* stream) {
+  if (!x || !scale || !amax || !x8 || !x8t) return kErrNullPointer;
+  if (rows < 0 || cols < 0 || (cols % QR_TILE) != 0 || ldt < rows) return kErrBadShape;
+  if (!aligned16(x) || !aligned16(x8)) return kErrBadAlignment;
+  if (rows == 0 || cols == 0) return kOk;
+  dim3 grid((unsigned)((rows + QR_TILE - 1) / QR_TILE), (unsigned)(cols / QR_TILE));
+  hipLaunchKernelGGL(quant_rowcol_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, rows, cols, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt);
+  return launch_status();
+}
+
+int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
+                    const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
+                    void* stream) {
+  if (!h || !norm_w || !scale || !amax || !x8 || !x8t || !rstd) return kErrNullPointer;
+  if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
+  if (!aligned16(h) || !aligned16(norm_w) || !aligned16(x8) || !aligned16(x8t)) return kErrBadAlignment;
+  if (ldt == 0) return kOk;
+  hipStream_t st = (hipStream_t)stream;
+  switch (D) {
+    case 128: return launch_norm_quant<128>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
+    case 256: return launch_norm_quant<256>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
+    case 512: return launch_norm_quant<512>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
+    case 1024: return launch_norm_quant<1024>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
+    case 2048: return launch_norm_quant<2048>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
+    case 4096: return launch_norm_quant<4096>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
+    default: return kErrBadShape;
+  }
+}
+
+int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partials, int64_t nparts_cap,
+                      float* q_out, void* w8, void* w8t, void* wbf16t, void* stream) {
+  if (!w || !partials || !q_out) return kErrNullPointer;
+  if (rows <= 0 || cols <= 0 || (cols % 4) != 0) return kErrBadShape;
+  if (nparts_cap < WQ_PARTS) return kErrWorkspaceTooSmall;
+  if (!aligned16(w)) return kErrBadAlignment;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t n = rows * cols;
+  int nparts = (int)((n / 4 + 255) / 256);
+  if (nparts > WQ_PARTS) nparts = WQ_PARTS;
+  if (nparts < 1) nparts = 1;
+  hipLaunchKernelGGL(weight_amax_kernel, dim3(nparts), dim3(256), 0, st, w, n, partials);
+  dim3 grid((unsigned)((rows + WQ_TILE - 1) / WQ_TILE), (unsigned)((cols + WQ_TILE - 1) / WQ_TILE));
+  hipLaunchKernelGGL(weight_quant_kernel, grid, dim3(256), 0, st, w, rows, cols, partials, nparts, q_out,
+                     (uint8_t*)w8, (uint8_t*)w8t, (uint16_t*)wbf16t);
+  return launch_status();
+}
+
+int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream) {
+  if (!scale || !amax) return kErrNullPointer;
+  if (nsets < 0) return kErrBadShape;
+  if (nsets == 0) return kOk;
+  const int n = (int)(nsets * 5);
+  hipLaunchKernelGGL(update_scales_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                     scale, amax, (int)nsets, 1);
+  return launch_status();
+}
+
+int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
+  switch (D) {
+    case 128: return ldt / NormCfg<128>::RT;
+    case 256: return ldt / NormCfg<256>::RT;
+    case 512: return ldt / NormCfg<512>::RT;
+    case 1024: return ldt / NormCfg<1024>::RT;
+    case 2048: return ldt / NormCfg<2048>::RT;
+    case 4096: return ldt / NormCfg<4096>::RT;
+    default: return -1;
+  }
+}
+
+int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                  int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
+                  float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream) {
+  if (!h || !rstd || !dxn || !dy || !norm_w || !scale || !amax || !dh || !dnw || !partials || !dy8t)
+    return kErrNullPointer;
+  if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
+  const int64_t nb = sfp8_norm_bwd_partials(D, ldt);
+  if (nb < 0) return kErrBadShape;
+  if (partials_cap < nb * D) return kErrWorkspaceTooSmall;
+  if (!aligned16(h) || !aligned16(dxn) || !aligned16(dy) || !aligned16(dh) || !aligned16(norm_w) ||
+      !aligned16(dy8t))
+    return kErrBadAlignment;
+  if (ldt == 0) return kOk;
+  hipStream_t st = (hipStream_t)stream;
+  switch (D) {
+    case 128: return launch_norm_bwd<128>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    case 256: return launch_norm_bwd<256>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    case 512: return launch_norm_bwd<512>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    case 1024: return launch_norm_bwd<1024>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    case 2048: return launch_norm_bwd<2048>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    case 4096: return launch_norm_bwd<4096>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    default: return kErrBadShape;
+  }
+}
+
+int sfp8_splitk_reduce(const float* ws, int64_t splits, int64_t M, int64_t N, const float* sa,
+                       const float* sb, float* out, void* stream) {
+  if (!ws || !sa || !sb || !out) return kErrNullPointer;
+  if (splits < 1 || M < 0 || N < 0 || ((M * N) % 4) != 0) return kErrBadShape;
+  const int64_t n4 = M * N / 4;
+  if (n4 == 0) return kOk;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, ws, (int)splits, n4, sa, sb, out);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,198 @@
+"""Torch-facing wrappers of the libsparkfp8 kernels.
+
+Each wrapper validates shapes/dtypes, allocates its outputs with torch's
+caching allocator (as the reference allocates with ``torch.empty``), and
+launches on torch's current stream.  Nothing here synchronises the device or
+reads device values back.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+E4M3 = torch.float8_e4m3fn
+E5M2 = torch.float8_e5m2
+FMT_E4M3 = 0
+FMT_E5M2 = 1
+TOKEN_ALIGN = 256  # leading dimension of token-contiguous fp8 copies
+
+
+def ldt_of(T: int) -> int:
+    """Leading dimension of the token-contiguous copies (x8t, h8t, d_gu8t, dy8t)."""
+    return -(-T // TOKEN_ALIGN) * TOKEN_ALIGN
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _cuda_contig(name: str, t: torch.Tensor, dtype: torch.dtype, ndim: int) -> None:
+    _need(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _need(t.dim() == ndim, f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _state(scale: torch.Tensor, amax: torch.Tensor) -> None:
+    for n, t in (("scale", scale), ("amax", amax)):
+        _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= 5,
+              f"{n} must be a contiguous fp32 device tensor of 5 slots")
+
+
+# ------------------------------------------------------------------ quantizers
+def quant_e4m3_rowcol(x: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor):
+    """x8 = e4m3(x * scale[0]), x8t = x8^T ([cols, rows]), amax[0] max|x|."""
+    _cuda_contig("x", x, torch.bfloat16, 2)
+    R, C = x.shape
+    _need(C % 128 == 0, "cols must be a multiple of 128")
+    x8 = torch.empty(R, C, dtype=E4M3, device=x.device)
+    x8t = torch.empty(C, R, dtype=E4M3, device=x.device)
+    _lib.call("sfp8_quant_e4m3_rowcol", x.data_ptr(), R, C, scale.data_ptr(), amax.data_ptr(),
+              x8.data_ptr(), x8t.data_ptr(), R, _lib.stream_of(x))
+    return x8, x8t
+
+
+def norm_quant(h: torch.Tensor, norm_w: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor, eps: float):
+    """(x8 [T, D], x8t [D, ldt], rstd [T]); amax[0] max-accumulated."""
+    _cuda_contig("h", h, torch.bfloat16, 2)
+    _cuda_contig("norm_w", norm_w, torch.float32, 1)
+    _state(scale, amax)
+    T, D = h.shape
+    ldt = ldt_of(T)
+    x8 = torch.empty(T, D, dtype=E4M3, device=h.device)
+    x8t = torch.empty(D, ldt, dtype=E4M3, device=h.device)
+    rstd = torch.empty(T, dtype=torch.float32, device=h.device)
+    _lib.call("sfp8_norm_quant", h.data_ptr(), norm_w.data_ptr(), T, D, float(eps), scale.data_ptr(),
+              amax.data_ptr(), x8.data_ptr(), x8t.data_ptr(), ldt, rstd.data_ptr(), _lib.stream_of(h))
+    return x8, x8t, rstd
+
+
+def weight_quant(w: torch.Tensor, q_out: torch.Tensor, *, w8: bool = True, w8t: bool = False,
+                 bf16t: bool = False):
+    """Just-in-time e4m3 copy of an fp32 master: returns (w8, w8t, w_bf16^T),
+    unrequested outputs None; the pow2 scale lands in q_out[0] (device)."""
+    _cuda_contig("w", w, torch.float32, 2)
+    R, C = w.shape
+    _need(C % 4 == 0, "weight columns must be a multiple of 4")
+    dev = w.device
+    o8 = torch.empty(R, C, dtype=E4M3, device=dev) if w8 else None
+    o8t = torch.empty(C, R, dtype=E4M3, device=dev) if w8t else None
+    obt = torch.empty(C, R, dtype=torch.bfloat16, device=dev) if bf16t else None
+    parts = torch.empty(512, dtype=torch.float32, device=dev)
+    _lib.call("sfp8_weight_quant", w.data_ptr(), R, C, parts.data_ptr(), parts.numel(), q_out.data_ptr(),
+              _lib.ptr(o8), _lib.ptr(o8t), _lib.ptr(obt), _lib.stream_of(w))
+    return o8, o8t, obt
+
+
+def update_scales(scale: torch.Tensor, amax: torch.Tensor) -> None:
+    """In-place delayed-scale roll of one or more contiguous 5-slot sets."""
+    _need(scale.is_cuda and amax.is_cuda, "scale/amax must be device tensors")
+    _need(scale.dtype == torch.float32 and amax.dtype == torch.float32, "scale/amax must be fp32")
+    _need(scale.is_contiguous() and amax.is_contiguous(), "scale/amax must be contiguous")
+    _need(scale.numel() == amax.numel() and scale.numel() % 5 == 0, "scale/amax: 5 slots per set")
+    _lib.call("sfp8_update_scales", scale.data_ptr(), amax.data_ptr(), scale.numel() // 5,
+              _lib.stream_of(scale))
+
+
+# ------------------------------------------------------------------ GEMMs
+def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I: int):
+    """(gu8 [T, 2I], h8 [T, I], h8t [I, ldt]); amax[1], amax[2] max-accumulated."""
+    _cuda_contig("x8", x8, E4M3, 2)
+    _cuda_contig("w8", w8, E4M3, 2)
+    T, D = x8.shape
+    _need(w8.shape == (2 * I, D), "w8 must be [2I, D]")
+    _need(D % 128 == 0 and I % 128 == 0, "D and I must be multiples of 128")
+    ldt = ldt_of(T)
+    dev = x8.device
+    gu8 = torch.empty(T, 2 * I, dtype=E4M3, device=dev)
+    h8 = torch.empty(T, I, dtype=E4M3, device=dev)
+    h8t = torch.empty(I, ldt, dtype=E4M3, device=dev)
+    _lib.call("sfp8_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), T, D, I, scale.data_ptr(),
+              wscale.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr(), ldt,
+              _lib.stream_of(x8))
+    return gu8, h8, h8t
+
+
+def down_fwd(h8, wd8, res, scale, wscale):
+    """y = bf16(res + bf16(h8 @ wd8^T / (s2 * q_d))), [T, D] bf16."""
+    _cuda_contig("h8", h8, E4M3, 2)
+    _cuda_contig("wd8", wd8, E4M3, 2)
+    _cuda_contig("res", res, torch.bfloat16, 2)
+    T, I = h8.shape
+    D = wd8.shape[0]
+    _need(wd8.shape == (D, I) and res.shape == (T, D), "shape mismatch in down_fwd")
+    _need(I % 128 == 0, "I must be a multiple of 128")
+    y = torch.empty(T, D, dtype=torch.bfloat16, device=h8.device)
+    _lib.call("sfp8_gemm_down_fwd", h8.data_ptr(), wd8.data_ptr(), res.data_ptr(), T, D, I, scale.data_ptr(),
+              wscale.data_ptr(), y.data_ptr(), _lib.stream_of(h8))
+    return y
+
+
+def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
+    """(dgu8 [T, 2I] e5m2, dgu8t [2I, ldt] e5m2); amax[3] max-accumulated."""
+    _cuda_contig("dy", dy, torch.bfloat16, 2)
+    _cuda_contig("wdt", wdt, torch.bfloat16, 2)
+    _cuda_contig("gu8", gu8, E4M3, 2)
+    T, D = dy.shape
+    I = wdt.shape[0]
+    _need(wdt.shape == (I, D) and gu8.shape == (T, 2 * I), "shape mismatch in down_dgrad_swiglu")
+    _need(D % 64 == 0 and I % 16 == 0, "D must be a multiple of 64")
+    ldt = ldt_of(T)
+    dgu8 = torch.empty(T, 2 * I, dtype=E5M2, device=dy.device)
+    dgu8t = torch.empty(2 * I, ldt, dtype=E5M2, device=dy.device)
+    _lib.call("sfp8_gemm_down_dgrad_swiglu", dy.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), T, D, I,
+              scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr(), ldt, _lib.stream_of(dy))
+    return dgu8, dgu8t
+
+
+def gateup_dgrad(dgu8, w8t, scale, wscale):
+    """dxn = bf16(dgu8 @ w8 / (s3 * q_gu)), [T, D] bf16; w8t is W8^T [D, 2I]."""
+    _cuda_contig("dgu8", dgu8, E5M2, 2)
+    _cuda_contig("w8t", w8t, E4M3, 2)
+    T, I2 = dgu8.shape
+    D = w8t.shape[0]
+    _need(w8t.shape == (D, I2) and I2 % 128 == 0, "shape mismatch in gateup_dgrad")
+    dxn = torch.empty(T, D, dtype=torch.bfloat16, device=dgu8.device)
+    _lib.call("sfp8_gemm_gateup_dgrad", dgu8.data_ptr(), w8t.data_ptr(), T, D, I2 // 2, scale.data_ptr(),
+              wscale.data_ptr(), dxn.data_ptr(), _lib.stream_of(dgu8))
+    return dxn
+
+
+def wgrad(at, bt, sa, sb):
+    """out[m, n] = sum_t at[m, t] bt[n, t] / (sa * sb), fp32 [M, N]; at e5m2
+    [M, ldt], bt e4m3 [N, ldt] (token-contiguous, zero-padded)."""
+    _cuda_contig("at", at, E5M2, 2)
+    _cuda_contig("bt", bt, E4M3, 2)
+    M, ldt = at.shape
+    N = bt.shape[0]
+    _need(bt.shape[1] == ldt and ldt % TOKEN_ALIGN == 0, "wgrad operands need a common padded ldt")
+    out = torch.empty(M, N, dtype=torch.float32, device=at.device)
+    nws = _lib.query("sfp8_wgrad_workspace_floats", M, N, ldt)
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=at.device)
+    _lib.call("sfp8_gemm_wgrad", at.data_ptr(), FMT_E5M2, bt.data_ptr(), FMT_E4M3, M, N, ldt, sa.data_ptr(),
+              sb.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(at))
+    return out
+
+
+# ------------------------------------------------------------------ norm backward
+def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
+    """(dh [T, D] bf16, dnw [D] fp32, dy8t [D, ldt] e5m2); amax[4] = max|dy|."""
+    for n, t in (("h", h), ("dxn", dxn), ("dy", dy)):
+        _cuda_contig(n, t, torch.bfloat16, 2)
+    _cuda_contig("rstd", rstd, torch.float32, 1)
+    _cuda_contig("norm_w", norm_w, torch.float32, 1)
+    T, D = h.shape
+    ldt = ldt_of(T)
+    dev = h.device
+    dh = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    dnw = torch.empty(D, dtype=torch.float32, device=dev)
+    dy8t = torch.empty(D, ldt, dtype=E5M2, device=dev)
+    nparts = _lib.query("sfp8_norm_bwd_partials", D, ldt)
+    _need(nparts >= 0, f"unsupported hidden size {D}")
+    parts = torch.empty(max(nparts * D, 1), dtype=torch.float32, device=dev)
+    _lib.call("sfp8_norm_bwd", h.data_ptr(), rstd.data_ptr(), dxn.data_ptr(), dy.data_ptr(), norm_w.data_ptr(),
+              T, D, scale.data_ptr(), amax.data_ptr(), dh.data_ptr(), dnw.data_ptr(), parts.data_ptr(),
+              parts.numel(), dy8t.data_ptr(), ldt, _lib.stream_of(h))
+    return dh, dnw, dy8t

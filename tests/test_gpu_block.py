@@ -1,0 +1,126 @@
+"""GPU parity of the whole FP8 MLP block (the reference's own test, mirrored,
+plus the oracle comparison, amax lifecycle and determinism)."""
+import pytest
+import torch
+import torch.nn as nn
+
+import spark_gpt_amd as sg
+from oracle import fp8_mlp as O
+
+pytestmark = pytest.mark.gpu
+
+
+class _Norm(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = 1e-6
+
+
+def _setup(dev, T, D, I, seed, wstd=None, norm_uniform=True):
+    torch.manual_seed(seed)
+    norm = _Norm(D)
+    mlp = sg.MLP(D, I)
+    with torch.no_grad():
+        if norm_uniform:
+            norm.weight.uniform_(0.5, 1.5)
+        if wstd is None:
+            mlp.gate_up_proj.weight.normal_(0, D ** -0.5)
+            mlp.down_proj.weight.normal_(0, I ** -0.5)
+        else:
+            mlp.gate_up_proj.weight.normal_(0, wstd)
+            mlp.down_proj.weight.normal_(0, wstd)
+    norm, mlp = norm.to(dev).train(), mlp.to(dev).train()
+    return norm, mlp
+
+
+def _step(h, probe, norm, mlp):
+    params = [norm.weight, mlp.gate_up_proj.weight, mlp.down_proj.weight]
+    x = h.clone().requires_grad_(True)
+    y = sg._FP8MLPBlock.apply(x, *params, mlp.fp8_scale, mlp.fp8_amax, norm.eps)
+    return (y,) + torch.autograd.grad((y.float() * probe).sum(), [x] + params)
+
+
+def test_fp8_mlp_block_tracks_fp32_reference(dev):
+    """Mirror of spark-gpt tests/test_fp8_mlp.py:10-53 (same shapes, init,
+    protocol and bound)."""
+    torch.manual_seed(0)
+    D, I, rows = 256, 768, 1000
+    norm, mlp = _setup(dev, rows, D, I, 0, wstd=0.05)
+    h = torch.randn(rows, D, device=dev).to(torch.bfloat16)
+    probe = torch.randn(rows, D, device=dev)
+    _step(h, probe, norm, mlp)  # prewarm: records amax under the initial scales
+    assert bool((mlp.fp8_amax > 0).all()), mlp.fp8_amax
+    sg.fp8_update_scales(mlp)
+    assert bool((mlp.fp8_amax == 0).all())
+    out = _step(h, probe, norm, mlp)
+    params = [norm.weight, mlp.gate_up_proj.weight, mlp.down_proj.weight]
+    ref = O.fp32_reference(h, *params, probe)
+    for name, a, r in zip(("mlp out", "dh", "dnorm_w", "dW_gate_up", "dW_down"), out, ref):
+        if name == "mlp out":
+            a, r = a.float() - h.float(), r - h.float()
+        err = O.rel_l2(a.float(), r)
+        assert torch.isfinite(a).all(), name
+        assert err < 0.12, f"{name}: rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("T,D,I", [(1000, 256, 768), (257, 128, 384), (2048, 1024, 3072)])
+def test_block_matches_oracle(dev, T, D, I):
+    """Same inputs, same delayed scales: every output and grad within rel-L2
+    1e-2 of the CPU emulation of the recipe; bit-exact amax slots 0 and 4."""
+    norm, mlp = _setup(dev, T, D, I, T + D)
+    g = torch.Generator().manual_seed(T)
+    h = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(T, D, generator=g) * 1e-3).to(torch.bfloat16)
+    params = [norm.weight, mlp.gate_up_proj.weight, mlp.down_proj.weight]
+
+    def gpu():
+        x = h.to(dev).requires_grad_(True)
+        y = sg._FP8MLPBlock.apply(x, *params, mlp.fp8_scale, mlp.fp8_amax, norm.eps)
+        return [y] + list(torch.autograd.grad(y, [x] + params, dy.to(dev)))
+
+    gpu()
+    sg.fp8_update_scales(mlp)
+    s = mlp.fp8_scale.cpu().clone()
+    out = [t.detach().cpu() for t in gpu()]
+    a_gpu = mlp.fp8_amax.cpu()
+    a_ref = torch.zeros(5)
+    cpu_params = [p.detach().cpu() for p in params]
+    y, saved = O.block_forward(h, *cpu_params, s.clone(), a_ref, 1e-6)
+    grads, _ = O.block_backward(dy, saved, s.clone(), a_ref)
+    ref = [y] + list(grads)
+    for name, a, r in zip(("y", "dh", "dnorm_w", "dW_gate_up", "dW_down"), out, ref):
+        if name == "y":
+            a, r = a.float() - h.float(), r.float() - h.float()
+        err = O.rel_l2(a.float(), r.float())
+        assert torch.isfinite(a.float()).all(), name
+        assert err < 1e-2, f"{name}: rel-L2 vs oracle {err:.3e}"
+    assert a_gpu[0] == a_ref[0] and a_gpu[4] == a_ref[4]
+    torch.testing.assert_close(a_gpu, a_ref, rtol=2e-2, atol=0)
+    # every scale a power of two
+    m, e = torch.frexp(mlp.fp8_scale.cpu())
+    assert torch.all(m == 0.5)
+
+
+def test_block_deterministic(dev):
+    T, D, I = 1000, 256, 768
+    norm, mlp = _setup(dev, T, D, I, 5)
+    h = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    probe = torch.randn(T, D, device=dev)
+    _step(h, probe, norm, mlp)
+    sg.fp8_update_scales(mlp)
+    s0 = mlp.fp8_scale.clone()
+    a = _step(h, probe, norm, mlp)
+    amax_a = mlp.fp8_amax.clone()
+    mlp.fp8_amax.zero_()
+    mlp.fp8_scale.copy_(s0)
+    b = _step(h, probe, norm, mlp)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    assert torch.equal(amax_a, mlp.fp8_amax)
+
+
+def test_guard_and_module_state():
+    m = sg.MLP(256, 768)
+    assert set(dict(m.named_parameters())) == {"gate_up_proj.weight", "down_proj.weight"}
+    assert "fp8_scale" not in m.state_dict() and "fp8_amax" not in m.state_dict()

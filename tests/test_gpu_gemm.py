@@ -1,0 +1,174 @@
+"""GPU parity of each GEMM kernel against the oracle on identical inputs.
+
+* exact-integer operands (every partial sum exact in fp32, so accumulation
+  order cannot matter): outputs bit-exact wherever no transcendental is
+  involved, fp8 epilogue outputs after a sigmoid within one code;
+* random operands: dequantized outputs within tolerance, fp8 codes within one.
+"""
+import pytest
+import torch
+
+import spark_gpt_amd as sg
+from oracle import fp8_mlp as O
+
+pytestmark = pytest.mark.gpu
+
+E4 = torch.float8_e4m3fn
+E5 = torch.float8_e5m2
+
+
+def u8(t):
+    return t.contiguous().view(torch.uint8).cpu()
+
+
+def code_dist(a, b):
+    """Distance in fp8 codes (sign-magnitude ordinal) between two byte tensors."""
+    def ordinal(x):
+        x = x.to(torch.int32)
+        return torch.where(x >= 128, -(x - 128), x)
+    return (ordinal(u8(a)) - ordinal(u8(b))).abs()
+
+
+def int_fp8(shape, dtype, g, lo=-8, hi=8):
+    return torch.randint(lo, hi + 1, shape, generator=g).float().to(dtype)
+
+
+SHAPES = [(1000, 256, 768), (257, 128, 384), (512, 512, 256), (1, 256, 128)]
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES)
+def test_swiglu_fwd_integer_operands(dev, T, D, I):
+    g = torch.Generator().manual_seed(T + D + I)
+    x8 = int_fp8((T, D), E4, g)
+    w8 = int_fp8((2 * I, D), E4, g)
+    s = torch.tensor([0.5, 2.0 ** -6, 4.0, 1, 1])
+    ws = torch.tensor([2.0 ** -3, 1.0])
+    amax = torch.zeros(5, device=dev)
+    gu8, h8, h8t = sg.ops.gateup_swiglu_fwd(x8.to(dev), w8.to(dev), s.to(dev), ws.to(dev), amax, I)
+    rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8, w8, s, ws, I)
+    assert torch.equal(u8(gu8), u8(rgu8))
+    assert int(code_dist(h8, rh8).max()) <= 1
+    assert float((code_dist(h8, rh8) > 0).float().mean()) < 0.01
+    ldt = sg.ops.ldt_of(T)
+    assert h8t.shape == (I, ldt)
+    assert torch.equal(u8(h8t)[:, :T], u8(h8).t())
+    assert torch.all(u8(h8t)[:, T:] == 0)
+    assert amax[1].item() == ra1.item()
+    torch.testing.assert_close(amax[2].cpu(), ra2, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES[:3])
+def test_swiglu_fwd_random(dev, T, D, I):
+    g = torch.Generator().manual_seed(1 + T + D + I)
+    h = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    nw = torch.ones(D)
+    s = torch.tensor([32.0, 64.0, 128.0, 1, 1])
+    x8, _, _, _ = O.norm_quant(h, nw, s[0], 1e-6)
+    w8, q = O.quantize_weight(torch.randn(2 * I, D, generator=g) * D ** -0.5)
+    ws = torch.stack([q, torch.tensor(1.0)])
+    amax = torch.zeros(5, device=dev)
+    gu8, h8, _ = sg.ops.gateup_swiglu_fwd(x8.to(dev), w8.to(dev), s.to(dev), ws.to(dev), amax, I)
+    rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8, w8, s, ws, I)
+    for got, ref in ((gu8, rgu8), (h8, rh8)):
+        d = code_dist(got, ref)
+        assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.02
+    torch.testing.assert_close(amax[1:3].cpu(), torch.stack([ra1, ra2]), rtol=1e-2, atol=0)
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES)
+def test_down_fwd_integer_operands(dev, T, D, I):
+    g = torch.Generator().manual_seed(2 + T + D + I)
+    h8 = int_fp8((T, I), E4, g)
+    wd8 = int_fp8((D, I), E4, g)
+    res = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    s = torch.tensor([1, 1, 2.0 ** 4, 1, 1])
+    ws = torch.tensor([1.0, 2.0 ** 3])
+    y = sg.ops.down_fwd(h8.to(dev), wd8.to(dev), res.to(dev), s.to(dev), ws.to(dev))
+    ry = O.down_fwd(h8, wd8, res, s, ws)
+    assert torch.equal(y.cpu(), ry)
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES)
+def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
+    g = torch.Generator().manual_seed(3 + T + D + I)
+    dy = torch.randint(-8, 9, (T, D), generator=g).float().to(torch.bfloat16)
+    wd = torch.randint(-8, 9, (D, I), generator=g).float().to(torch.bfloat16)
+    gu8 = O.e4m3(torch.randn(T, 2 * I, generator=g) * 64)
+    s = torch.tensor([1, 64.0, 1, 2.0 ** -12, 1])
+    amax = torch.zeros(5, device=dev)
+    dgu8, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), wd.t().contiguous().to(dev), gu8.to(dev), s.to(dev), amax)
+    rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
+    d = code_dist(dgu8, rdgu8)
+    assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.01
+    assert torch.equal(u8(dgu8t)[:, :T], u8(dgu8).t())
+    assert torch.all(u8(dgu8t)[:, T:] == 0)
+    torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES[:3])
+def test_down_dgrad_swiglu_random(dev, T, D, I):
+    g = torch.Generator().manual_seed(4 + T + D + I)
+    dy = (torch.randn(T, D, generator=g) * 1e-3).to(torch.bfloat16)
+    wd = (torch.randn(D, I, generator=g) * I ** -0.5).to(torch.bfloat16)
+    gu8 = O.e4m3(torch.randn(T, 2 * I, generator=g) * 64)
+    s = torch.tensor([1, 64.0, 1, 2.0 ** 18, 1])
+    amax = torch.zeros(5, device=dev)
+    dgu8, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), wd.t().contiguous().to(dev), gu8.to(dev), s.to(dev), amax)
+    rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
+    d = code_dist(dgu8, rdgu8)
+    assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.02
+    torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-2, atol=0)
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES)
+def test_gateup_dgrad_integer_operands(dev, T, D, I):
+    g = torch.Generator().manual_seed(5 + T + D + I)
+    dgu8 = int_fp8((T, 2 * I), E5, g)
+    w8 = int_fp8((2 * I, D), E4, g)
+    s = torch.tensor([1, 1, 1, 2.0 ** 5, 1])
+    ws = torch.tensor([2.0 ** 2, 1.0])
+    dxn = sg.ops.gateup_dgrad(dgu8.to(dev), w8.t().contiguous().to(dev), s.to(dev), ws.to(dev))
+    rdxn = O.gateup_dgrad(dgu8, w8, s, ws)
+    assert torch.equal(dxn.cpu(), rdxn)
+
+
+@pytest.mark.parametrize("T,M,N", [(1000, 256, 768), (257, 768, 128), (4099, 1024, 512), (65536, 256, 256)])
+def test_wgrad_integer_operands(dev, T, M, N):
+    g = torch.Generator().manual_seed(6 + T + M + N)
+    ldt = sg.ops.ldt_of(T)
+    a = int_fp8((T, M), E5, g, -4, 4)
+    b = int_fp8((T, N), E4, g, -4, 4)
+    at = torch.zeros(M, ldt, dtype=torch.uint8)
+    bt = torch.zeros(N, ldt, dtype=torch.uint8)
+    at[:, :T] = u8(a).t()
+    bt[:, :T] = u8(b).t()
+    sa, sb = torch.tensor([2.0 ** 3]), torch.tensor([0.5])
+    out = sg.ops.wgrad(at.view(E5).to(dev), bt.view(E4).to(dev), sa.to(dev), sb.to(dev))
+    ref = (a.float().t() @ b.float()) / (sa * sb)
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_wgrad_matches_oracle_forms(dev):
+    """Both weight gradients of the block through the kernel vs the oracle's
+    reference-shaped formulas (down: dy quantized e5m2 in 2 token splits;
+    gate/up: d_gu8^T x8)."""
+    T, D, I = 1000, 256, 768
+    g = torch.Generator().manual_seed(7)
+    dy = (torch.randn(T, D, generator=g) * 1e-3).to(torch.bfloat16)
+    h8 = O.e4m3(torch.randn(T, I, generator=g) * 30)
+    dgu8 = O.e5m2(torch.randn(T, 2 * I, generator=g) * 1000)
+    x8 = O.e4m3(torch.randn(T, D, generator=g) * 30)
+    s = torch.tensor([16.0, 1, 32.0, 2.0 ** 10, 2.0 ** 15])
+    ldt = sg.ops.ldt_of(T)
+
+    def tpad(t8):
+        out = torch.zeros(t8.shape[1], ldt, dtype=torch.uint8)
+        out[:, :T] = u8(t8).t()
+        return out.view(t8.dtype).to(dev)
+
+    dy8 = O.e5m2(dy.float() * s[4])
+    sd = s.to(dev)
+    dwd = sg.ops.wgrad(tpad(dy8), tpad(h8), sd[4:5], sd[2:3])
+    dwgu = sg.ops.wgrad(tpad(dgu8), tpad(x8), sd[3:4], sd[0:1])
+    torch.testing.assert_close(dwd.cpu(), O.down_wgrad(dy, h8, s), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(dwgu.cpu(), O.gateup_wgrad(dgu8, x8, s), rtol=1e-5, atol=1e-6)
