@@ -24,6 +24,7 @@ the independent second opinion that pins the torch-CPU oracle in
 from __future__ import annotations
 
 from decimal import Decimal, getcontext
+from functools import lru_cache
 
 import numpy as np
 
@@ -136,8 +137,13 @@ def band_nmax(K: int) -> int:
             return n
 
 
+@lru_cache(maxsize=None)
+def _band_table(kmin: int, kmax: int) -> tuple:
+    return tuple((K, band_nmax(K)) for K in range(kmin, kmax + 1))
+
+
 def band_table(kmin: int = -125, kmax: int = 128) -> dict[int, int]:
-    return {K: band_nmax(K) for K in range(kmin, kmax + 1)}
+    return dict(_band_table(kmin, kmax))
 
 
 def floor_log2_cr(r: np.ndarray) -> np.ndarray:
@@ -150,16 +156,26 @@ def floor_log2_cr(r: np.ndarray) -> np.ndarray:
     e = (bits >> 23) - 127
     m = bits & ((1 << 23) - 1)
     n = (1 << 23) - m
-    table = band_table()
-    nmax = np.array([table[int(k) + 1] for k in e.ravel()], dtype=np.int64).reshape(e.shape)
+    lut = np.array([n for _, n in _band_table(-125, 128)], dtype=np.int64)
+    K = e + 1
+    if np.any((K < -125) | (K > 128)):
+        raise ValueError("exponent outside the band table")
+    nmax = lut[K + 125]
     return e + ((m != 0) & (n <= nmax)).astype(np.int64)
 
 
-def pow2_scale(amax: np.ndarray, fmax: float, headroom: int) -> np.ndarray:
-    """exp2(floor(log2(fmax / max(amax, 1e-30))) - headroom) in fp32, exactly,
-    for finite amax >= 0 (spark-gpt ``train.py:943-944`` with headroom 1,
-    ``train.py:951`` with headroom 0)."""
+def pow2_scale(amax: np.ndarray, fmax: float, headroom: int, recip_first: bool = False) -> np.ndarray:
+    """exp2(floor(log2(r)) - headroom) in fp32, exactly, for finite amax >= 0.
+
+    r = fmax / max(amax, 1e-30) for the scale roll (spark-gpt ``train.py:943``,
+    a tensor/tensor divide, headroom 1); with ``recip_first`` r is
+    (1 / max(amax, 1e-30)) * fmax, which is how torch evaluates the weight rule
+    ``448.0 / tensor`` (``train.py:951``, headroom 0).  Each step is one
+    IEEE-rounded fp32 operation."""
     a = np.maximum(np.asarray(amax, dtype=np.float32), np.float32(1e-30))
-    r = (np.float32(fmax) / a).astype(np.float32)
+    if recip_first:
+        r = ((np.float32(1.0) / a).astype(np.float32) * np.float32(fmax)).astype(np.float32)
+    else:
+        r = (np.float32(fmax) / a).astype(np.float32)
     k = floor_log2_cr(r) - headroom
     return np.ldexp(np.float32(1.0), k.astype(np.int32)).astype(np.float32)

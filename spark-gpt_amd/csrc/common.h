@@ -55,19 +55,42 @@ SFP8_DEV float clamp_keep_nan(float x, float m) {
   return x;
 }
 
+// The gfx950 converters write an all-ones pattern (0xFF / 0xFE) for every NaN
+// input; torch writes 0x7F with the input's sign bit.  NaNs are rare, so the
+// fix-up runs only when one of the four inputs is NaN.
+SFP8_DEV uint32_t fix_nan4(uint32_t p, float a, float b, float c, float d) {
+  const float v[4] = {a, b, c, d};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (v[i] != v[i]) {
+      const uint32_t code = 0x7Fu | ((__float_as_uint(v[i]) >> 24) & 0x80u);
+      p = (p & ~(0xFFu << (8 * i))) | (code << (8 * i));
+    }
+  }
+  return p;
+}
+
+SFP8_DEV bool any_nan4(float a, float b, float c, float d) {
+  return (a != a) | (b != b) | (c != c) | (d != d);
+}
+
 // Four fp32 -> four e4m3 bytes packed little-endian (a = lowest byte).
 SFP8_DEV uint32_t pack4_e4m3(float a, float b, float c, float d) {
   int v = 0;
   v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_keep_nan(a, kE4M3Max), clamp_keep_nan(b, kE4M3Max), v, false);
   v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_keep_nan(c, kE4M3Max), clamp_keep_nan(d, kE4M3Max), v, true);
-  return (uint32_t)v;
+  uint32_t p = (uint32_t)v;
+  if (__builtin_expect(any_nan4(a, b, c, d), 0)) p = fix_nan4(p, a, b, c, d);
+  return p;
 }
 
 SFP8_DEV uint32_t pack4_e5m2(float a, float b, float c, float d) {
   int v = 0;
   v = __builtin_amdgcn_cvt_pk_bf8_f32(clamp_keep_nan(a, kE5M2Max), clamp_keep_nan(b, kE5M2Max), v, false);
   v = __builtin_amdgcn_cvt_pk_bf8_f32(clamp_keep_nan(c, kE5M2Max), clamp_keep_nan(d, kE5M2Max), v, true);
-  return (uint32_t)v;
+  uint32_t p = (uint32_t)v;
+  if (__builtin_expect(any_nan4(a, b, c, d), 0)) p = fix_nan4(p, a, b, c, d);
+  return p;
 }
 
 // fp8 byte -> fp32 (exact).  Hardware converter on gfx950.

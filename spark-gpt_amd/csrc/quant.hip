@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
   __syncthreads();
   if (threadIdx.x == 0) {
     const float a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float q = pow2_scale(a, kE4M3Max, 0);
+    const float q = pow2_scale(a, kE4M3Max, 0, true);
     qs = q;
     if (blockIdx.x == 0 && blockIdx.y == 0) *q_out = q;
   }
@@ -288,7 +288,7 @@ __global__ void update_scales_kernel(float* __restrict__ scale, float* __restric
   const int slot = i % 5;
   const float fmax = slot < 3 ? kE4M3Max : kE5M2Max;
   const float a = amax[i];
-  if (a > 0.0f) scale[i] = pow2_scale(a, fmax, headroom);
+  if (a > 0.0f) scale[i] = pow2_scale(a, fmax, headroom, false);
   amax[i] = 0.0f;
 }
 

@@ -28,12 +28,19 @@ __device__ __constant__ const uint8_t kLog2Band[254] = {
     44, 44, 44, 44, 44, 44, 44, 44, 44, 44, 44, 44, 44, 44,
 };
 
-// exp2(floor(log2(fmax / max(amax, 1e-30))) - headroom), fp32, for amax >= 0.
+// exp2(floor(log2(r)) - headroom), fp32, for amax >= 0, where
+//   r = fmax / max(amax, 1e-30)            (recip_first = false: the scale roll,
+//                                           tensor / tensor, train.py:943)
+//   r = (1 / max(amax, 1e-30)) * fmax      (recip_first = true: the weight rule
+//                                           `448.0 / tensor`, which torch
+//                                           evaluates as reciprocal(t) * 448,
+//                                           train.py:951)
+// each step an IEEE-rounded fp32 operation.
 // NaN amax gives NaN; +inf amax gives 0 (log2(0) = -inf, exp2(-inf) = 0).
-SFP8_DEV float pow2_scale(float amax, float fmax, int headroom) {
+SFP8_DEV float pow2_scale(float amax, float fmax, int headroom, bool recip_first) {
   if (amax != amax) return amax;
   const float a = fmaxf(amax, 1e-30f);
-  const float r = fmax / a;  // IEEE-rounded fp32 divide
+  const float r = recip_first ? (1.0f / a) * fmax : fmax / a;
   if (r == 0.0f) return 0.0f;
   const uint32_t b = __float_as_uint(r);
   const int e = (int)(b >> 23) - 127;  // r is normal: r >= 448 / 3.4e38

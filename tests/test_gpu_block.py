@@ -118,9 +118,3 @@ def test_block_deterministic(dev):
     for x, y in zip(a, b):
         assert torch.equal(x, y)
     assert torch.equal(amax_a, mlp.fp8_amax)
-
-
-def test_guard_and_module_state():
-    m = sg.MLP(256, 768)
-    assert set(dict(m.named_parameters())) == {"gate_up_proj.weight", "down_proj.weight"}
-    assert "fp8_scale" not in m.state_dict() and "fp8_amax" not in m.state_dict()

@@ -107,12 +107,12 @@ def _band_amax(fmax: float) -> list[float]:
     power of two (where the rounded log2 decides the binade)."""
     out = []
     for K in (-20, -7, -3, 2, 3, 5, 8, 9, 17, 40):
-        base = np.float32(2.0 ** K).view(np.uint32)
+        base = int(np.float32(2.0 ** K).view(np.uint32))
         for n in range(0, 50, 3):
             r = np.array([base - n], dtype=np.uint32).view(np.float32)[0]
-            a = np.float32(np.float32(fmax) / r)
+            a = int(np.float32(np.float32(fmax) / r).view(np.uint32))
             for da in range(-2, 3):
-                cand = np.array([a.view(np.uint32) + da], dtype=np.uint32).view(np.float32)[0]
+                cand = np.array([a + da], dtype=np.uint32).view(np.float32)[0]
                 out.append(float(cand))
     return out
 

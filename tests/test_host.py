@@ -1,0 +1,154 @@
+"""CPU tests of the host side: the C-ABI library loads and exports exactly the
+entry points include/sparkfp8.h declares (no kernel is launched), the device
+constant tables match the oracle's derivation, and the Python mirror of the
+reference interface (guard, module state, scale roll plumbing) behaves like
+spark-gpt train.py:914-946 / 247-262."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+import torch.nn as nn
+
+import spark_gpt_amd as sg
+from spark_gpt_amd import _lib, ops
+from oracle import fp8_bits
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sparkfp8.h")
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    return {n: t for t, n in re.findall(r"^\s*(int|int64_t)\s+(sfp8_\w+)\s*\(", text, flags=re.M)}
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    decl = header_functions()
+    assert len(decl) >= 14
+    for name in decl:
+        assert hasattr(lib, name), name
+    # ctypes table covers exactly the declared functions, with matching return types
+    assert set(_lib.SIGNATURES) == set(decl)
+    for name, ret in decl.items():
+        want = ctypes.c_int64 if ret == "int64_t" else ctypes.c_int
+        assert _lib.SIGNATURES[name][0] is want, name
+
+
+def test_header_argument_counts_match_binding():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for m in re.finditer(r"(sfp8_\w+)\s*\(([^)]*)\)\s*;", text):
+        name, args = m.group(1), m.group(2)
+        n = len([a for a in args.split(",") if a.strip()])
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+
+
+def test_size_queries_need_no_gpu():
+    assert _lib.query("sfp8_norm_bwd_partials", 1024, 65536) == 65536 // 64
+    assert _lib.query("sfp8_norm_bwd_partials", 4096, 16384) == 16384 // 16
+    assert _lib.query("sfp8_norm_bwd_partials", 96, 256) == -1
+    s = _lib.query("sfp8_wgrad_splits", 6144, 1024, 65536)
+    assert s >= 1 and 65536 % s == 0 and (65536 // s) % 128 == 0
+    assert _lib.query("sfp8_wgrad_workspace_floats", 6144, 1024, 65536) == (s * 6144 * 1024 if s > 1 else 0)
+    assert _lib.query("sfp8_wgrad_splits", 256, 256, 256) == 1
+
+
+def test_invalid_arguments_rejected_before_launch():
+    lib = _lib.load()
+    # null pointers and bad shapes return negative codes without touching the device
+    assert lib.sfp8_update_scales(None, None, 1, None) == -1
+    assert lib.sfp8_quant_e4m3_rowcol(None, 4, 100, None, None, None, None, 4, None) == -1
+    assert lib.sfp8_gemm_wgrad(16, 0, 16, 0, 256, 256, 256, 16, 16, 16, 16, 0, None) == -2  # A must be e5m2
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _lib.check(-1, "x")
+    with pytest.raises(RuntimeError, match="HIP error 1"):
+        _lib.check(1, "x")
+
+
+def test_device_band_table_matches_oracle():
+    src = open(os.path.join(ROOT, "spark-gpt_amd", "csrc", "scale.h")).read()
+    body = src[src.index("kLog2Band[254] = {") + len("kLog2Band[254] = {"):]
+    body = body[: body.index("};")]
+    vals = [int(v) for v in body.replace("\n", " ").split(",") if v.strip()]
+    want = fp8_bits.band_table(-125, 128)
+    assert vals == [want[k] for k in range(-125, 129)]
+
+
+def test_ops_reject_host_tensors():
+    h = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises((ValueError, RuntimeError)):
+        ops.norm_quant(h, torch.ones(128), torch.ones(5), torch.zeros(5), 1e-6)
+    with pytest.raises((ValueError, RuntimeError)):
+        ops.quant_e4m3_rowcol(h, torch.ones(5), torch.zeros(5))
+
+
+def test_ldt_padding():
+    assert ops.ldt_of(0) == 0 and ops.ldt_of(1) == 256 and ops.ldt_of(256) == 256 and ops.ldt_of(1000) == 1024
+
+
+def test_constants_match_reference_recipe():
+    assert sg.FP8_SITE_MAX == (448.0, 448.0, 448.0, 57344.0, 57344.0)
+    assert sg.FP8_HEADROOM_BINADES == 1
+
+
+def test_mlp_module_state_names():
+    m = sg.MLP(256, 768)
+    assert set(dict(m.named_parameters())) == {"gate_up_proj.weight", "down_proj.weight"}
+    assert m.gate_up_proj.weight.shape == (1536, 256) and m.down_proj.weight.shape == (256, 768)
+    assert "fp8_scale" not in m.state_dict() and "fp8_amax" not in m.state_dict()
+    assert torch.equal(m.fp8_scale, torch.ones(5)) and torch.equal(m.fp8_amax, torch.zeros(5))
+    x = torch.randn(3, 256)
+    g, u = m.gate_up_proj(x).chunk(2, -1)
+    torch.testing.assert_close(m(x), m.down_proj(torch.nn.functional.silu(g) * u))
+
+
+class _FakeBlock(nn.Module):
+    def __init__(self, d, inter, sparse=False):
+        super().__init__()
+        self.is_sparse = sparse
+        if not sparse:
+            self.mlp = sg.MLP(d, inter)
+
+
+class _FakeCudaTensor:
+    """Stands in for a device tensor in the guard (it reads only attributes)."""
+
+    def __init__(self, shape, dtype=torch.bfloat16, is_cuda=True):
+        self.shape, self.dtype, self.is_cuda = shape, dtype, is_cuda
+
+
+@pytest.mark.parametrize("d,inter,ok", [(1024, 3072, True), (256, 768, True), (384, 768, False),
+                                        (1024, 3000, False), (8192, 1024, False), (128, 128, True)])
+def test_guard_predicate(monkeypatch, d, inter, ok):
+    from spark_gpt_amd import mlp as M
+
+    monkeypatch.setattr(M, "FP8_MLP", True)
+    b = _FakeBlock(d, inter).train()
+    assert M._use_fp8_mlp(b, _FakeCudaTensor((10, d))) is ok
+    b.eval()
+    assert M._use_fp8_mlp(b, _FakeCudaTensor((10, d))) is False
+    b.train()
+    assert M._use_fp8_mlp(b, _FakeCudaTensor((10, d), dtype=torch.float32)) is False
+    assert M._use_fp8_mlp(b, _FakeCudaTensor((10, d), is_cuda=False)) is False
+    monkeypatch.setattr(M, "FP8_MLP", False)
+    assert M._use_fp8_mlp(b, _FakeCudaTensor((10, d))) is False
+
+
+def test_guard_checks_sparse_first(monkeypatch):
+    """Regression of spark-gpt tests/test_fp8_mlp.py:113-140: a sparse block has
+    no down_proj and the guard must not touch it."""
+    from spark_gpt_amd import mlp as M
+
+    monkeypatch.setattr(M, "FP8_MLP", True)
+    b = _FakeBlock(256, 768, sparse=True).train()
+    assert M._use_fp8_mlp(b, _FakeCudaTensor((10, 256))) is False
+
+
+def test_update_scales_walks_every_fp8_module(monkeypatch):
+    seen = []
+    monkeypatch.setattr(ops, "update_scales", lambda s, a: seen.append((s, a)))
+    model = nn.Sequential(sg.MLP(128, 256), nn.Linear(4, 4), nn.Sequential(sg.MLP(128, 256)))
+    sg.fp8_update_scales(model)
+    assert len(seen) == 2
