@@ -74,11 +74,14 @@ SFP8_DEV bool any_nan4(float a, float b, float c, float d) {
   return (a != a) | (b != b) | (c != c) | (d != d);
 }
 
-// Four fp32 -> four e4m3 bytes packed little-endian (a = lowest byte).
+// Four fp32 -> four e4m3 bytes packed little-endian (a = lowest byte).  The
+// clamp is one v_med3 per value; the converter itself does not saturate.
 SFP8_DEV uint32_t pack4_e4m3(float a, float b, float c, float d) {
   int v = 0;
-  v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_keep_nan(a, kE4M3Max), clamp_keep_nan(b, kE4M3Max), v, false);
-  v = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_keep_nan(c, kE4M3Max), clamp_keep_nan(d, kE4M3Max), v, true);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, -kE4M3Max, kE4M3Max),
+                                      __builtin_amdgcn_fmed3f(b, -kE4M3Max, kE4M3Max), v, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(c, -kE4M3Max, kE4M3Max),
+                                      __builtin_amdgcn_fmed3f(d, -kE4M3Max, kE4M3Max), v, true);
   uint32_t p = (uint32_t)v;
   if (__builtin_expect(any_nan4(a, b, c, d), 0)) p = fix_nan4(p, a, b, c, d);
   return p;
@@ -86,11 +89,33 @@ SFP8_DEV uint32_t pack4_e4m3(float a, float b, float c, float d) {
 
 SFP8_DEV uint32_t pack4_e5m2(float a, float b, float c, float d) {
   int v = 0;
-  v = __builtin_amdgcn_cvt_pk_bf8_f32(clamp_keep_nan(a, kE5M2Max), clamp_keep_nan(b, kE5M2Max), v, false);
-  v = __builtin_amdgcn_cvt_pk_bf8_f32(clamp_keep_nan(c, kE5M2Max), clamp_keep_nan(d, kE5M2Max), v, true);
+  v = __builtin_amdgcn_cvt_pk_bf8_f32(__builtin_amdgcn_fmed3f(a, -kE5M2Max, kE5M2Max),
+                                      __builtin_amdgcn_fmed3f(b, -kE5M2Max, kE5M2Max), v, false);
+  v = __builtin_amdgcn_cvt_pk_bf8_f32(__builtin_amdgcn_fmed3f(c, -kE5M2Max, kE5M2Max),
+                                      __builtin_amdgcn_fmed3f(d, -kE5M2Max, kE5M2Max), v, true);
   uint32_t p = (uint32_t)v;
   if (__builtin_expect(any_nan4(a, b, c, d), 0)) p = fix_nan4(p, a, b, c, d);
   return p;
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> two bf16 (hardware round-to-nearest-even), packed lo/hi.
+SFP8_DEV uint32_t pack2_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{a, b}, bf16x2_t));
+}
+
+// Round two fp32 values to bf16 precision (returned as fp32).
+SFP8_DEV void round2_bf16(float& a, float& b) {
+  const uint32_t p = pack2_bf16(a, b);
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+
+// Logistic sigmoid with the hardware exp2 / reciprocal (about 1 ulp each).
+SFP8_DEV float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
 // fp8 byte -> fp32 (exact).  Hardware converter on gfx950.

@@ -2,14 +2,9 @@
 //
 // Every GEMM here is C[m, n] = sum_k A[m, k] * B[n, k]: both operands are
 // K-contiguous rows in HBM.  One work-group (256 threads = 4 waves, one wave
-// per SIMD) computes a 256 x 256 output tile; each wave owns 128 x 128 as
-// 4 x 4 blocks of 32 x 32 MFMA accumulators (256 fp32 per lane).
-//
-// Main loop: stages of 128 bytes of K (64 fp8 / 64 bf16 elements... per row:
-// 128 fp8 or 64 bf16) are copied global -> registers -> LDS, double-buffered,
-// one barrier per stage.  LDS rows are 128 bytes with 16-byte chunk c of row r
-// stored at chunk (c ^ (r & 7)), so both the row-wise fills and the
-// 32-rows-by-16-bytes fragment reads are free of bank conflicts.
+// per SIMD) computes a 256 x 256 output tile with the pipelined main loop of
+// mainloop.h; each wave owns 128 x 128 as 4 x 4 blocks of 32 x 32 MFMA
+// accumulators.
 //
 // MFMA: v_mfma_f32_32x32x64_f8f6f4 (e4m3/e5m2 chosen per operand) or
 // v_mfma_f32_32x32x16_bf16.  The B fragment is passed as the instruction's
@@ -18,21 +13,12 @@
 // block is (m = lane % 32, n = 8*(v/4) + 4*(lane/32) + v%4).  Row-major
 // epilogue stores are therefore 4-element runs.  Within one instruction both
 // operands use the same (lane-half, byte) -> k assignment, so any consistent
-// placement of K inside a 64-byte fragment gives the same dot product; lane
-// half g reads bytes [64g, 64g+64) of each 128-byte stage row.
+// placement of K inside a fragment gives the same dot product.
 #include "common.h"
+#include "mainloop.h"
 #include "scale.h"
 
 namespace sfp8 {
-
-constexpr int kTile = 256;       // rows of the A tile and of the B tile
-constexpr int kStageK = 128;     // bytes of K per stage
-constexpr int kStageBytes = 2 * kTile * kStageK;  // A + B, 64 KiB
-constexpr int kMainLds = 2 * kStageBytes;          // double buffered, 128 KiB
-constexpr int kFmtE4M3 = 0;
-constexpr int kFmtE5M2 = 1;
-
-SFP8_DEV int swz(int row, int chunk) { return row * kStageK + ((chunk ^ (row & 7)) << 4); }
 
 // Work-group -> tile mapping.  Work-groups are dispatched round-robin over
 // the 8 XCDs; consecutive logical tiles are placed on the same XCD (each XCD
@@ -50,123 +36,9 @@ SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, i
   tn = (lid % group) / gsz;
 }
 
-// Main loop.  a_off/b_off: per-thread byte offsets (from a_base/b_base) of the
-// 8 A rows and 8 B rows this thread copies (rows tid/8 + 32*i, chunk tid%8).
-// wb_row[nb]: LDS row (within the B tile) of this wave's B block nb.
-template <bool BF16, int FMT_A, int FMT_B>
-SFP8_DEV void mainloop(const uint8_t* __restrict__ a_base, const int (&a_off)[8],
-                       const uint8_t* __restrict__ b_base, const int (&b_off)[8], int64_t k_begin,
-                       int nk, uint8_t* lds, const int (&wb_row)[4], int wa_row, floatx16 (&acc)[4][4]) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int chunk = tid & 7;
-  const int wrow0 = tid >> 3;
-  const int lds_w = swz(wrow0, chunk);  // + i * 32 rows
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
-                                                     0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  intx4 ra[8], rb[8];
-  const uint8_t* ag = a_base + k_begin + chunk * 16;
-  const uint8_t* bg = b_base + k_begin + chunk * 16;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    ra[i] = *reinterpret_cast<const intx4*>(ag + a_off[i]);
-    rb[i] = *reinterpret_cast<const intx4*>(bg + b_off[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    *reinterpret_cast<intx4*>(lds + lds_w + i * 32 * kStageK) = ra[i];
-    *reinterpret_cast<intx4*>(lds + kTile * kStageK + lds_w + i * 32 * kStageK) = rb[i];
-  }
-  __syncthreads();
-
-  const int fr = lane & 31, g = lane >> 5;
-  for (int kt = 0; kt < nk; ++kt) {
-    uint8_t* buf = lds + (kt & 1) * kStageBytes;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const int64_t ko = (int64_t)(kt + 1) * kStageK;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ra[i] = *reinterpret_cast<const intx4*>(ag + ko + a_off[i]);
-        rb[i] = *reinterpret_cast<const intx4*>(bg + ko + b_off[i]);
-      }
-    }
-    if constexpr (!BF16) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        intx8 af[4], bfr[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const int r = wa_row + 32 * tb + fr;
-          const intx4 lo = *reinterpret_cast<const intx4*>(buf + swz(r, 4 * g + 2 * c));
-          const intx4 hi = *reinterpret_cast<const intx4*>(buf + swz(r, 4 * g + 2 * c + 1));
-          af[tb] = intx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int r = kTile + wb_row[nb] + fr;
-          const intx4 lo = *reinterpret_cast<const intx4*>(buf + swz(r, 4 * g + 2 * c));
-          const intx4 hi = *reinterpret_cast<const intx4*>(buf + swz(r, 4 * g + 2 * c + 1));
-          bfr[nb] = intx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-            acc[tb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                bfr[nb], af[tb], acc[tb][nb], FMT_B, FMT_A, 0, 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        bf16x8 af[4], bfr[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const int r = wa_row + 32 * tb + fr;
-          af[tb] = *reinterpret_cast<const bf16x8*>(buf + swz(r, 4 * g + c));
-        }
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int r = kTile + wb_row[nb] + fr;
-          bfr[nb] = *reinterpret_cast<const bf16x8*>(buf + swz(r, 4 * g + c));
-        }
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-            acc[tb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[nb], af[tb], acc[tb][nb], 0, 0, 0);
-      }
-    }
-    if (more) {
-      uint8_t* nbuf = lds + ((kt + 1) & 1) * kStageBytes;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        *reinterpret_cast<intx4*>(nbuf + lds_w + i * 32 * kStageK) = ra[i];
-        *reinterpret_cast<intx4*>(nbuf + kTile * kStageK + lds_w + i * 32 * kStageK) = rb[i];
-      }
-    }
-    __syncthreads();
-  }
-}
-
-// Row offsets for the A tile (rows m0.., clamped to M-1).
-SFP8_DEV void a_offsets(int64_t m0, int64_t M, int64_t lda, int (&off)[8]) {
-  const int r0 = threadIdx.x >> 3;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int64_t m = m0 + r0 + 32 * i;
-    m = m < M ? m : M - 1;
-    off[i] = (int)((m - m0) * lda);
-  }
-}
-
 SFP8_DEV floatx16 zero16() {
   return floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 }
-
-SFP8_DEV float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // Row-major copy-out of a byte tile staged in LDS: rows x cols bytes (cols
 // multiple of 16), row r -> out + r*ldo, rows >= rows_valid skipped.
@@ -228,18 +100,10 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  int a_off[8], b_off[8];
-  a_offsets(m0, T, D, a_off);
-  const uint8_t* b_base = w8 + n0 * D;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = (tid >> 3) + 32 * i;
-    b_off[i] = (int)((r < 128 ? (int64_t)r : I + (r - 128)) * D);
-  }
-  const int wb_row[4] = {64 * wn, 64 * wn + 32, 128 + 64 * wn, 128 + 64 * wn + 32};
   floatx16 acc[4][4];
-  mainloop<false, kFmtE4M3, kFmtE4M3>(x8 + m0 * D, a_off, b_base, b_off, 0, (int)(D / kStageK), lds,
-                                      wb_row, 128 * wm, acc);
+  MainLoop<false, kFmtE4M3, kFmtE4M3, true>::run(
+      lds, x8 + m0 * D, (T - m0) * D, [=](int r) { return r * (int)D; }, w8 + n0 * D, (2 * I - n0) * D,
+      [=](int r) { return (r < 128 ? r : (int)I + r - 128) * (int)D; }, 0, (int)(D / kStage), acc);
   // ---- epilogue
   const float deq = 1.0f / (scale[0] * wscale[0]);
   const float q1 = scale[1], q2 = scale[2];
@@ -259,21 +123,32 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
         float gg[4], uu[4], hh[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          gg[e] = round_bf16(acc[tb][nb][4 * q + e] * deq);
-          uu[e] = round_bf16(acc[tb][nb + 2][4 * q + e] * deq);
-          hh[e] = gg[e] * sigmoidf_(gg[e]) * uu[e];
-          if (valid) {
-            m_gu = fmaxf(m_gu, fmaxf(fabsf(gg[e]), fabsf(uu[e])));
-            m_h = fmaxf(m_h, fabsf(hh[e]));
-          }
+          gg[e] = acc[tb][nb][4 * q + e] * deq;
+          uu[e] = acc[tb][nb + 2][4 * q + e] * deq;
+        }
+        // g, u rounded to bf16 as in the bf16 path (train.py:1006-1007)
+        round2_bf16(gg[0], gg[1]);
+        round2_bf16(gg[2], gg[3]);
+        round2_bf16(uu[0], uu[1]);
+        round2_bf16(uu[2], uu[3]);
+        float mg = 0.f, mh = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hh[e] = gg[e] * sigmoid_fast(gg[e]) * uu[e];
+          mg = fmaxf(mg, fmaxf(fabsf(gg[e]), fabsf(uu[e])));
+          mh = fmaxf(mh, fabsf(hh[e]));
+        }
+        if (valid) {
+          m_gu = fmaxf(m_gu, mg);
+          m_h = fmaxf(m_h, mh);
         }
         const int col = 64 * wn + 32 * nb + 8 * q + 4 * g;  // column within the 128-wide tile
         const uint32_t pg = pack4_e4m3(gg[0] * q1, gg[1] * q1, gg[2] * q1, gg[3] * q1);
         const uint32_t pu = pack4_e4m3(uu[0] * q1, uu[1] * q1, uu[2] * q1, uu[3] * q1);
-        const uint32_t ph = valid ? pack4_e4m3(hh[0] * q2, hh[1] * q2, hh[2] * q2, hh[3] * q2) : 0u;
+        const uint32_t ph = pack4_e4m3(hh[0] * q2, hh[1] * q2, hh[2] * q2, hh[3] * q2);
         *reinterpret_cast<uint32_t*>(Gt + row * kEpiStride + col) = pg;
         *reinterpret_cast<uint32_t*>(Ut + row * kEpiStride + col) = pu;
-        *reinterpret_cast<uint32_t*>(Ht + row * kEpiStride + col) = ph;
+        *reinterpret_cast<uint32_t*>(Ht + row * kEpiStride + col) = valid ? ph : 0u;
       }
     }
   }
@@ -294,17 +169,6 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Plain-tile B offsets: B rows n0.. (clamped to N-1).
-SFP8_DEV void b_offsets_plain(int64_t n0, int64_t N, int64_t ldb, int (&off)[8]) {
-  const int r0 = threadIdx.x >> 3;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int64_t n = n0 + r0 + 32 * i;
-    n = n < N ? n : N - 1;
-    off[i] = (int)((n - n0) * ldb);
-  }
-}
-
 // (a7) down forward + residual (spark-gpt train.py:1019-1046):
 //   y = bf16(res + bf16(acc / (s2 * q_d)))
 __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
@@ -317,13 +181,11 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  int a_off[8], b_off[8];
-  a_offsets(m0, T, I, a_off);
-  b_offsets_plain(n0, D, I, b_off);
   const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
-  mainloop<false, kFmtE4M3, kFmtE4M3>(h8 + m0 * I, a_off, wd8 + n0 * I, b_off, 0, (int)(I / kStageK), lds,
-                                      wb_row, 128 * wm, acc);
+  MainLoop<false, kFmtE4M3, kFmtE4M3, false>::run(
+      lds, h8 + m0 * I, (T - m0) * I, [=](int r) { return r * (int)I; }, wd8 + n0 * I, (D - n0) * I,
+      [=](int r) { return r * (int)I; }, 0, (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[1]);
   const int fr = lane & 31, g = lane >> 5;
 #pragma unroll
@@ -339,14 +201,16 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
         const intx2 rv = *reinterpret_cast<const intx2*>(res + t * D + n);
         float o[4];
 #pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = acc[tb][nb][4 * q + e] * deq;
+        // out rounded to bf16 before the residual add (train.py:1043)
+        round2_bf16(o[0], o[1]);
+        round2_bf16(o[2], o[3]);
+#pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t u = (uint32_t)rv[e >> 1];
-          const float r = bf16_bits_to_f32((e & 1) ? (u >> 16) : (u & 0xffffu));
-          o[e] = r + round_bf16(acc[tb][nb][4 * q + e] * deq);
+          o[e] += bf16_bits_to_f32((e & 1) ? (u >> 16) : (u & 0xffffu));
         }
-        *reinterpret_cast<intx2*>(y + t * D + n) =
-            intx2{(int)(f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16)),
-                  (int)(f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16))};
+        *reinterpret_cast<intx2*>(y + t * D + n) = intx2{(int)pack2_bf16(o[0], o[1]), (int)pack2_bf16(o[2], o[3])};
       }
   }
 }
@@ -371,14 +235,12 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t ldb = D * 2;  // bytes
-  int a_off[8], b_off[8];
-  a_offsets(m0, T, ldb, a_off);
-  b_offsets_plain(n0, I, ldb, b_off);
   const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
-  mainloop<true, 0, 0>(reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, a_off,
-                       reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, b_off, 0, (int)(ldb / kStageK), lds,
-                       wb_row, 128 * wm, acc);
+  MainLoop<true, 0, 0, false>::run(
+      lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
+      reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb, [=](int r) { return r * (int)ldb; }, 0,
+      (int)(ldb / kStage), acc);
   const float s_gu = 1.0f / scale[1];
   const float q3 = scale[3];
   uint8_t* Gt = lds;
@@ -400,15 +262,19 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
         if (valid && j < I) {
           const uint32_t wg = *reinterpret_cast<const uint32_t*>(gu8 + t * 2 * I + j);
           const uint32_t wu = *reinterpret_cast<const uint32_t*>(gu8 + t * 2 * I + I + j);
-          float dg[4], du[4];
+          float dh[4], dg[4], du[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dh[e] = acc[tb][nb][4 * q + e];
+          // dh rounded to bf16 (train.py:1082)
+          round2_bf16(dh[0], dh[1]);
+          round2_bf16(dh[2], dh[3]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float dh = round_bf16(acc[tb][nb][4 * q + e]);
             const float gv = e4m3_to_f32(wg, e) * s_gu;
             const float uv = e4m3_to_f32(wu, e) * s_gu;
-            const float sg = sigmoidf_(gv);
-            dg[e] = dh * uv * (sg * (1.0f + gv * (1.0f - sg)));
-            du[e] = dh * gv * sg;
+            const float sg = sigmoid_fast(gv);
+            dg[e] = dh[e] * uv * (sg * (1.0f + gv * (1.0f - sg)));
+            du[e] = dh[e] * gv * sg;
             m3 = fmaxf(m3, fmaxf(fabsf(dg[e]), fabsf(du[e])));
           }
           pg = pack4_e5m2(dg[0] * q3, dg[1] * q3, dg[2] * q3, dg[3] * q3);
@@ -442,13 +308,11 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t K = 2 * I;
-  int a_off[8], b_off[8];
-  a_offsets(m0, T, K, a_off);
-  b_offsets_plain(n0, D, K, b_off);
   const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
-  mainloop<false, kFmtE5M2, kFmtE4M3>(dgu8 + m0 * K, a_off, w8t + n0 * K, b_off, 0, (int)(K / kStageK), lds,
-                                      wb_row, 128 * wm, acc);
+  MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
+      lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, w8t + n0 * K, (D - n0) * K,
+      [=](int r) { return r * (int)K; }, 0, (int)(K / kStage), acc);
   const float sa = 1.0f / scale[3], sb = 1.0f / wscale[0];
   const int fr = lane & 31, g = lane >> 5;
 #pragma unroll
@@ -464,9 +328,7 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = acc[tb][nb][4 * q + e] * sa * sb;
-        *reinterpret_cast<intx2*>(dxn + t * D + n) =
-            intx2{(int)(f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16)),
-                  (int)(f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16))};
+        *reinterpret_cast<intx2*>(dxn + t * D + n) = intx2{(int)pack2_bf16(o[0], o[1]), (int)pack2_bf16(o[2], o[3])};
       }
   }
 }
@@ -489,14 +351,12 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  int a_off[8], b_off[8];
-  a_offsets(m0, M, ldt, a_off);
-  b_offsets_plain(n0, N, ldt, b_off);
   const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
   const int64_t kb = (int64_t)blockIdx.y * kchunk;
-  mainloop<false, FMT_A, FMT_B>(at + m0 * ldt, a_off, bt + n0 * ldt, b_off, kb, (int)(kchunk / kStageK), lds,
-                                wb_row, 128 * wm, acc);
+  MainLoop<false, FMT_A, FMT_B, false>::run(
+      lds, at + m0 * ldt, (M - m0) * ldt, [=](int r) { return r * (int)ldt; }, bt + n0 * ldt, (N - n0) * ldt,
+      [=](int r) { return r * (int)ldt; }, kb, (int)(kchunk / kStage), acc);
   const bool split = gridDim.y > 1;
   const float deq = split ? 1.0f : 1.0f / (sa[0] * sb[0]);
   float* dst = out + (split ? (int64_t)blockIdx.y * M * N : 0);
@@ -557,7 +417,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
                                 void* h8t, int64_t ldt, void* stream) {
   if (!x8 || !w8 || !scale || !wscale || !amax || !gu8 || !h8 || !h8t) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || D % kStageK || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || D % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
   if (!fits32(kTile, D) || !fits32(2 * I, D)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -573,7 +433,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
 int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
                        const float* scale, const float* wscale, void* y, void* stream) {
   if (!h8 || !wd8 || !res || !scale || !wscale || !y) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || I % kStageK || D % 4) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 4) return kErrBadShape;
   if (!fits32(kTile, I)) return kErrBadShape;
   if (!al16(h8) || !al16(wd8) || !al16(res) || !al16(y)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -590,7 +450,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream) {
   if (!dy || !wdt || !gu8 || !scale || !amax || !dgu8 || !dgu8t) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || (2 * D) % kStageK || I % 16 || ldt < T || ldt % kTile) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 16 || ldt < T || ldt % kTile) return kErrBadShape;
   if (!fits32(kTile, 2 * D)) return kErrBadShape;
   if (!al16(dy) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -606,7 +466,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
 int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
                            const float* scale, const float* wscale, void* dxn, void* stream) {
   if (!dgu8 || !w8t || !scale || !wscale || !dxn) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || (2 * I) % kStageK || D % 4) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 4) return kErrBadShape;
   if (!fits32(kTile, 2 * I)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -624,7 +484,8 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
 int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
   const int64_t tiles = (int64_t)cdiv(M, kTile) * cdiv(N, kTile);
   int64_t s = 1;
-  while (tiles * s < 512 && (ldt / (s * 2)) % kStageK == 0 && ldt / (s * 2) >= 2048) s *= 2;
+  while (tiles * s < 512 && ldt % (s * 2) == 0 && (ldt / (s * 2)) % (2 * kStage) == 0 && ldt / (s * 2) >= 2048)
+    s *= 2;
   return s;
 }
 

@@ -371,8 +371,7 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
       if (valid) {
         intx4 ov;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          ov[j] = (int)(f32_to_bf16_bits(o[2 * j]) | (f32_to_bf16_bits(o[2 * j + 1]) << 16));
+        for (int j = 0; j < 4; ++j) ov[j] = (int)pack2_bf16(o[2 * j], o[2 * j + 1]);
         *reinterpret_cast<intx4*>(dh + t * D + d) = ov;
         lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
         hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
@@ -404,14 +403,20 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   block_amax_atomic<4>(m, red, amax + 4);
 }
 
-// Fixed-order column sums: out[d] = sum_b part[b][d] (b ascending).
+// Fixed-order column sums: out[d] = sum_b part[b][d].  Work-group x owns 64
+// columns; thread (r, c) sums rows r, r+4, r+8, ... of column c in ascending
+// order, then the 4 partial sums are added in the order r = 0, 1, 2, 3.
 __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, int64_t nb,
                                                      int64_t D, float* __restrict__ out) {
-  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (d >= D) return;
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, r = threadIdx.x >> 6;
+  const int64_t d = (int64_t)blockIdx.x * 64 + c;
   float s = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) s += part[b * D + d];
-  out[d] = s;
+  if (d < D)
+    for (int64_t b = r; b < nb; b += 4) s += part[b * D + d];
+  red[r][c] = s;
+  __syncthreads();
+  if (r == 0 && d < D) out[d] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
 }
 
 // Split-K reduction: out = (sum_s ws[s]) * (1 / (sa * sb)), s ascending.
@@ -475,7 +480,7 @@ static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, co
   hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, rstd,
                      (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, scale, amax, (uint16_t*)dh, part,
                      (uint8_t*)dy8t, ldt);
-  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, part,
+  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, st, part,
                      (int64_t)nblk, (int64_t)D, dnw);
   return launch_status();
 }
