@@ -98,6 +98,35 @@ SFP8_DEV uint32_t pack4_e5m2(float a, float b, float c, float d) {
   return p;
 }
 
+// Scaled conversions: bytes of e4m3/e5m2(clamp(x * m)) for a power-of-two m,
+// given inv_m = 1/m and bound = fmax/m.  Clamping x to +-bound before the
+// scaling is the same as clamping x*m to +-fmax because m is a power of two;
+// the converter divides by its scale operand.  NaN inputs are left to the
+// caller (med3 maps NaN to -bound).
+typedef short shortx2 __attribute__((ext_vector_type(2)));
+
+template <bool HI>
+SFP8_DEV uint32_t pack2_e4m3_scaled(uint32_t old, float a, float b, float inv_m, float bound) {
+  const shortx2 o = __builtin_bit_cast(shortx2, old);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(
+      o, __builtin_amdgcn_fmed3f(a, -bound, bound), __builtin_amdgcn_fmed3f(b, -bound, bound), inv_m, HI));
+}
+
+template <bool HI>
+SFP8_DEV uint32_t pack2_e5m2_scaled(uint32_t old, float a, float b, float inv_m, float bound) {
+  const shortx2 o = __builtin_bit_cast(shortx2, old);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(
+      o, __builtin_amdgcn_fmed3f(a, -bound, bound), __builtin_amdgcn_fmed3f(b, -bound, bound), inv_m, HI));
+}
+
+SFP8_DEV uint32_t pack4_e4m3_scaled(float a, float b, float c, float d, float inv_m, float bound) {
+  return pack2_e4m3_scaled<true>(pack2_e4m3_scaled<false>(0u, a, b, inv_m, bound), c, d, inv_m, bound);
+}
+
+SFP8_DEV uint32_t pack4_e5m2_scaled(float a, float b, float c, float d, float inv_m, float bound) {
+  return pack2_e5m2_scaled<true>(pack2_e5m2_scaled<false>(0u, a, b, inv_m, bound), c, d, inv_m, bound);
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 

@@ -8,12 +8,17 @@
 //
 // MFMA: v_mfma_f32_32x32x64_f8f6f4 (e4m3/e5m2 chosen per operand) or
 // v_mfma_f32_32x32x16_bf16.  The B fragment is passed as the instruction's
-// first operand and the A fragment as its second, so each lane ends up holding
-// ONE row m (lane % 32) and runs of 4 consecutive n: element v of a 32x32
-// block is (m = lane % 32, n = 8*(v/4) + 4*(lane/32) + v%4).  Row-major
-// epilogue stores are therefore 4-element runs.  Within one instruction both
+// first operand and the A fragment as its second, so each lane holds ONE A
+// row (lane % 32) and, in a 32x32 block, 16 accumulators for B-tile rows
+// 8*(v/4) + 4*(lane/32) + v%4, v = 0..15.  Within one instruction both
 // operands use the same (lane-half, byte) -> k assignment, so any consistent
 // placement of K inside a fragment gives the same dot product.
+//
+// Output-column permutation: the B tile is filled with its rows permuted
+// (plain_col / paired_col below), so that accumulator v of block nb of the
+// lane in half g is output column  base + 16*nb + v  -- 16 (and across blocks
+// 64 or 32) consecutive columns per lane.  Every epilogue access is then a
+// 16-byte vector; LDS staging remains only for the transposed copies.
 #include "common.h"
 #include "mainloop.h"
 #include "scale.h"
@@ -36,24 +41,26 @@ SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, i
   tn = (lid % group) / gsz;
 }
 
-SFP8_DEV floatx16 zero16() {
-  return floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+// Output column (within the 256-column tile) held in B-tile row r, plain
+// layout: wave column wn owns rows 128*wn.., lane half g of block nb element
+// v (row 32*nb + 8*(v/4) + 4*g + v%4) gets column 128*wn + 64*g + 16*nb + v.
+SFP8_DEV int plain_col(int r) {
+  const int rl = r & 127;
+  return (r & 128) + 64 * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
 }
 
-// Row-major copy-out of a byte tile staged in LDS: rows x cols bytes (cols
-// multiple of 16), row r -> out + r*ldo, rows >= rows_valid skipped.
-SFP8_DEV void lds_tile_store_rows(const uint8_t* lds, int rows, int cols, int stride, uint8_t* out,
-                                  int64_t ldo, int rows_valid) {
-  const int cpr = cols >> 4;
-  for (int idx = threadIdx.x; idx < rows * cpr; idx += 256) {
-    const int r = idx / cpr, c = idx % cpr;
-    if (r < rows_valid)
-      *reinterpret_cast<intx4*>(out + (int64_t)r * ldo + c * 16) =
-          *reinterpret_cast<const intx4*>(lds + r * stride + c * 16);
-  }
+// Paired (gate/up) layout: rows 0..127 are gate, 128..255 up; wave column wn
+// owns rows 64*wn.. of each half; column (within the 128-column half)
+// 64*wn + 32*g + 16*nb + v.
+SFP8_DEV int paired_col(int r) {
+  const int rl = r & 63;
+  return (r & 64) + 32 * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
 }
 
-// Transposed copy-out of an LDS byte tile (see quant.hip for the scheme).
+// Transposed copy-out of an LDS byte tile: out[c * ldo + r] = tile[r][c] for
+// rows < rows (16-multiple), columns < cols (4-multiple); rows >= rows_valid
+// are written as zeros.  Each thread gathers a 16-row x 4-column block with
+// dword reads, transposes it in registers and writes four 16-byte runs.
 SFP8_DEV void lds_tile_store_cols(const uint8_t* lds, int rows, int cols, int stride, uint8_t* out,
                                   int64_t ldo, int rows_valid) {
   const int nb_c = cols >> 2;
@@ -81,11 +88,25 @@ SFP8_DEV void lds_tile_store_cols(const uint8_t* lds, int rows, int cols, int st
   }
 }
 
+SFP8_DEV void store16(void* p, const uint32_t (&w)[4]) {
+  *reinterpret_cast<intx4*>(p) = intx4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+// Round 16 accumulators to bf16 (as fp32 values), after scaling by s.
+SFP8_DEV void round16_bf16(const floatx16& a, float s, float (&o)[16]) {
+#pragma unroll
+  for (int v = 0; v < 16; v += 2) {
+    const uint32_t p = pack2_bf16(a[v] * s, a[v + 1] * s);
+    o[v] = __uint_as_float(p << 16);
+    o[v + 1] = __uint_as_float(p & 0xffff0000u);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // (a6) gate/up forward + SwiGLU epilogue (spark-gpt train.py:975-1016).
 // Tile: 256 tokens x 128 intermediate columns; the B tile holds gate rows
-// n0..n0+127 then up rows I+n0..I+n0+127, and each wave's B blocks pair a gate
-// block with the up block of the same columns.
+// n0..n0+127 then up rows I+n0..I+n0+127 (paired layout), so a lane holds g and
+// u of the same 32 consecutive columns.
 constexpr int kEpiStride = 144;
 
 __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
@@ -103,60 +124,83 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   floatx16 acc[4][4];
   MainLoop<false, kFmtE4M3, kFmtE4M3, true>::run(
       lds, x8 + m0 * D, (T - m0) * D, [=](int r) { return r * (int)D; }, w8 + n0 * D, (2 * I - n0) * D,
-      [=](int r) { return (r < 128 ? r : (int)I + r - 128) * (int)D; }, 0, (int)(D / kStage), acc);
-  // ---- epilogue
+      [=](int r) { return ((r >> 7) * (int)I + paired_col(r & 127)) * (int)D; }, 0, (int)(D / kStage), acc);
+  // All scales are powers of two, so the dequantization factor commutes with
+  // every rounding step: with gb, ub = bf16(acc) (unscaled),
+  //   g = gb*deq, u = ub*deq, h = (g*sig(g))*u = hb*deq^2, hb = (gb*sig)*ub,
+  //   gu8 = e4m3(g*q1) = e4m3(gb*(deq*q1)),  h8 = e4m3(hb*(deq^2*q2)),
+  //   amax1 = deq*max(|gb|,|ub|),  amax2 = deq^2*max|hb|.
+  // Rows past T read as zero (buffer range check): they add 0 to the amax
+  // and 0 bytes to h8t's padding.
   const float deq = 1.0f / (scale[0] * wscale[0]);
-  const float q1 = scale[1], q2 = scale[2];
-  uint8_t* Gt = lds;
-  uint8_t* Ut = lds + kTile * kEpiStride;
-  uint8_t* Ht = lds + 2 * kTile * kEpiStride;
+  const float c_exp = deq * -1.4426950408889634f;
+  const float m1 = deq * scale[1], m2 = deq * deq * scale[2];
+  const float inv1 = 1.0f / m1, inv2 = 1.0f / m2;
+  const float bnd1 = kE4M3Max * inv1, bnd2 = kE4M3Max * inv2;
+  uint8_t* Ht = lds;
   float m_gu = 0.f, m_h = 0.f;
   const int fr = lane & 31, g = lane >> 5;
+  const int cb = 64 * wn + 32 * g;  // first of this lane's 32 columns
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;  // token within the tile
-    const bool valid = m0 + row < T;
+    const int64_t t = m0 + row;
+    uint32_t gw[8], uw[8], hw[8];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float gg[4], uu[4], hh[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          gg[e] = acc[tb][nb][4 * q + e] * deq;
-          uu[e] = acc[tb][nb + 2][4 * q + e] * deq;
-        }
+        float gb[4], ub[4], hb[4];
         // g, u rounded to bf16 as in the bf16 path (train.py:1006-1007)
-        round2_bf16(gg[0], gg[1]);
-        round2_bf16(gg[2], gg[3]);
-        round2_bf16(uu[0], uu[1]);
-        round2_bf16(uu[2], uu[3]);
-        float mg = 0.f, mh = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const uint32_t pg = pack2_bf16(acc[tb][nb][4 * q + e], acc[tb][nb][4 * q + e + 1]);
+          const uint32_t pu = pack2_bf16(acc[tb][nb + 2][4 * q + e], acc[tb][nb + 2][4 * q + e + 1]);
+          gb[e] = __uint_as_float(pg << 16);
+          gb[e + 1] = __uint_as_float(pg & 0xffff0000u);
+          ub[e] = __uint_as_float(pu << 16);
+          ub[e + 1] = __uint_as_float(pu & 0xffff0000u);
+        }
+        bool nan = false;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          hh[e] = gg[e] * sigmoid_fast(gg[e]) * uu[e];
-          mg = fmaxf(mg, fmaxf(fabsf(gg[e]), fabsf(uu[e])));
-          mh = fmaxf(mh, fabsf(hh[e]));
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c_exp));
+          hb[e] = gb[e] * sg * ub[e];
+          m_gu = fmaxf(m_gu, fmaxf(fabsf(gb[e]), fabsf(ub[e])));
+          nan |= hb[e] != hb[e];  // a NaN g or u always reaches h
         }
-        if (valid) {
-          m_gu = fmaxf(m_gu, mg);
-          m_h = fmaxf(m_h, mh);
+        m_h = fmaxf(fmaxf(m_h, fmaxf(fabsf(hb[0]), fabsf(hb[1]))), fmaxf(fabsf(hb[2]), fabsf(hb[3])));
+        uint32_t pg = pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], inv1, bnd1);
+        uint32_t pu = pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], inv1, bnd1);
+        uint32_t ph = pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], inv2, bnd2);
+        if (__builtin_amdgcn_ballot_w64(nan)) {  // wave-uniform, taken only with NaN data
+          asm volatile("" ::: "memory");
+          pg = fix_nan4(pg, gb[0], gb[1], gb[2], gb[3]);
+          pu = fix_nan4(pu, ub[0], ub[1], ub[2], ub[3]);
+          ph = fix_nan4(ph, hb[0], hb[1], hb[2], hb[3]);
         }
-        const int col = 64 * wn + 32 * nb + 8 * q + 4 * g;  // column within the 128-wide tile
-        const uint32_t pg = pack4_e4m3(gg[0] * q1, gg[1] * q1, gg[2] * q1, gg[3] * q1);
-        const uint32_t pu = pack4_e4m3(uu[0] * q1, uu[1] * q1, uu[2] * q1, uu[3] * q1);
-        const uint32_t ph = pack4_e4m3(hh[0] * q2, hh[1] * q2, hh[2] * q2, hh[3] * q2);
-        *reinterpret_cast<uint32_t*>(Gt + row * kEpiStride + col) = pg;
-        *reinterpret_cast<uint32_t*>(Ut + row * kEpiStride + col) = pu;
-        *reinterpret_cast<uint32_t*>(Ht + row * kEpiStride + col) = valid ? ph : 0u;
+        gw[4 * nb + q] = pg;
+        uw[4 * nb + q] = pu;
+        hw[4 * nb + q] = ph;
       }
     }
+    if (t < T) {
+      uint8_t* gp = gu8 + t * 2 * I + n0 + cb;
+      uint8_t* hp = h8 + t * I + n0 + cb;
+      store16(gp, {gw[0], gw[1], gw[2], gw[3]});
+      store16(gp + 16, {gw[4], gw[5], gw[6], gw[7]});
+      store16(gp + I, {uw[0], uw[1], uw[2], uw[3]});
+      store16(gp + I + 16, {uw[4], uw[5], uw[6], uw[7]});
+      store16(hp, {hw[0], hw[1], hw[2], hw[3]});
+      store16(hp + 16, {hw[4], hw[5], hw[6], hw[7]});
+    }
+    store16(Ht + row * kEpiStride + cb, {hw[0], hw[1], hw[2], hw[3]});
+    store16(Ht + row * kEpiStride + cb + 16, {hw[4], hw[5], hw[6], hw[7]});
   }
+  m_gu *= deq;
+  m_h *= deq * deq;
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
-  lds_tile_store_rows(Gt, kTile, 128, kEpiStride, gu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
-  lds_tile_store_rows(Ut, kTile, 128, kEpiStride, gu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
-  lds_tile_store_rows(Ht, kTile, 128, kEpiStride, h8 + m0 * I + n0, I, rows_valid);
   lds_tile_store_cols(Ht, kTile, 128, kEpiStride, h8t + n0 * ldt + m0, ldt, rows_valid);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
@@ -181,37 +225,38 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
   MainLoop<false, kFmtE4M3, kFmtE4M3, false>::run(
       lds, h8 + m0 * I, (T - m0) * I, [=](int r) { return r * (int)I; }, wd8 + n0 * I, (D - n0) * I,
-      [=](int r) { return r * (int)I; }, 0, (int)(I / kStage), acc);
+      [=](int r) { return plain_col(r) * (int)I; }, 0, (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[1]);
   const int fr = lane & 31, g = lane >> 5;
+  const int cb = 128 * wn + 64 * g;
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int64_t t = m0 + 128 * wm + 32 * tb + fr;
     if (t >= T) continue;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < 4; ++nb) {
+      const int64_t n = n0 + cb + 16 * nb;
+      if (n >= D) continue;
+      float o[16];
+      // out rounded to bf16 before the residual add (train.py:1043)
+      round16_bf16(acc[tb][nb], deq, o);
+      const uint16_t* rp = res + t * D + n;
+      const intx4 r0 = *reinterpret_cast<const intx4*>(rp);
+      const intx4 r1 = *reinterpret_cast<const intx4*>(rp + 8);
+      uint32_t w0[4], w1[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wb_row[nb] + 8 * q + 4 * g;
-        if (n >= D) continue;
-        const intx2 rv = *reinterpret_cast<const intx2*>(res + t * D + n);
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = acc[tb][nb][4 * q + e] * deq;
-        // out rounded to bf16 before the residual add (train.py:1043)
-        round2_bf16(o[0], o[1]);
-        round2_bf16(o[2], o[3]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t u = (uint32_t)rv[e >> 1];
-          o[e] += bf16_bits_to_f32((e & 1) ? (u >> 16) : (u & 0xffffu));
-        }
-        *reinterpret_cast<intx2*>(y + t * D + n) = intx2{(int)pack2_bf16(o[0], o[1]), (int)pack2_bf16(o[2], o[3])};
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t a = (uint32_t)r0[i], b = (uint32_t)r1[i];
+        w0[i] = pack2_bf16(o[2 * i] + __uint_as_float(a << 16), o[2 * i + 1] + __uint_as_float(a & 0xffff0000u));
+        w1[i] = pack2_bf16(o[8 + 2 * i] + __uint_as_float(b << 16),
+                           o[8 + 2 * i + 1] + __uint_as_float(b & 0xffff0000u));
       }
+      store16(y + t * D + n, w0);
+      store16(y + t * D + n + 8, w1);
+    }
   }
 }
 
@@ -235,60 +280,79 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t ldb = D * 2;  // bytes
-  const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
   MainLoop<true, 0, 0, false>::run(
       lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
-      reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb, [=](int r) { return r * (int)ldb; }, 0,
-      (int)(ldb / kStage), acc);
+      reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb,
+      [=](int r) { return plain_col(r) * (int)ldb; }, 0, (int)(ldb / kStage), acc);
+  // g = g8*s_gu, u = u8*s_gu with g8, u8 the stored e4m3 values; as the scales
+  // are powers of two, d_gate = dg*s_gu and d_up = du*s_gu with
+  //   dg = (dh*u8)*(sig*(1 + g*(1-sig))),  du = (dh*g8)*sig,
+  //   dgu8 = e5m2(d*q3) = e5m2(d'*(s_gu*q3)),  amax3 = s_gu*max(|dg|,|du|).
   const float s_gu = 1.0f / scale[1];
-  const float q3 = scale[3];
+  const float c_exp = s_gu * -1.4426950408889634f;
+  const float m3s = s_gu * scale[3];
+  const float inv3 = 1.0f / m3s, bnd3 = kE5M2Max * inv3;
   uint8_t* Gt = lds;
   uint8_t* Ut = lds + kTile * kEpiStride2;
+  // gu8 rows of this tile through a range-checked descriptor: rows past T
+  // read as zero (and their dh is zero: dy rows past T read as zero)
+  const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 2 * I, (T - m0) * 2 * I);
   float m3 = 0.f;
   const int fr = lane & 31, g = lane >> 5;
+  const int cb = 128 * wn + 64 * g;
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;
     const int64_t t = m0 + row;
-    const bool valid = t < T;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < 4; ++nb) {
+      const int col = cb + 16 * nb;
+      const int64_t j = n0 + col;
+      uint32_t pg[4] = {0u, 0u, 0u, 0u}, pu[4] = {0u, 0u, 0u, 0u};
+      if (j < I) {
+        const uint32_t jo = (uint32_t)(row * 2 * I + j);
+        const intx4 wg = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
+        const intx4 wu = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)I, 0, 0);
+        float dh[16];
+        // dh rounded to bf16 (train.py:1082)
+        round16_bf16(acc[tb][nb], 1.0f, dh);
+        bool nan = false;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = wb_row[nb] + 8 * q + 4 * g;
-        const int64_t j = n0 + col;
-        uint32_t pg = 0u, pu = 0u;
-        if (valid && j < I) {
-          const uint32_t wg = *reinterpret_cast<const uint32_t*>(gu8 + t * 2 * I + j);
-          const uint32_t wu = *reinterpret_cast<const uint32_t*>(gu8 + t * 2 * I + I + j);
-          float dh[4], dg[4], du[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dh[e] = acc[tb][nb][4 * q + e];
-          // dh rounded to bf16 (train.py:1082)
-          round2_bf16(dh[0], dh[1]);
-          round2_bf16(dh[2], dh[3]);
+        for (int w = 0; w < 4; ++w) {
+          float dg[4], du[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float gv = e4m3_to_f32(wg, e) * s_gu;
-            const float uv = e4m3_to_f32(wu, e) * s_gu;
-            const float sg = sigmoid_fast(gv);
-            dg[e] = dh[e] * uv * (sg * (1.0f + gv * (1.0f - sg)));
-            du[e] = dh[e] * gv * sg;
+            const float g8 = e4m3_to_f32((uint32_t)wg[w], e);
+            const float u8 = e4m3_to_f32((uint32_t)wu[w], e);
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g8 * c_exp));
+            const float d = dh[4 * w + e];
+            dg[e] = d * u8 * (sg * __builtin_fmaf(g8 * s_gu, 1.0f - sg, 1.0f));
+            du[e] = d * g8 * sg;
             m3 = fmaxf(m3, fmaxf(fabsf(dg[e]), fabsf(du[e])));
+            nan |= (dg[e] != dg[e]) | (du[e] != du[e]);
           }
-          pg = pack4_e5m2(dg[0] * q3, dg[1] * q3, dg[2] * q3, dg[3] * q3);
-          pu = pack4_e5m2(du[0] * q3, du[1] * q3, du[2] * q3, du[3] * q3);
+          pg[w] = pack4_e5m2_scaled(dg[0], dg[1], dg[2], dg[3], inv3, bnd3);
+          pu[w] = pack4_e5m2_scaled(du[0], du[1], du[2], du[3], inv3, bnd3);
+          if (__builtin_amdgcn_ballot_w64(nan)) {  // wave-uniform, taken only with NaN data
+            asm volatile("" ::: "memory");
+            pg[w] = fix_nan4(pg[w], dg[0], dg[1], dg[2], dg[3]);
+            pu[w] = fix_nan4(pu[w], du[0], du[1], du[2], du[3]);
+          }
         }
-        *reinterpret_cast<uint32_t*>(Gt + row * kEpiStride2 + col) = pg;
-        *reinterpret_cast<uint32_t*>(Ut + row * kEpiStride2 + col) = pu;
+        if (t < T) {
+          store16(dgu8 + t * 2 * I + j, pg);
+          store16(dgu8 + t * 2 * I + I + j, pu);
+        }
       }
+      store16(Gt + row * kEpiStride2 + col, pg);
+      store16(Ut + row * kEpiStride2 + col, pu);
+    }
   }
+  m3 *= s_gu;
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);
-  lds_tile_store_rows(Gt, kTile, cols, kEpiStride2, dgu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
-  lds_tile_store_rows(Ut, kTile, cols, kEpiStride2, dgu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
   lds_tile_store_cols(Gt, kTile, cols, kEpiStride2, dgu8t + n0 * ldt + m0, ldt, rows_valid);
   lds_tile_store_cols(Ut, kTile, cols, kEpiStride2, dgu8t + (I + n0) * ldt + m0, ldt, rows_valid);
   block_amax_atomic<4>(m3, red, amax + 3);
@@ -308,28 +372,30 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t K = 2 * I;
-  const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
   MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
       lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, w8t + n0 * K, (D - n0) * K,
-      [=](int r) { return r * (int)K; }, 0, (int)(K / kStage), acc);
+      [=](int r) { return plain_col(r) * (int)K; }, 0, (int)(K / kStage), acc);
   const float sa = 1.0f / scale[3], sb = 1.0f / wscale[0];
   const int fr = lane & 31, g = lane >> 5;
+  const int cb = 128 * wn + 64 * g;
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int64_t t = m0 + 128 * wm + 32 * tb + fr;
     if (t >= T) continue;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < 4; ++nb) {
+      const int64_t n = n0 + cb + 16 * nb;
+      if (n >= D) continue;
+      uint32_t w0[4], w1[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wb_row[nb] + 8 * q + 4 * g;
-        if (n >= D) continue;
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = acc[tb][nb][4 * q + e] * sa * sb;
-        *reinterpret_cast<intx2*>(dxn + t * D + n) = intx2{(int)pack2_bf16(o[0], o[1]), (int)pack2_bf16(o[2], o[3])};
+      for (int i = 0; i < 4; ++i) {
+        w0[i] = pack2_bf16(acc[tb][nb][2 * i] * sa * sb, acc[tb][nb][2 * i + 1] * sa * sb);
+        w1[i] = pack2_bf16(acc[tb][nb][8 + 2 * i] * sa * sb, acc[tb][nb][8 + 2 * i + 1] * sa * sb);
       }
+      store16(dxn + t * D + n, w0);
+      store16(dxn + t * D + n + 8, w1);
+    }
   }
 }
 
@@ -351,31 +417,30 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int wb_row[4] = {128 * wn, 128 * wn + 32, 128 * wn + 64, 128 * wn + 96};
   floatx16 acc[4][4];
   const int64_t kb = (int64_t)blockIdx.y * kchunk;
   MainLoop<false, FMT_A, FMT_B, false>::run(
       lds, at + m0 * ldt, (M - m0) * ldt, [=](int r) { return r * (int)ldt; }, bt + n0 * ldt, (N - n0) * ldt,
-      [=](int r) { return r * (int)ldt; }, kb, (int)(kchunk / kStage), acc);
+      [=](int r) { return plain_col(r) * (int)ldt; }, kb, (int)(kchunk / kStage), acc);
   const bool split = gridDim.y > 1;
   const float deq = split ? 1.0f : 1.0f / (sa[0] * sb[0]);
   float* dst = out + (split ? (int64_t)blockIdx.y * M * N : 0);
   const int fr = lane & 31, g = lane >> 5;
+  const int cb = 128 * wn + 64 * g;
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int64_t m = m0 + 128 * wm + 32 * tb + fr;
     if (m >= M) continue;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < 4; ++nb) {
+      const int64_t n = n0 + cb + 16 * nb;
+      if (n >= N) continue;
+      floatx4* p = reinterpret_cast<floatx4*>(dst + m * N + n);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wb_row[nb] + 8 * q + 4 * g;
-        if (n >= N) continue;
-        floatx4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = acc[tb][nb][4 * q + e] * deq;
-        *reinterpret_cast<floatx4*>(dst + m * N + n) = o;
-      }
+      for (int i = 0; i < 4; ++i)
+        p[i] = floatx4{acc[tb][nb][4 * i] * deq, acc[tb][nb][4 * i + 1] * deq, acc[tb][nb][4 * i + 2] * deq,
+                       acc[tb][nb][4 * i + 3] * deq};
+    }
   }
 }
 
@@ -388,7 +453,6 @@ using namespace sfp8;
 
 namespace {
 
-constexpr int kSwigluLds = 3 * kTile * kEpiStride;   // 110592 < kMainLds
 constexpr int kDgradLds = 2 * kTile * kEpiStride2;   // 139264 > kMainLds
 
 template <typename K>
