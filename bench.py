@@ -7,15 +7,24 @@ backward of the block (7-argument autograd Function, all kernels on the
 current stream).  Value = 18*T*D*I FLOP / step time, in TFLOP/s.
 
 Also reported on the same JSON line:
-  roofline      the dominant GEMM kernel, timed alone with HIP events on the
-                stream it runs on; algorithmic FLOP per launch / mean duration
-                vs the 5.0 PFLOP/s dense FP8 MFMA peak
+  roofline      the kernel taking the most time per step: HIP events recorded
+                on its stream around each of its launches inside the timed
+                steps; algorithmic FLOP per launch / mean duration vs the dense
+                MFMA peak of its input type; `traffic` = HBM bytes per launch
+                from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+                (profiles/traffic_fwd_bwd_T65536_D1024_I3072.md), null for
+                other workloads
   quantizer     the standalone quantizer (bf16 65536x4096 with 0.1% x50 outlier
                 columns -> e4m3 row-major + transposed + amax): 4 B/element
                 algorithmic traffic / mean duration vs 8 TB/s HBM
-  kernels       per-kernel mean durations of one step
+  kernels       per-kernel mean durations (each kernel alone, 10 launches),
+                with TFLOP/s or algorithmic GB/s
   cpu_baseline  the same FP8 recipe emulated in torch on the host cores (the
                 CPU oracle) on a bounded token sample, in TFLOP/s
+
+``--probe`` runs, instead of the benchmark, one calibration copy (fp32 negate
+of 256 Mi elements: 1 GiB read + 1 GiB written) and then every kernel of the
+step once, for ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` passes.
 """
 from __future__ import annotations
 
@@ -29,7 +38,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP8_PEAK_TFLOPS = 5033.0   # MI355X dense FP8 MFMA (256 CU x 2.4 GHz x 8192 FLOP/clk)
+BF16_PEAK_TFLOPS = 2516.5  # MI355X dense bf16 MFMA
 HBM_PEAK_GBPS = 8000.0     # MI355X HBM3E
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_fwd_bwd_T65536_D1024_I3072.md")
+TRAFFIC_WORKLOAD = (65536, 1024, 3072)
 
 
 def parse():
@@ -44,7 +56,22 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=16384)
     p.add_argument("--quant-rows", type=int, default=65536)
     p.add_argument("--quant-cols", type=int, default=4096)
+    p.add_argument("--probe", action="store_true", help="one launch of each kernel, for counter passes")
     return p.parse_args()
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary: the
+    table row `| kernel | ... | traffic_bytes |` (last column)."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 2 and cells[0] == kernel:
+                    return int(float(cells[-1]))
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 def timed_launches(fn, reps: int, stream) -> float:
@@ -120,7 +147,7 @@ def main() -> None:
     import torch
 
     import spark_gpt_amd as sg
-    from spark_gpt_amd import ops
+    from spark_gpt_amd import _lib, ops
 
     dev = torch.device("cuda:0")
     T, D, I = args.tokens, args.d_model, args.ffn
@@ -143,57 +170,110 @@ def main() -> None:
 
     step()                            # prewarm: records amax under scale 1
     ops.update_scales(scale, amax)    # roll, as the trainer does after the prewarm step
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    flop = 18.0 * T * D * I
-    tflops = flop / (ms * 1e-3) / 1e12
 
-    # ---- per-kernel timing (HIP events on the current stream) ----
+    # ---- every kernel of the step, alone (HIP events on the current stream) ----
     stream = torch.cuda.current_stream(dev)
-    x8, x8t, rstd = ops.norm_quant(h, nw.detach(), scale, amax, 1e-6)
+    nwd = nw.detach()
+    x8, x8t, rstd = ops.norm_quant(h, nwd, scale, amax, 1e-6)
     wscale = torch.empty(2, device=dev)
     w8, w8t, _ = ops.weight_quant(wgu.detach(), wscale[0:1], w8=True, w8t=True)
     wd8, _, wdt = ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True)
     gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I)
     dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale)
-    dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nw.detach(), scale, amax)
-    reps = 10
+    dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax)
+    # name -> (call, C-ABI symbol, predicate on the symbol's arguments, FLOP, algorithmic bytes)
     kern = {
-        "norm_quant": (lambda: ops.norm_quant(h, nw.detach(), scale, amax, 1e-6), None),
-        "weight_quant_gu": (lambda: ops.weight_quant(wgu.detach(), wscale[0:1], w8=True, w8t=True), None),
-        "weight_quant_down": (lambda: ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True), None),
-        "gateup_swiglu_fwd": (lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I), 4.0 * T * D * I),
-        "down_fwd": (lambda: ops.down_fwd(h8, wd8, h, scale, wscale), 2.0 * T * D * I),
-        "down_dgrad_swiglu_bf16": (lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax), 2.0 * T * D * I),
-        "gateup_dgrad": (lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale), 4.0 * T * D * I),
-        "norm_bwd": (lambda: ops.norm_bwd(h, rstd, dxn, dy, nw.detach(), scale, amax), None),
-        "wgrad_down": (lambda: ops.wgrad(dy8t, h8t, scale[4:5], scale[2:3]), 2.0 * T * D * I),
-        "wgrad_gateup": (lambda: ops.wgrad(dgu8t, x8t, scale[3:4], scale[0:1]), 4.0 * T * D * I),
+        "norm_quant": (lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6), "sfp8_norm_quant", None,
+                       None, T * (4.0 * D + 4)),
+        "weight_quant_gu": (lambda: ops.weight_quant(wgu.detach(), wscale[0:1], w8=True, w8t=True),
+                            "sfp8_weight_quant", None, None, 10.0 * 2 * I * D),
+        "weight_quant_down": (lambda: ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True),
+                              "sfp8_weight_quant", None, None, 11.0 * D * I),
+        "gateup_swiglu_fwd": (lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I),
+                              "sfp8_gemm_gateup_swiglu_fwd", None, 4.0 * T * D * I, None),
+        "down_fwd": (lambda: ops.down_fwd(h8, wd8, h, scale, wscale), "sfp8_gemm_down_fwd", None,
+                     2.0 * T * D * I, None),
+        "down_dgrad_swiglu_bf16": (lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax),
+                                   "sfp8_gemm_down_dgrad_swiglu", None, 2.0 * T * D * I, None),
+        "gateup_dgrad": (lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale), "sfp8_gemm_gateup_dgrad", None,
+                         4.0 * T * D * I, None),
+        "norm_bwd": (lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax), "sfp8_norm_bwd", None,
+                     None, T * (9.0 * D + 4)),
+        "wgrad_down": (lambda: ops.wgrad(dy8t, h8t, scale[4:5], scale[2:3]), "sfp8_gemm_wgrad",
+                       lambda a: a[4] == D, 2.0 * T * D * I, None),
+        "wgrad_gateup": (lambda: ops.wgrad(dgu8t, x8t, scale[3:4], scale[0:1]), "sfp8_gemm_wgrad",
+                         lambda a: a[4] == 2 * I, 4.0 * T * D * I, None),
     }
+
+    if args.probe:
+        # calibration copy of known size, then one launch of each kernel
+        src = torch.ones(256 << 20, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+        for name, (fn, *_rest) in kern.items():
+            fn()
+            torch.cuda.synchronize()
+            print(f"probe {name} done", flush=True)
+        print(json.dumps({"probe": list(kern), "copy_bytes_read": 1 << 30, "copy_bytes_written": 1 << 30}))
+        return
+
     kernels = {}
-    for name, (fn, fl) in kern.items():
-        kms = timed_launches(fn, reps, stream)
+    for name, (fn, _sym, _pred, fl, by) in kern.items():
+        kms = timed_launches(fn, 10, stream)
         rec = {"ms": round(kms, 4)}
         if fl:
             rec["tflops"] = round(fl / (kms * 1e-3) / 1e12, 1)
+        if by:
+            rec["GB/s"] = round(by / (kms * 1e-3) / 1e9, 1)
         kernels[name] = rec
-    # dominant kernel: the GEMM taking the most time
-    gemms = {k: v for k, v in kernels.items() if "tflops" in v}
-    dom = max(gemms, key=lambda k: gemms[k]["ms"])
-    dom_flop = kern[dom][1]
-    dom_ms = gemms[dom]["ms"]
-    achieved = dom_flop / (dom_ms * 1e-3) / 1e12
-    peak = FP8_PEAK_TFLOPS if "bf16" not in dom else FP8_PEAK_TFLOPS / 2
-    roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
-                "flop_per_launch": dom_flop}
+    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+    _fn, dom_sym, dom_pred, dom_flop, dom_bytes = kern[dom]
+
+    # ---- timed steps; events around each launch of the dominant kernel ----
+    for _ in range(args.warmup):
+        step()
+    marks = []
+    plain_call = _lib.call
+
+    def traced_call(name, *a):
+        if name != dom_sym or (dom_pred is not None and not dom_pred(a)):
+            return plain_call(name, *a)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        plain_call(name, *a)
+        e1.record(stream)
+        marks.append((e0, e1))
+
+    torch.cuda.synchronize()
+    _lib.call = traced_call
+    try:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    finally:
+        _lib.call = plain_call
+    flop = 18.0 * T * D * I
+    tflops = flop / (ms * 1e-3) / 1e12
+    dom_ms = sum(a.elapsed_time(b) for a, b in marks) / max(1, len(marks))
+
+    traffic = read_traffic(dom) if (T, D, I) == TRAFFIC_WORKLOAD else None
+    if dom_flop:
+        achieved = dom_flop / (dom_ms * 1e-3) / 1e12
+        peak = BF16_PEAK_TFLOPS if "bf16" in dom else FP8_PEAK_TFLOPS
+        roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
+                    "flop_per_launch": dom_flop, "launches_timed": len(marks), "ms_per_launch": round(dom_ms, 4)}
+    else:
+        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                    "bytes_per_launch": dom_bytes, "launches_timed": len(marks), "ms_per_launch": round(dom_ms, 4)}
 
     # ---- standalone quantizer (HBM-bound) ----
     R, C = args.quant_rows, args.quant_cols

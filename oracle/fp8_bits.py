@@ -165,17 +165,22 @@ def floor_log2_cr(r: np.ndarray) -> np.ndarray:
 
 
 def pow2_scale(amax: np.ndarray, fmax: float, headroom: int, recip_first: bool = False) -> np.ndarray:
-    """exp2(floor(log2(r)) - headroom) in fp32, exactly, for finite amax >= 0.
+    """exp2(floor(log2(r)) - headroom) in fp32, exactly, for amax >= 0 (inf
+    included).
 
     r = fmax / max(amax, 1e-30) for the scale roll (spark-gpt ``train.py:943``,
     a tensor/tensor divide, headroom 1); with ``recip_first`` r is
     (1 / max(amax, 1e-30)) * fmax, which is how torch evaluates the weight rule
     ``448.0 / tensor`` (``train.py:951``, headroom 0).  Each step is one
-    IEEE-rounded fp32 operation."""
+    IEEE-rounded fp32 operation.  An infinite amax gives r = 0, log2 = -inf and
+    a scale of 0, as the reference's expression does."""
     a = np.maximum(np.asarray(amax, dtype=np.float32), np.float32(1e-30))
-    if recip_first:
-        r = ((np.float32(1.0) / a).astype(np.float32) * np.float32(fmax)).astype(np.float32)
-    else:
-        r = (np.float32(fmax) / a).astype(np.float32)
-    k = floor_log2_cr(r) - headroom
-    return np.ldexp(np.float32(1.0), k.astype(np.int32)).astype(np.float32)
+    with np.errstate(over="ignore", divide="ignore"):
+        if recip_first:
+            r = ((np.float32(1.0) / a).astype(np.float32) * np.float32(fmax)).astype(np.float32)
+        else:
+            r = (np.float32(fmax) / a).astype(np.float32)
+    zero = r == 0
+    k = floor_log2_cr(np.where(zero, np.float32(1.0), r)) - headroom
+    out = np.ldexp(np.float32(1.0), k.astype(np.int32)).astype(np.float32)
+    return np.where(zero, np.float32(0.0), out).astype(np.float32)

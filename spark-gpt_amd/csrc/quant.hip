@@ -403,21 +403,31 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   block_amax_atomic<4>(m, red, amax + 4);
 }
 
-// Fixed-order column sums: out[d] = sum_b part[b][d].  Work-group x owns 64
-// columns; thread (r, c) sums rows r, r+4, r+8, ... of column c in ascending
-// order, then the 4 partial sums are added in the order r = 0, 1, 2, 3.
+// Fixed-order column sums over row groups: out[y][d] = sum of part[b][d] for
+// b in [y*rpg, min(nb, (y+1)*rpg)).  Work-group (x, y) owns 64 columns of
+// group y; thread (r, c) sums rows r, r+4, r+8, ... of the group in ascending
+// order, then the 4 partial sums are added in the order r = 0, 1, 2, 3.  Two
+// launches (groups, then one group over the group sums) give a sum whose
+// order depends only on nb.
+constexpr int kColsumGroups = 32;
+
 __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, int64_t nb,
-                                                     int64_t D, float* __restrict__ out) {
+                                                     int64_t rpg, int64_t D, float* __restrict__ out) {
   __shared__ float red[4][64];
   const int c = threadIdx.x & 63, r = threadIdx.x >> 6;
   const int64_t d = (int64_t)blockIdx.x * 64 + c;
+  const int64_t b0 = (int64_t)blockIdx.y * rpg;
+  const int64_t b1 = (b0 + rpg) < nb ? (b0 + rpg) : nb;
   float s = 0.0f;
   if (d < D)
-    for (int64_t b = r; b < nb; b += 4) s += part[b * D + d];
+    for (int64_t b = b0 + r; b < b1; b += 4) s += part[b * D + d];
   red[r][c] = s;
   __syncthreads();
-  if (r == 0 && d < D) out[d] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
+  if (r == 0 && d < D) out[(int64_t)blockIdx.y * D + d] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
 }
+
+// Row groups of the first colsum pass for nb partial rows.
+static inline int64_t colsum_groups(int64_t nb) { return nb < kColsumGroups ? nb : kColsumGroups; }
 
 // Split-K reduction: out = (sum_s ws[s]) * (1 / (sa * sb)), s ascending.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits,
@@ -480,8 +490,14 @@ static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, co
   hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, rstd,
                      (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, scale, amax, (uint16_t*)dh, part,
                      (uint8_t*)dy8t, ldt);
-  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, st, part,
-                     (int64_t)nblk, (int64_t)D, dnw);
+  // partial rows: nblk from the norm kernel, then the group sums after them
+  const int64_t nb = (int64_t)nblk, G = colsum_groups(nb), rpg = (nb + G - 1) / G;
+  float* group_sums = part + nb * D;
+  const unsigned cblk = (unsigned)((D + 63) / 64);
+  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, (unsigned)G), dim3(256), 0, st, part, nb, rpg, (int64_t)D,
+                     group_sums);
+  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, 1), dim3(256), 0, st, (const float*)group_sums, G, G,
+                     (int64_t)D, dnw);
   return launch_status();
 }
 
@@ -546,7 +562,7 @@ int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream) {
   return launch_status();
 }
 
-int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
+static int64_t norm_bwd_blocks(int64_t D, int64_t ldt) {
   switch (D) {
     case 128: return ldt / NormCfg<128>::RT;
     case 256: return ldt / NormCfg<256>::RT;
@@ -556,6 +572,11 @@ int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
     case 4096: return ldt / NormCfg<4096>::RT;
     default: return -1;
   }
+}
+
+int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
+  const int64_t nb = norm_bwd_blocks(D, ldt);
+  return nb < 0 ? -1 : nb + colsum_groups(nb);
 }
 
 int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
