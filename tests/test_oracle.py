@@ -244,6 +244,29 @@ def test_swiglu_backward_is_derivative():
     torch.testing.assert_close(dh * gd * sig, u.grad)
 
 
+def test_down_dgrad_swiglu_is_derivative():
+    """O.down_dgrad_swiglu against fp64 autograd of dy @ Wd -> silu(g) * u, with
+    g, u the dequantized gu8 it is given: each d_gu code within one e5m2 step
+    (the oracle rounds dh to bf16 first), amax slots exact in form."""
+    T, D, I = 24, 64, 32
+    g = torch.Generator().manual_seed(12)
+    s = torch.tensor([1.0, 8.0, 1.0, 2.0 ** 12, 2.0 ** 14])
+    gu8 = _fp8((T, 2 * I), torch.float8_e4m3fn, g, 16.0)
+    wd = (torch.randn(D, I, generator=g) * 0.2).to(torch.bfloat16)
+    dy = (torch.randn(T, D, generator=g) * 1e-2).to(torch.bfloat16)
+    dgu8, a3, a4 = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
+    gg = (gu8[:, :I].double() / 8.0).requires_grad_(True)
+    uu = (gu8[:, I:].double() / 8.0).requires_grad_(True)
+    dh = dy.double() @ wd.double()
+    dgate, dup = torch.autograd.grad((torch.nn.functional.silu(gg) * uu * dh).sum(), [gg, uu])
+    want = torch.cat([dgate, dup], 1)
+    got = O.f(dgu8).double() / 2.0 ** 12
+    # e5m2 has 2 mantissa bits: one step is 25 % relative; dh's bf16 rounding moves a value < 1 %
+    assert torch.all((got - want).abs() <= 0.26 * want.abs() + 2.0 ** -16 / 2.0 ** 12)
+    assert abs(a3.item() - want.abs().max().item()) <= 0.01 * want.abs().max().item()
+    assert a4.item() == dy.float().abs().max().item()
+
+
 def test_norm_backward_is_derivative():
     g = torch.Generator().manual_seed(8)
     h = torch.randn(8, 64, generator=g).to(torch.bfloat16)
