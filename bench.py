@@ -200,9 +200,9 @@ def main() -> None:
                          4.0 * T * D * I, None),
         "norm_bwd": (lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax), "sfp8_norm_bwd", None,
                      None, T * (9.0 * D + 4)),
-        "wgrad_down": (lambda: ops.wgrad(dy8t, h8t, scale[4:5], scale[2:3]), "sfp8_gemm_wgrad",
+        "wgrad_down": (lambda: ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3]), "sfp8_gemm_wgrad",
                        lambda a: a[4] == D, 2.0 * T * D * I, None),
-        "wgrad_gateup": (lambda: ops.wgrad(dgu8t, x8t, scale[3:4], scale[0:1]), "sfp8_gemm_wgrad",
+        "wgrad_gateup": (lambda: ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1]), "sfp8_gemm_wgrad",
                          lambda a: a[4] == 2 * I, 4.0 * T * D * I, None),
     }
 
@@ -218,7 +218,13 @@ def main() -> None:
             fn()
             torch.cuda.synchronize()
             print(f"probe {name} done", flush=True)
-        print(json.dumps({"probe": list(kern), "copy_bytes_read": 1 << 30, "copy_bytes_written": 1 << 30}))
+        xq = torch.randn(args.quant_rows, args.quant_cols, device=dev).to(torch.bfloat16)
+        torch.cuda.synchronize()
+        ops.quant_e4m3_rowcol(xq, scale, amax)
+        torch.cuda.synchronize()
+        print("probe quantizer done", flush=True)
+        print(json.dumps({"probe": list(kern) + ["quantizer"], "copy_bytes_read": 1 << 30,
+                          "copy_bytes_written": 1 << 30}))
         return
 
     kernels = {}

@@ -16,9 +16,15 @@
  *    max-accumulate into `amax`; nothing is read back to the host.
  *  - `wscale` points at the 2 just-in-time weight scales [q_gu, q_d]
  *    (train.py:1213).
- *  - Token-contiguous ("transposed") FP8 copies have leading dimension
- *    `ldt` = T rounded up to a multiple of 256; producers write zeros in
- *    columns T..ldt-1 so weight-gradient GEMMs reduce over ldt tokens.
+ *  - Token-contiguous FP8 copies (x8t, h8t, dgu8t, dy8t: the weight-gradient
+ *    GEMM operands) cover `ldt` = T rounded up to a multiple of 256 tokens
+ *    and use the K-slab layout: [ldt / 64][rpad][64] bytes with
+ *    rpad = rows rounded up to a multiple of 256; element (r, t) is at
+ *    (t / 64) * rpad * 64 + r * 64 + t % 64.  One 64-token stage of a
+ *    256-row GEMM tile is one contiguous 16 KiB block.  Producers write zeros
+ *    for tokens T..ldt-1 (padding rows r >= rows are never written and never
+ *    reach an output).  sfp8_slab_bytes(rows, ldt) gives the buffer size.
+ *    The standalone quantizer's x8t is a plain [cols, ldt] transpose.
  *  - `stream` is a hipStream_t; every call is asynchronous on it, never
  *    synchronises the device and never allocates device memory.  Callers
  *    provide every output and workspace buffer.
@@ -53,7 +59,7 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
 
 /* Norm-fused quantizer, replaces _fp8_norm_quant_kernel (train.py:955-972,
  * launched at train.py:1208-1210).  h [T, D] bf16, norm_w [D] fp32 ->
- * x8 [T, D] e4m3, x8t [D, ldt] e4m3, rstd [T] fp32; amax[0] max-accumulated.
+ * x8 [T, D] e4m3, x8t (K-slab, D rows) e4m3, rstd [T] fp32; amax[0] max-accumulated.
  * D in {128, 256, 512, 1024, 2048, 4096}; ldt = T rounded up to 256. */
 int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
                     const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
@@ -81,7 +87,7 @@ int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
 /* gate/up forward + SwiGLU epilogue, replaces _fp8_swiglu_fwd_kernel
  * (train.py:975-1016, launched at train.py:1216-1218).
  * x8 [T, D] e4m3, w8 [2I, D] e4m3 -> gu8 [T, 2I] e4m3, h8 [T, I] e4m3,
- * h8t [I, ldt] e4m3 (token-contiguous copy of h8 for the down wgrad);
+ * h8t (K-slab, I rows) e4m3 (token-contiguous copy of h8 for the down wgrad);
  * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0. */
 int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
@@ -96,7 +102,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
 /* bf16 down dgrad + SwiGLU backward, replaces _fp8_down_dgrad_swiglu_kernel
  * (train.py:1049-1094, launched at train.py:1236-1238).  dy [T, D] bf16,
  * wdt [I, D] bf16 (= w_down^T), gu8 [T, 2I] e4m3 -> dgu8 [T, 2I] e5m2,
- * dgu8t [2I, ldt] e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is
+ * dgu8t (K-slab, 2I rows) e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is
  * recorded by sfp8_norm_bwd.)  D % 64 == 0. */
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
@@ -112,24 +118,26 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
  * (train.py:1150-1187, call at train.py:1247) and _fp8_mm_kernel with A read
  * transposed (train.py:1097-1127, call at train.py:1249-1251):
  * out[m, n] = sum_t at[m, t] * bt[n, t] / (sa[0] * sb[0]), fp32 [M, N].
- * at [M, ldt] e5m2 (fmt_a = 1), bt [N, ldt] e4m3 (fmt_b = 0).
+ * at: K-slab copy of M rows over ldt tokens, e5m2 (fmt_a = 1); bt: K-slab
+ * copy of N rows, e4m3 (fmt_b = 0).
  * ws: fp32 workspace of sfp8_wgrad_workspace_floats(M, N, ldt) floats (may be
- * NULL when that is 0).  Deterministic (split-K partials summed in order). */
+ * NULL when that is 0).  Deterministic: split-K partials are summed in split
+ * order by a second kernel on the same stream. */
 int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
                     const float* sa, const float* sb, float* out, float* ws, int64_t ws_floats, void* stream);
 int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt);
+/* Bytes of a K-slab token-contiguous copy of `rows` rows over ldt tokens
+ * (-1 if ldt is not a multiple of 256). */
+int64_t sfp8_slab_bytes(int64_t rows, int64_t ldt);
 int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt);
 
-/* Split-K partial sum: out = (sum_s ws[s]) / (sa[0] * sb[0]), s ascending. */
-int sfp8_splitk_reduce(const float* ws, int64_t splits, int64_t M, int64_t N, const float* sa,
-                       const float* sb, float* out, void* stream);
 
 /* ---- norm backward ------------------------------------------------------ */
 
 /* RMSNorm backward + residual, replaces _fp8_norm_bwd_kernel
  * (train.py:1130-1147, launched at train.py:1243-1246) and the dnw sum
  * (train.py:1252).  h, dxn, dy [T, D] bf16, rstd [T] -> dh [T, D] bf16,
- * dnw [D] fp32; also dy8t [D, ldt] = e5m2(dy * scale[4])^T (the down wgrad
+ * dnw [D] fp32; also dy8t = e5m2(dy * scale[4]) as a K-slab copy (the down wgrad
  * operand quantized in registers at train.py:1171-1172) and amax[4] = max|dy|
  * (train.py:1074-1081).  partials: fp32 workspace of
  * sfp8_norm_bwd_partials(D, ldt) * D floats. */

@@ -33,7 +33,7 @@ SIGNATURES = {
     "sfp8_gemm_wgrad": (_INT, [_P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "sfp8_wgrad_splits": (_I64, [_I64, _I64, _I64]),
     "sfp8_wgrad_workspace_floats": (_I64, [_I64, _I64, _I64]),
-    "sfp8_splitk_reduce": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "sfp8_slab_bytes": (_I64, [_I64, _I64]),
     "sfp8_norm_bwd": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "sfp8_norm_bwd_partials": (_I64, [_I64, _I64]),
 }

@@ -221,4 +221,49 @@ SFP8_DEV void transpose4x4_bytes(const uint32_t in[4], uint32_t out[4]) {
   out[3] = __builtin_amdgcn_perm(a23hi, a01hi, 0x07060302u);
 }
 
+// K-slab layout of a token-contiguous FP8 copy of an R-row operand (the weight
+// gradients' operands x8t, h8t, d_gu8t, dy8t): [ldt / 64][slab_rows(R)][64]
+// bytes, element (r, t) at
+//   (t / 64) * slab_rows(R) * 64 + r * 64 + t % 64.
+// One 64-token K stage of a 256-row GEMM tile is then one contiguous 16 KiB
+// block.  Rows are padded to a multiple of 256 (the tile), so every tile read
+// stays inside the buffer; padding rows only feed discarded output rows.
+__host__ __device__ inline int64_t slab_rows(int64_t R) { return (R + 255) / 256 * 256; }
+
+// Writes an LDS tile of tokens x columns into a K-slab copy:
+//   out(c0 + c, t0 + t) = tile[t][c]  for t < ntok, c < ncols,
+// with tokens t >= tvalid written as zeros.  ntok % 16 == 0, ncols % 4 == 0,
+// t0 % 16 == 0 (a 16-token block never straddles two slabs).  Consecutive
+// threads take consecutive 16-token blocks of the same 4 columns, so the
+// stores of a wave fill whole 64-byte slab rows.
+template <int NT>
+SFP8_DEV void lds_tile_store_slab(const uint8_t* lds, int ntok, int ncols, int stride, uint8_t* out,
+                                  int64_t rpad, int64_t t0, int64_t c0, int tvalid) {
+  const int na = ntok >> 4;
+  const int nblocks = na * (ncols >> 2);
+  for (int idx = threadIdx.x; idx < nblocks; idx += NT) {
+    const int a = idx % na, b = idx / na;
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = a * 16 + i;
+      w[i] = (r < tvalid) ? *reinterpret_cast<const uint32_t*>(lds + r * stride + b * 4) : 0u;
+    }
+    uint32_t t4[4][4];  // t4[c][q]: column 4b+c, tokens 4q..4q+3 of the block
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t o[4];
+      transpose4x4_bytes(&w[4 * q], o);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) t4[c][q] = o[c];
+    }
+    const int64_t t = t0 + 16 * a;
+    uint8_t* base = out + (t >> 6) * rpad * 64 + (t & 63) + (c0 + 4 * b) * 64;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<intx4*>(base + c * 64) =
+          intx4{(int)t4[c][0], (int)t4[c][1], (int)t4[c][2], (int)t4[c][3]};
+  }
+}
+
 }  // namespace sfp8

@@ -25,20 +25,42 @@
 
 namespace sfp8 {
 
-// Work-group -> tile mapping.  Work-groups are dispatched round-robin over
-// the 8 XCDs; consecutive logical tiles are placed on the same XCD (each XCD
-// has its own L2), then grouped 8 tile-rows at a time so a column of B tiles
-// is reused from L2 across neighbouring A tiles.
-SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int per = nwg >> 3, rem = nwg & 7;
-  const int xcd = pid & 7, local = pid >> 3;
-  const int lid = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+// Logical tile lid -> (tm, tn): tile rows in groups of 8, walking the tile
+// columns of a group before the next group, so a column of B tiles is reused
+// from L2 across the group's A tiles.
+SFP8_DEV void raster(int lid, int tiles_m, int tiles_n, int& tm, int& tn) {
   constexpr int G = 8;
   const int group = G * tiles_n;
   const int first_m = (lid / group) * G;
   const int gsz = (tiles_m - first_m) < G ? (tiles_m - first_m) : G;
   tm = first_m + (lid % group) % gsz;
   tn = (lid % group) / gsz;
+}
+
+// Work-group -> tile mapping.  Work-groups are dispatched round-robin over
+// the 8 XCDs (pid % 8); each XCD (with its own L2) gets a contiguous run of
+// logical tiles, rastered as above.  A bijection of [0, nwg) for any nwg.
+SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int per = nwg >> 3, rem = nwg & 7;
+  const int xcd = pid & 7, local = pid >> 3;
+  const int lid = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  raster(lid, tiles_m, tiles_n, tm, tn);
+}
+
+// Split-K mapping of a 1-D grid of tiles * splits work-groups.  With splits a
+// multiple of 8, XCD x runs splits [x*splits/8, (x+1)*splits/8) over every
+// tile, so the work-groups resident on one XCD read the same K range of A
+// and B and share it in that XCD's L2.  Otherwise split = pid / tiles.
+SFP8_DEV void split_tile_coords(int pid, int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
+  const int tiles = tiles_m * tiles_n;
+  if ((splits & 7) == 0) {
+    const int xcd = pid & 7, local = pid >> 3;
+    split = xcd * (splits >> 3) + local / tiles;
+    raster(local % tiles, tiles_m, tiles_n, tm, tn);
+  } else {
+    split = pid / tiles;
+    tile_coords(pid % tiles, tiles, tiles_m, tiles_n, tm, tn);
+  }
 }
 
 // Output column (within the 256-column tile) held in B-tile row r, plain
@@ -55,37 +77,6 @@ SFP8_DEV int plain_col(int r) {
 SFP8_DEV int paired_col(int r) {
   const int rl = r & 63;
   return (r & 64) + 32 * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
-}
-
-// Transposed copy-out of an LDS byte tile: out[c * ldo + r] = tile[r][c] for
-// rows < rows (16-multiple), columns < cols (4-multiple); rows >= rows_valid
-// are written as zeros.  Each thread gathers a 16-row x 4-column block with
-// dword reads, transposes it in registers and writes four 16-byte runs.
-SFP8_DEV void lds_tile_store_cols(const uint8_t* lds, int rows, int cols, int stride, uint8_t* out,
-                                  int64_t ldo, int rows_valid) {
-  const int nb_c = cols >> 2;
-  const int nblocks = (rows >> 4) * nb_c;
-  for (int idx = threadIdx.x; idx < nblocks; idx += 256) {
-    const int b = idx % nb_c, a = idx / nb_c;
-    uint32_t w[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = a * 16 + i;
-      w[i] = (r < rows_valid) ? *reinterpret_cast<const uint32_t*>(lds + r * stride + b * 4) : 0u;
-    }
-    uint32_t t[4][4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t o[4];
-      transpose4x4_bytes(&w[4 * q], o);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) t[c][q] = o[c];
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<intx4*>(out + (int64_t)(b * 4 + c) * ldo + a * 16) =
-          intx4{(int)t[c][0], (int)t[c][1], (int)t[c][2], (int)t[c][3]};
-  }
 }
 
 SFP8_DEV void store16(void* p, const uint32_t (&w)[4]) {
@@ -123,8 +114,8 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   const int wm = wave & 1, wn = wave >> 1;
   floatx16 acc[4][4];
   MainLoop<false, kFmtE4M3, kFmtE4M3, true>::run(
-      lds, x8 + m0 * D, (T - m0) * D, [=](int r) { return r * (int)D; }, w8 + n0 * D, (2 * I - n0) * D,
-      [=](int r) { return ((r >> 7) * (int)I + paired_col(r & 127)) * (int)D; }, 0, (int)(D / kStage), acc);
+      lds, x8 + m0 * D, (T - m0) * D, [=](int r) { return r * (int)D; }, kStage, w8 + n0 * D, (2 * I - n0) * D,
+      [=](int r) { return ((r >> 7) * (int)I + paired_col(r & 127)) * (int)D; }, kStage, (int)(D / kStage), acc);
   // All scales are powers of two, so the dequantization factor commutes with
   // every rounding step: with gb, ub = bf16(acc) (unscaled),
   //   g = gb*deq, u = ub*deq, h = (g*sig(g))*u = hb*deq^2, hb = (gb*sig)*ub,
@@ -201,7 +192,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   m_h *= deq * deq;
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
-  lds_tile_store_cols(Ht, kTile, 128, kEpiStride, h8t + n0 * ldt + m0, ldt, rows_valid);
+  lds_tile_store_slab<256>(Ht, kTile, 128, kEpiStride, h8t, slab_rows(I), m0, n0, rows_valid);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
   if (lane == 0) { red[wave] = m_gu; red[4 + wave] = m_h; }
@@ -227,8 +218,8 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
   const int wm = wave & 1, wn = wave >> 1;
   floatx16 acc[4][4];
   MainLoop<false, kFmtE4M3, kFmtE4M3, false>::run(
-      lds, h8 + m0 * I, (T - m0) * I, [=](int r) { return r * (int)I; }, wd8 + n0 * I, (D - n0) * I,
-      [=](int r) { return plain_col(r) * (int)I; }, 0, (int)(I / kStage), acc);
+      lds, h8 + m0 * I, (T - m0) * I, [=](int r) { return r * (int)I; }, kStage, wd8 + n0 * I, (D - n0) * I,
+      [=](int r) { return plain_col(r) * (int)I; }, kStage, (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[1]);
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
@@ -283,8 +274,8 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   floatx16 acc[4][4];
   MainLoop<true, 0, 0, false>::run(
       lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
-      reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb,
-      [=](int r) { return plain_col(r) * (int)ldb; }, 0, (int)(ldb / kStage), acc);
+      kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb,
+      [=](int r) { return plain_col(r) * (int)ldb; }, kStage, (int)(ldb / kStage), acc);
   // g = g8*s_gu, u = u8*s_gu with g8, u8 the stored e4m3 values; as the scales
   // are powers of two, d_gate = dg*s_gu and d_up = du*s_gu with
   //   dg = (dh*u8)*(sig*(1 + g*(1-sig))),  du = (dh*g8)*sig,
@@ -353,8 +344,8 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);
-  lds_tile_store_cols(Gt, kTile, cols, kEpiStride2, dgu8t + n0 * ldt + m0, ldt, rows_valid);
-  lds_tile_store_cols(Ut, kTile, cols, kEpiStride2, dgu8t + (I + n0) * ldt + m0, ldt, rows_valid);
+  lds_tile_store_slab<256>(Gt, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0, rows_valid);
+  lds_tile_store_slab<256>(Ut, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0, rows_valid);
   block_amax_atomic<4>(m3, red, amax + 3);
 }
 
@@ -374,8 +365,8 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
   const int64_t K = 2 * I;
   floatx16 acc[4][4];
   MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
-      lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, w8t + n0 * K, (D - n0) * K,
-      [=](int r) { return plain_col(r) * (int)K; }, 0, (int)(K / kStage), acc);
+      lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, kStage, w8t + n0 * K, (D - n0) * K,
+      [=](int r) { return plain_col(r) * (int)K; }, kStage, (int)(K / kStage), acc);
   const float sa = 1.0f / scale[3], sb = 1.0f / wscale[0];
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
@@ -402,29 +393,51 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
 // ---------------------------------------------------------------------------
 // (a12, a13) weight gradients, reduced over tokens:
 //   out[m, n] = sum_t A[m, t] * B[n, t] / (sa * sb)
-// A, B are the token-contiguous (transposed) fp8 copies with leading
-// dimension ldt (zero-padded past T).  blockIdx.y splits K; with splits > 1
-// each split writes raw fp32 partials to ws[split] and splitk_reduce sums
-// them in split order (deterministic).
+// A, B are K-slab token-contiguous fp8 copies (common.h) over ldt tokens
+// (zeros past T): a tile's K stage is one contiguous 16 KiB block of each.
+// The grid is tiles * splits work-groups (split_tile_coords); with splits > 1
+// each split writes its raw fp32 accumulators to ws in accumulator order
+// (frag_offset below: each wave store instruction is one contiguous 1 KiB
+// run) and splitk_reduce_kernel sums them in split order (deterministic) and
+// scatters them to [M, N].
 template <int FMT_A, int FMT_B>
 __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldt,
     int64_t kchunk, const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int splits) {
   extern __shared__ __align__(16) uint8_t lds[];
-  int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  int tm, tn, sp;
+  split_tile_coords(blockIdx.x, tiles_m, tiles_n, splits, tm, tn, sp);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   floatx16 acc[4][4];
-  const int64_t kb = (int64_t)blockIdx.y * kchunk;
+  // K-slab operands: slab (kb / 64) of A starts at (kb / 64) * rpa * 64
+  const int64_t kb = (int64_t)sp * kchunk;
+  const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
+  const uint8_t* a0 = at + (kb / kStage) * rpa * kStage + m0 * kStage;
+  const uint8_t* b0 = bt + (kb / kStage) * rpb * kStage + n0 * kStage;
+  const uint8_t* a_end = at + ldt * rpa;
+  const uint8_t* b_end = bt + ldt * rpb;
   MainLoop<false, FMT_A, FMT_B, false>::run(
-      lds, at + m0 * ldt, (M - m0) * ldt, [=](int r) { return r * (int)ldt; }, bt + n0 * ldt, (N - n0) * ldt,
-      [=](int r) { return plain_col(r) * (int)ldt; }, kb, (int)(kchunk / kStage), acc);
-  const bool split = gridDim.y > 1;
-  const float deq = split ? 1.0f : 1.0f / (sa[0] * sb[0]);
-  float* dst = out + (split ? (int64_t)blockIdx.y * M * N : 0);
+      lds, a0, a_end - a0, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_end - b0,
+      [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)(kchunk / kStage), acc);
+  if (splits > 1) {
+    // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
+    float* frag = out + ((int64_t)sp * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
+                  wave * (kTile * kTile / 4);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          reinterpret_cast<floatx4*>(frag + (tb * 4 + nb) * 1024 + i * 256)[lane] =
+              floatx4{acc[tb][nb][4 * i], acc[tb][nb][4 * i + 1], acc[tb][nb][4 * i + 2], acc[tb][nb][4 * i + 3]};
+    return;
+  }
+  const float deq = 1.0f / (sa[0] * sb[0]);
+  float* dst = out;
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
 #pragma unroll
@@ -441,6 +454,32 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
         p[i] = floatx4{acc[tb][nb][4 * i] * deq, acc[tb][nb][4 * i + 1] * deq, acc[tb][nb][4 * i + 2] * deq,
                        acc[tb][nb][4 * i + 3] * deq};
     }
+  }
+}
+
+// Split-K reduction of the accumulator-order partials of wgrad_kernel:
+// out[m, n] = (sum over s ascending of ws[s]) / (sa * sb).  Thread q owns the
+// q-th float4 of one split's partials; its (m, n) follows from the MFMA
+// accumulator layout (B-tile rows permuted by plain_col: accumulator v of
+// block nb, lane half g is column 128*wn + 64*g + 16*nb + v).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits,
+                                                            int64_t n4, int tiles_n, int64_t M, int64_t N,
+                                                            const float* __restrict__ sa,
+                                                            const float* __restrict__ sb, float* __restrict__ out) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= n4) return;
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
+  floatx4 acc = w4[q];
+  for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  const int lane = (int)(q & 63), i = (int)(q >> 6) & 3, nb = (int)(q >> 8) & 3, tb = (int)(q >> 10) & 3;
+  const int wave = (int)(q >> 12) & 3;
+  const int64_t tile = q >> 14;
+  const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
+  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
+  const int64_t n = tn * kTile + 128 * (wave >> 1) + 64 * (lane >> 5) + 16 * nb + 4 * i;
+  if (m < M && n < N) {
+    const float deq = 1.0f / (sa[0] * sb[0]);
+    *reinterpret_cast<floatx4*>(out + m * N + n) = acc * deq;
   }
 }
 
@@ -553,36 +592,44 @@ int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
   return s;
 }
 
-int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
-  const int64_t s = sfp8_wgrad_splits(M, N, ldt);
-  return s > 1 ? s * M * N : 0;
+int64_t sfp8_slab_bytes(int64_t rows, int64_t ldt) {
+  if (rows < 0 || ldt < 0 || ldt % kTile) return -1;
+  return slab_rows(rows) * ldt;
 }
 
-int sfp8_splitk_reduce(const float* ws, int64_t splits, int64_t M, int64_t N, const float* sa,
-                       const float* sb, float* out, void* stream);
+int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
+  // one 256 x 256 fp32 tile per (split, tile)
+  const int64_t s = sfp8_wgrad_splits(M, N, ldt);
+  return s > 1 ? s * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile : 0;
+}
+
 
 int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
                     const float* sa, const float* sb, float* out, float* ws, int64_t ws_floats, void* stream) {
   if (!at || !bt || !sa || !sb || !out) return kErrNullPointer;
   if (M <= 0 || N <= 0 || ldt < 0 || ldt % kTile || N % 4) return kErrBadShape;
   if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3) return kErrBadShape;
-  if (!fits32(kTile, ldt)) return kErrBadShape;
+  // every K-slab offset (stage * rows * 64 + row * 64) is 32-bit
+  if (!fits32(slab_rows(M), ldt) || !fits32(slab_rows(N), ldt)) return kErrBadShape;
   if (!al16(at) || !al16(bt) || !al16(out)) return kErrBadAlignment;
   hipStream_t st = (hipStream_t)stream;
   const int64_t splits = sfp8_wgrad_splits(M, N, ldt);
-  if (splits > 1 && (!ws || ws_floats < splits * M * N)) return kErrWorkspaceTooSmall;
+  if (splits > 1 && (!ws || ws_floats < sfp8_wgrad_workspace_floats(M, N, ldt))) return kErrWorkspaceTooSmall;
   if (ldt == 0) {
     return hipMemsetAsync(out, 0, (size_t)(M * N * 4), st) == hipSuccess ? kOk : status();
   }
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
   int rc = prep(wgrad_kernel<kFmtE5M2, kFmtE4M3>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((wgrad_kernel<kFmtE5M2, kFmtE4M3>), dim3(tiles_m * tiles_n, (unsigned)splits), dim3(256),
+  hipLaunchKernelGGL((wgrad_kernel<kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
                      kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
-                     splits > 1 ? ws : out, tiles_m, tiles_n);
+                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits);
   rc = status();
   if (rc || splits == 1) return rc;
-  return sfp8_splitk_reduce(ws, splits, M, N, sa, sb, out, stream);
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws,
+                     (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  return status();
 }
 
 }  // extern "C"

@@ -11,9 +11,11 @@
 // bank conflicts.
 //
 // Global -> LDS: buffer_load_dwordx4 ... lds (one 1 KiB block of 16 rows per
-// wave instruction, 8 per wave per stage), issued three stages ahead.  The
-// buffer descriptor's range check returns zeros for rows past the operand's
-// end, so tail tiles need no clamping.
+// wave instruction, 8 per wave per stage), issued three stages ahead.  Row
+// offsets go in the per-lane voffset, the stage offset in soffset.  For
+// row-major operands the descriptor's range check returns zeros for rows past
+// the operand's end (their voffset alone is out of range), so tail tiles need
+// no clamping; K-slab operands are row-padded so every read is in bounds.
 //
 // Per stage kt (branch-free body):
 //   wait until stage kt+1 has landed (vmcnt: one younger stage may be in
@@ -56,16 +58,17 @@ template <bool BF16, int FMT_A, int FMT_B, bool PAIRED>
 struct MainLoop {
   // Issue this wave's 8 DMA instructions of one stage.
   static SFP8_DEV void load_stage(uint8_t* lds, int buf, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                  const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[4], int soff, int wave) {
+                                  const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[4], int soff_a, int soff_b,
+                                  int wave) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint8_t* dst = lds + buf * kStageA + (64 * wave + 16 * j) * kStage;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, voff_a[j], soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, voff_a[j], soff_a, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint8_t* dst = lds + kLdsB + buf * kStageA + (64 * wave + 16 * j) * kStage;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, voff_b[j], soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, voff_b[j], soff_b, 0, 0);
     }
   }
 
@@ -140,16 +143,18 @@ struct MainLoop {
   }
 
   // a_bytes/b_bytes: bytes available from a_base/b_base (range-checked);
-  // a_rowoff(r)/b_rowoff(r): byte offset of tile row r (0..255) from the base;
-  // nk: number of 64-byte K stages, even.
+  // a_rowoff(r)/b_rowoff(r): byte offset of tile row r (0..255) from the base
+  // within one K stage; a_sstride/b_sstride: bytes from one 64-byte K stage to
+  // the next (64 for row-major operands, rows * 64 for K-slab operands);
+  // nk: number of K stages, even.
   template <class ARow, class BRow>
-  static SFP8_DEV void run(uint8_t* lds, const uint8_t* a_base, int64_t a_bytes, ARow a_rowoff,
-                           const uint8_t* b_base, int64_t b_bytes, BRow b_rowoff, int64_t k_begin, int nk,
+  static SFP8_DEV void run(uint8_t* lds, const uint8_t* a_base, int64_t a_bytes, ARow a_rowoff, int a_sstride,
+                           const uint8_t* b_base, int64_t b_bytes, BRow b_rowoff, int b_sstride, int nk,
                            floatx16 (&acc)[4][4]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a_base + k_begin, a_bytes - k_begin);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(b_base + k_begin, b_bytes - k_begin);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a_base, a_bytes);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(b_base, b_bytes);
     // DMA lane offsets: instruction j covers tile rows 64*wave + 16*j + lane/4,
     // physical chunk lane%4 <- logical chunk (lane%4) ^ ((row >> 1) & 3)
     uint32_t voff_a[4], voff_b[4];
@@ -177,7 +182,10 @@ struct MainLoop {
     const int last = nk - 1;
     // prologue: stages 0, 1, 2 in flight; stage 0 landed; its fragments read
 #pragma unroll
-    for (int s = 0; s < 3; ++s) load_stage(lds, s, ra, rb, voff_a, voff_b, (s < last ? s : last) * kStage, wave);
+    for (int s = 0; s < 3; ++s) {
+      const int ld = s < last ? s : last;
+      load_stage(lds, s, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
+    }
     asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
     Frag f0, f1;
     read_frags(lds, 0, aoff, boff, f0);
@@ -187,7 +195,7 @@ struct MainLoop {
       asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
       {
         const int ld = kt + 3 < last ? kt + 3 : last;
-        load_stage(lds, (kt + 3) & 3, ra, rb, voff_a, voff_b, ld * kStage, wave);
+        load_stage(lds, (kt + 3) & 3, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
         read_frags(lds, (kt + 1) & 3, aoff, boff, f1);
         mfma_stage(f0, acc);
         schedule();
@@ -196,7 +204,7 @@ struct MainLoop {
       asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
       {
         const int ld = kt + 4 < last ? kt + 4 : last;
-        load_stage(lds, kt & 3, ra, rb, voff_a, voff_b, ld * kStage, wave);
+        load_stage(lds, kt & 3, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
         read_frags(lds, (kt + 2) & 3, aoff, boff, f0);
         mfma_stage(f1, acc);
         schedule();

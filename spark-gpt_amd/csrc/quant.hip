@@ -15,6 +15,17 @@
 
 namespace sfp8 {
 
+// Row block of work-group pid in a 1-D grid of nblk row blocks.  Work-groups
+// are dispatched round-robin over the 8 XCDs (pid % 8); XCD x gets a
+// contiguous run of row blocks, so neighbouring blocks -- whose token-
+// contiguous (transposed) outputs share 128-byte lines -- run on the same XCD
+// and their partial lines merge in its L2.  A bijection of [0, nblk).
+SFP8_DEV int xcd_row_block(int pid, int nblk) {
+  const int per = nblk >> 3, rem = nblk & 7;
+  const int xcd = pid & 7, local = pid >> 3;
+  return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
 // --------------------------------------------------------------------------
 // Transposed write-out of an fp8 tile held in LDS.
 //   lds:      tile of `rows` rows x `cols` bytes, row stride `stride` bytes
@@ -109,8 +120,9 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
 // Norm-fused quantizer (spark-gpt train.py:955-972).
 //   rstd[t] = fl32(1/sqrt(fl64(fl32(sum h^2)/D + eps)))   (sum exact in fp64)
 //   n = (h * rstd) * w;  x8 = e4m3(n * s0);  amax0 = max |n|
-// x8t has leading dimension ldt (>= T, multiple of 16); columns T..ldt-1 of
-// every x8t row are written as zeros so a GEMM can reduce over ldt tokens.
+// x8t is the K-slab token-contiguous copy (common.h) over ldt tokens (a
+// multiple of 256); tokens T..ldt-1 are written as zeros so a GEMM can
+// reduce over ldt tokens.
 // Each work-group owns RT rows; a row is split over LPR lanes holding CPL
 // 8-element chunks each.
 template <int D>
@@ -133,7 +145,8 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
   uint8_t* tile = smem;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
-  const int64_t t0 = (int64_t)blockIdx.x * Cfg::RT;
+  const int blk = xcd_row_block(blockIdx.x, gridDim.x);
+  const int64_t t0 = (int64_t)blk * Cfg::RT;
   const float s0 = scale[0];
   float m = 0.0f;
   // norm weight for this lane's chunks
@@ -194,7 +207,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
   }
   __syncthreads();
   const int rows_valid = (int)((T - t0) < Cfg::RT ? (T - t0) : Cfg::RT);
-  lds_tile_store_transposed<256>(tile, Cfg::RT, D, Cfg::STRIDE, x8t, ldt, t0, rows_valid, ldt);
+  lds_tile_store_slab<256>(tile, Cfg::RT, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0, rows_valid);
   block_amax_atomic<4>(m, red, amax);
 }
 
@@ -297,8 +310,9 @@ __global__ void update_scales_kernel(float* __restrict__ scale, float* __restric
 //   g = dxn, gw = g*w, S = sum_d gw*h
 //   dh = bf16(gw*r - h*(S*r*r*r*(1/D)) + dy)
 //   dnw_part[block][d] = sum over the block's rows of g*(h*r)
-// plus, for the down-proj weight gradient, dy8t = e5m2(dy * s4)^T with zero
-// columns T..ldt-1, and amax slot 4 = max|dy| (recorded at train.py:1074-1081).
+// plus, for the down-proj weight gradient, dy8t = e5m2(dy * s4) as a K-slab
+// token-contiguous copy (zeros for tokens T..ldt-1), and amax slot 4 = max|dy|
+// (recorded at train.py:1074-1081).
 template <int D>
 __global__ __launch_bounds__(256) void norm_bwd_kernel(
     const uint16_t* __restrict__ h, const float* __restrict__ rstd, const uint16_t* __restrict__ dxn,
@@ -312,7 +326,8 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   float* dnw_red = reinterpret_cast<float*>(smem + Cfg::RT * Cfg::STRIDE);  // [4 waves][D]
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
-  const int64_t t0 = (int64_t)blockIdx.x * Cfg::RT;
+  const int blk = xcd_row_block(blockIdx.x, gridDim.x);
+  const int64_t t0 = (int64_t)blk * Cfg::RT;
   const float s4 = scale[4];
   float m = 0.0f;
   float w[Cfg::CPL][8], acc[Cfg::CPL][8];
@@ -396,10 +411,10 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   }
   __syncthreads();
   for (int d = threadIdx.x; d < D; d += 256)
-    dnw_part[(int64_t)blockIdx.x * D + d] =
+    dnw_part[(int64_t)blk * D + d] =
         ((dnw_red[d] + dnw_red[D + d]) + dnw_red[2 * D + d]) + dnw_red[3 * D + d];
   const int rows_valid = (int)((T - t0) < Cfg::RT ? (T - t0) : Cfg::RT);
-  lds_tile_store_transposed<256>(tile, Cfg::RT, D, Cfg::STRIDE, dy8t, ldt, t0, rows_valid, ldt);
+  lds_tile_store_slab<256>(tile, Cfg::RT, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0, rows_valid);
   block_amax_atomic<4>(m, red, amax + 4);
 }
 
@@ -428,19 +443,6 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ p
 
 // Row groups of the first colsum pass for nb partial rows.
 static inline int64_t colsum_groups(int64_t nb) { return nb < kColsumGroups ? nb : kColsumGroups; }
-
-// Split-K reduction: out = (sum_s ws[s]) * (1 / (sa * sb)), s ascending.
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits,
-                                                            int64_t n4, const float* __restrict__ sa,
-                                                            const float* __restrict__ sb,
-                                                            float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n4) return;
-  const float deq = 1.0f / (sa[0] * sb[0]);
-  floatx4 acc = reinterpret_cast<const floatx4*>(ws)[i];
-  for (int s = 1; s < splits; ++s) acc += reinterpret_cast<const floatx4*>(ws)[(int64_t)s * n4 + i];
-  reinterpret_cast<floatx4*>(out)[i] = acc * deq;
-}
 
 }  // namespace sfp8
 
@@ -604,15 +606,5 @@ int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void*
   }
 }
 
-int sfp8_splitk_reduce(const float* ws, int64_t splits, int64_t M, int64_t N, const float* sa,
-                       const float* sb, float* out, void* stream) {
-  if (!ws || !sa || !sb || !out) return kErrNullPointer;
-  if (splits < 1 || M < 0 || N < 0 || ((M * N) % 4) != 0) return kErrBadShape;
-  const int64_t n4 = M * N / 4;
-  if (n4 == 0) return kOk;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, ws, (int)splits, n4, sa, sb, out);
-  return launch_status();
-}
 
 }  // extern "C"

@@ -116,8 +116,8 @@ class _FP8MLPBlock(torch.autograd.Function):
         del dgu8
         dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nw, scale, amax)
         del dxn
-        dwd = ops.wgrad(dy8t, h8t, scale[4:5], scale[2:3])
-        dwgu = ops.wgrad(dgu8t, x8t, scale[3:4], scale[0:1])
+        dwd = ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3])
+        dwgu = ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1])
         assert dwd.shape == (D, I) and dwgu.shape == (2 * I, D)
         return dh, dnw, dwgu, dwd, None, None, None
 

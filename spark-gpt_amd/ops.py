@@ -19,8 +19,38 @@ TOKEN_ALIGN = 256  # leading dimension of token-contiguous fp8 copies
 
 
 def ldt_of(T: int) -> int:
-    """Leading dimension of the token-contiguous copies (x8t, h8t, d_gu8t, dy8t)."""
+    """Tokens covered by the token-contiguous copies (x8t, h8t, d_gu8t, dy8t):
+    T rounded up to a multiple of 256, zero past T."""
     return -(-T // TOKEN_ALIGN) * TOKEN_ALIGN
+
+
+SLAB = 64  # tokens per K slab
+
+
+def slab_rows(R: int) -> int:
+    """Rows of a K-slab copy: R rounded up to the 256-row GEMM tile."""
+    return -(-R // 256) * 256
+
+
+def slab_empty(R: int, T: int, dtype, device) -> torch.Tensor:
+    """A K-slab token-contiguous copy of R rows over ldt_of(T) tokens:
+    [ldt / 64, slab_rows(R), 64]; element (r, t) at [t // 64, r, t % 64]."""
+    return torch.empty(ldt_of(T) // SLAB, slab_rows(R), SLAB, dtype=dtype, device=device)
+
+
+def unslab(t: torch.Tensor, R: int) -> torch.Tensor:
+    """The plain [R, ldt] view-copy of a K-slab tensor (for inspection and tests)."""
+    n, rp, _ = t.shape
+    return t.view(torch.uint8).permute(1, 0, 2).reshape(rp, n * SLAB)[:R].view(t.dtype)
+
+
+def to_slab(x: torch.Tensor) -> torch.Tensor:
+    """K-slab copy of a plain [R, ldt] tensor (ldt % 256 == 0); padding rows zero."""
+    R, L = x.shape
+    _need(L % TOKEN_ALIGN == 0, "token count must be a multiple of 256")
+    out = torch.zeros(L // SLAB, slab_rows(R), SLAB, dtype=torch.uint8, device=x.device)
+    out[:, :R] = x.contiguous().view(torch.uint8).view(R, L // SLAB, SLAB).permute(1, 0, 2)
+    return out.view(x.dtype)
 
 
 def _need(cond: bool, msg: str) -> None:
@@ -55,14 +85,15 @@ def quant_e4m3_rowcol(x: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor):
 
 
 def norm_quant(h: torch.Tensor, norm_w: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor, eps: float):
-    """(x8 [T, D], x8t [D, ldt], rstd [T]); amax[0] max-accumulated."""
+    """(x8 [T, D], x8t K-slab [ldt/64, slab_rows(D), 64], rstd [T]); amax[0]
+    max-accumulated."""
     _cuda_contig("h", h, torch.bfloat16, 2)
     _cuda_contig("norm_w", norm_w, torch.float32, 1)
     _state(scale, amax)
     T, D = h.shape
     ldt = ldt_of(T)
     x8 = torch.empty(T, D, dtype=E4M3, device=h.device)
-    x8t = torch.empty(D, ldt, dtype=E4M3, device=h.device)
+    x8t = slab_empty(D, T, E4M3, h.device)
     rstd = torch.empty(T, dtype=torch.float32, device=h.device)
     _lib.call("sfp8_norm_quant", h.data_ptr(), norm_w.data_ptr(), T, D, float(eps), scale.data_ptr(),
               amax.data_ptr(), x8.data_ptr(), x8t.data_ptr(), ldt, rstd.data_ptr(), _lib.stream_of(h))
@@ -98,7 +129,8 @@ def update_scales(scale: torch.Tensor, amax: torch.Tensor) -> None:
 
 # ------------------------------------------------------------------ GEMMs
 def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I: int):
-    """(gu8 [T, 2I], h8 [T, I], h8t [I, ldt]); amax[1], amax[2] max-accumulated."""
+    """(gu8 [T, 2I], h8 [T, I], h8t K-slab of I rows); amax[1], amax[2]
+    max-accumulated."""
     _cuda_contig("x8", x8, E4M3, 2)
     _cuda_contig("w8", w8, E4M3, 2)
     T, D = x8.shape
@@ -108,7 +140,7 @@ def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I: int):
     dev = x8.device
     gu8 = torch.empty(T, 2 * I, dtype=E4M3, device=dev)
     h8 = torch.empty(T, I, dtype=E4M3, device=dev)
-    h8t = torch.empty(I, ldt, dtype=E4M3, device=dev)
+    h8t = slab_empty(I, T, E4M3, dev)
     _lib.call("sfp8_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), T, D, I, scale.data_ptr(),
               wscale.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr(), ldt,
               _lib.stream_of(x8))
@@ -131,7 +163,7 @@ def down_fwd(h8, wd8, res, scale, wscale):
 
 
 def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
-    """(dgu8 [T, 2I] e5m2, dgu8t [2I, ldt] e5m2); amax[3] max-accumulated."""
+    """(dgu8 [T, 2I] e5m2, dgu8t K-slab of 2I rows e5m2); amax[3] max-accumulated."""
     _cuda_contig("dy", dy, torch.bfloat16, 2)
     _cuda_contig("wdt", wdt, torch.bfloat16, 2)
     _cuda_contig("gu8", gu8, E4M3, 2)
@@ -141,7 +173,7 @@ def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
     _need(D % 64 == 0 and I % 16 == 0, "D must be a multiple of 64")
     ldt = ldt_of(T)
     dgu8 = torch.empty(T, 2 * I, dtype=E5M2, device=dy.device)
-    dgu8t = torch.empty(2 * I, ldt, dtype=E5M2, device=dy.device)
+    dgu8t = slab_empty(2 * I, T, E5M2, dy.device)
     _lib.call("sfp8_gemm_down_dgrad_swiglu", dy.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), T, D, I,
               scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr(), ldt, _lib.stream_of(dy))
     return dgu8, dgu8t
@@ -160,14 +192,16 @@ def gateup_dgrad(dgu8, w8t, scale, wscale):
     return dxn
 
 
-def wgrad(at, bt, sa, sb):
+def wgrad(at, bt, M: int, N: int, sa, sb):
     """out[m, n] = sum_t at[m, t] bt[n, t] / (sa * sb), fp32 [M, N]; at e5m2
-    [M, ldt], bt e4m3 [N, ldt] (token-contiguous, zero-padded)."""
-    _cuda_contig("at", at, E5M2, 2)
-    _cuda_contig("bt", bt, E4M3, 2)
-    M, ldt = at.shape
-    N = bt.shape[0]
-    _need(bt.shape[1] == ldt and ldt % TOKEN_ALIGN == 0, "wgrad operands need a common padded ldt")
+    and bt e4m3 are K-slab token-contiguous copies of M and N rows (zeros past
+    the last token)."""
+    _cuda_contig("at", at, E5M2, 3)
+    _cuda_contig("bt", bt, E4M3, 3)
+    ldt = at.shape[0] * SLAB
+    _need(at.shape == (ldt // SLAB, slab_rows(M), SLAB), "at must be a K-slab copy of M rows")
+    _need(bt.shape == (ldt // SLAB, slab_rows(N), SLAB), "bt must be a K-slab copy of N rows over the same tokens")
+    _need(ldt % TOKEN_ALIGN == 0, "token count must be a multiple of 256")
     out = torch.empty(M, N, dtype=torch.float32, device=at.device)
     nws = _lib.query("sfp8_wgrad_workspace_floats", M, N, ldt)
     ws = torch.empty(max(nws, 1), dtype=torch.float32, device=at.device)
@@ -178,7 +212,7 @@ def wgrad(at, bt, sa, sb):
 
 # ------------------------------------------------------------------ norm backward
 def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
-    """(dh [T, D] bf16, dnw [D] fp32, dy8t [D, ldt] e5m2); amax[4] = max|dy|."""
+    """(dh [T, D] bf16, dnw [D] fp32, dy8t K-slab of D rows e5m2); amax[4] = max|dy|."""
     for n, t in (("h", h), ("dxn", dxn), ("dy", dy)):
         _cuda_contig(n, t, torch.bfloat16, 2)
     _cuda_contig("rstd", rstd, torch.float32, 1)
@@ -188,7 +222,7 @@ def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
     dev = h.device
     dh = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     dnw = torch.empty(D, dtype=torch.float32, device=dev)
-    dy8t = torch.empty(D, ldt, dtype=E5M2, device=dev)
+    dy8t = slab_empty(D, T, E5M2, dev)
     nparts = _lib.query("sfp8_norm_bwd_partials", D, ldt)
     _need(nparts >= 0, f"unsupported hidden size {D}")
     parts = torch.empty(max(nparts * D, 1), dtype=torch.float32, device=dev)

@@ -54,9 +54,10 @@ def test_swiglu_fwd_integer_operands(dev, T, D, I):
     assert int(code_dist(h8, rh8).max()) <= 1
     assert float((code_dist(h8, rh8) > 0).float().mean()) < 0.01
     ldt = sg.ops.ldt_of(T)
-    assert h8t.shape == (I, ldt)
-    assert torch.equal(u8(h8t)[:, :T], u8(h8).t())
-    assert torch.all(u8(h8t)[:, T:] == 0)
+    assert h8t.shape == (ldt // 64, sg.ops.slab_rows(I), 64)
+    ht = u8(sg.ops.unslab(h8t, I))
+    assert torch.equal(ht[:, :T], u8(h8).t())
+    assert torch.all(ht[:, T:] == 0)
     assert amax[1].item() == ra1.item()
     torch.testing.assert_close(amax[2].cpu(), ra2, rtol=1e-5, atol=0)
 
@@ -110,8 +111,9 @@ def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     d = code_dist(dgu8, rdgu8)
     assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.01
-    assert torch.equal(u8(dgu8t)[:, :T], u8(dgu8).t())
-    assert torch.all(u8(dgu8t)[:, T:] == 0)
+    dt = u8(sg.ops.unslab(dgu8t, 2 * I))
+    assert torch.equal(dt[:, :T], u8(dgu8).t())
+    assert torch.all(dt[:, T:] == 0)
     torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-5, atol=0)
 
 
@@ -153,7 +155,12 @@ def test_wgrad_integer_operands(dev, T, M, N):
     at[:, :T] = u8(a).t()
     bt[:, :T] = u8(b).t()
     sa, sb = torch.tensor([2.0 ** 3]), torch.tensor([0.5])
-    out = sg.ops.wgrad(at.view(E5).to(dev), bt.view(E4).to(dev), sa.to(dev), sb.to(dev))
+    at_s = sg.ops.to_slab(at.view(E5)).view(torch.uint8)
+    bt_s = sg.ops.to_slab(bt.view(E4)).view(torch.uint8)
+    # padding rows (beyond M, N) hold NaN codes: they must not reach the output
+    at_s[:, M:] = 0x7F
+    bt_s[:, N:] = 0x7F
+    out = sg.ops.wgrad(at_s.view(E5).to(dev), bt_s.view(E4).to(dev), M, N, sa.to(dev), sb.to(dev))
     ref = (a.float().t() @ b.float()) / (sa * sb)
     assert torch.equal(out.cpu(), ref)
 
@@ -174,12 +181,12 @@ def test_wgrad_matches_oracle_forms(dev):
     def tpad(t8):
         out = torch.zeros(t8.shape[1], ldt, dtype=torch.uint8)
         out[:, :T] = u8(t8).t()
-        return out.view(t8.dtype).to(dev)
+        return sg.ops.to_slab(out.view(t8.dtype)).to(dev)
 
     dy8 = O.e5m2(dy.float() * s[4])
     sd = s.to(dev)
-    dwd = sg.ops.wgrad(tpad(dy8), tpad(h8), sd[4:5], sd[2:3])
-    dwgu = sg.ops.wgrad(tpad(dgu8), tpad(x8), sd[3:4], sd[0:1])
+    dwd = sg.ops.wgrad(tpad(dy8), tpad(h8), D, I, sd[4:5], sd[2:3])
+    dwgu = sg.ops.wgrad(tpad(dgu8), tpad(x8), 2 * I, D, sd[3:4], sd[0:1])
     for got, ref in ((dwd, O.down_wgrad(dy, h8, s)), (dwgu, O.gateup_wgrad(dgu8, x8, s))):
         torch.testing.assert_close(got.cpu(), ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()))
         assert O.rel_l2(got.cpu(), ref) < 1e-4

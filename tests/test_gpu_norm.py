@@ -29,9 +29,10 @@ def test_norm_quant_bit_exact(dev, T, D):
     assert torch.equal(rstd.cpu(), rr)
     assert torch.equal(u8(x8), u8(r8))
     ldt = sg.ops.ldt_of(T)
-    assert x8t.shape == (D, ldt)
-    assert torch.equal(u8(x8t)[:, :T], u8(r8t))
-    assert torch.all(u8(x8t)[:, T:] == 0)
+    assert x8t.shape == (ldt // 64, sg.ops.slab_rows(D), 64)
+    xt = u8(sg.ops.unslab(x8t, D))
+    assert torch.equal(xt[:, :T], u8(r8t))
+    assert torch.all(xt[:, T:] == 0)
     assert amax[0].item() == ra.item()
 
 
@@ -70,6 +71,7 @@ def test_norm_bwd(dev, T, D):
     assert O.rel_l2(dh.cpu().float(), rdh.float()) < 1e-3
     torch.testing.assert_close(dnw.cpu(), rdnw, rtol=1e-4, atol=1e-4)
     ref8 = O.e5m2(dy.float() * 2.0 ** 15)
-    assert torch.equal(u8(dy8t)[:, :T], u8(ref8).t())
-    assert torch.all(u8(dy8t)[:, T:] == 0)
+    yt = u8(sg.ops.unslab(dy8t, D))
+    assert torch.equal(yt[:, :T], u8(ref8).t())
+    assert torch.all(yt[:, T:] == 0)
     assert amax[4].item() == dy.float().abs().max().item()

@@ -54,6 +54,9 @@ def test_size_queries_need_no_gpu():
     s = _lib.query("sfp8_wgrad_splits", 6144, 1024, 65536)
     assert s >= 1 and 65536 % s == 0 and (65536 // s) % 128 == 0
     assert _lib.query("sfp8_wgrad_workspace_floats", 6144, 1024, 65536) == (s * 6144 * 1024 if s > 1 else 0)
+    # partials are whole 256 x 256 tiles per split
+    s2 = _lib.query("sfp8_wgrad_splits", 384, 128, 65536)
+    assert s2 > 1 and _lib.query("sfp8_wgrad_workspace_floats", 384, 128, 65536) == s2 * 2 * 256 * 256
     assert _lib.query("sfp8_wgrad_splits", 256, 256, 256) == 1
 
 
@@ -84,6 +87,25 @@ def test_ops_reject_host_tensors():
         ops.norm_quant(h, torch.ones(128), torch.ones(5), torch.zeros(5), 1e-6)
     with pytest.raises((ValueError, RuntimeError)):
         ops.quant_e4m3_rowcol(h, torch.ones(5), torch.zeros(5))
+
+
+def test_slab_layout_roundtrip():
+    """K-slab copies: element (r, t) at [t // 64, r, t % 64], rows padded to 256."""
+    assert ops.slab_rows(1) == 256 and ops.slab_rows(256) == 256 and ops.slab_rows(768) == 768
+    assert ops.slab_rows(384) == 512
+    g = torch.Generator().manual_seed(9)
+    x = torch.randint(0, 256, (384, 512), generator=g, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    s = ops.to_slab(x)
+    assert s.shape == (8, 512, 64) and s.dtype == x.dtype
+    su = s.view(torch.uint8)
+    xu = x.view(torch.uint8)
+    for r, t in ((0, 0), (383, 511), (17, 64), (200, 300)):
+        assert su[t // 64, r, t % 64] == xu[r, t]
+    assert torch.all(su[:, 384:] == 0)
+    assert torch.equal(ops.unslab(s, 384).view(torch.uint8), xu)
+    assert _lib.query("sfp8_slab_bytes", 384, 512) == 512 * 512
+    assert _lib.query("sfp8_slab_bytes", 6144, 65536) == 6144 * 65536
+    assert _lib.query("sfp8_slab_bytes", 128, 100) == -1
 
 
 def test_ldt_padding():
