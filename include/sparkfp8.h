@@ -95,7 +95,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
 
 /* down forward + residual, replaces _fp8_down_fwd_kernel (train.py:1019-1046,
  * launched at train.py:1220-1222).  h8 [T, I] e4m3, wd8 [D, I] e4m3,
- * res [T, D] bf16 -> y [T, D] bf16.  I % 128 == 0. */
+ * res [T, D] bf16 -> y [T, D] bf16.  I % 128 == 0, D % 16 == 0. */
 int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
                        const float* scale, const float* wscale, void* y, void* stream);
 
@@ -110,7 +110,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
 
 /* gate/up dgrad, replaces torch._scaled_mm (train.py:1239-1241):
  * dxn = bf16((dgu8 @ w8) / (scale[3] * wscale[0])), dgu8 [T, 2I] e5m2,
- * w8t [D, 2I] e4m3 -> dxn [T, D] bf16. */
+ * w8t [D, 2I] e4m3 -> dxn [T, D] bf16.  I % 64 == 0, D % 16 == 0. */
 int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
                            const float* scale, const float* wscale, void* dxn, void* stream);
 

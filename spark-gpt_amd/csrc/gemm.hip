@@ -79,6 +79,21 @@ SFP8_DEV int paired_col(int r) {
   return (r & 64) + 32 * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
 }
 
+// Coalesced copy of an LDS tile to a row-major global matrix: nrows rows of
+// (16 << cpr_log2) bytes, LDS row stride `stride`, global row r at
+// dst + r * ld; rows >= rows_valid are skipped.  Consecutive threads take
+// consecutive 16-byte chunks, so a wave store covers whole rows.
+SFP8_DEV void lds_rows_to_global(const uint8_t* lds, int nrows, int cpr_log2, int stride, uint8_t* dst,
+                                 int64_t ld, int rows_valid) {
+  const int total = nrows << cpr_log2;
+  const int cmask = (1 << cpr_log2) - 1;
+  for (int idx = threadIdx.x; idx < total; idx += 256) {
+    const int r = idx >> cpr_log2, c = idx & cmask;
+    if (r < rows_valid)
+      *reinterpret_cast<intx4*>(dst + r * ld + c * 16) = *reinterpret_cast<const intx4*>(lds + r * stride + c * 16);
+  }
+}
+
 SFP8_DEV void store16(void* p, const uint32_t (&w)[4]) {
   *reinterpret_cast<intx4*>(p) = intx4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
@@ -106,7 +121,6 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
     uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int64_t ldt,
     int tiles_m, int tiles_n) {
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ float red[8];
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 128;
@@ -128,14 +142,17 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   const float m1 = deq * scale[1], m2 = deq * deq * scale[2];
   const float inv1 = 1.0f / m1, inv2 = 1.0f / m2;
   const float bnd1 = kE4M3Max * inv1, bnd2 = kE4M3Max * inv2;
-  uint8_t* Ht = lds;
+  // epilogue LDS: the tile's g8, u8 and h8 bytes (256 x 128 each), then the amax slots
+  uint8_t* Gt = lds;
+  uint8_t* Ut = lds + kTile * kEpiStride;
+  uint8_t* Ht = lds + 2 * kTile * kEpiStride;
+  float* red = reinterpret_cast<float*>(lds + 3 * kTile * kEpiStride);
   float m_gu = 0.f, m_h = 0.f;
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 64 * wn + 32 * g;  // first of this lane's 32 columns
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;  // token within the tile
-    const int64_t t = m0 + row;
     uint32_t gw[8], uw[8], hw[8];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
@@ -175,23 +192,21 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
         hw[4 * nb + q] = ph;
       }
     }
-    if (t < T) {
-      uint8_t* gp = gu8 + t * 2 * I + n0 + cb;
-      uint8_t* hp = h8 + t * I + n0 + cb;
-      store16(gp, {gw[0], gw[1], gw[2], gw[3]});
-      store16(gp + 16, {gw[4], gw[5], gw[6], gw[7]});
-      store16(gp + I, {uw[0], uw[1], uw[2], uw[3]});
-      store16(gp + I + 16, {uw[4], uw[5], uw[6], uw[7]});
-      store16(hp, {hw[0], hw[1], hw[2], hw[3]});
-      store16(hp + 16, {hw[4], hw[5], hw[6], hw[7]});
-    }
+    store16(Gt + row * kEpiStride + cb, {gw[0], gw[1], gw[2], gw[3]});
+    store16(Gt + row * kEpiStride + cb + 16, {gw[4], gw[5], gw[6], gw[7]});
+    store16(Ut + row * kEpiStride + cb, {uw[0], uw[1], uw[2], uw[3]});
+    store16(Ut + row * kEpiStride + cb + 16, {uw[4], uw[5], uw[6], uw[7]});
     store16(Ht + row * kEpiStride + cb, {hw[0], hw[1], hw[2], hw[3]});
     store16(Ht + row * kEpiStride + cb + 16, {hw[4], hw[5], hw[6], hw[7]});
   }
   m_gu *= deq;
   m_h *= deq * deq;
   __syncthreads();
+  // whole 128-byte rows: gate and up halves of gu8, h8, then the K-slab h8t
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
+  lds_rows_to_global(Gt, kTile, 3, kEpiStride, gu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
+  lds_rows_to_global(Ut, kTile, 3, kEpiStride, gu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
+  lds_rows_to_global(Ht, kTile, 3, kEpiStride, h8 + m0 * I + n0, I, rows_valid);
   lds_tile_store_slab<256>(Ht, kTile, 128, kEpiStride, h8t, slab_rows(I), m0, n0, rows_valid);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
@@ -200,6 +215,58 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   if (tid == 0) {
     atomic_max_nonneg(amax + 1, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
     atomic_max_nonneg(amax + 2, fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+  }
+}
+
+// bf16 epilogues stage the tile in two passes of 128 rows (256 bf16 columns,
+// row stride kBf16Stride: consecutive rows shift by 4 banks) and then write
+// whole rows.  Pass P holds tile rows 64P..64P+63 and 128+64P..128+64P+63.
+constexpr int kBf16Stride = 528;
+
+template <int P>
+SFP8_DEV void stage_bf16_half(uint8_t* lds, const floatx16 (&acc)[4][4], float s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
+  const int fr = lane & 31, g = lane >> 5, cb = 128 * wn + 64 * g;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int lr = 64 * wm + 32 * tt + fr;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      uint32_t w0[4], w1[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w0[i] = pack2_bf16(acc[2 * P + tt][nb][2 * i] * s, acc[2 * P + tt][nb][2 * i + 1] * s);
+        w1[i] = pack2_bf16(acc[2 * P + tt][nb][8 + 2 * i] * s, acc[2 * P + tt][nb][8 + 2 * i + 1] * s);
+      }
+      uint8_t* q = lds + lr * kBf16Stride + (cb + 16 * nb) * 2;
+      store16(q, w0);
+      store16(q + 16, w1);
+    }
+  }
+}
+
+// Tile row held in staging row lr of pass p.
+SFP8_DEV int half_tile_row(int lr, int p) { return 128 * (lr >> 6) + 64 * p + (lr & 63); }
+
+// Writes one staged pass to out[t, n] (bf16, leading dimension ld), adding the
+// bf16 residual res[t, n] first when res is given: out = bf16(res + staged).
+SFP8_DEV void write_bf16_half(const uint8_t* lds, int p, int64_t m0, int64_t n0, int64_t T, int64_t N,
+                              int64_t ld, const uint16_t* __restrict__ res, uint16_t* __restrict__ out) {
+  for (int idx = threadIdx.x; idx < 128 * 32; idx += 256) {
+    const int lr = idx >> 5, c = idx & 31;
+    const int64_t t = m0 + half_tile_row(lr, p), n = n0 + 8 * c;
+    if (t >= T || n >= N) continue;
+    intx4 o = *reinterpret_cast<const intx4*>(lds + lr * kBf16Stride + c * 16);
+    if (res) {
+      const intx4 r = *reinterpret_cast<const intx4*>(res + t * ld + n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t a = (uint32_t)r[i], b = (uint32_t)o[i];
+        o[i] = (int)pack2_bf16(__uint_as_float(b << 16) + __uint_as_float(a << 16),
+                               __uint_as_float(b & 0xffff0000u) + __uint_as_float(a & 0xffff0000u));
+      }
+    }
+    *reinterpret_cast<intx4*>(out + t * ld + n) = o;
   }
 }
 
@@ -214,13 +281,13 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
   floatx16 acc[4][4];
   MainLoop<false, kFmtE4M3, kFmtE4M3, false>::run(
       lds, h8 + m0 * I, (T - m0) * I, [=](int r) { return r * (int)I; }, kStage, wd8 + n0 * I, (D - n0) * I,
       [=](int r) { return plain_col(r) * (int)I; }, kStage, (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[1]);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
 #pragma unroll
@@ -264,7 +331,6 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, float* __restrict__ amax,
     uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n) {
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ float red[4];
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
@@ -286,6 +352,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   const float inv3 = 1.0f / m3s, bnd3 = kE5M2Max * inv3;
   uint8_t* Gt = lds;
   uint8_t* Ut = lds + kTile * kEpiStride2;
+  float* red = reinterpret_cast<float*>(lds + 2 * kTile * kEpiStride2);  // 4 floats after both tiles
   // gu8 rows of this tile through a range-checked descriptor: rows past T
   // read as zero (and their dh is zero: dy rows past T read as zero)
   const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 2 * I, (T - m0) * 2 * I);
@@ -295,7 +362,6 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;
-    const int64_t t = m0 + row;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int col = cb + 16 * nb;
@@ -331,10 +397,6 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
             pu[w] = fix_nan4(pu[w], du[0], du[1], du[2], du[3]);
           }
         }
-        if (t < T) {
-          store16(dgu8 + t * 2 * I + j, pg);
-          store16(dgu8 + t * 2 * I + I + j, pu);
-        }
       }
       store16(Gt + row * kEpiStride2 + col, pg);
       store16(Ut + row * kEpiStride2 + col, pu);
@@ -343,7 +405,9 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   m3 *= s_gu;
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
-  const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);
+  const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
+  lds_rows_to_global(Gt, kTile, cols == kTile ? 4 : 3, kEpiStride2, dgu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
+  lds_rows_to_global(Ut, kTile, cols == kTile ? 4 : 3, kEpiStride2, dgu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
   lds_tile_store_slab<256>(Gt, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0, rows_valid);
   lds_tile_store_slab<256>(Ut, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0, rows_valid);
   block_amax_atomic<4>(m3, red, amax + 3);
@@ -360,34 +424,19 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
   const int64_t K = 2 * I;
   floatx16 acc[4][4];
   MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
       lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, kStage, w8t + n0 * K, (D - n0) * K,
       [=](int r) { return plain_col(r) * (int)K; }, kStage, (int)(K / kStage), acc);
-  const float sa = 1.0f / scale[3], sb = 1.0f / wscale[0];
-  const int fr = lane & 31, g = lane >> 5;
-  const int cb = 128 * wn + 64 * g;
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int64_t t = m0 + 128 * wm + 32 * tb + fr;
-    if (t >= T) continue;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int64_t n = n0 + cb + 16 * nb;
-      if (n >= D) continue;
-      uint32_t w0[4], w1[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w0[i] = pack2_bf16(acc[tb][nb][2 * i] * sa * sb, acc[tb][nb][2 * i + 1] * sa * sb);
-        w1[i] = pack2_bf16(acc[tb][nb][8 + 2 * i] * sa * sb, acc[tb][nb][8 + 2 * i + 1] * sa * sb);
-      }
-      store16(dxn + t * D + n, w0);
-      store16(dxn + t * D + n + 8, w1);
-    }
-  }
+  const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
+  stage_bf16_half<0>(lds, acc, sab);
+  __syncthreads();
+  write_bf16_half(lds, 0, m0, n0, T, D, D, nullptr, dxn);
+  __syncthreads();
+  stage_bf16_half<1>(lds, acc, sab);
+  __syncthreads();
+  write_bf16_half(lds, 1, m0, n0, T, D, D, nullptr, dxn);
 }
 
 // ---------------------------------------------------------------------------
@@ -485,6 +534,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 }  // namespace sfp8
 
+static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
+static_assert(128 * sfp8::kBf16Stride <= sfp8::kMainLds, "bf16 epilogue staging fits the main loop's LDS");
+
 // ============================================================================
 // C ABI
 // ============================================================================
@@ -492,7 +544,9 @@ using namespace sfp8;
 
 namespace {
 
-constexpr int kDgradLds = 2 * kTile * kEpiStride2;   // 139264 > kMainLds
+// epilogue tiles (2 x 256 x 272) + 4 amax floats, or the main loop's ring
+constexpr int kDgradEpiLds = 2 * kTile * kEpiStride2 + 16;
+constexpr int kDgradLds = kDgradEpiLds > kMainLds ? kDgradEpiLds : kMainLds;
 
 template <typename K>
 int prep(K kernel, int lds_bytes) {
@@ -536,7 +590,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
 int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
                        const float* scale, const float* wscale, void* y, void* stream) {
   if (!h8 || !wd8 || !res || !scale || !wscale || !y) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 4) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 16) return kErrBadShape;
   if (!fits32(kTile, I)) return kErrBadShape;
   if (!al16(h8) || !al16(wd8) || !al16(res) || !al16(y)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -569,7 +623,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
 int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
                            const float* scale, const float* wscale, void* dxn, void* stream) {
   if (!dgu8 || !w8t || !scale || !wscale || !dxn) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 4) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 16) return kErrBadShape;
   if (!fits32(kTile, 2 * I)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
   if (T == 0) return kOk;

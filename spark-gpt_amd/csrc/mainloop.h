@@ -6,9 +6,10 @@
 //
 // K advances in 64-byte stages.  Four LDS stages of (A 16 KiB + B 16 KiB):
 //   A stage s at s*16 KiB, B stage s at 64 KiB + s*16 KiB.
-// A 64-byte LDS row r holds its 16-byte chunk c at chunk (c ^ ((r >> 1) & 3)),
-// which keeps both the 16-row DMA fills and the 32-row fragment reads free of
-// bank conflicts.
+// A 64-byte LDS row r holds its 16-byte chunk c at chunk (c ^ ((r >> 2) & 3)).
+// gfx950's LDS serves a 16-byte-per-lane read 16 lanes at a time over 64
+// banks (256 bytes); with this swizzle the 16 rows a lane group reads land on
+// 16 distinct 4-bank groups.  The DMA fills are contiguous 1 KiB writes.
 //
 // Global -> LDS: buffer_load_dwordx4 ... lds (one 1 KiB block of 16 rows per
 // wave instruction, 8 per wave per stage), issued three stages ahead.  Row
@@ -31,7 +32,7 @@ namespace sfp8 {
 
 constexpr int kTile = 256;
 constexpr int kStage = 64;                   // bytes of K per stage
-constexpr int kStages = 4;
+constexpr int kStages = 4;                   // LDS ring depth (>= 3)
 constexpr int kStageA = kTile * kStage;      // 16 KiB
 constexpr int kLdsB = kStages * kStageA;     // 64 KiB: start of the B stages
 constexpr int kMainLds = 2 * kStages * kStageA;  // 128 KiB
@@ -156,9 +157,9 @@ struct MainLoop {
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a_base, a_bytes);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(b_base, b_bytes);
     // DMA lane offsets: instruction j covers tile rows 64*wave + 16*j + lane/4,
-    // physical chunk lane%4 <- logical chunk (lane%4) ^ ((row >> 1) & 3)
+    // physical chunk lane%4 <- logical chunk (lane%4) ^ ((row >> 2) & 3)
     uint32_t voff_a[4], voff_b[4];
-    const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 3) & 3)) << 4);
+    const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int r = 64 * wave + 16 * j + (lane >> 2);
@@ -167,7 +168,7 @@ struct MainLoop {
     }
     // fragment read offsets (lane half g reads logical chunks 2g, 2g+1)
     const int fr = lane & 31, g = lane >> 5;
-    const int sw = (fr >> 1) & 3;
+    const int sw = (fr >> 2) & 3;
     uint32_t aoff[2], boff[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -180,32 +181,36 @@ struct MainLoop {
       for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                                        0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int last = nk - 1;
-    // prologue: stages 0, 1, 2 in flight; stage 0 landed; its fragments read
+    // prologue: stages 0 .. kStages-2 in flight; stage 0 landed; its fragments read
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
+    for (int s = 0; s < kStages - 1; ++s) {
       const int ld = s < last ? s : last;
       load_stage(lds, s, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
     }
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    // 8 DMA instructions per wave per stage: stages 1 .. kStages-2 may still fly
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(8 * (kStages - 2)) : "memory");
     Frag f0, f1;
     read_frags(lds, 0, aoff, boff, f0);
-    // two stages per trip so the register sets alternate statically (nk is even)
+    // two stages per trip so the register sets alternate statically (nk is even).
+    // Stage s lives in ring buffer s % kStages; at stage kt the DMA refills the
+    // buffer of stage kt-1, whose fragments were consumed one stage earlier.
     for (int kt = 0; kt < nk; kt += 2) {
-      // stage kt on f0, prefetch stage kt+1 into f1
-      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+      // stage kt on f0, prefetch stage kt+1 into f1; stages kt+2 .. kt+kStages-2 may fly
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(8 * (kStages - 3)) : "memory");
       {
-        const int ld = kt + 3 < last ? kt + 3 : last;
-        load_stage(lds, (kt + 3) & 3, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
-        read_frags(lds, (kt + 1) & 3, aoff, boff, f1);
+        const int ld = kt + kStages - 1 < last ? kt + kStages - 1 : last;
+        load_stage(lds, (kt + kStages - 1) % kStages, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride,
+                   wave);
+        read_frags(lds, (kt + 1) % kStages, aoff, boff, f1);
         mfma_stage(f0, acc);
         schedule();
       }
       // stage kt+1 on f1, prefetch stage kt+2 into f0
-      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(8 * (kStages - 3)) : "memory");
       {
-        const int ld = kt + 4 < last ? kt + 4 : last;
-        load_stage(lds, kt & 3, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
-        read_frags(lds, (kt + 2) & 3, aoff, boff, f0);
+        const int ld = kt + kStages < last ? kt + kStages : last;
+        load_stage(lds, kt % kStages, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
+        read_frags(lds, (kt + 2) % kStages, aoff, boff, f0);
         mfma_stage(f1, acc);
         schedule();
       }
