@@ -87,6 +87,27 @@ SFP8_DEV uint32_t pack4_e4m3(float a, float b, float c, float d) {
   return p;
 }
 
+// pack4_e4m3 without the NaN fix-up: NaN inputs come out as the code of -448
+// (v_med3 maps NaN to the low bound); callers patch them with fix_nan4 on a
+// wave-uniform rare path.
+SFP8_DEV uint32_t pack4_e4m3_nofix(float a, float b, float c, float d) {
+  int v = 0;
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, -kE4M3Max, kE4M3Max),
+                                      __builtin_amdgcn_fmed3f(b, -kE4M3Max, kE4M3Max), v, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(c, -kE4M3Max, kE4M3Max),
+                                      __builtin_amdgcn_fmed3f(d, -kE4M3Max, kE4M3Max), v, true);
+  return (uint32_t)v;
+}
+
+// gfx950 LDS transpose read (ds_read_b64_tr_b8).  Within each group of 16
+// lanes, lane i receives byte (i % 8) of the 8-byte rows addressed by the
+// group's lanes 2b + i/8, b = 0..7, as its byte b.  With lane 2b + h pointing
+// at row R + b, columns C + 8h .. C + 8h + 7 of a byte matrix, lane i gets
+// rows R .. R+7 of column C + i.
+SFP8_DEV intx2 lds_read_tr8(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) intx2*)p);
+}
+
 SFP8_DEV uint32_t pack4_e5m2(float a, float b, float c, float d) {
   int v = 0;
   v = __builtin_amdgcn_cvt_pk_bf8_f32(__builtin_amdgcn_fmed3f(a, -kE5M2Max, kE5M2Max),
@@ -187,7 +208,12 @@ SFP8_DEV float wave_sum_f32(float v) {
 // |x| is non-negative, so the unsigned order of its bits is the float order
 // (NaN patterns sort above +inf, so a NaN amax sticks, as torch.amax would).
 SFP8_DEV void atomic_max_nonneg(float* addr, float v) {
-  atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
+  // An amax slot only grows within a kernel, so a read of it is never above
+  // its current value: when it already holds >= v the atomic is skipped.  (A
+  // stale low read costs one unneeded atomic, never a lost maximum.)  This
+  // keeps thousands of work-groups from serialising on one L2 address.
+  const unsigned int u = __float_as_uint(v);
+  if (u > *reinterpret_cast<volatile unsigned int*>(addr)) atomicMax(reinterpret_cast<unsigned int*>(addr), u);
 }
 
 // Work-group max of a non-negative value; one atomic per work-group.

@@ -71,6 +71,15 @@ SFP8_DEV int plain_col(int r) {
   return (r & 128) + 64 * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
 }
 
+// The same for a 64*NB-row B tile (NB blocks of 32 per wave): B row r holds
+// column 32*NB*wn + 16*NB*g + 16*nb + v, so a lane's NB blocks cover 16*NB
+// consecutive columns.  plain_col_nb<4> == plain_col.
+template <int NB>
+SFP8_DEV int plain_col_nb(int r) {
+  const int wn = r / (32 * NB), rl = r % (32 * NB);
+  return 32 * NB * wn + 16 * NB * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
+}
+
 // Paired (gate/up) layout: rows 0..127 are gate, 128..255 up; wave column wn
 // owns rows 64*wn.. of each half; column (within the 128-column half)
 // 64*wn + 32*g + 16*nb + v.
@@ -416,27 +425,66 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
 // ---------------------------------------------------------------------------
 // (a10) gate/up dgrad (spark-gpt train.py:1239-1241):
 //   dxn = bf16(acc * (1/s3) * (1/q_gu)), A = d_gu8 (e5m2, [T, 2I]), B = W8^T (e4m3, [D, 2I]).
-__global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
+// Persistent form for NB == 2: gridDim.x = 2 work-groups per CU, each looping
+// over tiles pid, pid + gridDim.x, ...  Work-groups [n_cu, 2*n_cu) are the
+// second on their CU; they start after a bounded sleep of about half a tile
+// so that the two work-groups of a CU alternate main loop and epilogue.
+SFP8_DEV void stagger_second_wg(int n_cu, int sleep_iters) {
+  if ((int)blockIdx.x >= n_cu)
+    for (int i = 0; i < sleep_iters; ++i) __builtin_amdgcn_s_sleep(127);
+}
+
+template <int NB>
+__global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gateup_dgrad_kernel(
     const uint8_t* __restrict__ dgu8, const uint8_t* __restrict__ w8t, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, uint16_t* __restrict__ dxn,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int n_cu, int sleep_iters) {
+  using ML = MainLoop<false, kFmtE5M2, kFmtE4M3, false, NB, NB == 2 ? 3 : kStages>;
   extern __shared__ __align__(16) uint8_t lds[];
-  int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int64_t K = 2 * I;
-  floatx16 acc[4][4];
-  MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
-      lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, kStage, w8t + n0 * K, (D - n0) * K,
-      [=](int r) { return plain_col(r) * (int)K; }, kStage, (int)(K / kStage), acc);
   const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
-  stage_bf16_half<0>(lds, acc, sab);
-  __syncthreads();
-  write_bf16_half(lds, 0, m0, n0, T, D, D, nullptr, dxn);
-  __syncthreads();
-  stage_bf16_half<1>(lds, acc, sab);
-  __syncthreads();
-  write_bf16_half(lds, 1, m0, n0, T, D, D, nullptr, dxn);
+  const int ntiles = tiles_m * tiles_n;
+  if constexpr (NB == 2) stagger_second_wg(n_cu, sleep_iters);
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    int tm, tn;
+    tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * ML::kTileN;
+    floatx16 acc[4][NB];
+    ML::run(lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, kStage, w8t + n0 * K,
+            (D - n0) * K, [=](int r) { return plain_col_nb<NB>(r) * (int)K; }, kStage, (int)(K / kStage), acc);
+    if constexpr (NB == 4) {
+      stage_bf16_half<0>(lds, acc, sab);
+      __syncthreads();
+      write_bf16_half(lds, 0, m0, n0, T, D, D, nullptr, dxn);
+      __syncthreads();
+      stage_bf16_half<1>(lds, acc, sab);
+      __syncthreads();
+      write_bf16_half(lds, 1, m0, n0, T, D, D, nullptr, dxn);
+    } else {
+      // each lane: 32 consecutive columns of one row per tb
+      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
+      const int fr = lane & 31, g = lane >> 5;
+      const int64_t n = n0 + 32 * NB * wn + 16 * NB * g;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int64_t t = m0 + 128 * wm + 32 * tb + fr;
+        if (t >= T) continue;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          if (n + 16 * nb >= D) continue;  // D % 16 == 0
+          uint32_t w0[4], w1[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            w0[i] = pack2_bf16(acc[tb][nb][2 * i] * sab, acc[tb][nb][2 * i + 1] * sab);
+            w1[i] = pack2_bf16(acc[tb][nb][8 + 2 * i] * sab, acc[tb][nb][8 + 2 * i + 1] * sab);
+          }
+          store16(dxn + t * D + n + 16 * nb, w0);
+          store16(dxn + t * D + n + 16 * nb + 8, w1);
+        }
+      }
+    }
+    __syncthreads();  // the next tile's DMA overwrites the LDS
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -534,6 +582,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 }  // namespace sfp8
 
+// B blocks per wave of the gate/up dgrad (4: 256 x 256 tiles, one work-group
+// per CU; 2: 256 x 128 tiles, two per CU)
+constexpr int kGateupDgradNB = 4;
 static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
 static_assert(128 * sfp8::kBf16Stride <= sfp8::kMainLds, "bf16 epilogue staging fits the main loop's LDS");
 
@@ -563,6 +614,16 @@ inline int status() {
 
 inline bool al16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// Compute units of the current device (queried on every call: no cached state).
+inline int cu_count(int* n) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return (int)e;
+  if (*n <= 0) *n = 1;
+  return 0;
+}
 // offsets inside one operand tile are 32-bit
 inline bool fits32(int64_t rows, int64_t ld) { return rows * ld < (int64_t)1 << 31; }
 
@@ -627,12 +688,21 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
   if (!fits32(kTile, 2 * I)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
   if (T == 0) return kOk;
-  const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
-  int rc = prep(gateup_dgrad_kernel, kMainLds);
+  using ML = MainLoop<false, kFmtE5M2, kFmtE4M3, false, kGateupDgradNB, kGateupDgradNB == 2 ? 3 : kStages>;
+  const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, ML::kTileN);
+  const int ntiles = tiles_m * tiles_n;
+  int n_cu = 0;
+  int rc = cu_count(&n_cu);
   if (rc) return rc;
-  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  // NB == 2: persistent, two work-groups per CU; NB == 4: one work-group per tile
+  const int grid = kGateupDgradNB == 2 ? (ntiles < 2 * n_cu ? ntiles : 2 * n_cu) : ntiles;
+  // about half a tile of main loop: (K / 64) stages of ~1.2k cycles, s_sleep 127 ~ 8k cycles
+  const int sleep_iters = (int)((2 * I / kStage) * 1200 / 2 / 8128);
+  rc = prep(gateup_dgrad_kernel<kGateupDgradNB>, ML::kLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(gateup_dgrad_kernel<kGateupDgradNB>, dim3(grid), dim3(256), ML::kLds, (hipStream_t)stream,
                      (const uint8_t*)dgu8, (const uint8_t*)w8t, T, D, I, scale, wscale, (uint16_t*)dxn, tiles_m,
-                     tiles_n);
+                     tiles_n, n_cu, sleep_iters);
   return status();
 }
 

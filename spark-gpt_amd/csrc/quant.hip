@@ -73,7 +73,11 @@ SFP8_DEV void lds_tile_store_transposed(const uint8_t* lds, int rows, int cols, 
 
 // --------------------------------------------------------------------------
 // Standalone quantizer: x8 = e4m3(x * s), x8t = x8^T, amax = max|x|.
-// Tile 128 rows x 128 cols, 256 threads.
+// Tile 128 rows x 128 cols, 256 threads.  Every thread issues its eight
+// 16-byte row loads before converting any of them; NaN lanes are patched on a
+// wave-uniform path taken only when the wave saw a NaN.  The transposed copy
+// is read out of the LDS tile with the transpose read (lds_read_tr8): a
+// 16-lane group turns a 16 x 16 byte block into 16 column runs of 16 rows.
 constexpr int QR_TILE = 128;
 constexpr int QR_STRIDE = QR_TILE + 8;
 
@@ -82,37 +86,89 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
     float* __restrict__ amax, uint8_t* __restrict__ x8, uint8_t* __restrict__ x8t, int64_t ldt) {
   __shared__ __align__(16) uint8_t tile[QR_TILE * QR_STRIDE];
   __shared__ float red[4];
-  const int64_t r0 = (int64_t)blockIdx.x * QR_TILE;
-  const int64_t c0 = (int64_t)blockIdx.y * QR_TILE;
+  // consecutive work-groups take consecutive column blocks of the same rows,
+  // so each input row is read while its DRAM page is open
+  const int64_t r0 = (int64_t)blockIdx.y * QR_TILE;
+  const int64_t c0 = (int64_t)blockIdx.x * QR_TILE;
   const float s = scale[0];
-  float m = 0.0f;
-  const int c8 = threadIdx.x & 15;  // 8-element chunk within the tile row
-#pragma unroll 4
+  const int c8 = threadIdx.x & 15;   // 8-element chunk within the tile row
+  const int rr = threadIdx.x >> 4;   // row within a 16-row pass
+  intx4 v[8];
+#pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int r = (threadIdx.x >> 4) + 16 * i;
-    const int64_t gr = r0 + r;
-    uint32_t lo = 0u, hi = 0u;
-    if (gr < R) {
-      const intx4 v = *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8);
+    const int64_t gr = r0 + rr + 16 * i;
+    v[i] = gr < R ? *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8) : intx4{0, 0, 0, 0};
+  }
+  float m = 0.0f;
+  bool nan = false;
+  uint32_t lo[8], hi[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = (uint32_t)v[i][j];
+      f[2 * j] = bf16_bits_to_f32(u & 0xffffu);
+      f[2 * j + 1] = bf16_bits_to_f32(u >> 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      m = fmaxf(m, fabsf(f[j]));
+      nan |= f[j] != f[j];
+    }
+    lo[i] = pack4_e4m3_nofix(f[0] * s, f[1] * s, f[2] * s, f[3] * s);
+    hi[i] = pack4_e4m3_nofix(f[4] * s, f[5] * s, f[6] * s, f[7] * s);
+  }
+  if (__builtin_amdgcn_ballot_w64(nan)) {  // wave-uniform, taken only with NaN data
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // re-read the row chunk (keeps the loaded vectors dead after the cast)
+      const int64_t gr = r0 + rr + 16 * i;
+      const intx4 w = gr < R ? *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8) : intx4{0, 0, 0, 0};
       float f[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t u = (uint32_t)v[j];
+        const uint32_t u = (uint32_t)w[j];
         f[2 * j] = bf16_bits_to_f32(u & 0xffffu);
         f[2 * j + 1] = bf16_bits_to_f32(u >> 16);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(f[j]));
-      lo = pack4_e4m3(f[0] * s, f[1] * s, f[2] * s, f[3] * s);
-      hi = pack4_e4m3(f[4] * s, f[5] * s, f[6] * s, f[7] * s);
-      *reinterpret_cast<intx2*>(x8 + gr * C + c0 + c8 * 8) = intx2{(int)lo, (int)hi};
+      lo[i] = fix_nan4(lo[i], f[0] * s, f[1] * s, f[2] * s, f[3] * s);
+      hi[i] = fix_nan4(hi[i], f[4] * s, f[5] * s, f[6] * s, f[7] * s);
     }
-    *reinterpret_cast<intx2*>(tile + r * QR_STRIDE + c8 * 8) = intx2{(int)lo, (int)hi};
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = rr + 16 * i;
+    const int64_t gr = r0 + r;
+    if (gr < R) *reinterpret_cast<intx2*>(x8 + gr * C + c0 + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};
+    *reinterpret_cast<intx2*>(tile + r * QR_STRIDE + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};  // zeros past R
   }
   __syncthreads();
-  const int rows_valid = (int)((R - r0) < QR_TILE ? (R - r0) : QR_TILE);
-  lds_tile_store_transposed<256>(tile, QR_TILE, QR_TILE, QR_STRIDE, x8t + c0 * ldt, ldt, r0,
-                                 rows_valid, ldt);
+  // Transposed copy: wave w, pass p covers columns 16*(2w + p/2) .. +15 and
+  // rows 64*(p%2) .. +63; its 16-lane group q takes rows 16q .. 16q+15 of
+  // those, so a wave's stores are 64 contiguous bytes of each of 16 columns.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, li = lane & 15;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int cb = 16 * (2 * wave + (p >> 1));
+    const int rb = 64 * (p & 1) + 16 * q;
+    // source lane li = 2b + h points at tile row rb + b (+8), columns cb + 8h ..
+    const uint8_t* src = tile + (rb + (li >> 1)) * QR_STRIDE + cb + 8 * (li & 1);
+    const intx2 t0 = lds_read_tr8(src);
+    const intx2 t1 = lds_read_tr8(src + 8 * QR_STRIDE);
+    const int64_t rbase = r0 + rb;
+    if (rbase >= ldt) continue;
+    uint8_t* dst = x8t + (c0 + cb + li) * ldt + rbase;
+    const intx4 w = {t0[0], t0[1], t1[0], t1[1]};
+    if (rbase + 16 <= ldt && ((((uintptr_t)dst) & 15u) == 0)) {
+      *reinterpret_cast<intx4*>(dst) = w;
+    } else {
+      const int nv = (int)((ldt - rbase) < 16 ? (ldt - rbase) : 16);
+      for (int k = 0; k < nv; ++k) dst[k] = (uint8_t)((uint32_t)w[k >> 2] >> (8 * (k & 3)));
+    }
+  }
   block_amax_atomic<4>(m, red, amax);
 }
 
@@ -130,8 +186,13 @@ struct NormCfg {
   static constexpr int LPR = (D / 8) < 64 ? (D / 8) : 64;  // lanes per row
   static constexpr int RPW = 64 / LPR;                       // rows per wave pass
   static constexpr int CPL = D / (8 * LPR);                  // chunks per lane
-  static constexpr int RT = (65536 / D) < 64 ? (65536 / D) : 64;  // rows per WG
+  static constexpr int RT = (65536 / D) < 32 ? (65536 / D) : 32;  // rows per WG
   static constexpr int STRIDE = D + 8;                             // LDS row stride
+  static constexpr int PASSES = RT / (4 * RPW);                    // row passes per wave
+  // passes whose loads are issued together (about 8 chunks of 16 bytes per lane)
+  static constexpr int PB = (8 / CPL) < PASSES ? ((8 / CPL) > 0 ? 8 / CPL : 1) : PASSES;
+  static constexpr int PB_BWD = (4 / CPL) < PASSES ? ((4 / CPL) > 0 ? 4 / CPL : 1) : PASSES;
+  static_assert(PASSES % PB == 0 && PASSES % PB_BWD == 0, "whole load batches");
 };
 
 template <int D>
@@ -159,50 +220,59 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; }
   }
-  for (int rr = wid * Cfg::RPW; rr < Cfg::RT; rr += 4 * Cfg::RPW) {
-    const int r = rr + sr;
-    const int64_t t = t0 + r;
-    const bool valid = t < T;
-    intx4 v[Cfg::CPL];
+  // wave wid takes row passes wid, wid + 4, ...; PB passes' loads are issued
+  // before any of them is reduced
+  for (int pb = 0; pb < Cfg::PASSES; pb += Cfg::PB) {
+    intx4 v[Cfg::PB][Cfg::CPL];
 #pragma unroll
-    for (int c = 0; c < Cfg::CPL; ++c) {
-      const int d = (c * Cfg::LPR + li) * 8;
-      v[c] = valid ? *reinterpret_cast<const intx4*>(h + t * D + d) : intx4{0, 0, 0, 0};
+    for (int q = 0; q < Cfg::PB; ++q) {
+      const int64_t t = t0 + (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+#pragma unroll
+      for (int c = 0; c < Cfg::CPL; ++c) {
+        const int d = (c * Cfg::LPR + li) * 8;
+        v[q][c] = t < T ? *reinterpret_cast<const intx4*>(h + t * D + d) : intx4{0, 0, 0, 0};
+      }
     }
-    double ss = 0.0;
-    float f[Cfg::CPL][8];
 #pragma unroll
-    for (int c = 0; c < Cfg::CPL; ++c)
+    for (int q = 0; q < Cfg::PB; ++q) {
+      const int r = (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const int64_t t = t0 + r;
+      const bool valid = t < T;
+      double ss = 0.0;
+      float f[Cfg::CPL][8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t u = (uint32_t)v[c][j];
-        f[c][2 * j] = bf16_bits_to_f32(u & 0xffffu);
-        f[c][2 * j + 1] = bf16_bits_to_f32(u >> 16);
-        // squares of bf16 values are exact in fp64
-        ss = __builtin_fma((double)f[c][2 * j], (double)f[c][2 * j], ss);
-        ss = __builtin_fma((double)f[c][2 * j + 1], (double)f[c][2 * j + 1], ss);
+      for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t u = (uint32_t)v[q][c][j];
+          f[c][2 * j] = bf16_bits_to_f32(u & 0xffffu);
+          f[c][2 * j + 1] = bf16_bits_to_f32(u >> 16);
+          // squares of bf16 values are exact in fp64
+          ss = __builtin_fma((double)f[c][2 * j], (double)f[c][2 * j], ss);
+          ss = __builtin_fma((double)f[c][2 * j + 1], (double)f[c][2 * j + 1], ss);
+        }
+#pragma unroll
+      for (int o = Cfg::LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float var = (float)ss / (float)D + eps;
+      const float r_ = (float)(1.0 / __builtin_sqrt((double)var));
+      if (valid && li == 0) rstd[t] = r_;
+#pragma unroll
+      for (int c = 0; c < Cfg::CPL; ++c) {
+        const int d = (c * Cfg::LPR + li) * 8;
+        float n[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          n[j] = (f[c][j] * r_) * w[c][j];
+          if (valid) m = fmaxf(m, fabsf(n[j]));
+        }
+        uint32_t lo = 0u, hi = 0u;
+        if (valid) {
+          lo = pack4_e4m3(n[0] * s0, n[1] * s0, n[2] * s0, n[3] * s0);
+          hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
+          *reinterpret_cast<intx2*>(x8 + t * D + d) = intx2{(int)lo, (int)hi};
+        }
+        *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
-#pragma unroll
-    for (int o = Cfg::LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float var = (float)ss / (float)D + eps;
-    const float r_ = (float)(1.0 / __builtin_sqrt((double)var));
-    if (valid && li == 0) rstd[t] = r_;
-#pragma unroll
-    for (int c = 0; c < Cfg::CPL; ++c) {
-      const int d = (c * Cfg::LPR + li) * 8;
-      float n[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        n[j] = (f[c][j] * r_) * w[c][j];
-        if (valid) m = fmaxf(m, fabsf(n[j]));
-      }
-      uint32_t lo = 0u, hi = 0u;
-      if (valid) {
-        lo = pack4_e4m3(n[0] * s0, n[1] * s0, n[2] * s0, n[3] * s0);
-        hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
-        *reinterpret_cast<intx2*>(x8 + t * D + d) = intx2{(int)lo, (int)hi};
-      }
-      *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
     }
   }
   __syncthreads();
@@ -339,59 +409,71 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; acc[c][j] = 0.f; acc[c][4 + j] = 0.f; }
   }
-  for (int rr = wid * Cfg::RPW; rr < Cfg::RT; rr += 4 * Cfg::RPW) {
-    const int r = rr + sr;
-    const int64_t t = t0 + r;
-    const bool valid = t < T;
-    intx4 vh[Cfg::CPL], vg[Cfg::CPL], vd[Cfg::CPL];
+  // wave wid takes row passes wid, wid + 4, ...; PB_BWD passes' loads are
+  // issued before any of them is used
+  for (int pb = 0; pb < Cfg::PASSES; pb += Cfg::PB_BWD) {
+    intx4 vh[Cfg::PB_BWD][Cfg::CPL], vg[Cfg::PB_BWD][Cfg::CPL], vd[Cfg::PB_BWD][Cfg::CPL];
+    float rsv[Cfg::PB_BWD];
 #pragma unroll
-    for (int c = 0; c < Cfg::CPL; ++c) {
-      const int d = (c * Cfg::LPR + li) * 8;
-      const intx4 z = {0, 0, 0, 0};
-      vh[c] = valid ? *reinterpret_cast<const intx4*>(h + t * D + d) : z;
-      vg[c] = valid ? *reinterpret_cast<const intx4*>(dxn + t * D + d) : z;
-      vd[c] = valid ? *reinterpret_cast<const intx4*>(dy + t * D + d) : z;
+    for (int q = 0; q < Cfg::PB_BWD; ++q) {
+      const int64_t t = t0 + (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const bool valid = t < T;
+#pragma unroll
+      for (int c = 0; c < Cfg::CPL; ++c) {
+        const int d = (c * Cfg::LPR + li) * 8;
+        const intx4 z = {0, 0, 0, 0};
+        vh[q][c] = valid ? *reinterpret_cast<const intx4*>(h + t * D + d) : z;
+        vg[q][c] = valid ? *reinterpret_cast<const intx4*>(dxn + t * D + d) : z;
+        vd[q][c] = valid ? *reinterpret_cast<const intx4*>(dy + t * D + d) : z;
+      }
+      rsv[q] = valid ? rstd[t] : 0.0f;
     }
-    const float rs = valid ? rstd[t] : 0.0f;
-    float S = 0.0f;
 #pragma unroll
-    for (int c = 0; c < Cfg::CPL; ++c)
+    for (int q = 0; q < Cfg::PB_BWD; ++q) {
+      const int r = (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const int64_t t = t0 + r;
+      const bool valid = t < T;
+      const float rs = rsv[q];
+      float S = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t uh = (uint32_t)vh[c][j >> 1], ug = (uint32_t)vg[c][j >> 1];
-        const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
-        const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
-        S += (g * w[c][j]) * hf;
+      for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t uh = (uint32_t)vh[q][c][j >> 1], ug = (uint32_t)vg[q][c][j >> 1];
+          const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
+          const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
+          S += (g * w[c][j]) * hf;
+        }
+#pragma unroll
+      for (int o = Cfg::LPR / 2; o > 0; o >>= 1) S += __shfl_xor(S, o, 64);
+      const float coef = S * rs * rs * rs * (1.0f / (float)D);
+#pragma unroll
+      for (int c = 0; c < Cfg::CPL; ++c) {
+        const int d = (c * Cfg::LPR + li) * 8;
+        float o[8], dyf[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t uh = (uint32_t)vh[q][c][j >> 1], ug = (uint32_t)vg[q][c][j >> 1];
+          const uint32_t ud = (uint32_t)vd[q][c][j >> 1];
+          const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
+          const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
+          dyf[j] = bf16_bits_to_f32((j & 1) ? (ud >> 16) : (ud & 0xffffu));
+          const float gw = g * w[c][j];
+          o[j] = (gw * rs - hf * coef) + dyf[j];
+          acc[c][j] += g * (hf * rs);
+          m = fmaxf(m, fabsf(dyf[j]));
+        }
+        uint32_t lo = 0u, hi = 0u;
+        if (valid) {
+          intx4 ov;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ov[j] = (int)pack2_bf16(o[2 * j], o[2 * j + 1]);
+          *reinterpret_cast<intx4*>(dh + t * D + d) = ov;
+          lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
+          hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
+        }
+        *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
-#pragma unroll
-    for (int o = Cfg::LPR / 2; o > 0; o >>= 1) S += __shfl_xor(S, o, 64);
-    const float coef = S * rs * rs * rs * (1.0f / (float)D);
-#pragma unroll
-    for (int c = 0; c < Cfg::CPL; ++c) {
-      const int d = (c * Cfg::LPR + li) * 8;
-      float o[8], dyf[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t uh = (uint32_t)vh[c][j >> 1], ug = (uint32_t)vg[c][j >> 1];
-        const uint32_t ud = (uint32_t)vd[c][j >> 1];
-        const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
-        const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
-        dyf[j] = bf16_bits_to_f32((j & 1) ? (ud >> 16) : (ud & 0xffffu));
-        const float gw = g * w[c][j];
-        o[j] = (gw * rs - hf * coef) + dyf[j];
-        acc[c][j] += g * (hf * rs);
-        m = fmaxf(m, fabsf(dyf[j]));
-      }
-      uint32_t lo = 0u, hi = 0u;
-      if (valid) {
-        intx4 ov;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ov[j] = (int)pack2_bf16(o[2 * j], o[2 * j + 1]);
-        *reinterpret_cast<intx4*>(dh + t * D + d) = ov;
-        lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
-        hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
-      }
-      *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
     }
   }
   // fold this lane's dnw accumulators over the rows sharing its columns
@@ -511,7 +593,7 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
   if (rows < 0 || cols < 0 || (cols % QR_TILE) != 0 || ldt < rows) return kErrBadShape;
   if (!aligned16(x) || !aligned16(x8)) return kErrBadAlignment;
   if (rows == 0 || cols == 0) return kOk;
-  dim3 grid((unsigned)((rows + QR_TILE - 1) / QR_TILE), (unsigned)(cols / QR_TILE));
+  dim3 grid((unsigned)(cols / QR_TILE), (unsigned)((rows + QR_TILE - 1) / QR_TILE));
   hipLaunchKernelGGL(quant_rowcol_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x, rows, cols, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt);
   return launch_status();
