@@ -227,6 +227,328 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// (a6) gate/up forward + SwiGLU, persistent with a deferred epilogue.
+//
+// Tile 256 tokens x 64 (gate, up) column pairs: B tile = 64 gate rows + 64 up
+// rows (MainLoop NB = 2, paired), so each lane holds g and u of the same 16
+// consecutive columns for each of its 4 row blocks.  One work-group per CU
+// walks its tiles; after tile i's K loop the lane packs bf16(g), bf16(u) of
+// its 64 pairs into 64 registers (E), and the SwiGLU of tile i runs in 16
+// units of 4 pairs spread over the K stages of tile i+1, in the same
+// instruction stream as its MFMAs (the matrix pipe runs them while the vector
+// ALU does the epilogue).  The h bytes of a tile also go to one of two LDS
+// tiles; its token-contiguous (K-slab) copy is written at the next tile
+// boundary with LDS transpose reads.  The last tile's epilogue runs alone.
+// NK = D / 64 K stages, fully unrolled so each unit has a fixed stage.
+constexpr int kPipeHStride = 80;                    // 64 h bytes + 16 per LDS row
+constexpr int kPipeHBytes = kTile * kPipeHStride;   // one h tile
+constexpr int kPipeRing = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4>::kLds;  // 96 KiB
+constexpr int kPipeLds = kPipeRing + 2 * kPipeHBytes + 64;
+
+// B-tile row r of the 128-row paired tile -> (half, column within 64):
+// half = r / 64 (gate, up); column = 32*wn + 16*g + v for the lane layout.
+SFP8_DEV int paired_col64(int r) {
+  const int rl = r & 63, wn = rl >> 5, w = rl & 31;
+  return 32 * wn + 16 * ((w >> 2) & 1) + 4 * (w >> 3) + (w & 3);
+}
+
+template <int NK>
+struct SwigluPipe {
+  using ML = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4>;
+  static constexpr int kUnits = 16;  // 4 pairs each: unit u = row block u/4, pairs 4*(u%4) ..
+  static constexpr int kSt = 4;      // LDS ring stages
+  static constexpr int kDma = ML::kDma;
+  static_assert(NK >= 2 && NK % 2 == 0, "even K stages");
+
+  // units run in stage kt: [ubeg(kt), ubeg(kt+1))
+  static constexpr int ubeg(int kt) { return (kt * kUnits + NK - 1) / NK; }
+
+  struct Ctx {
+    // main loop
+    uint8_t* lds;
+    __amdgpu_buffer_rsrc_t ra, rb;
+    uint32_t voff_a[4], voff_b[2], aoff[2], boff[2];
+    int wave;
+    typename ML::Frag f[2];
+    floatx16 acc[4][2];
+    // previous tile's epilogue
+    uint32_t E[4][16];
+    uint32_t gw[4], uw[4], hw[4];
+    bool nan;
+    float m_gu, m_h;
+    bool prev;            // a previous tile exists
+    int64_t pm0, pn0;     // its origin
+    uint8_t* hbuf;        // its LDS h tile
+    // scales and outputs
+    float c_exp, inv1, bnd1, inv2, bnd2;
+    int64_t T, I;
+    uint8_t* gu8;
+    uint8_t* h8;
+  };
+
+  // One unit: 4 pairs of row block TB, packed into byte Q of gw/uw/hw.
+  template <int U>
+  static SFP8_DEV void unit_compute(Ctx& c) {
+    constexpr int TB = U / 4, Q = U % 4;
+    float gb[4], ub[4], hb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t p = c.E[TB][4 * Q + e];
+      gb[e] = __uint_as_float(p << 16);
+      ub[e] = __uint_as_float(p & 0xffff0000u);
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c.c_exp));
+      hb[e] = gb[e] * sg * ub[e];
+      c.nan |= hb[e] != hb[e];  // a NaN g or u always reaches h
+    }
+    c.m_gu = fmaxf(c.m_gu, fmaxf(fmaxf(fabsf(gb[0]), fabsf(ub[0])), fmaxf(fabsf(gb[1]), fabsf(ub[1]))));
+    c.m_gu = fmaxf(c.m_gu, fmaxf(fmaxf(fabsf(gb[2]), fabsf(ub[2])), fmaxf(fabsf(gb[3]), fabsf(ub[3]))));
+    c.m_h = fmaxf(c.m_h, fmaxf(fmaxf(fabsf(hb[0]), fabsf(hb[1])), fmaxf(fabsf(hb[2]), fabsf(hb[3]))));
+    c.gw[Q] = pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], c.inv1, c.bnd1);
+    c.uw[Q] = pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], c.inv1, c.bnd1);
+    c.hw[Q] = pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], c.inv2, c.bnd2);
+  }
+
+  // After the last unit of row block TB: NaN patch (wave-uniform, rare), the
+  // three 16-byte global stores and the h bytes into the LDS tile.
+  template <int TB>
+  static SFP8_DEV void block_store(Ctx& c) {
+    const int lane = threadIdx.x & 63, wm = c.wave & 1, wn = c.wave >> 1;
+    const int fr = lane & 31, g = lane >> 5;
+    if (__builtin_amdgcn_ballot_w64(c.nan)) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float gb[4], ub[4], hb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t p = c.E[TB][4 * q + e];
+          gb[e] = __uint_as_float(p << 16);
+          ub[e] = __uint_as_float(p & 0xffff0000u);
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c.c_exp));
+          hb[e] = gb[e] * sg * ub[e];
+        }
+        c.gw[q] = fix_nan4(c.gw[q], gb[0], gb[1], gb[2], gb[3]);
+        c.uw[q] = fix_nan4(c.uw[q], ub[0], ub[1], ub[2], ub[3]);
+        c.hw[q] = fix_nan4(c.hw[q], hb[0], hb[1], hb[2], hb[3]);
+      }
+    }
+    c.nan = false;
+    const int row = 128 * wm + 32 * TB + fr;
+    const int col = 32 * wn + 16 * g;
+    const int64_t t = c.pm0 + row;
+    if (c.prev && t < c.T) {
+      uint8_t* gp = c.gu8 + t * 2 * c.I + c.pn0 + col;
+      store16(gp, c.gw);
+      store16(gp + c.I, c.uw);
+      store16(c.h8 + t * c.I + c.pn0 + col, c.hw);
+    }
+    store16(c.hbuf + row * kPipeHStride + col, c.hw);
+  }
+
+  // Stage KT: wait for stage KT+1 (vector stores count in vmcnt too; they
+  // complete in order after the DMA issued before them, so this wait is at
+  // worst slightly conservative after a stage that stored), barrier, DMA of
+  // stage KT+3, fragments of stage KT+1, the MFMAs of stage KT with this
+  // stage's epilogue units, then the row-block stores the units completed.
+  template <int KT>
+  static SFP8_DEV void stage(Ctx& c, int a_ss, int b_ss) {
+    constexpr int cur = KT & 1, nxt = cur ^ 1;
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (kSt - 3)) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int ld = KT + kSt - 1 < NK - 1 ? KT + kSt - 1 : NK - 1;
+    ML::load_stage(c.lds, (KT + kSt - 1) % kSt, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
+    ML::read_frags(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
+    ML::template mfma_range<0, ML::kMfma>(c.f[cur], c.acc);
+    fences<ubeg(KT), ubeg(KT + 1)>(c);
+    units<ubeg(KT), ubeg(KT + 1)>(c);
+    // 8 MFMAs, 12 LDS reads, 6 DMAs, the units' vector ALU work spread
+    // after every MFMA (about 90 instructions per unit)
+    constexpr int nv = (ubeg(KT + 1) - ubeg(KT)) * 96 / ML::kMfma;
+    sched_interleave_valu<ML::kMfma, nv, 2 * (4 + 2), kDma>();
+    pins<ubeg(KT), ubeg(KT + 1)>(c);
+    stores<ubeg(KT), ubeg(KT + 1)>(c);
+  }
+
+  // An empty asm that "rewrites" a unit's inputs after the stage's barrier
+  // keeps the compiler from hoisting the unit's arithmetic into an earlier
+  // stage.
+  template <int U0, int U1>
+  static SFP8_DEV void fences(Ctx& c) {
+    if constexpr (U0 < U1) {
+      constexpr int TB = U0 / 4, Q = U0 % 4;
+      asm volatile("" : "+v"(c.E[TB][4 * Q]), "+v"(c.E[TB][4 * Q + 1]), "+v"(c.E[TB][4 * Q + 2]),
+                   "+v"(c.E[TB][4 * Q + 3]));
+      fences<U0 + 1, U1>(c);
+    }
+  }
+
+  // An empty asm that reads a unit's packed bytes keeps the compiler from
+  // sinking the unit's arithmetic into a later stage (next to its store).
+  template <int U0, int U1>
+  static SFP8_DEV void pins(Ctx& c) {
+    if constexpr (U0 < U1) {
+      constexpr int Q = U0 % 4;
+      asm volatile("" ::"v"(c.gw[Q]), "v"(c.uw[Q]), "v"(c.hw[Q]));
+      pins<U0 + 1, U1>(c);
+    }
+  }
+
+  template <int U0, int U1>
+  static SFP8_DEV void units(Ctx& c) {
+    if constexpr (U0 < U1) {
+      unit_compute<U0>(c);
+      units<U0 + 1, U1>(c);
+    }
+  }
+  template <int U0, int U1>
+  static SFP8_DEV void stores(Ctx& c) {
+    if constexpr (U0 < U1) {
+      if constexpr (U0 % 4 == 3) block_store<U0 / 4>(c);
+      stores<U0 + 1, U1>(c);
+    }
+  }
+  template <int KT>
+  static SFP8_DEV void stages(Ctx& c, int a_ss, int b_ss) {
+    if constexpr (KT < NK) {
+      stage<KT>(c, a_ss, b_ss);
+      stages<KT + 1>(c, a_ss, b_ss);
+    }
+  }
+  template <int U0>
+  static SFP8_DEV void tail_units(Ctx& c) {
+    if constexpr (U0 < kUnits) {
+      unit_compute<U0>(c);
+      if constexpr (U0 % 4 == 3) block_store<U0 / 4>(c);
+      tail_units<U0 + 1>(c);
+    }
+  }
+};
+
+// Token-contiguous (K-slab) copy of a finished LDS h tile (256 tokens x 64
+// features): 16-lane group q of wave w turns a 16 x 16 byte block into 16
+// feature runs of 16 tokens; a wave's stores are 16 whole 64-byte slab rows.
+SFP8_DEV void pipe_h_slab(const uint8_t* hb, int64_t pm0, int64_t pn0, uint8_t* h8t, int64_t rpad) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, li = lane & 15;
+  const int cb = 16 * wave;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int rb = 16 * (4 * p + q);
+    const uint8_t* src = hb + (rb + (li >> 1)) * kPipeHStride + cb + 8 * (li & 1);
+    const intx2 t0 = lds_read_tr8(src);
+    const intx2 t1 = lds_read_tr8(src + 8 * kPipeHStride);
+    const int64_t t = pm0 + rb;
+    *reinterpret_cast<intx4*>(h8t + (t >> 6) * rpad * 64 + (pn0 + cb + li) * 64 + (t & 63)) =
+        intx4{t0[0], t0[1], t1[0], t1[1]};
+  }
+}
+
+template <int NK>
+__global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
+    const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
+    const float* __restrict__ scale, const float* __restrict__ wscale, float* __restrict__ amax,
+    uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int tiles_m, int tiles_n) {
+  using P = SwigluPipe<NK>;
+  using ML = typename P::ML;
+  extern __shared__ __align__(16) uint8_t lds[];
+  typename P::Ctx c;
+  c.lds = lds;
+  c.wave = threadIdx.x >> 6;
+  // scales folded as in swiglu_fwd_kernel (all powers of two)
+  const float deq = 1.0f / (scale[0] * wscale[0]);
+  c.c_exp = deq * -1.4426950408889634f;
+  const float m1 = deq * scale[1], m2 = deq * deq * scale[2];
+  c.inv1 = 1.0f / m1;
+  c.inv2 = 1.0f / m2;
+  c.bnd1 = kE4M3Max * c.inv1;
+  c.bnd2 = kE4M3Max * c.inv2;
+  c.T = T;
+  c.I = I;
+  c.gu8 = gu8;
+  c.h8 = h8;
+  c.m_gu = 0.f;
+  c.m_h = 0.f;
+  c.nan = false;
+  c.prev = false;
+  c.pm0 = 0;
+  c.pn0 = 0;
+  c.hbuf = lds + kPipeRing;
+  // the first tile's K loop runs the epilogue units with no previous tile:
+  // on zeros they add nothing to the amax slots (and store nothing)
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) c.E[tb][v] = 0u;
+  const int lane = threadIdx.x & 63, wm = c.wave & 1, wn = c.wave >> 1;
+  const int fr = lane & 31, g = lane >> 5;
+  const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+  const int sw = (fr >> 2) & 3;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    c.aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+    c.boff[h] = (uint32_t)(ML::kLdsB + (BLayout<true, 2>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+  }
+  const int64_t rpad = slab_rows(I);
+  const int ntiles = tiles_m * tiles_n;
+  int it = 0;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x, ++it) {
+    int tm, tn;
+    tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 64;
+    c.ra = make_rsrc(x8 + m0 * D, (T - m0) * D);
+    c.rb = make_rsrc(w8 + n0 * D, (2 * I - n0) * D);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * (int)D) + chunk;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 32 * c.wave + 16 * j + (lane >> 2);
+      c.voff_b[j] = (uint32_t)(((r >> 6) * (int)I + paired_col64(r)) * (int)D) + chunk;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) c.acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
+                                                          0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // prologue: stages 0..2 in flight, stage 0 landed, its fragments read
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      const int ld = s < NK - 1 ? s : NK - 1;
+      ML::load_stage(lds, s, c.ra, c.rb, c.voff_a, c.voff_b, ld * kStage, ld * kStage, c.wave);
+    }
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * ML::kDma) : "memory");
+    ML::read_frags(lds, 0, c.aoff, c.boff, c.f[0]);
+    P::template stages<0>(c, kStage, kStage);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // the previous tile's h tile is complete: its K-slab copy
+    if (c.prev) pipe_h_slab(c.hbuf, c.pm0, c.pn0, h8t, rpad);
+    // this tile's g, u (bf16, unscaled) become the next epilogue's input
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) c.E[tb][v] = pack2_bf16(c.acc[tb][0][v], c.acc[tb][1][v]);
+    c.prev = true;
+    c.pm0 = m0;
+    c.pn0 = n0;
+    c.hbuf = lds + kPipeRing + (it & 1) * kPipeHBytes;
+  }
+  if (c.prev) {
+    P::template tail_units<0>(c);
+    __syncthreads();
+    pipe_h_slab(c.hbuf, c.pm0, c.pn0, h8t, rpad);
+  }
+  float* red = reinterpret_cast<float*>(lds + kPipeRing + 2 * kPipeHBytes);
+  float mg = wave_max(c.m_gu * deq), mh = wave_max(c.m_h * (deq * deq));
+  if (lane == 0) {
+    red[c.wave] = mg;
+    red[4 + c.wave] = mh;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomic_max_nonneg(amax + 1, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    atomic_max_nonneg(amax + 2, fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+  }
+}
+
 // bf16 epilogues stage the tile in two passes of 128 rows (256 bf16 columns,
 // row stride kBf16Stride: consecutive rows shift by 4 banks) and then write
 // whole rows.  Pass P holds tile rows 64P..64P+63 and 128+64P..128+64P+63.
@@ -586,6 +908,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // per CU; 2: 256 x 128 tiles, two per CU)
 constexpr int kGateupDgradNB = 4;
 static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
+static_assert(sfp8::kPipeLds <= 160 * 1024, "deferred-epilogue SwiGLU fits the 160 KiB LDS");
 static_assert(128 * sfp8::kBf16Stride <= sfp8::kMainLds, "bf16 epilogue staging fits the main loop's LDS");
 
 // ============================================================================
@@ -639,6 +962,21 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
   if (!fits32(kTile, D) || !fits32(2 * I, D)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
+  if (D == 1024) {
+    // persistent, one work-group per CU, SwiGLU of each tile overlapped with
+    // the next tile's K loop
+    const int tiles_m = cdiv(T, kTile), tiles_n = (int)(I / 64);
+    const int ntiles = tiles_m * tiles_n;
+    int n_cu = 0;
+    int rc = cu_count(&n_cu);
+    if (rc) return rc;
+    rc = prep(swiglu_pipe_kernel<16>, kPipeLds);
+    if (rc) return rc;
+    hipLaunchKernelGGL(swiglu_pipe_kernel<16>, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kPipeLds,
+                       (hipStream_t)stream, (const uint8_t*)x8, (const uint8_t*)w8, T, D, I, scale, wscale, amax,
+                       (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, tiles_m, tiles_n);
+    return status();
+  }
   const int tiles_m = cdiv(T, kTile), tiles_n = (int)(I / 128);
   int rc = prep(swiglu_fwd_kernel, kMainLds);
   if (rc) return rc;

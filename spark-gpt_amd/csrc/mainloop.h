@@ -76,6 +76,22 @@ SFP8_DEV void sched_interleave() {
   }
 }
 
+// The same with up to N_VALU vector-ALU instructions (other work of the wave,
+// such as a deferred epilogue) placed after each MFMA.
+template <int N_MFMA, int N_VALU, int N_DS, int N_VM, int I = 0>
+SFP8_DEV void sched_interleave_valu() {
+  if constexpr (I < N_MFMA) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, N_VALU, 0);  // VALU
+    constexpr int ds = (N_DS * (I + 1) + N_MFMA - 1) / N_MFMA - (N_DS * I + N_MFMA - 1) / N_MFMA;
+    if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);  // DS read
+    constexpr int half = N_MFMA / 2;
+    constexpr int vm = I < half ? (N_VM * (I + 1) + half - 1) / half - (N_VM * I + half - 1) / half : 0;
+    if constexpr (vm > 0) __builtin_amdgcn_sched_group_barrier(0x020, vm, 0);  // VMEM (DMA)
+    sched_interleave_valu<N_MFMA, N_VALU, N_DS, N_VM, I + 1>();
+  }
+}
+
 template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0>
 struct MainLoop {
   static_assert(NB == 2 || NB == 4, "2 or 4 B blocks per wave");

@@ -38,9 +38,13 @@ def int_fp8(shape, dtype, g, lo=-8, hi=8):
 
 
 SHAPES = [(1000, 256, 768), (257, 128, 384), (512, 512, 256), (1, 256, 128)]
+# D = 1024 runs the persistent SwiGLU kernel whose epilogue of one tile is
+# overlapped with the next tile's K loop: fewer tiles than CUs (one each),
+# slightly more (some work-groups take two), several per work-group; ragged T.
+SHAPES_PIPE = [(1000, 1024, 768), (2049, 1024, 1920), (4099, 1024, 3072), (1, 1024, 128)]
 
 
-@pytest.mark.parametrize("T,D,I", SHAPES)
+@pytest.mark.parametrize("T,D,I", SHAPES + SHAPES_PIPE)
 def test_swiglu_fwd_integer_operands(dev, T, D, I):
     g = torch.Generator().manual_seed(T + D + I)
     x8 = int_fp8((T, D), E4, g)
