@@ -148,6 +148,20 @@ SFP8_DEV uint32_t pack4_e5m2_scaled(float a, float b, float c, float d, float in
   return pack2_e5m2_scaled<true>(pack2_e5m2_scaled<false>(0u, a, b, inv_m, bound), c, d, inv_m, bound);
 }
 
+// The same without the clamp, for callers that have checked every input is
+// finite and within +-bound (the clamp is then the identity).  Both halves
+// of `any` are overwritten; passing a live register saves zeroing one.
+SFP8_DEV uint32_t pack4_e5m2_scaled_noclamp(float a, float b, float c, float d, float inv_m, uint32_t any) {
+  shortx2 o = __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(__builtin_bit_cast(shortx2, any), a, b, inv_m, false);
+  o = __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(o, c, d, inv_m, true);
+  return __builtin_bit_cast(uint32_t, o);
+}
+
+// max(a, b, c) that returns NaN when any input is NaN (v_maximum3_f32).
+SFP8_DEV float max3_nan(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 

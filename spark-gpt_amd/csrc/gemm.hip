@@ -656,84 +656,124 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
 //   dgu8 = e5m2(d * s3) row-major and transposed (ldt), amax slot 3.
 // B = Wd^T (bf16, [I, D]).  Tile 256 tokens x 256 intermediate columns.
 constexpr int kEpiStride2 = 272;
+constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 16;  // after Gt, Ut and the reduction slots
 
 __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ wdt, const uint8_t* __restrict__ gu8,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, float* __restrict__ amax,
-    uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n) {
+    uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n,
+    int stagger_iters) {
   extern __shared__ __align__(16) uint8_t lds[];
-  int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t ldb = D * 2;  // bytes
-  floatx16 acc[4][4];
-  MainLoop<true, 0, 0, false>::run(
-      lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
-      kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb,
-      [=](int r) { return plain_col(r) * (int)ldb; }, kStage, (int)(ldb / kStage), acc);
+  // The gate operand of the SwiGLU backward is an e4m3 code here, so its two
+  // factors take 256 values per launch: entry b of this table holds
+  //   sig = sigmoid(g), sig * (1 + g * (1 - sig))   for g = e4m3(b) / s1,
+  // rounded in the reference's order (train.py:1083-1087, no contraction).
+  // Its LDS range is disjoint from the main loop's ring and the staging
+  // tiles; the main loop's first barrier publishes it.
+  floatx2* lut = reinterpret_cast<floatx2*>(lds + kDgradLutOff);
+  {
+#pragma clang fp contract(off)
+    const float gl = __builtin_amdgcn_cvt_f32_fp8(tid, 0) * (1.0f / scale[1]);
+    const float sig = 1.0f / (1.0f + expf(-gl));
+    lut[tid] = floatx2{sig, sig * (1.0f + gl * (1.0f - sig))};
+  }
   // g = g8*s_gu, u = u8*s_gu with g8, u8 the stored e4m3 values; as the scales
   // are powers of two, d_gate = dg*s_gu and d_up = du*s_gu with
-  //   dg = (dh*u8)*(sig*(1 + g*(1-sig))),  du = (dh*g8)*sig,
+  //   dg = (dh*u8)*(sig*(1 + g*(1-sig))),  du = (dh*g8)*sig  (factors from lut),
   //   dgu8 = e5m2(d*q3) = e5m2(d'*(s_gu*q3)),  amax3 = s_gu*max(|dg|,|du|).
   const float s_gu = 1.0f / scale[1];
-  const float c_exp = s_gu * -1.4426950408889634f;
   const float m3s = s_gu * scale[3];
   const float inv3 = 1.0f / m3s, bnd3 = kE5M2Max * inv3;
   uint8_t* Gt = lds;
   uint8_t* Ut = lds + kTile * kEpiStride2;
   float* red = reinterpret_cast<float*>(lds + 2 * kTile * kEpiStride2);  // 4 floats after both tiles
-  // gu8 rows of this tile through a range-checked descriptor: rows past T
-  // read as zero (and their dh is zero: dy rows past T read as zero)
-  const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 2 * I, (T - m0) * 2 * I);
   float m3 = 0.f;
+  // Persistent: work-group pid runs tiles pid, pid + gridDim.x, ...  Every
+  // tile ends in a burst of 256 KiB of stores; work-groups that share an XCD
+  // start a quarter of a tile apart (a bounded sleep) so that their bursts
+  // do not coincide.
+  for (int i = 0; i < ((int)(blockIdx.x >> 3) & 3) * stagger_iters; ++i) __builtin_amdgcn_s_sleep(127);
+  const int ntiles = tiles_m * tiles_n;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  int tm, tn;
+  tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+  floatx16 acc[4][4];
+  MainLoop<true, 0, 0, false>::run(
+      lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
+      kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb,
+      [=](int r) { return plain_col(r) * (int)ldb; }, kStage, (int)(ldb / kStage), acc);
+  // gu8 rows of this tile through a range-checked descriptor: rows past T
+  // read as zero (and their dh is zero: dy rows past T read as zero).  All
+  // 32 words of this lane are requested at once, so one memory latency covers
+  // the whole epilogue; blocks past column I get an out-of-range offset and
+  // read zeros (g = u = 0 gives zero gradients, and nothing there is stored).
+  const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 2 * I, (T - m0) * 2 * I);
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
+  intx4 wg[4][4], wu[4][4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int row = 128 * wm + 32 * tb + fr;
+      const int64_t j = n0 + cb + 16 * nb;
+      const uint32_t jo = j < I ? (uint32_t)(row * 2 * I + j) : 0x80000000u;
+      wg[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
+      wu[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)I, 0, 0);
+    }
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int col = cb + 16 * nb;
-      const int64_t j = n0 + col;
-      uint32_t pg[4] = {0u, 0u, 0u, 0u}, pu[4] = {0u, 0u, 0u, 0u};
-      if (j < I) {
-        const uint32_t jo = (uint32_t)(row * 2 * I + j);
-        const intx4 wg = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
-        const intx4 wu = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)I, 0, 0);
-        float dh[16];
-        // dh rounded to bf16 (train.py:1082)
-        round16_bf16(acc[tb][nb], 1.0f, dh);
-        bool nan = false;
+      uint32_t pg[4], pu[4];
+      float dh[16];
+      // dh rounded to bf16 (train.py:1082)
+      round16_bf16(acc[tb][nb], 1.0f, dh);
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          float dg[4], du[4];
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t gw = (uint32_t)wg[tb][nb][w];
+        const floatx2 g01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, false);
+        const floatx2 g23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, true);
+        const floatx2 u01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[tb][nb][w], 1.0f, false);
+        const floatx2 u23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[tb][nb][w], 1.0f, true);
+        const float g8v[4] = {g01.x, g01.y, g23.x, g23.y}, u8v[4] = {u01.x, u01.y, u23.x, u23.y};
+        float dg[4], du[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float g8 = e4m3_to_f32((uint32_t)wg[w], e);
-            const float u8 = e4m3_to_f32((uint32_t)wu[w], e);
-            const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g8 * c_exp));
-            const float d = dh[4 * w + e];
-            dg[e] = d * u8 * (sg * __builtin_fmaf(g8 * s_gu, 1.0f - sg, 1.0f));
-            du[e] = d * g8 * sg;
-            m3 = fmaxf(m3, fmaxf(fabsf(dg[e]), fabsf(du[e])));
-            nan |= (dg[e] != dg[e]) | (du[e] != du[e]);
-          }
-          pg[w] = pack4_e5m2_scaled(dg[0], dg[1], dg[2], dg[3], inv3, bnd3);
-          pu[w] = pack4_e5m2_scaled(du[0], du[1], du[2], du[3], inv3, bnd3);
-          if (__builtin_amdgcn_ballot_w64(nan)) {  // wave-uniform, taken only with NaN data
-            asm volatile("" ::: "memory");
-            pg[w] = fix_nan4(pg[w], dg[0], dg[1], dg[2], dg[3]);
-            pu[w] = fix_nan4(pu[w], du[0], du[1], du[2], du[3]);
-          }
+        for (int e = 0; e < 4; ++e) {
+          const floatx2 f = lut[(gw >> (8 * e)) & 0xFFu];  // (sig, sig * (1 + g * (1 - sig)))
+          const float d = dh[4 * w + e];
+          dg[e] = (d * u8v[e]) * f.y;
+          du[e] = (d * g8v[e]) * f.x;
         }
+        // NaN-propagating maximum of the eight magnitudes: one compare tells
+        // whether every value is finite and inside the e5m2 range (then the
+        // clamp is a no-op and no NaN needs patching)
+        float mw = max3_nan(fabsf(dg[0]), fabsf(du[0]), fabsf(dg[1]));
+        mw = max3_nan(mw, fabsf(du[1]), fabsf(dg[2]));
+        mw = max3_nan(mw, fabsf(du[2]), fabsf(dg[3]));
+        mw = __builtin_elementwise_maximum(mw, fabsf(du[3]));
+        pg[w] = pack4_e5m2_scaled_noclamp(dg[0], dg[1], dg[2], dg[3], inv3, gw);
+        pu[w] = pack4_e5m2_scaled_noclamp(du[0], du[1], du[2], du[3], inv3, gw);
+        if (__builtin_amdgcn_ballot_w64(!(mw <= bnd3))) {  // wave-uniform; NaN or out-of-range data only
+          asm volatile("" ::: "memory");
+          pg[w] = fix_nan4(pack4_e5m2_scaled(dg[0], dg[1], dg[2], dg[3], inv3, bnd3), dg[0], dg[1], dg[2], dg[3]);
+          pu[w] = fix_nan4(pack4_e5m2_scaled(du[0], du[1], du[2], du[3], inv3, bnd3), du[0], du[1], du[2], du[3]);
+          mw = 0.f;  // amax over the non-NaN values
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mw = fmaxf(mw, fmaxf(fabsf(dg[e]), fabsf(du[e])));
+        }
+        m3 = fmaxf(m3, mw);
       }
       store16(Gt + row * kEpiStride2 + col, pg);
       store16(Ut + row * kEpiStride2 + col, pu);
     }
   }
-  m3 *= s_gu;
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
@@ -741,6 +781,9 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   lds_rows_to_global(Ut, kTile, cols == kTile ? 4 : 3, kEpiStride2, dgu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
   lds_tile_store_slab<256>(Gt, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0, rows_valid);
   lds_tile_store_slab<256>(Ut, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0, rows_valid);
+  __syncthreads();  // the next tile's DMA overwrites the staging tiles
+  }
+  m3 *= s_gu;
   block_amax_atomic<4>(m3, red, amax + 3);
 }
 
@@ -919,7 +962,7 @@ using namespace sfp8;
 namespace {
 
 // epilogue tiles (2 x 256 x 272) + 4 amax floats, or the main loop's ring
-constexpr int kDgradEpiLds = 2 * kTile * kEpiStride2 + 16;
+constexpr int kDgradEpiLds = kDgradLutOff + 256 * 8;
 constexpr int kDgradLds = kDgradEpiLds > kMainLds ? kDgradEpiLds : kMainLds;
 
 template <typename K>
@@ -1011,11 +1054,19 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
   if (!al16(dy) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(I, kTile);
-  int rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
+  const int ntiles = tiles_m * tiles_n;
+  int n_cu = 0;
+  int rc = cu_count(&n_cu);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(tiles_m * tiles_n), dim3(256), kDgradLds,
-                     (hipStream_t)stream, (const uint16_t*)dy, (const uint16_t*)wdt, (const uint8_t*)gu8, T, D,
-                     I, scale, amax, (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n);
+  const int grid = ntiles < n_cu ? ntiles : n_cu;
+  // a quarter of a tile: (2D / 64) K stages of ~4k cycles with the epilogue,
+  // s_sleep 127 ~ 8k cycles; only worth it when every work-group runs several tiles
+  const int stagger = ntiles >= 4 * n_cu ? (int)((2 * D / kStage) * 4000 / 4 / 8128) : 0;
+  rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(grid), dim3(256), kDgradLds, (hipStream_t)stream,
+                     (const uint16_t*)dy, (const uint16_t*)wdt, (const uint8_t*)gu8, T, D, I, scale, amax,
+                     (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, stagger);
   return status();
 }
 

@@ -92,8 +92,10 @@ SFP8_DEV void sched_interleave_valu() {
   }
 }
 
-template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0>
+template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0,
+          bool A_TR = false>
 struct MainLoop {
+  static_assert(!(A_TR && BF16), "token-slab A operands are fp8");
   static_assert(NB == 2 || NB == 4, "2 or 4 B blocks per wave");
   static_assert(STAGES >= 3, "at least three LDS stages");
   static constexpr int kTileN = 64 * NB;                  // B rows per tile
@@ -103,20 +105,26 @@ struct MainLoop {
   static constexpr int kDma = 4 + NB;                      // DMA instructions per wave per stage
   using Acc = floatx16[4][NB];
 
+  // DMA instruction j of this wave's share of one stage: J < 4 are A blocks,
+  // the rest B blocks (16 rows = 1 KiB each).
+  static SFP8_DEV void load_one(int j, uint8_t* lds, int buf, __amdgpu_buffer_rsrc_t ra,
+                                __amdgpu_buffer_rsrc_t rb, const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB],
+                                int soff_a, int soff_b, int wave) {
+    if (j < 4) {
+      uint8_t* dst = lds + buf * kStageA + (64 * wave + 16 * j) * kStage;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, voff_a[j], soff_a, 0, 0);
+    } else {
+      uint8_t* dst = lds + kLdsB + buf * kStageB + (16 * NB * wave + 16 * (j - 4)) * kStage;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, voff_b[j - 4], soff_b, 0, 0);
+    }
+  }
+
   // Issue this wave's DMA instructions of one stage.
   static SFP8_DEV void load_stage(uint8_t* lds, int buf, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                   const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB], int soff_a, int soff_b,
                                   int wave) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint8_t* dst = lds + buf * kStageA + (64 * wave + 16 * j) * kStage;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, voff_a[j], soff_a, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      uint8_t* dst = lds + kLdsB + buf * kStageB + (16 * NB * wave + 16 * j) * kStage;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, voff_b[j], soff_b, 0, 0);
-    }
+    for (int j = 0; j < kDma; ++j) load_one(j, lds, buf, ra, rb, voff_a, voff_b, soff_a, soff_b, wave);
   }
 
   // Fragments of one stage: per block 32 bytes per lane (lane half g holds
@@ -126,21 +134,42 @@ struct MainLoop {
     intx8 b[NB];
   };
 
-  static SFP8_DEV void read_frags(const uint8_t* lds, int buf, const uint32_t (&aoff)[2], const uint32_t (&boff)[2],
-                                  Frag& f) {
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const uint8_t* p = lds + buf * kStageA + tb * 32 * kStage;
+  // Fragment I of one stage (I < 4: A block I, else B block I - 4): two
+  // 16-byte LDS reads.
+  template <int I>
+  static SFP8_DEV void read_frag(const uint8_t* lds, int buf, const uint32_t (&aoff)[2], const uint32_t (&boff)[2],
+                                 Frag& f) {
+    if constexpr (I < 4 && A_TR) {
+      // token-slab A: block tb of 32 tokens is half (tb & 1) of 64-token
+      // block tb >> 1; four transposing reads give 8 K bytes each
+      const uint8_t* p = lds + buf * kStageA + (I >> 1) * 4096 + aoff[I & 1];
+      const intx2 q0 = lds_read_tr8(p), q1 = lds_read_tr8(p + 512), q2 = lds_read_tr8(p + 1024),
+                  q3 = lds_read_tr8(p + 1536);
+      f.a[I] = intx8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+    } else if constexpr (I < 4) {
+      const uint8_t* p = lds + buf * kStageA + I * 32 * kStage;
       const intx4 lo = *reinterpret_cast<const intx4*>(p + aoff[0]);
       const intx4 hi = *reinterpret_cast<const intx4*>(p + aoff[1]);
-      f.a[tb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB>::off(nb) * kStage;
+      f.a[I] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB>::off(I - 4) * kStage;
       const intx4 lo = *reinterpret_cast<const intx4*>(p + boff[0]);
       const intx4 hi = *reinterpret_cast<const intx4*>(p + boff[1]);
-      f.b[nb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      f.b[I - 4] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  }
+
+  static SFP8_DEV void read_frags(const uint8_t* lds, int buf, const uint32_t (&aoff)[2], const uint32_t (&boff)[2],
+                                  Frag& f) {
+    read_frag<0>(lds, buf, aoff, boff, f);
+    read_frag<1>(lds, buf, aoff, boff, f);
+    read_frag<2>(lds, buf, aoff, boff, f);
+    read_frag<3>(lds, buf, aoff, boff, f);
+    read_frag<4>(lds, buf, aoff, boff, f);
+    read_frag<5>(lds, buf, aoff, boff, f);
+    if constexpr (NB == 4) {
+      read_frag<6>(lds, buf, aoff, boff, f);
+      read_frag<7>(lds, buf, aoff, boff, f);
     }
   }
 
@@ -175,25 +204,68 @@ struct MainLoop {
   // Per stage after the barrier: kMfma - kPre MFMAs, 2*(4+NB) LDS reads, 4+NB DMAs.
   static SFP8_DEV void schedule() { sched_interleave<kMfma - kPre, 2 * (4 + NB), kDma>(); }
 
-  // One stage: the first kPre MFMAs on `cur`, the barrier (stage kt+1 landed
-  // everywhere, buffer `dma_buf` free), the DMA of stage `ld` into it, the
-  // fragment reads of stage kt+1 into `nxt` and the remaining MFMAs.
+  // MFMA M of the stage, then fragment reads [R0, R1) of the next stage, as
+  // one group the scheduler may not reorder with its neighbours.
+  template <int M, int R0, int R1>
+  static SFP8_DEV void mfma_then_reads(const uint8_t* lds, const Frag& cur, Frag& nxt, Acc& acc, int rd_buf,
+                                       const uint32_t (&aoff)[2], const uint32_t (&boff)[2]) {
+    mfma_range<M, M + 1>(cur, acc);
+    if constexpr (R0 < R1) read_frag<R0>(lds, rd_buf, aoff, boff, nxt);
+    if constexpr (R0 + 1 < R1) read_frag<R0 + 1>(lds, rd_buf, aoff, boff, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // MFMA M of the stage, then DMA instructions [J0, J1) of stage `ld`.
+  template <int M, int J0, int J1>
+  static SFP8_DEV void mfma_then_dma(uint8_t* lds, const Frag& cur, Acc& acc, int dma_buf,
+                                     __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                     const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB], int soff_a,
+                                     int soff_b, int wave) {
+    mfma_range<M, M + 1>(cur, acc);
+    if constexpr (J0 < J1) load_one(J0, lds, dma_buf, ra, rb, voff_a, voff_b, soff_a, soff_b, wave);
+    if constexpr (J0 + 1 < J1) load_one(J0 + 1, lds, dma_buf, ra, rb, voff_a, voff_b, soff_a, soff_b, wave);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // One stage, in a fixed order:
+  //   kSchedPre MFMAs of stage kt (registers only: they keep the matrix pipe busy
+  //   while the waves meet at the barrier);
+  //   wait for stage kt+1 to land, barrier;
+  //   4+NB MFMAs, each followed by one fragment (two 16-byte reads) of stage
+  //   kt+1 from `rd_buf`: all reads are issued early in the stage, so they
+  //   have landed long before stage kt+1 starts;
+  //   (4+NB)/2 MFMAs, each followed by two DMA instructions of stage `ld` into
+  //   `dma_buf` (the buffer stage kt-1 used: every wave finished reading it
+  //   before this barrier);
+  //   the remaining MFMAs.
+  static constexpr int kSchedPre = 2;
+  static_assert(kMfma >= kSchedPre + (4 + NB) / 2 + (4 + NB) / 2, "stage too short for the schedule");
   static SFP8_DEV void stage(uint8_t* lds, const Frag& cur, Frag& nxt, Acc& acc, int dma_buf, int ld, int rd_buf,
                              __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, const uint32_t (&voff_a)[4],
                              const uint32_t (&voff_b)[NB], int a_sstride, int b_sstride, const uint32_t (&aoff)[2],
                              const uint32_t (&boff)[2], int wave) {
-    if constexpr (kPre > 0) {
-      mfma_range<0, kPre>(cur, acc);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    constexpr int P = kSchedPre;
+    mfma_range<0, P>(cur, acc);
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (STAGES - 3)) : "memory");
     __builtin_amdgcn_sched_barrier(0);
-    load_stage(lds, dma_buf, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
-    read_frags(lds, rd_buf, aoff, boff, nxt);
-    mfma_range<kPre, kMfma>(cur, acc);
-    schedule();
+    const int sa = ld * a_sstride, sb = ld * b_sstride;
+    mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    mfma_then_reads<P + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    mfma_then_reads<P + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    if constexpr (NB == 4) mfma_then_reads<P + 3, 6, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    constexpr int Q = P + (4 + NB) / 2;
+    mfma_then_dma<Q + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    mfma_then_dma<Q + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    mfma_then_dma<Q + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    if constexpr (NB == 4) mfma_then_dma<Q + 3, 6, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    mfma_range<Q + (4 + NB) / 2, kMfma>(cur, acc);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
+  // A_TR: A is a token slab (64-token blocks of K rows of 64 bytes, tokens
+  // contiguous); a_rowoff(w) is the byte offset of the tile's 64-token block
+  // w and a_sstride is 64 * 64 (one stage = 64 K rows of every block).
   // a_bytes/b_bytes: bytes available from a_base/b_base (range-checked);
   // a_rowoff(r)/b_rowoff(r): byte offset of tile row r from the base within
   // one K stage; a_sstride/b_sstride: bytes from one 64-byte K stage to the
@@ -211,8 +283,16 @@ struct MainLoop {
     // <- logical chunk (lane%4) ^ ((row >> 2) & 3)
     uint32_t voff_a[4], voff_b[NB];
     const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+    if constexpr (A_TR) {
+      // wave w copies 64-token block w: K rows 16j + lane/4, 16-byte chunk
+      // (lane & 3) ^ (((row >> 2) & 1) << 1) of the row's 64 tokens
+      const uint32_t chunk_tr = (uint32_t)(((lane & 3) ^ (((lane >> 4) & 1) << 1)) << 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + chunk;
+      for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(wave) + (uint32_t)((16 * j + (lane >> 2)) * 64) + chunk_tr;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + chunk;
+    }
 #pragma unroll
     for (int j = 0; j < NB; ++j) voff_b[j] = (uint32_t)b_rowoff(16 * NB * wave + 16 * j + (lane >> 2)) + chunk;
     // fragment read offsets (lane half g reads logical chunks 2g, 2g+1)
@@ -221,7 +301,16 @@ struct MainLoop {
     uint32_t aoff[2], boff[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+      if constexpr (A_TR) {
+        // transposing reads (index h = block parity): group lane j = lane % 16
+        // points at K row 32*(lane/32) + j/2 (+ 8 per read) and tokens
+        // 32h + 16*((lane/16) & 1) + 8*(j & 1) of the wave's 64-token block
+        const int kl = 32 * (lane >> 5) + ((lane & 15) >> 1);
+        const int cl = (2 * h + ((lane >> 4) & 1)) ^ (((lane >> 3) & 1) << 1);
+        aoff[h] = (uint32_t)(2 * wm * 4096 + kl * 64 + 16 * cl + 8 * (lane & 1));
+      } else {
+        aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+      }
       boff[h] = (uint32_t)(kLdsB + (BLayout<PAIRED, NB>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
     }
 #pragma unroll

@@ -121,6 +121,34 @@ def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-5, atol=0)
 
 
+def test_down_dgrad_swiglu_every_gate_code(dev):
+    """Every e4m3 code as gate and as up value, the two NaN codes included.
+    The kernel takes sigmoid(g) and sig*(1 + g*(1 - sig)) from a table over
+    the 256 gate codes and multiplies in the reference's order, so only a
+    sigmoid that differs from torch's by an ulp can move a byte.  NaN outputs
+    must carry a NaN code (the sign of a NaN is not specified)."""
+    T, D, I = 512, 256, 256
+    g = torch.Generator().manual_seed(11)
+    dy = torch.randint(-8, 9, (T, D), generator=g).float().to(torch.bfloat16)
+    wd = torch.randint(-8, 9, (D, I), generator=g).float().to(torch.bfloat16)
+    codes = torch.arange(T * I, dtype=torch.int64)
+    gate = (codes % 256).to(torch.uint8).view(T, I)
+    up = ((codes * 97 + codes // 256) % 256).to(torch.uint8).view(T, I)
+    gu8 = torch.cat([gate, up], dim=1).view(E4)
+    s = torch.tensor([1, 64.0, 1, 2.0 ** -6, 1])
+    amax = torch.zeros(5, device=dev)
+    dgu8, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), wd.t().contiguous().to(dev), gu8.to(dev), s.to(dev), amax)
+    rdgu8, _, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
+    nan = torch.isnan(rdgu8.float())
+    assert int(nan.sum()) > 0
+    got = u8(dgu8)
+    assert torch.all((got[nan] & 0x7F) == 0x7F)
+    d = code_dist(dgu8, rdgu8)[~nan]
+    assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 1e-3
+    dt = u8(sg.ops.unslab(dgu8t, 2 * I))
+    assert torch.equal(dt[:, :T], got.t())
+
+
 @pytest.mark.parametrize("T,D,I", SHAPES[:3])
 def test_down_dgrad_swiglu_random(dev, T, D, I):
     g = torch.Generator().manual_seed(4 + T + D + I)
