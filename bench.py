@@ -178,9 +178,9 @@ def main() -> None:
     wscale = torch.empty(2, device=dev)
     w8, w8t, _ = ops.weight_quant(wgu.detach(), wscale[0:1], w8=True, w8t=True)
     wd8, _, wdt = ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True)
-    gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I)
+    gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I)
     dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
-    dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale)
+    dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
     dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax)
     # name -> (call, C-ABI symbol, predicate on the symbol's arguments, FLOP, algorithmic bytes)
     kern = {
@@ -190,13 +190,13 @@ def main() -> None:
                             "sfp8_weight_quant", None, None, 10.0 * 2 * I * D),
         "weight_quant_down": (lambda: ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True),
                               "sfp8_weight_quant", None, None, 11.0 * D * I),
-        "gateup_swiglu_fwd": (lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I),
+        "gateup_swiglu_fwd": (lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I),
                               "sfp8_gemm_gateup_swiglu_fwd", None, 4.0 * T * D * I, None),
         "down_fwd": (lambda: ops.down_fwd(h8, wd8, h, scale, wscale), "sfp8_gemm_down_fwd", None,
                      2.0 * T * D * I, None),
         "down_dgrad_swiglu_bf16": (lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax),
                                    "sfp8_gemm_down_dgrad_swiglu", None, 2.0 * T * D * I, None),
-        "gateup_dgrad": (lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale), "sfp8_gemm_gateup_dgrad", None,
+        "gateup_dgrad": (lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D), "sfp8_gemm_gateup_dgrad", None,
                          4.0 * T * D * I, None),
         "norm_bwd": (lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax), "sfp8_norm_bwd", None,
                      None, T * (9.0 * D + 4)),

@@ -16,15 +16,20 @@
  *    max-accumulate into `amax`; nothing is read back to the host.
  *  - `wscale` points at the 2 just-in-time weight scales [q_gu, q_d]
  *    (train.py:1213).
- *  - Token-contiguous FP8 copies (x8t, h8t, dgu8t, dy8t: the weight-gradient
- *    GEMM operands) cover `ldt` = T rounded up to a multiple of 256 tokens
- *    and use the K-slab layout: [ldt / 64][rpad][64] bytes with
- *    rpad = rows rounded up to a multiple of 256; element (r, t) is at
- *    (t / 64) * rpad * 64 + r * 64 + t % 64.  One 64-token stage of a
- *    256-row GEMM tile is one contiguous 16 KiB block.  Producers write zeros
- *    for tokens T..ldt-1 (padding rows r >= rows are never written and never
- *    reach an output).  sfp8_slab_bytes(rows, ldt) gives the buffer size.
- *    The standalone quantizer's x8t is a plain [cols, ldt] transpose.
+ *  - K-slab layout.  Every FP8 GEMM operand, and the bf16 W_down^T, is stored
+ *    as a K-slab of a row-major matrix X [R, L] (L = the GEMM's reduction
+ *    dimension K, in bytes): [L / 64][rpad][64] bytes, rpad = R rounded up to
+ *    a multiple of 256, element (r, l) at (l / 64) * rpad * 64 + r * 64 + l % 64.
+ *    One 64-byte K stage of a 256-row GEMM tile is then one contiguous 16 KiB
+ *    block (row-major rows K bytes apart put a stage's rows into few memory
+ *    channels).  Padding rows r >= R hold zeros; producers write them.
+ *    sfp8_slab_bytes(R, L) gives the buffer size.  Token-major activations
+ *    (x8, h8, dgu8: R = T) have rpad = ldt = T rounded up to 256.
+ *    The token-contiguous copies for the weight gradients (x8t, h8t, dgu8t,
+ *    dy8t) are K-slabs of the transposed activation over ldt tokens
+ *    (R = features, L = ldt); producers write zeros for tokens T..ldt-1.
+ *    The standalone quantizer's outputs are plain row-major x8 and [cols, ldt]
+ *    x8t.
  *  - `stream` is a hipStream_t; every call is asynchronous on it, never
  *    synchronises the device and never allocates device memory.  Callers
  *    provide every output and workspace buffer.
@@ -59,7 +64,8 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
 
 /* Norm-fused quantizer, replaces _fp8_norm_quant_kernel (train.py:955-972,
  * launched at train.py:1208-1210).  h [T, D] bf16, norm_w [D] fp32 ->
- * x8 [T, D] e4m3, x8t (K-slab, D rows) e4m3, rstd [T] fp32; amax[0] max-accumulated.
+ * x8 (K-slab of [T, D]: [D/64][ldt][64]) e4m3, x8t (K-slab of [D, ldt])
+ * e4m3, rstd [T] fp32; amax[0] max-accumulated.
  * D in {128, 256, 512, 1024, 2048, 4096}; ldt = T rounded up to 256. */
 int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
                     const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
@@ -71,9 +77,11 @@ int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, fl
  * transposed bf16 copy of the master (the down-proj dgrad operand; the
  * reference saves w_down.to(bf16), train.py:1224).
  * w [rows, cols] fp32 -> q_out[0] = exp2(floor(log2(448/max(amax,1e-30)))),
- * w8 [rows, cols] e4m3 (optional), w8t [cols, rows] e4m3 (optional),
- * wbf16t [cols, rows] bf16 (optional).  partials: device workspace of
- * nparts_cap >= 512 floats.  cols % 4 == 0. */
+ * w8 = K-slab of e4m3(w * q) [rows, cols] (optional), w8t = K-slab of its
+ * transpose [cols, rows] (optional), wbf16t = K-slab of bf16(w)^T
+ * [cols, rows] bf16 (bytes: [2*rows/64][cols padded][64]) (optional).
+ * partials: device workspace of nparts_cap >= 512 floats.  cols % 64 == 0;
+ * rows % 64 == 0 with w8t, rows % 32 == 0 with wbf16t. */
 int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partials, int64_t nparts_cap,
                       float* q_out, void* w8, void* w8t, void* wbf16t, void* stream);
 
@@ -86,33 +94,37 @@ int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
 
 /* gate/up forward + SwiGLU epilogue, replaces _fp8_swiglu_fwd_kernel
  * (train.py:975-1016, launched at train.py:1216-1218).
- * x8 [T, D] e4m3, w8 [2I, D] e4m3 -> gu8 [T, 2I] e4m3, h8 [T, I] e4m3,
- * h8t (K-slab, I rows) e4m3 (token-contiguous copy of h8 for the down wgrad);
+ * x8 (K-slab of [T, D]) e4m3, w8 (K-slab of [2I, D], gate rows first) e4m3
+ * -> gu8 [T, 2I] e4m3 row-major, h8 (K-slab of [T, I]) e4m3, h8t (K-slab of
+ * [I, ldt]: token-contiguous copy of h8 for the down wgrad) e4m3;
  * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0. */
 int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
                                 void* h8t, int64_t ldt, void* stream);
 
 /* down forward + residual, replaces _fp8_down_fwd_kernel (train.py:1019-1046,
- * launched at train.py:1220-1222).  h8 [T, I] e4m3, wd8 [D, I] e4m3,
- * res [T, D] bf16 -> y [T, D] bf16.  I % 128 == 0, D % 16 == 0. */
+ * launched at train.py:1220-1222).  h8 (K-slab of [T, I], rpad = ldt) e4m3,
+ * wd8 (K-slab of [D, I]) e4m3, res [T, D] bf16 -> y [T, D] bf16.
+ * I % 128 == 0, D % 16 == 0. */
 int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
-                       const float* scale, const float* wscale, void* y, void* stream);
+                       const float* scale, const float* wscale, void* y, int64_t ldt, void* stream);
 
 /* bf16 down dgrad + SwiGLU backward, replaces _fp8_down_dgrad_swiglu_kernel
- * (train.py:1049-1094, launched at train.py:1236-1238).  dy [T, D] bf16,
- * wdt [I, D] bf16 (= w_down^T), gu8 [T, 2I] e4m3 -> dgu8 [T, 2I] e5m2,
- * dgu8t (K-slab, 2I rows) e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is
- * recorded by sfp8_norm_bwd.)  D % 64 == 0. */
+ * (train.py:1049-1094, launched at train.py:1236-1238).  dy [T, D] bf16
+ * row-major, wdt (K-slab of w_down^T [I, D], bf16) , gu8 [T, 2I] e4m3
+ * row-major -> dgu8 (K-slab of [T, 2I]) e5m2, dgu8t (K-slab of [2I, ldt])
+ * e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is recorded by
+ * sfp8_norm_bwd.)  D % 64 == 0, I % 128 == 0. */
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream);
 
 /* gate/up dgrad, replaces torch._scaled_mm (train.py:1239-1241):
- * dxn = bf16((dgu8 @ w8) / (scale[3] * wscale[0])), dgu8 [T, 2I] e5m2,
- * w8t [D, 2I] e4m3 -> dxn [T, D] bf16.  I % 64 == 0, D % 16 == 0. */
+ * dxn = bf16((dgu8 @ w8) / (scale[3] * wscale[0])), dgu8 (K-slab of
+ * [T, 2I], rpad = ldt) e5m2, w8t (K-slab of W8^T [D, 2I]) e4m3 ->
+ * dxn [T, D] bf16.  I % 64 == 0, D % 16 == 0. */
 int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
-                           const float* scale, const float* wscale, void* dxn, void* stream);
+                           const float* scale, const float* wscale, void* dxn, int64_t ldt, void* stream);
 
 /* Weight gradient reduced over tokens, replaces _fp8_wgrad / _fp8_wgrad_kernel
  * (train.py:1150-1187, call at train.py:1247) and _fp8_mm_kernel with A read
@@ -126,9 +138,9 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
 int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
                     const float* sa, const float* sb, float* out, float* ws, int64_t ws_floats, void* stream);
 int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt);
-/* Bytes of a K-slab token-contiguous copy of `rows` rows over ldt tokens
- * (-1 if ldt is not a multiple of 256). */
-int64_t sfp8_slab_bytes(int64_t rows, int64_t ldt);
+/* Bytes of a K-slab of a [rows, k] matrix (k bytes per row; -1 if k is not
+ * a multiple of 64). */
+int64_t sfp8_slab_bytes(int64_t rows, int64_t k);
 int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt);
 
 

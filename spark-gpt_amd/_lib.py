@@ -27,9 +27,9 @@ SIGNATURES = {
     "sfp8_weight_quant": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P]),
     "sfp8_update_scales": (_INT, [_P, _P, _I64, _P]),
     "sfp8_gemm_gateup_swiglu_fwd": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
-    "sfp8_gemm_down_fwd": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "sfp8_gemm_down_fwd": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "sfp8_gemm_down_dgrad_swiglu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
-    "sfp8_gemm_gateup_dgrad": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "sfp8_gemm_gateup_dgrad": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "sfp8_gemm_wgrad": (_INT, [_P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "sfp8_wgrad_splits": (_I64, [_I64, _I64, _I64]),
     "sfp8_wgrad_workspace_floats": (_I64, [_I64, _I64, _I64]),

@@ -103,6 +103,22 @@ SFP8_DEV void lds_rows_to_global(const uint8_t* lds, int nrows, int cpr_log2, in
   }
 }
 
+// Copy of an LDS tile (nrows rows of 64 * NP bytes, LDS row stride `stride`)
+// into a K-slab matrix: 64-byte column block p of tile row r goes to
+// dst + (c0 / 64 + p) * ldrows * 64 + (r0 + r) * 64.  Sixteen consecutive
+// threads read one contiguous LDS row (no bank conflicts for NP = 4); the
+// global writes are 256-byte runs of 4 rows per block.
+template <int NP>
+SFP8_DEV void lds_rows_to_kslab(const uint8_t* lds, int nrows, int stride, uint8_t* dst, int64_t ldrows, int64_t r0,
+                                int64_t c0) {
+  const int total = nrows * NP * 4;
+  for (int idx = threadIdx.x; idx < total; idx += 256) {
+    const int ch = idx & 3, pb = (idx >> 2) % NP, r = idx / (4 * NP);
+    *reinterpret_cast<intx4*>(dst + (c0 / 64 + pb) * ldrows * 64 + (r0 + r) * 64 + ch * 16) =
+        *reinterpret_cast<const intx4*>(lds + r * stride + pb * 64 + ch * 16);
+  }
+}
+
 SFP8_DEV void store16(void* p, const uint32_t (&w)[4]) {
   *reinterpret_cast<intx4*>(p) = intx4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
 }
@@ -136,16 +152,19 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   floatx16 acc[4][4];
+  // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64]; one K stage of
+  // the tile is 256 contiguous rows of A and two runs of 128 rows of B
   MainLoop<false, kFmtE4M3, kFmtE4M3, true>::run(
-      lds, x8 + m0 * D, (T - m0) * D, [=](int r) { return r * (int)D; }, kStage, w8 + n0 * D, (2 * I - n0) * D,
-      [=](int r) { return ((r >> 7) * (int)I + paired_col(r & 127)) * (int)D; }, kStage, (int)(D / kStage), acc);
+      lds, x8 + m0 * kStage, D * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage), w8,
+      D * 2 * I, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
+      (int)(2 * I * kStage), (int)(D / kStage), acc);
   // All scales are powers of two, so the dequantization factor commutes with
   // every rounding step: with gb, ub = bf16(acc) (unscaled),
   //   g = gb*deq, u = ub*deq, h = (g*sig(g))*u = hb*deq^2, hb = (gb*sig)*ub,
   //   gu8 = e4m3(g*q1) = e4m3(gb*(deq*q1)),  h8 = e4m3(hb*(deq^2*q2)),
   //   amax1 = deq*max(|gb|,|ub|),  amax2 = deq^2*max|hb|.
-  // Rows past T read as zero (buffer range check): they add 0 to the amax
-  // and 0 bytes to h8t's padding.
+  // Rows past T are zero in x8 (K-slab padding): they add 0 to the amax and
+  // 0 bytes to the padding of h8 and h8t.
   const float deq = 1.0f / (scale[0] * wscale[0]);
   const float c_exp = deq * -1.4426950408889634f;
   const float m1 = deq * scale[1], m2 = deq * deq * scale[2];
@@ -211,11 +230,13 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   m_gu *= deq;
   m_h *= deq * deq;
   __syncthreads();
-  // whole 128-byte rows: gate and up halves of gu8, h8, then the K-slab h8t
+  // whole 128-byte rows of the gate and up halves of gu8, then h8 as two
+  // 64-column K-slab blocks (every tile row: rows past T are zero padding)
+  // and the token-contiguous h8t
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
   lds_rows_to_global(Gt, kTile, 3, kEpiStride, gu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
   lds_rows_to_global(Ut, kTile, 3, kEpiStride, gu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
-  lds_rows_to_global(Ht, kTile, 3, kEpiStride, h8 + m0 * I + n0, I, rows_valid);
+  lds_rows_to_kslab<2>(Ht, kTile, kEpiStride, h8, ldt, m0, n0);
   lds_tile_store_slab<256>(Ht, kTile, 128, kEpiStride, h8t, slab_rows(I), m0, n0, rows_valid);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
@@ -282,7 +303,7 @@ struct SwigluPipe {
     uint8_t* hbuf;        // its LDS h tile
     // scales and outputs
     float c_exp, inv1, bnd1, inv2, bnd2;
-    int64_t T, I;
+    int64_t T, I, ldt;
     uint8_t* gu8;
     uint8_t* h8;
   };
@@ -337,11 +358,15 @@ struct SwigluPipe {
     const int row = 128 * wm + 32 * TB + fr;
     const int col = 32 * wn + 16 * g;
     const int64_t t = c.pm0 + row;
-    if (c.prev && t < c.T) {
-      uint8_t* gp = c.gu8 + t * 2 * c.I + c.pn0 + col;
-      store16(gp, c.gw);
-      store16(gp + c.I, c.uw);
-      store16(c.h8 + t * c.I + c.pn0 + col, c.hw);
+    if (c.prev) {
+      if (t < c.T) {
+        uint8_t* gp = c.gu8 + t * 2 * c.I + c.pn0 + col;
+        store16(gp, c.gw);
+        store16(gp + c.I, c.uw);
+      }
+      // h8 is a K-slab [I/64][ldt][64]: the tile's 64 columns are one block
+      // (rows past T hold the zeros computed from x8's zero padding)
+      store16(c.h8 + (c.pn0 >> 6) * c.ldt * 64 + t * 64 + col, c.hw);
     }
     store16(c.hbuf + row * kPipeHStride + col, c.hw);
   }
@@ -447,7 +472,8 @@ template <int NK>
 __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, float* __restrict__ amax,
-    uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int tiles_m, int tiles_n) {
+    uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int64_t ldt, int tiles_m,
+    int tiles_n) {
   using P = SwigluPipe<NK>;
   using ML = typename P::ML;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -464,6 +490,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   c.bnd2 = kE4M3Max * c.inv2;
   c.T = T;
   c.I = I;
+  c.ldt = ldt;
   c.gu8 = gu8;
   c.h8 = h8;
   c.m_gu = 0.f;
@@ -495,14 +522,15 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     int tm, tn;
     tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 64;
-    c.ra = make_rsrc(x8 + m0 * D, (T - m0) * D);
-    c.rb = make_rsrc(w8 + n0 * D, (2 * I - n0) * D);
+    // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64]
+    c.ra = make_rsrc(x8 + m0 * kStage, D * ldt - m0 * kStage);
+    c.rb = make_rsrc(w8, D * 2 * I);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * (int)D) + chunk;
+    for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * kStage) + chunk;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = 32 * c.wave + 16 * j + (lane >> 2);
-      c.voff_b[j] = (uint32_t)(((r >> 6) * (int)I + paired_col64(r)) * (int)D) + chunk;
+      c.voff_b[j] = (uint32_t)(((r >> 6) * (int)I + (int)n0 + paired_col64(r)) * kStage) + chunk;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -510,14 +538,15 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
       for (int j = 0; j < 2; ++j) c.acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                                           0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     // prologue: stages 0..2 in flight, stage 0 landed, its fragments read
+    const int a_ss = (int)(ldt * kStage), b_ss = (int)(2 * I * kStage);
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       const int ld = s < NK - 1 ? s : NK - 1;
-      ML::load_stage(lds, s, c.ra, c.rb, c.voff_a, c.voff_b, ld * kStage, ld * kStage, c.wave);
+      ML::load_stage(lds, s, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
     }
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * ML::kDma) : "memory");
     ML::read_frags(lds, 0, c.aoff, c.boff, c.f[0]);
-    P::template stages<0>(c, kStage, kStage);
+    P::template stages<0>(c, a_ss, b_ss);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     // the previous tile's h tile is complete: its K-slab copy
     if (c.prev) pipe_h_slab(c.hbuf, c.pm0, c.pn0, h8t, rpad);
@@ -607,15 +636,18 @@ SFP8_DEV void write_bf16_half(const uint8_t* lds, int p, int64_t m0, int64_t n0,
 __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
     const uint8_t* __restrict__ h8, const uint8_t* __restrict__ wd8, const uint16_t* __restrict__ res,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, const float* __restrict__ wscale,
-    uint16_t* __restrict__ y, int tiles_m, int tiles_n) {
+    uint16_t* __restrict__ y, int64_t ldt, int tiles_m, int tiles_n) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   floatx16 acc[4][4];
+  // K-slab operands: h8 [I/64][ldt][64], wd8 [I/64][slab_rows(D)][64]
+  const int64_t dp = slab_rows(D);
   MainLoop<false, kFmtE4M3, kFmtE4M3, false>::run(
-      lds, h8 + m0 * I, (T - m0) * I, [=](int r) { return r * (int)I; }, kStage, wd8 + n0 * I, (D - n0) * I,
-      [=](int r) { return plain_col(r) * (int)I; }, kStage, (int)(I / kStage), acc);
+      lds, h8 + m0 * kStage, I * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage),
+      wd8 + n0 * kStage, I * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
+      (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[1]);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -667,6 +699,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t ldb = D * 2;  // bytes
+  const int64_t ip = slab_rows(I);
   // The gate operand of the SwiGLU backward is an e4m3 code here, so its two
   // factors take 256 values per launch: entry b of this table holds
   //   sig = sigmoid(g), sig * (1 + g * (1 - sig))   for g = e4m3(b) / s1,
@@ -702,10 +735,12 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   floatx16 acc[4][4];
+  // A = dy row-major (rows past T read as zero through the range check);
+  // B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
   MainLoop<true, 0, 0, false>::run(
       lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
-      kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * ldb, (I - n0) * ldb,
-      [=](int r) { return plain_col(r) * (int)ldb; }, kStage, (int)(ldb / kStage), acc);
+      kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * kStage, ldb * ip - n0 * kStage,
+      [=](int r) { return plain_col(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
   // gu8 rows of this tile through a range-checked descriptor: rows past T
   // read as zero (and their dh is zero: dy rows past T read as zero).  All
   // 32 words of this lane are requested at once, so one memory latency covers
@@ -777,8 +812,16 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   __syncthreads();
   const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
-  lds_rows_to_global(Gt, kTile, cols == kTile ? 4 : 3, kEpiStride2, dgu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
-  lds_rows_to_global(Ut, kTile, cols == kTile ? 4 : 3, kEpiStride2, dgu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
+  // dgu8 is a K-slab [2I/64][ldt][64] (the gate/up dgrad's A operand): the
+  // tile's gate and up columns are 64-column blocks of every tile row (rows
+  // past T hold zeros: their dh is zero)
+  if (cols == kTile) {
+    lds_rows_to_kslab<4>(Gt, kTile, kEpiStride2, dgu8, ldt, m0, n0);
+    lds_rows_to_kslab<4>(Ut, kTile, kEpiStride2, dgu8, ldt, m0, I + n0);
+  } else {
+    lds_rows_to_kslab<2>(Gt, kTile, kEpiStride2, dgu8, ldt, m0, n0);
+    lds_rows_to_kslab<2>(Ut, kTile, kEpiStride2, dgu8, ldt, m0, I + n0);
+  }
   lds_tile_store_slab<256>(Gt, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0, rows_valid);
   lds_tile_store_slab<256>(Ut, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0, rows_valid);
   __syncthreads();  // the next tile's DMA overwrites the staging tiles
@@ -803,10 +846,11 @@ template <int NB>
 __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gateup_dgrad_kernel(
     const uint8_t* __restrict__ dgu8, const uint8_t* __restrict__ w8t, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, uint16_t* __restrict__ dxn,
-    int tiles_m, int tiles_n, int n_cu, int sleep_iters) {
+    int64_t ldt, int tiles_m, int tiles_n, int n_cu, int sleep_iters) {
   using ML = MainLoop<false, kFmtE5M2, kFmtE4M3, false, NB, NB == 2 ? 3 : kStages>;
   extern __shared__ __align__(16) uint8_t lds[];
   const int64_t K = 2 * I;
+  const int64_t dp = slab_rows(D);
   const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
   const int ntiles = tiles_m * tiles_n;
   if constexpr (NB == 2) stagger_second_wg(n_cu, sleep_iters);
@@ -815,8 +859,10 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gateup_dgrad_kernel(
     tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * ML::kTileN;
     floatx16 acc[4][NB];
-    ML::run(lds, dgu8 + m0 * K, (T - m0) * K, [=](int r) { return r * (int)K; }, kStage, w8t + n0 * K,
-            (D - n0) * K, [=](int r) { return plain_col_nb<NB>(r) * (int)K; }, kStage, (int)(K / kStage), acc);
+    // K-slab operands: dgu8 [2I/64][ldt][64], w8t [2I/64][slab_rows(D)][64]
+    ML::run(lds, dgu8 + m0 * kStage, K * ldt - m0 * kStage, [=](int r) { return r * kStage; },
+            (int)(ldt * kStage), w8t + n0 * kStage, K * dp - n0 * kStage,
+            [=](int r) { return plain_col_nb<NB>(r) * kStage; }, (int)(dp * kStage), (int)(K / kStage), acc);
     if constexpr (NB == 4) {
       stage_bf16_half<0>(lds, acc, sab);
       __syncthreads();
@@ -1002,7 +1048,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
                                 void* h8t, int64_t ldt, void* stream) {
   if (!x8 || !w8 || !scale || !wscale || !amax || !gu8 || !h8 || !h8t) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || D % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
-  if (!fits32(kTile, D) || !fits32(2 * I, D)) return kErrBadShape;
+  if (!fits32(ldt, D) || !fits32(2 * I, D) || !fits32(ldt, I) || !fits32(ldt, 2 * I)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
   if (D == 1024) {
@@ -1017,7 +1063,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
     if (rc) return rc;
     hipLaunchKernelGGL(swiglu_pipe_kernel<16>, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kPipeLds,
                        (hipStream_t)stream, (const uint8_t*)x8, (const uint8_t*)w8, T, D, I, scale, wscale, amax,
-                       (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, tiles_m, tiles_n);
+                       (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n);
     return status();
   }
   const int tiles_m = cdiv(T, kTile), tiles_n = (int)(I / 128);
@@ -1030,10 +1076,10 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
 }
 
 int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
-                       const float* scale, const float* wscale, void* y, void* stream) {
+                       const float* scale, const float* wscale, void* y, int64_t ldt, void* stream) {
   if (!h8 || !wd8 || !res || !scale || !wscale || !y) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 16) return kErrBadShape;
-  if (!fits32(kTile, I)) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 16 || ldt < T || ldt % kTile) return kErrBadShape;
+  if (!fits32(ldt, I) || !fits32(slab_rows(D), I)) return kErrBadShape;
   if (!al16(h8) || !al16(wd8) || !al16(res) || !al16(y)) return kErrBadAlignment;
   if (T == 0) return kOk;
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
@@ -1041,7 +1087,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
   if (rc) return rc;
   hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)h8, (const uint8_t*)wd8, (const uint16_t*)res, T, D, I, scale, wscale,
-                     (uint16_t*)y, tiles_m, tiles_n);
+                     (uint16_t*)y, ldt, tiles_m, tiles_n);
   return status();
 }
 
@@ -1049,8 +1095,8 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream) {
   if (!dy || !wdt || !gu8 || !scale || !amax || !dgu8 || !dgu8t) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 16 || ldt < T || ldt % kTile) return kErrBadShape;
-  if (!fits32(kTile, 2 * D)) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
+  if (!fits32(kTile, 2 * D) || !fits32(slab_rows(I), 2 * D) || !fits32(ldt, 2 * I)) return kErrBadShape;
   if (!al16(dy) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(I, kTile);
@@ -1071,10 +1117,10 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
 }
 
 int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
-                           const float* scale, const float* wscale, void* dxn, void* stream) {
+                           const float* scale, const float* wscale, void* dxn, int64_t ldt, void* stream) {
   if (!dgu8 || !w8t || !scale || !wscale || !dxn) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 16) return kErrBadShape;
-  if (!fits32(kTile, 2 * I)) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 16 || ldt < T || ldt % kTile) return kErrBadShape;
+  if (!fits32(ldt, 2 * I) || !fits32(slab_rows(D), 2 * I)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
   if (T == 0) return kOk;
   using ML = MainLoop<false, kFmtE5M2, kFmtE4M3, false, kGateupDgradNB, kGateupDgradNB == 2 ? 3 : kStages>;
@@ -1090,8 +1136,8 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
   rc = prep(gateup_dgrad_kernel<kGateupDgradNB>, ML::kLds);
   if (rc) return rc;
   hipLaunchKernelGGL(gateup_dgrad_kernel<kGateupDgradNB>, dim3(grid), dim3(256), ML::kLds, (hipStream_t)stream,
-                     (const uint8_t*)dgu8, (const uint8_t*)w8t, T, D, I, scale, wscale, (uint16_t*)dxn, tiles_m,
-                     tiles_n, n_cu, sleep_iters);
+                     (const uint8_t*)dgu8, (const uint8_t*)w8t, T, D, I, scale, wscale, (uint16_t*)dxn, ldt,
+                     tiles_m, tiles_n, n_cu, sleep_iters);
   return status();
 }
 
@@ -1105,9 +1151,9 @@ int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
   return s;
 }
 
-int64_t sfp8_slab_bytes(int64_t rows, int64_t ldt) {
-  if (rows < 0 || ldt < 0 || ldt % kTile) return -1;
-  return slab_rows(rows) * ldt;
+int64_t sfp8_slab_bytes(int64_t rows, int64_t k) {
+  if (rows < 0 || k < 0 || k % kStage) return -1;
+  return slab_rows(rows) * k;
 }
 
 int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {

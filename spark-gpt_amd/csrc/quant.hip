@@ -26,50 +26,6 @@ SFP8_DEV int xcd_row_block(int pid, int nblk) {
   return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
-// --------------------------------------------------------------------------
-// Transposed write-out of an fp8 tile held in LDS.
-//   lds:      tile of `rows` rows x `cols` bytes, row stride `stride` bytes
-//   out:      destination, out[c * ldo + r0 + r] = tile[r][c]
-//   rows_valid: rows >= rows_valid are written as zero bytes
-// rows % 16 == 0, cols % 4 == 0, (r0 % 16 == 0 and ldo % 16 == 0) for the
-// vector path.  `nthreads` threads cooperate.
-template <int NTHREADS>
-SFP8_DEV void lds_tile_store_transposed(const uint8_t* lds, int rows, int cols, int stride,
-                                        uint8_t* out, int64_t ldo, int64_t r0, int rows_valid,
-                                        int64_t rows_total) {
-  const int nb_c = cols >> 2;
-  const int nblocks = (rows >> 4) * nb_c;
-  for (int idx = threadIdx.x; idx < nblocks; idx += NTHREADS) {
-    const int b = idx % nb_c;  // column block (4 bytes)
-    const int a = idx / nb_c;  // row block (16 rows)
-    uint32_t w[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = a * 16 + i;
-      w[i] = (r < rows_valid) ? *reinterpret_cast<const uint32_t*>(lds + r * stride + b * 4) : 0u;
-    }
-    uint32_t t[4][4];  // t[c][q]: column (4b+c), rows 4q..4q+3 of the block
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t o[4];
-      transpose4x4_bytes(&w[4 * q], o);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) t[c][q] = o[c];
-    }
-    const int64_t rbase = r0 + a * 16;
-    if (rbase >= rows_total) continue;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint8_t* dst = out + (int64_t)(b * 4 + c) * ldo + rbase;
-      if (rbase + 16 <= rows_total && ((((uintptr_t)dst) & 15u) == 0)) {
-        *reinterpret_cast<intx4*>(dst) = intx4{(int)t[c][0], (int)t[c][1], (int)t[c][2], (int)t[c][3]};
-      } else {
-        const int nv = (int)((rows_total - rbase) < 16 ? (rows_total - rbase) : 16);
-        for (int k = 0; k < nv; ++k) dst[k] = (uint8_t)(t[c][k >> 2] >> (8 * (k & 3)));
-      }
-    }
-  }
-}
 
 // --------------------------------------------------------------------------
 // Standalone quantizer: x8 = e4m3(x * s), x8t = x8^T, amax = max|x|.
@@ -269,8 +225,10 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
         if (valid) {
           lo = pack4_e4m3(n[0] * s0, n[1] * s0, n[2] * s0, n[3] * s0);
           hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
-          *reinterpret_cast<intx2*>(x8 + t * D + d) = intx2{(int)lo, (int)hi};
         }
+        // x8 is a K-slab [D/64][ldt][64] (the gate/up GEMM's A operand),
+        // zeros for tokens T..ldt-1
+        *reinterpret_cast<intx2*>(x8 + (int64_t)(d >> 6) * ldt * 64 + t * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
         *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
     }
@@ -286,8 +244,9 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
 //   weight_amax_kernel:  per-block max|w| partials (no zero-init needed)
 //   weight_quant_kernel: every block folds the partials into amax and
 //     q = exp2(floor(log2(448 / max(amax, 1e-30)))), then writes its tile of
-//     w8 = e4m3(w * q) row-major and/or transposed, and optionally a
-//     transposed bf16 copy of w.  Block 0 stores q.
+//     w8 = e4m3(w * q) as a K-slab over W's columns and/or over its rows
+//     (the GEMMs' B operands: rows of 64 contiguous K bytes), and optionally
+//     a bf16 K-slab of W^T.  Block 0 stores q.
 constexpr int WQ_PARTS = 512;
 
 __global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restrict__ w, int64_t n,
@@ -332,7 +291,10 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
   }
   __syncthreads();
   const float q = qs;
+  // The grid covers rows and columns up to multiples of 256, so that the
+  // padding rows of every K-slab output are written (as zeros).
   const int64_t r0 = (int64_t)blockIdx.x * WQ_TILE, c0 = (int64_t)blockIdx.y * WQ_TILE;
+  const int64_t rp = (R + 255) / 256 * 256, cp = (C + 255) / 256 * 256;
   // each thread: 4 consecutive columns of 4 rows (64x64 tile = 1024 quads)
   for (int idx = threadIdx.x; idx < WQ_TILE * WQ_TILE / 4; idx += 256) {
     const int r = idx / (WQ_TILE / 4), c4 = idx % (WQ_TILE / 4);
@@ -340,23 +302,37 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
     floatx4 v = {0.f, 0.f, 0.f, 0.f};
     if (gr < R && gc < C) v = *reinterpret_cast<const floatx4*>(w + gr * C + gc);
     const uint32_t p = pack4_e4m3(v[0] * q, v[1] * q, v[2] * q, v[3] * q);
-    if (gr < R && gc < C) {
-      if (w8) *reinterpret_cast<uint32_t*>(w8 + gr * C + gc) = p;
-    }
+    // w8: K-slab of W over its columns, [C/64][rp][64]
+    if (w8 && c0 < C) *reinterpret_cast<uint32_t*>(w8 + (gc >> 6) * rp * 64 + gr * 64 + (gc & 63)) = p;
     *reinterpret_cast<uint32_t*>(t8 + r * (WQ_TILE + 8) + c4 * 4) = p;
 #pragma unroll
     for (int j = 0; j < 4; ++j) t16[(c4 * 4 + j) * (WQ_TILE + 2) + r] = (uint16_t)f32_to_bf16_bits(v[j]);
   }
   __syncthreads();
+  if (r0 >= R) return;  // row padding of w8 only
+  // w8t: K-slab of W^T over its columns (W's rows), [R/64][cp][64]: this
+  // tile is 64 slab rows (W columns c0..) of 64 bytes (W rows r0..)
   if (w8t) {
-    const int rows_valid = (int)((R - r0) < WQ_TILE ? (R - r0) : WQ_TILE);
-    const int cols = (int)((C - c0) < WQ_TILE ? (C - c0) : WQ_TILE);
-    lds_tile_store_transposed<256>(t8, WQ_TILE, cols, WQ_TILE + 8, w8t + c0 * R, R, r0, rows_valid, R);
+    const int c = threadIdx.x >> 2, ch = threadIdx.x & 3;
+    uint32_t wv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t word = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) word |= (uint32_t)t8[(16 * ch + 4 * k + b) * (WQ_TILE + 8) + c] << (8 * b);
+      wv[k] = word;
+    }
+    *reinterpret_cast<intx4*>(w8t + (r0 >> 6) * cp * 64 + (c0 + c) * 64 + 16 * ch) =
+        intx4{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
   }
+  // wbt: K-slab of bf16(W)^T, [R/32][cp][32] bf16 (64-byte rows of 32 W rows)
   if (wbt) {
-    for (int idx = threadIdx.x; idx < WQ_TILE * WQ_TILE; idx += 256) {
-      const int c = idx / WQ_TILE, r = idx % WQ_TILE;
-      if (r0 + r < R && c0 + c < C) wbt[(c0 + c) * R + r0 + r] = t16[c * (WQ_TILE + 2) + r];
+    for (int idx = threadIdx.x; idx < 512; idx += 256) {
+      const int c = idx >> 3, hp = (idx >> 2) & 1, j = idx & 3;
+      if (r0 + 32 * hp >= R) continue;  // R % 64 == 32: the tile's second panel is past the end
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(t16 + c * (WQ_TILE + 2) + 32 * hp + 8 * j);
+      *reinterpret_cast<intx4*>(wbt + ((r0 >> 5) + hp) * cp * 32 + (c0 + c) * 32 + 8 * j) =
+          intx4{(int)src[0], (int)src[1], (int)src[2], (int)src[3]};
     }
   }
 }
@@ -621,7 +597,8 @@ int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, fl
 int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partials, int64_t nparts_cap,
                       float* q_out, void* w8, void* w8t, void* wbf16t, void* stream) {
   if (!w || !partials || !q_out) return kErrNullPointer;
-  if (rows <= 0 || cols <= 0 || (cols % 4) != 0) return kErrBadShape;
+  if (rows <= 0 || cols <= 0 || (cols % 64) != 0 || (w8t && rows % 64) || (wbf16t && rows % 32))
+    return kErrBadShape;
   if (nparts_cap < WQ_PARTS) return kErrWorkspaceTooSmall;
   if (!aligned16(w)) return kErrBadAlignment;
   hipStream_t st = (hipStream_t)stream;
@@ -630,7 +607,8 @@ int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partial
   if (nparts > WQ_PARTS) nparts = WQ_PARTS;
   if (nparts < 1) nparts = 1;
   hipLaunchKernelGGL(weight_amax_kernel, dim3(nparts), dim3(256), 0, st, w, n, partials);
-  dim3 grid((unsigned)((rows + WQ_TILE - 1) / WQ_TILE), (unsigned)((cols + WQ_TILE - 1) / WQ_TILE));
+  // 64 x 64 tiles over rows and columns rounded up to 256 (K-slab padding)
+  dim3 grid((unsigned)((rows + 255) / 256 * 4), (unsigned)((cols + 255) / 256 * 4));
   hipLaunchKernelGGL(weight_quant_kernel, grid, dim3(256), 0, st, w, rows, cols, partials, nparts, q_out,
                      (uint8_t*)w8, (uint8_t*)w8t, (uint16_t*)wbf16t);
   return launch_status();

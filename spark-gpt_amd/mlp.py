@@ -96,7 +96,7 @@ class _FP8MLPBlock(torch.autograd.Function):
         wscale = torch.empty(2, dtype=torch.float32, device=h.device)
         w8, w8t, _ = ops.weight_quant(_master(w_gu), wscale[0:1], w8=True, w8t=True)
         wd8, _, wdt = ops.weight_quant(_master(w_down), wscale[1:2], w8=True, bf16t=True)
-        gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I)
+        gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, h.shape[0], I)
         y = ops.down_fwd(h8, wd8, h, scale, wscale)
         # backward needs the token-contiguous x8t / h8t (weight grads), gu8
         # (SwiGLU backward), W8^T (gate/up dgrad) and bf16 Wd^T (down dgrad)
@@ -110,9 +110,9 @@ class _FP8MLPBlock(torch.autograd.Function):
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
         D = h.shape[1]
-        I = wdt.shape[0]
+        I = gu8.shape[1] // 2
         dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
-        dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale)
+        dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, h.shape[0], D)
         del dgu8
         dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nw, scale, amax)
         del dxn

@@ -24,32 +24,45 @@ def ldt_of(T: int) -> int:
     return -(-T // TOKEN_ALIGN) * TOKEN_ALIGN
 
 
-SLAB = 64  # tokens per K slab
+SLAB = 64  # bytes of K per slab row
 
 
 def slab_rows(R: int) -> int:
-    """Rows of a K-slab copy: R rounded up to the 256-row GEMM tile."""
+    """Rows of a K-slab: R rounded up to the 256-row GEMM tile."""
     return -(-R // 256) * 256
 
 
+def kslab_empty(R: int, L: int, dtype, device) -> torch.Tensor:
+    """A K-slab of a row-major [R, L] matrix (L elements of K per row):
+    [L*size/64, slab_rows(R), 64/size] for elements of `size` bytes; element
+    (r, l) at [l // n, r, l % n] with n = 64 / size.  Every FP8 GEMM operand
+    (and the bf16 W_down^T) uses this layout; one 64-byte K stage of a
+    256-row tile is one contiguous 16 KiB block."""
+    n = SLAB // torch.empty((), dtype=dtype).element_size()
+    _need(L % n == 0, f"K extent {L} must be a multiple of {n}")
+    return torch.empty(L // n, slab_rows(R), n, dtype=dtype, device=device)
+
+
 def slab_empty(R: int, T: int, dtype, device) -> torch.Tensor:
-    """A K-slab token-contiguous copy of R rows over ldt_of(T) tokens:
-    [ldt / 64, slab_rows(R), 64]; element (r, t) at [t // 64, r, t % 64]."""
-    return torch.empty(ldt_of(T) // SLAB, slab_rows(R), SLAB, dtype=dtype, device=device)
+    """A token-contiguous K-slab copy of R feature rows over ldt_of(T) tokens
+    (the weight gradients' operands): [ldt / 64, slab_rows(R), 64]; element
+    (r, t) at [t // 64, r, t % 64]."""
+    return kslab_empty(R, ldt_of(T), dtype, device)
 
 
 def unslab(t: torch.Tensor, R: int) -> torch.Tensor:
-    """The plain [R, ldt] view-copy of a K-slab tensor (for inspection and tests)."""
+    """The plain [R, L] matrix of a K-slab tensor (for inspection and tests)."""
     n, rp, _ = t.shape
     return t.view(torch.uint8).permute(1, 0, 2).reshape(rp, n * SLAB)[:R].view(t.dtype)
 
 
 def to_slab(x: torch.Tensor) -> torch.Tensor:
-    """K-slab copy of a plain [R, ldt] tensor (ldt % 256 == 0); padding rows zero."""
+    """K-slab of a plain [R, L] tensor (64-byte multiple rows); padding rows zero."""
     R, L = x.shape
-    _need(L % TOKEN_ALIGN == 0, "token count must be a multiple of 256")
-    out = torch.zeros(L // SLAB, slab_rows(R), SLAB, dtype=torch.uint8, device=x.device)
-    out[:, :R] = x.contiguous().view(torch.uint8).view(R, L // SLAB, SLAB).permute(1, 0, 2)
+    nb = L * x.element_size()
+    _need(nb % SLAB == 0, "row length must be a multiple of 64 bytes")
+    out = torch.zeros(nb // SLAB, slab_rows(R), SLAB, dtype=torch.uint8, device=x.device)
+    out[:, :R] = x.contiguous().view(torch.uint8).view(R, nb // SLAB, SLAB).permute(1, 0, 2)
     return out.view(x.dtype)
 
 
@@ -85,14 +98,14 @@ def quant_e4m3_rowcol(x: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor):
 
 
 def norm_quant(h: torch.Tensor, norm_w: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor, eps: float):
-    """(x8 [T, D], x8t K-slab [ldt/64, slab_rows(D), 64], rstd [T]); amax[0]
-    max-accumulated."""
+    """(x8 K-slab of [T, D] ([D/64, ldt, 64]), x8t K-slab of [D, ldt], rstd
+    [T]); amax[0] max-accumulated."""
     _cuda_contig("h", h, torch.bfloat16, 2)
     _cuda_contig("norm_w", norm_w, torch.float32, 1)
     _state(scale, amax)
     T, D = h.shape
     ldt = ldt_of(T)
-    x8 = torch.empty(T, D, dtype=E4M3, device=h.device)
+    x8 = kslab_empty(ldt, D, E4M3, h.device)
     x8t = slab_empty(D, T, E4M3, h.device)
     rstd = torch.empty(T, dtype=torch.float32, device=h.device)
     _lib.call("sfp8_norm_quant", h.data_ptr(), norm_w.data_ptr(), T, D, float(eps), scale.data_ptr(),
@@ -102,15 +115,18 @@ def norm_quant(h: torch.Tensor, norm_w: torch.Tensor, scale: torch.Tensor, amax:
 
 def weight_quant(w: torch.Tensor, q_out: torch.Tensor, *, w8: bool = True, w8t: bool = False,
                  bf16t: bool = False):
-    """Just-in-time e4m3 copy of an fp32 master: returns (w8, w8t, w_bf16^T),
-    unrequested outputs None; the pow2 scale lands in q_out[0] (device)."""
+    """Just-in-time e4m3 copy of an fp32 master [R, C]: returns (w8 K-slab of
+    [R, C], w8t K-slab of [C, R], bf16 K-slab of W^T [C, R]), unrequested
+    outputs None; the pow2 scale lands in q_out[0] (device)."""
     _cuda_contig("w", w, torch.float32, 2)
     R, C = w.shape
-    _need(C % 4 == 0, "weight columns must be a multiple of 4")
+    _need(C % 64 == 0, "weight columns must be a multiple of 64")
+    _need(not w8t or R % 64 == 0, "weight rows must be a multiple of 64 for the transposed copy")
+    _need(not bf16t or R % 32 == 0, "weight rows must be a multiple of 32 for the bf16 copy")
     dev = w.device
-    o8 = torch.empty(R, C, dtype=E4M3, device=dev) if w8 else None
-    o8t = torch.empty(C, R, dtype=E4M3, device=dev) if w8t else None
-    obt = torch.empty(C, R, dtype=torch.bfloat16, device=dev) if bf16t else None
+    o8 = kslab_empty(R, C, E4M3, dev) if w8 else None
+    o8t = kslab_empty(C, R, E4M3, dev) if w8t else None
+    obt = kslab_empty(C, R, torch.bfloat16, dev) if bf16t else None
     parts = torch.empty(512, dtype=torch.float32, device=dev)
     _lib.call("sfp8_weight_quant", w.data_ptr(), R, C, parts.data_ptr(), parts.numel(), q_out.data_ptr(),
               _lib.ptr(o8), _lib.ptr(o8t), _lib.ptr(obt), _lib.stream_of(w))
@@ -128,18 +144,25 @@ def update_scales(scale: torch.Tensor, amax: torch.Tensor) -> None:
 
 
 # ------------------------------------------------------------------ GEMMs
-def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I: int):
-    """(gu8 [T, 2I], h8 [T, I], h8t K-slab of I rows); amax[1], amax[2]
+def _kslab(name: str, t: torch.Tensor, dtype, R: int, L: int) -> None:
+    n = SLAB // torch.empty((), dtype=dtype).element_size()
+    _cuda_contig(name, t, dtype, 3)
+    _need(tuple(t.shape) == (L // n, slab_rows(R), n), f"{name} must be a K-slab of [{R}, {L}]")
+
+
+def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T: int, I: int):
+    """(gu8 [T, 2I] row-major, h8 K-slab of [T, I], h8t K-slab of [I, ldt]);
+    x8 is the K-slab of [T, D], w8 that of [2I, D]; amax[1], amax[2]
     max-accumulated."""
-    _cuda_contig("x8", x8, E4M3, 2)
-    _cuda_contig("w8", w8, E4M3, 2)
-    T, D = x8.shape
-    _need(w8.shape == (2 * I, D), "w8 must be [2I, D]")
-    _need(D % 128 == 0 and I % 128 == 0, "D and I must be multiples of 128")
+    _need(x8.dim() == 3, "x8 must be a K-slab")
+    D = x8.shape[0] * SLAB
     ldt = ldt_of(T)
+    _kslab("x8", x8, E4M3, ldt, D)
+    _kslab("w8", w8, E4M3, 2 * I, D)
+    _need(D % 128 == 0 and I % 128 == 0, "D and I must be multiples of 128")
     dev = x8.device
     gu8 = torch.empty(T, 2 * I, dtype=E4M3, device=dev)
-    h8 = torch.empty(T, I, dtype=E4M3, device=dev)
+    h8 = kslab_empty(ldt, I, E4M3, dev)
     h8t = slab_empty(I, T, E4M3, dev)
     _lib.call("sfp8_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), T, D, I, scale.data_ptr(),
               wscale.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr(), ldt,
@@ -148,47 +171,52 @@ def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, I: int):
 
 
 def down_fwd(h8, wd8, res, scale, wscale):
-    """y = bf16(res + bf16(h8 @ wd8^T / (s2 * q_d))), [T, D] bf16."""
-    _cuda_contig("h8", h8, E4M3, 2)
-    _cuda_contig("wd8", wd8, E4M3, 2)
+    """y = bf16(res + bf16(h8 @ wd8^T / (s2 * q_d))), [T, D] bf16; h8 is the
+    K-slab of [T, I], wd8 that of [D, I]."""
     _cuda_contig("res", res, torch.bfloat16, 2)
-    T, I = h8.shape
-    D = wd8.shape[0]
-    _need(wd8.shape == (D, I) and res.shape == (T, D), "shape mismatch in down_fwd")
+    T, D = res.shape
+    _need(h8.dim() == 3, "h8 must be a K-slab")
+    I = h8.shape[0] * SLAB
+    ldt = ldt_of(T)
+    _kslab("h8", h8, E4M3, ldt, I)
+    _kslab("wd8", wd8, E4M3, D, I)
     _need(I % 128 == 0, "I must be a multiple of 128")
     y = torch.empty(T, D, dtype=torch.bfloat16, device=h8.device)
     _lib.call("sfp8_gemm_down_fwd", h8.data_ptr(), wd8.data_ptr(), res.data_ptr(), T, D, I, scale.data_ptr(),
-              wscale.data_ptr(), y.data_ptr(), _lib.stream_of(h8))
+              wscale.data_ptr(), y.data_ptr(), ldt, _lib.stream_of(h8))
     return y
 
 
 def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
-    """(dgu8 [T, 2I] e5m2, dgu8t K-slab of 2I rows e5m2); amax[3] max-accumulated."""
+    """(dgu8 K-slab of [T, 2I] e5m2, dgu8t K-slab of [2I, ldt] e5m2); wdt is
+    the bf16 K-slab of W_down^T [I, D]; amax[3] max-accumulated."""
     _cuda_contig("dy", dy, torch.bfloat16, 2)
-    _cuda_contig("wdt", wdt, torch.bfloat16, 2)
     _cuda_contig("gu8", gu8, E4M3, 2)
     T, D = dy.shape
-    I = wdt.shape[0]
-    _need(wdt.shape == (I, D) and gu8.shape == (T, 2 * I), "shape mismatch in down_dgrad_swiglu")
-    _need(D % 64 == 0 and I % 16 == 0, "D must be a multiple of 64")
+    I = gu8.shape[1] // 2
+    _need(gu8.shape == (T, 2 * I), "shape mismatch in down_dgrad_swiglu")
+    _kslab("wdt", wdt, torch.bfloat16, I, D)
+    _need(D % 64 == 0 and I % 128 == 0, "D must be a multiple of 64 and I of 128")
     ldt = ldt_of(T)
-    dgu8 = torch.empty(T, 2 * I, dtype=E5M2, device=dy.device)
+    dgu8 = kslab_empty(ldt, 2 * I, E5M2, dy.device)
     dgu8t = slab_empty(2 * I, T, E5M2, dy.device)
     _lib.call("sfp8_gemm_down_dgrad_swiglu", dy.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), T, D, I,
               scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr(), ldt, _lib.stream_of(dy))
     return dgu8, dgu8t
 
 
-def gateup_dgrad(dgu8, w8t, scale, wscale):
-    """dxn = bf16(dgu8 @ w8 / (s3 * q_gu)), [T, D] bf16; w8t is W8^T [D, 2I]."""
-    _cuda_contig("dgu8", dgu8, E5M2, 2)
-    _cuda_contig("w8t", w8t, E4M3, 2)
-    T, I2 = dgu8.shape
-    D = w8t.shape[0]
-    _need(w8t.shape == (D, I2) and I2 % 128 == 0, "shape mismatch in gateup_dgrad")
+def gateup_dgrad(dgu8, w8t, scale, wscale, T: int, D: int):
+    """dxn = bf16(dgu8 @ w8 / (s3 * q_gu)), [T, D] bf16; dgu8 is the K-slab
+    of [T, 2I], w8t that of W8^T [D, 2I]."""
+    _need(dgu8.dim() == 3, "dgu8 must be a K-slab")
+    I2 = dgu8.shape[0] * SLAB
+    ldt = ldt_of(T)
+    _kslab("dgu8", dgu8, E5M2, ldt, I2)
+    _kslab("w8t", w8t, E4M3, D, I2)
+    _need(I2 % 128 == 0, "2I must be a multiple of 128")
     dxn = torch.empty(T, D, dtype=torch.bfloat16, device=dgu8.device)
     _lib.call("sfp8_gemm_gateup_dgrad", dgu8.data_ptr(), w8t.data_ptr(), T, D, I2 // 2, scale.data_ptr(),
-              wscale.data_ptr(), dxn.data_ptr(), _lib.stream_of(dgu8))
+              wscale.data_ptr(), dxn.data_ptr(), ldt, _lib.stream_of(dgu8))
     return dxn
 
 

@@ -33,6 +33,11 @@ def code_dist(a, b):
     return (ordinal(u8(a)) - ordinal(u8(b))).abs()
 
 
+def slab(x, dev):
+    """K-slab device copy of a plain [R, K] operand (zero padding rows)."""
+    return sg.ops.to_slab(x.contiguous()).to(dev)
+
+
 def int_fp8(shape, dtype, g, lo=-8, hi=8):
     return torch.randint(lo, hi + 1, shape, generator=g).float().to(dtype)
 
@@ -52,12 +57,15 @@ def test_swiglu_fwd_integer_operands(dev, T, D, I):
     s = torch.tensor([0.5, 2.0 ** -6, 4.0, 1, 1])
     ws = torch.tensor([2.0 ** -3, 1.0])
     amax = torch.zeros(5, device=dev)
-    gu8, h8, h8t = sg.ops.gateup_swiglu_fwd(x8.to(dev), w8.to(dev), s.to(dev), ws.to(dev), amax, I)
+    gu8, h8s, h8t = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
     rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8, w8, s, ws, I)
     assert torch.equal(u8(gu8), u8(rgu8))
+    ldt = sg.ops.ldt_of(T)
+    assert h8s.shape == (I // 64, ldt, 64)
+    h8 = sg.ops.unslab(h8s, T)
+    assert torch.all(u8(sg.ops.unslab(h8s, ldt))[T:] == 0)
     assert int(code_dist(h8, rh8).max()) <= 1
     assert float((code_dist(h8, rh8) > 0).float().mean()) < 0.01
-    ldt = sg.ops.ldt_of(T)
     assert h8t.shape == (ldt // 64, sg.ops.slab_rows(I), 64)
     ht = u8(sg.ops.unslab(h8t, I))
     assert torch.equal(ht[:, :T], u8(h8).t())
@@ -76,7 +84,8 @@ def test_swiglu_fwd_random(dev, T, D, I):
     w8, q = O.quantize_weight(torch.randn(2 * I, D, generator=g) * D ** -0.5)
     ws = torch.stack([q, torch.tensor(1.0)])
     amax = torch.zeros(5, device=dev)
-    gu8, h8, _ = sg.ops.gateup_swiglu_fwd(x8.to(dev), w8.to(dev), s.to(dev), ws.to(dev), amax, I)
+    gu8, h8s, _ = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
+    h8 = sg.ops.unslab(h8s, T)
     rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8, w8, s, ws, I)
     for got, ref in ((gu8, rgu8), (h8, rh8)):
         d = code_dist(got, ref)
@@ -98,7 +107,7 @@ def test_down_fwd_integer_operands(dev, T, D, I):
     res = torch.randn(T, D, generator=g).to(torch.bfloat16)
     s = torch.tensor([1, 1, 2.0 ** 4, 1, 1])
     ws = torch.tensor([1.0, 2.0 ** 3])
-    y = sg.ops.down_fwd(h8.to(dev), wd8.to(dev), res.to(dev), s.to(dev), ws.to(dev))
+    y = sg.ops.down_fwd(slab(h8, dev), slab(wd8, dev), res.to(dev), s.to(dev), ws.to(dev))
     ry = O.down_fwd(h8, wd8, res, s, ws)
     assert torch.equal(y.cpu(), ry)
 
@@ -111,7 +120,9 @@ def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     gu8 = O.e4m3(torch.randn(T, 2 * I, generator=g) * 64)
     s = torch.tensor([1, 64.0, 1, 2.0 ** -12, 1])
     amax = torch.zeros(5, device=dev)
-    dgu8, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), wd.t().contiguous().to(dev), gu8.to(dev), s.to(dev), amax)
+    dgu8s, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), gu8.to(dev), s.to(dev), amax)
+    dgu8 = sg.ops.unslab(dgu8s, T)
+    assert torch.all(u8(sg.ops.unslab(dgu8s, sg.ops.ldt_of(T)))[T:] == 0)
     rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     d = code_dist(dgu8, rdgu8)
     assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.01
@@ -137,7 +148,8 @@ def test_down_dgrad_swiglu_every_gate_code(dev):
     gu8 = torch.cat([gate, up], dim=1).view(E4)
     s = torch.tensor([1, 64.0, 1, 2.0 ** -6, 1])
     amax = torch.zeros(5, device=dev)
-    dgu8, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), wd.t().contiguous().to(dev), gu8.to(dev), s.to(dev), amax)
+    dgu8s, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), gu8.to(dev), s.to(dev), amax)
+    dgu8 = sg.ops.unslab(dgu8s, T)
     rdgu8, _, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     nan = torch.isnan(rdgu8.float())
     assert int(nan.sum()) > 0
@@ -157,7 +169,8 @@ def test_down_dgrad_swiglu_random(dev, T, D, I):
     gu8 = O.e4m3(torch.randn(T, 2 * I, generator=g) * 64)
     s = torch.tensor([1, 64.0, 1, 2.0 ** 18, 1])
     amax = torch.zeros(5, device=dev)
-    dgu8, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), wd.t().contiguous().to(dev), gu8.to(dev), s.to(dev), amax)
+    dgu8s, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), gu8.to(dev), s.to(dev), amax)
+    dgu8 = sg.ops.unslab(dgu8s, T)
     rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     d = code_dist(dgu8, rdgu8)
     assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.02
@@ -171,7 +184,7 @@ def test_gateup_dgrad_integer_operands(dev, T, D, I):
     w8 = int_fp8((2 * I, D), E4, g)
     s = torch.tensor([1, 1, 1, 2.0 ** 5, 1])
     ws = torch.tensor([2.0 ** 2, 1.0])
-    dxn = sg.ops.gateup_dgrad(dgu8.to(dev), w8.t().contiguous().to(dev), s.to(dev), ws.to(dev))
+    dxn = sg.ops.gateup_dgrad(slab(dgu8, dev), slab(w8.t(), dev), s.to(dev), ws.to(dev), T, D)
     rdxn = O.gateup_dgrad(dgu8, w8, s, ws)
     assert torch.equal(dxn.cpu(), rdxn)
 

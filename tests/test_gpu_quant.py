@@ -139,24 +139,43 @@ def test_update_scales_bit_exact(dev):
 
 
 @pytest.mark.parametrize("R,C,std", [(768, 256, 0.05), (6144, 1024, 1 / 32), (1024, 3072, 1e-4),
-                                     (130, 132, 3.0)])
+                                     (192, 320, 3.0)])
 def test_weight_quant_bit_exact(dev, R, C, std):
+    """The three K-slab copies (W8, W8^T, bf16 W^T) against the reference
+    recipe, padding rows (to multiples of 256) zero."""
     g = torch.Generator().manual_seed(R + C)
     w = torch.randn(R, C, generator=g) * std
     q = torch.empty(1, device=dev)
     w8, w8t, wbt = sg.ops.weight_quant(w.to(dev), q, w8=True, w8t=True, bf16t=True)
     r8, rq = O.quantize_weight(w)
     assert q.item() == rq.item()
-    assert torch.equal(u8(w8), u8(r8))
-    assert torch.equal(u8(w8t), u8(r8).t())
-    assert torch.equal(wbt.cpu(), w.to(torch.bfloat16).t())
+    assert w8.shape == (C // 64, sg.ops.slab_rows(R), 64)
+    assert torch.equal(u8(sg.ops.unslab(w8, R)), u8(r8))
+    assert torch.equal(u8(sg.ops.unslab(w8t, C)), u8(r8).t())
+    assert torch.equal(sg.ops.unslab(wbt, C).cpu(), w.to(torch.bfloat16).t())
+    for t in (w8, w8t, wbt):
+        rows = R if t is w8 else C
+        assert torch.all(t.view(torch.uint8)[:, rows:].cpu() == 0)
+
+
+def test_weight_quant_ragged_rows(dev):
+    """130 rows (not a multiple of 64): W8 only, padding rows 130..255 zero."""
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(130, 128, generator=g)
+    q = torch.empty(1, device=dev)
+    w8, _, _ = sg.ops.weight_quant(w.to(dev), q, w8=True)
+    r8, rq = O.quantize_weight(w)
+    assert q.item() == rq.item()
+    assert torch.equal(u8(sg.ops.unslab(w8, 130)), u8(r8))
+    assert torch.all(w8.view(torch.uint8)[:, 130:].cpu() == 0)
 
 
 def test_weight_scale_band(dev):
     """Weights whose amax puts 448/amax in the log2 rounding band."""
     amaxes = [a for a in _band_amax(448.0) if np.isfinite(a) and a > 0][:200]
     for a in amaxes[::7]:
-        w = torch.tensor([[a, -a / 3, 0.1 * a, 0.0]], dtype=torch.float32)
+        w = torch.zeros(1, 64)
+        w[0, :3] = torch.tensor([a, -a / 3, 0.1 * a], dtype=torch.float32)
         q = torch.empty(1, device=dev)
         sg.ops.weight_quant(w.to(dev), q, w8=True)
         _, rq = O.quantize_weight(w)
