@@ -222,5 +222,5 @@ def fp32_reference(h, norm_w, w_gu, w_down, probe, eps=1e-6):
 
 
 def rel_l2(a: torch.Tensor, r: torch.Tensor) -> float:
-    a, r = a.double(), r.double()
+    a, r = a.detach().double(), r.detach().double()
     return float((a - r).norm() / r.norm().clamp(min=1e-300))

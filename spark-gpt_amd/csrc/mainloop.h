@@ -38,6 +38,7 @@ constexpr int kStage = 64;                   // bytes of K per stage
 constexpr int kStages = 4;                   // LDS ring depth (>= 3)
 constexpr int kStageA = kTile * kStage;      // 16 KiB
 constexpr int kMainLds = 2 * kStages * kStageA;  // 128 KiB: the 256 x 256 tile's ring
+constexpr bool kDmaFirst = false;  // stage order: DMA issues before the fragment reads
 constexpr int kFmtE4M3 = 0;
 constexpr int kFmtE5M2 = 1;
 
@@ -250,16 +251,27 @@ struct MainLoop {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (STAGES - 3)) : "memory");
     __builtin_amdgcn_sched_barrier(0);
     const int sa = ld * a_sstride, sb = ld * b_sstride;
-    mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-    mfma_then_reads<P + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-    mfma_then_reads<P + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-    if constexpr (NB == 4) mfma_then_reads<P + 3, 6, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-    constexpr int Q = P + (4 + NB) / 2;
-    mfma_then_dma<Q + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-    mfma_then_dma<Q + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-    mfma_then_dma<Q + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-    if constexpr (NB == 4) mfma_then_dma<Q + 3, 6, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-    mfma_range<Q + (4 + NB) / 2, kMfma>(cur, acc);
+    constexpr int H = (4 + NB) / 2;  // MFMAs carrying reads (and DMA issues)
+    if constexpr (kDmaFirst) {
+      mfma_then_dma<P + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_dma<P + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_dma<P + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      if constexpr (NB == 4) mfma_then_dma<P + 3, 6, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + H + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + H + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + H + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      if constexpr (NB == 4) mfma_then_reads<P + H + 3, 6, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    } else {
+      mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      if constexpr (NB == 4) mfma_then_reads<P + 3, 6, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + H + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_dma<P + H + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_dma<P + H + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      if constexpr (NB == 4) mfma_then_dma<P + H + 3, 6, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    }
+    mfma_range<P + 2 * H, kMfma>(cur, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 

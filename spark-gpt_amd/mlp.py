@@ -22,6 +22,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
+from . import torch_ops  # noqa: F401  (registers the sparkfp8:: operators)
 
 FP8_MLP = False  # set True to route dense MLP sub-blocks through _FP8MLPBlock while training
 
@@ -71,13 +72,6 @@ class MLP(nn.Module):
         return self.down_proj(F.silu(gate) * up)
 
 
-def _master(w: torch.Tensor) -> torch.Tensor:
-    w = w.detach()
-    if w.dtype != torch.float32:
-        w = w.float()
-    return w.contiguous()
-
-
 class _FP8MLPBlock(torch.autograd.Function):
     """y = h + down(SwiGLU(gate_up(rmsnorm(h)))) with fp8 activations.
 
@@ -85,40 +79,26 @@ class _FP8MLPBlock(torch.autograd.Function):
     epilogue -> down FP8 GEMM with residual epilogue.
     Backward: bf16 down dgrad with SwiGLU-backward epilogue (d_gu e5m2) ->
     gate/up FP8 dgrad -> RMSNorm backward (+ e5m2 dy^T) -> the two FP8 weight
-    gradients reduced over tokens."""
+    gradients reduced over tokens.
+
+    The two halves run as the custom operators ``sparkfp8::block_fwd`` and
+    ``sparkfp8::block_bwd`` (torch_ops.py), so a ``torch.compile``d model
+    (train.py:3787) traces them as two opaque nodes."""
 
     @staticmethod
     def forward(ctx, h, norm_w, w_gu, w_down, scale, amax, eps):
-        I = w_down.shape[1]
-        h = h.contiguous()
-        nw = _master(norm_w)
-        x8, x8t, rstd = ops.norm_quant(h, nw, scale, amax, eps)
-        wscale = torch.empty(2, dtype=torch.float32, device=h.device)
-        w8, w8t, _ = ops.weight_quant(_master(w_gu), wscale[0:1], w8=True, w8t=True)
-        wd8, _, wdt = ops.weight_quant(_master(w_down), wscale[1:2], w8=True, bf16t=True)
-        gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, h.shape[0], I)
-        y = ops.down_fwd(h8, wd8, h, scale, wscale)
+        y, wdt, x8t, rstd, w8t, wscale, gu8, h8t = torch.ops.sparkfp8.block_fwd(
+            h, norm_w, w_gu, w_down, scale, amax, eps)
         # backward needs the token-contiguous x8t / h8t (weight grads), gu8
         # (SwiGLU backward), W8^T (gate/up dgrad) and bf16 Wd^T (down dgrad)
-        ctx.save_for_backward(h, nw, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax)
+        ctx.save_for_backward(h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        h, nw, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax = ctx.saved_tensors
-        dy = dy.contiguous()
-        if dy.dtype != torch.bfloat16:
-            dy = dy.to(torch.bfloat16)
-        D = h.shape[1]
-        I = gu8.shape[1] // 2
-        dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
-        dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, h.shape[0], D)
-        del dgu8
-        dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nw, scale, amax)
-        del dxn
-        dwd = ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3])
-        dwgu = ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1])
-        assert dwd.shape == (D, I) and dwgu.shape == (2 * I, D)
+        h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax = ctx.saved_tensors
+        dh, dnw, dwgu, dwd = torch.ops.sparkfp8.block_bwd(dy, h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t,
+                                                          scale, amax)
         return dh, dnw, dwgu, dwd, None, None, None
 
 

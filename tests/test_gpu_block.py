@@ -118,3 +118,59 @@ def test_block_deterministic(dev):
     for x, y in zip(a, b):
         assert torch.equal(x, y)
     assert torch.equal(amax_a, mlp.fp8_amax)
+
+
+def test_custom_ops_opcheck(dev):
+    """Fake implementations of the two operators against real runs (shapes,
+    dtypes, strides).  opcheck's schema test perturbs tensors arithmetically,
+    which torch does not implement for float8 device tensors, so it is not
+    run; the mutation of amax is covered by the compile test below."""
+    T, D, I = 300, 256, 384
+    norm, mlp = _setup(dev, T, D, I, 21)
+    h = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    dy = (torch.randn(T, D, device=dev) * 1e-3).to(torch.bfloat16)
+    args = (h, norm.weight.detach(), mlp.gate_up_proj.weight.detach(), mlp.down_proj.weight.detach(),
+            mlp.fp8_scale, mlp.fp8_amax, norm.eps)
+    utils = ("test_faketensor",)
+    torch.library.opcheck(torch.ops.sparkfp8.block_fwd.default, args, test_utils=utils)
+    out = torch.ops.sparkfp8.block_fwd(*args)
+    bargs = (dy, h, norm.weight.detach()) + tuple(out[1:]) + (mlp.fp8_scale, mlp.fp8_amax)
+    torch.library.opcheck(torch.ops.sparkfp8.block_bwd.default, bargs, test_utils=utils)
+
+
+class _Block(nn.Module):
+    def __init__(self, norm, mlp):
+        super().__init__()
+        self.norm, self.mlp = norm, mlp
+
+    def forward(self, h):
+        return sg.fp8_mlp_block(h, self.norm, self.mlp)
+
+
+def test_compiled_block_matches_eager(dev):
+    """torch.compile (train.py:3787) traces the block as the two custom
+    operators: no graph break, and the same bytes as eager for y, every
+    gradient and the amax slots."""
+    T, D, I = 300, 256, 384
+    norm, mlp = _setup(dev, T, D, I, 22)
+    blk = _Block(norm, mlp)
+    h = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    dy = (torch.randn(T, D, device=dev) * 1e-3).to(torch.bfloat16)
+    mlp.fp8_scale.copy_(torch.tensor([16.0, 2.0 ** -6, 64.0, 2.0 ** 10, 2.0 ** 15], device=dev))
+
+    def run(m):
+        mlp.fp8_amax.zero_()
+        for p in blk.parameters():
+            p.grad = None
+        x = h.clone().requires_grad_(True)
+        y = m(x)
+        y.backward(dy)
+        return [y.detach(), x.grad] + [p.grad.clone() for p in blk.parameters()] + [mlp.fp8_amax.clone()]
+
+    ref = run(blk)
+    explain = torch._dynamo.explain(blk)(h.clone().requires_grad_(True))
+    assert explain.graph_break_count == 0, explain.break_reasons
+    torch._dynamo.reset()
+    got = run(torch.compile(blk, backend="aot_eager", dynamic=False))
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)

@@ -176,3 +176,32 @@ def test_update_scales_walks_every_fp8_module(monkeypatch):
     model = nn.Sequential(sg.MLP(128, 256), nn.Linear(4, 4), nn.Sequential(sg.MLP(128, 256)))
     sg.fp8_update_scales(model)
     assert len(seen) == 2
+
+
+def test_custom_op_fake_shapes_match_allocations():
+    """The fake (shape-only) implementations used under torch.compile return
+    the shapes and dtypes the real wrappers allocate (checked with fake CUDA
+    tensors: no GPU needed)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    T, D, I = 300, 256, 384
+    with FakeTensorMode():
+        dev = "cuda"
+        h = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+        nw, wgu, wd = torch.empty(D, device=dev), torch.empty(2 * I, D, device=dev), torch.empty(D, I, device=dev)
+        s, a = torch.empty(5, device=dev), torch.empty(5, device=dev)
+        out = torch.ops.sparkfp8.block_fwd(h, nw, wgu, wd, s, a, 1e-6)
+        grads = torch.ops.sparkfp8.block_bwd(torch.empty(T, D, dtype=torch.bfloat16, device=dev), h, nw,
+                                             *out[1:], s, a)
+    meta = "meta"
+    want = [torch.empty(T, D, dtype=torch.bfloat16, device=meta),
+            ops.kslab_empty(I, D, torch.bfloat16, meta),
+            ops.slab_empty(D, T, ops.E4M3, meta),
+            torch.empty(T, device=meta),
+            ops.kslab_empty(D, 2 * I, ops.E4M3, meta),
+            torch.empty(2, device=meta),
+            torch.empty(T, 2 * I, dtype=ops.E4M3, device=meta),
+            ops.slab_empty(I, T, ops.E4M3, meta)]
+    for got, w in zip(out, want):
+        assert got.shape == w.shape and got.dtype == w.dtype
+    assert [tuple(g.shape) for g in grads] == [(T, D), (D,), (2 * I, D), (D, I)]
+    assert [g.dtype for g in grads] == [torch.bfloat16] + [torch.float32] * 3
