@@ -653,6 +653,19 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
   const int wm = wave & 1, wn = wave >> 1;
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
+  // every residual word of this lane is requested at once (one memory
+  // latency for the epilogue); rows past T read as zero through the
+  // descriptor's range check and are not stored
+  const __amdgpu_buffer_rsrc_t rres = make_rsrc(res + m0 * D, (T - m0) * D * 2);
+  intx4 rv[4][4][2];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const uint32_t off = (uint32_t)(((128 * wm + 32 * tb + fr) * D + n0 + cb + 16 * nb) * 2);
+      rv[tb][nb][0] = __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0);
+      rv[tb][nb][1] = __builtin_amdgcn_raw_buffer_load_b128(rres, off + 16, 0, 0);
+    }
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int64_t t = m0 + 128 * wm + 32 * tb + fr;
@@ -664,9 +677,8 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
       float o[16];
       // out rounded to bf16 before the residual add (train.py:1043)
       round16_bf16(acc[tb][nb], deq, o);
-      const uint16_t* rp = res + t * D + n;
-      const intx4 r0 = *reinterpret_cast<const intx4*>(rp);
-      const intx4 r1 = *reinterpret_cast<const intx4*>(rp + 8);
+      const intx4 r0 = rv[tb][nb][0];
+      const intx4 r1 = rv[tb][nb][1];
       uint32_t w0[4], w1[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
