@@ -95,8 +95,9 @@ int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
 /* gate/up forward + SwiGLU epilogue, replaces _fp8_swiglu_fwd_kernel
  * (train.py:975-1016, launched at train.py:1216-1218).
  * x8 (K-slab of [T, D]) e4m3, w8 (K-slab of [2I, D], gate rows first) e4m3
- * -> gu8 [T, 2I] e4m3 row-major, h8 (K-slab of [T, I]) e4m3, h8t (K-slab of
- * [I, ldt]: token-contiguous copy of h8 for the down wgrad) e4m3;
+ * -> gu8 (K-slab of [T, 2I], gate columns first, rpad = ldt) e4m3, h8
+ * (K-slab of [T, I]) e4m3, h8t (K-slab of [I, ldt]: token-contiguous copy
+ * of h8 for the down wgrad) e4m3; rows T..ldt of gu8 and h8 are zeros;
  * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0. */
 int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
@@ -111,8 +112,9 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
 
 /* bf16 down dgrad + SwiGLU backward, replaces _fp8_down_dgrad_swiglu_kernel
  * (train.py:1049-1094, launched at train.py:1236-1238).  dy [T, D] bf16
- * row-major, wdt (K-slab of w_down^T [I, D], bf16) , gu8 [T, 2I] e4m3
- * row-major -> dgu8 (K-slab of [T, 2I]) e5m2, dgu8t (K-slab of [2I, ldt])
+ * row-major, wdt (K-slab of w_down^T [I, D], bf16), gu8 (K-slab of [T, 2I],
+ * rpad = ldt, as the forward wrote it) e4m3 -> dgu8 (K-slab of [T, 2I]) e5m2,
+ * dgu8t (K-slab of [2I, ldt])
  * e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is recorded by
  * sfp8_norm_bwd.)  D % 64 == 0, I % 128 == 0. */
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,

@@ -157,6 +157,12 @@ SFP8_DEV uint32_t pack4_e5m2_scaled_noclamp(float a, float b, float c, float d, 
   return __builtin_bit_cast(uint32_t, o);
 }
 
+SFP8_DEV uint32_t pack4_e4m3_scaled_noclamp(float a, float b, float c, float d, float inv_m, uint32_t any) {
+  shortx2 o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(__builtin_bit_cast(shortx2, any), a, b, inv_m, false);
+  o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, c, d, inv_m, true);
+  return __builtin_bit_cast(uint32_t, o);
+}
+
 // max(a, b, c) that returns NaN when any input is NaN (v_maximum3_f32).
 SFP8_DEV float max3_nan(float a, float b, float c) {
   return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
@@ -303,6 +309,32 @@ SFP8_DEV void lds_tile_store_slab(const uint8_t* lds, int ntok, int ncols, int s
     for (int c = 0; c < 4; ++c)
       *reinterpret_cast<intx4*>(base + c * 64) =
           intx4{(int)t4[c][0], (int)t4[c][1], (int)t4[c][2], (int)t4[c][3]};
+  }
+}
+
+// The same for a 256-token LDS tile of NC16 * 16 columns (row stride
+// `stride` bytes) through transposing LDS reads:
+//   out(c0 + c, t0 + t) = tile[t][c]  for t < 256, c < NC16 * 16.
+// Every tile row is copied (callers keep zero codes in rows past the last
+// token); t0 % 64 == 0.  The 16-lane group q of a wave turns a 16 x 16 byte
+// block into 16 column runs of 16 tokens (two ds_read_b64_tr_b8), and the
+// four groups take consecutive 16-token blocks, so each wave store covers 16
+// whole 64-byte slab rows.  Work unit u (64-token block u % 4, 16-column
+// block u / 4) goes to wave u % 4.
+template <int NC16>
+SFP8_DEV void lds_tile_store_slab_tr(const uint8_t* lds, int stride, uint8_t* out, int64_t rpad, int64_t t0,
+                                     int64_t c0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, li = lane & 15;
+#pragma unroll 4
+  for (int p = 0; p < NC16; ++p) {
+    const int u = p * 4 + wave;
+    const int r = 64 * (u & 3) + 16 * q, c = 16 * (u >> 2);
+    const uint8_t* src = lds + (r + (li >> 1)) * stride + c + 8 * (li & 1);
+    const intx2 a = lds_read_tr8(src);
+    const intx2 b = lds_read_tr8(src + 8 * stride);
+    const int64_t t = t0 + r;
+    *reinterpret_cast<intx4*>(out + (t >> 6) * rpad * 64 + (c0 + c + li) * 64 + (t & 63)) =
+        intx4{a[0], a[1], b[0], b[1]};
   }
 }
 

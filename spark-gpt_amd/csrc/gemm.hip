@@ -88,21 +88,6 @@ SFP8_DEV int paired_col(int r) {
   return (r & 64) + 32 * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
 }
 
-// Coalesced copy of an LDS tile to a row-major global matrix: nrows rows of
-// (16 << cpr_log2) bytes, LDS row stride `stride`, global row r at
-// dst + r * ld; rows >= rows_valid are skipped.  Consecutive threads take
-// consecutive 16-byte chunks, so a wave store covers whole rows.
-SFP8_DEV void lds_rows_to_global(const uint8_t* lds, int nrows, int cpr_log2, int stride, uint8_t* dst,
-                                 int64_t ld, int rows_valid) {
-  const int total = nrows << cpr_log2;
-  const int cmask = (1 << cpr_log2) - 1;
-  for (int idx = threadIdx.x; idx < total; idx += 256) {
-    const int r = idx >> cpr_log2, c = idx & cmask;
-    if (r < rows_valid)
-      *reinterpret_cast<intx4*>(dst + r * ld + c * 16) = *reinterpret_cast<const intx4*>(lds + r * stride + c * 16);
-  }
-}
-
 // Copy of an LDS tile (nrows rows of 64 * NP bytes, LDS row stride `stride`)
 // into a K-slab matrix: 64-byte column block p of tile row r goes to
 // dst + (c0 / 64 + p) * ldrows * 64 + (r0 + r) * 64.  Sixteen consecutive
@@ -230,14 +215,12 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   m_gu *= deq;
   m_h *= deq * deq;
   __syncthreads();
-  // whole 128-byte rows of the gate and up halves of gu8, then h8 as two
-  // 64-column K-slab blocks (every tile row: rows past T are zero padding)
-  // and the token-contiguous h8t
-  const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
-  lds_rows_to_global(Gt, kTile, 3, kEpiStride, gu8 + m0 * 2 * I + n0, 2 * I, rows_valid);
-  lds_rows_to_global(Ut, kTile, 3, kEpiStride, gu8 + m0 * 2 * I + I + n0, 2 * I, rows_valid);
+  // gu8 (gate and up halves) and h8 as 64-column K-slab blocks (every tile
+  // row: rows past T are zero padding), then the token-contiguous h8t
+  lds_rows_to_kslab<2>(Gt, kTile, kEpiStride, gu8, ldt, m0, n0);
+  lds_rows_to_kslab<2>(Ut, kTile, kEpiStride, gu8, ldt, m0, I + n0);
   lds_rows_to_kslab<2>(Ht, kTile, kEpiStride, h8, ldt, m0, n0);
-  lds_tile_store_slab<256>(Ht, kTile, 128, kEpiStride, h8t, slab_rows(I), m0, n0, rows_valid);
+  lds_tile_store_slab_tr<8>(Ht, kEpiStride, h8t, slab_rows(I), m0, n0);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
   if (lane == 0) { red[wave] = m_gu; red[4 + wave] = m_h; }
@@ -296,7 +279,7 @@ struct SwigluPipe {
     // previous tile's epilogue
     uint32_t E[4][16];
     uint32_t gw[4], uw[4], hw[4];
-    bool nan;
+    bool bad;  // a unit of the current row block saw NaN or out-of-range data
     float m_gu, m_h;
     bool prev;            // a previous tile exists
     int64_t pm0, pn0;     // its origin
@@ -320,23 +303,33 @@ struct SwigluPipe {
       ub[e] = __uint_as_float(p & 0xffff0000u);
       const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c.c_exp));
       hb[e] = gb[e] * sg * ub[e];
-      c.nan |= hb[e] != hb[e];  // a NaN g or u always reaches h
     }
-    c.m_gu = fmaxf(c.m_gu, fmaxf(fmaxf(fabsf(gb[0]), fabsf(ub[0])), fmaxf(fabsf(gb[1]), fabsf(ub[1]))));
-    c.m_gu = fmaxf(c.m_gu, fmaxf(fmaxf(fabsf(gb[2]), fabsf(ub[2])), fmaxf(fabsf(gb[3]), fabsf(ub[3]))));
-    c.m_h = fmaxf(c.m_h, fmaxf(fmaxf(fabsf(hb[0]), fabsf(hb[1])), fmaxf(fabsf(hb[2]), fabsf(hb[3]))));
-    c.gw[Q] = pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], c.inv1, c.bnd1);
-    c.uw[Q] = pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], c.inv1, c.bnd1);
-    c.hw[Q] = pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], c.inv2, c.bnd2);
+    // NaN-propagating maxima of the magnitudes: when both are inside the
+    // e4m3 range (after scaling) no clamp can act and no NaN needs patching,
+    // so the unclamped conversions are exact; otherwise the row block's
+    // block_store redoes them (wave-uniform, rare)
+    float a = max3_nan(fabsf(gb[0]), fabsf(ub[0]), fabsf(gb[1]));
+    a = max3_nan(a, fabsf(ub[1]), fabsf(gb[2]));
+    a = max3_nan(a, fabsf(ub[2]), fabsf(gb[3]));
+    a = __builtin_elementwise_maximum(a, fabsf(ub[3]));
+    float b = max3_nan(fabsf(hb[0]), fabsf(hb[1]), fabsf(hb[2]));
+    b = __builtin_elementwise_maximum(b, fabsf(hb[3]));
+    c.bad |= !(a <= c.bnd1) | !(b <= c.bnd2);
+    c.m_gu = fmaxf(c.m_gu, a);  // a NaN here is redone by the exact path
+    c.m_h = fmaxf(c.m_h, b);
+    c.gw[Q] = pack4_e4m3_scaled_noclamp(gb[0], gb[1], gb[2], gb[3], c.inv1, c.gw[Q]);
+    c.uw[Q] = pack4_e4m3_scaled_noclamp(ub[0], ub[1], ub[2], ub[3], c.inv1, c.uw[Q]);
+    c.hw[Q] = pack4_e4m3_scaled_noclamp(hb[0], hb[1], hb[2], hb[3], c.inv2, c.hw[Q]);
   }
 
-  // After the last unit of row block TB: NaN patch (wave-uniform, rare), the
+  // After the last unit of row block TB: the exact conversions when a unit
+  // of the block saw NaN or out-of-range data (wave-uniform, rare), the
   // three 16-byte global stores and the h bytes into the LDS tile.
   template <int TB>
   static SFP8_DEV void block_store(Ctx& c) {
     const int lane = threadIdx.x & 63, wm = c.wave & 1, wn = c.wave >> 1;
     const int fr = lane & 31, g = lane >> 5;
-    if (__builtin_amdgcn_ballot_w64(c.nan)) {
+    if (__builtin_amdgcn_ballot_w64(c.bad)) {
       asm volatile("" ::: "memory");
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -348,24 +341,25 @@ struct SwigluPipe {
           ub[e] = __uint_as_float(p & 0xffff0000u);
           const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c.c_exp));
           hb[e] = gb[e] * sg * ub[e];
+          // amax over the non-NaN values
+          c.m_gu = fmaxf(c.m_gu, fmaxf(fabsf(gb[e]), fabsf(ub[e])));
+          c.m_h = fmaxf(c.m_h, fabsf(hb[e]));
         }
-        c.gw[q] = fix_nan4(c.gw[q], gb[0], gb[1], gb[2], gb[3]);
-        c.uw[q] = fix_nan4(c.uw[q], ub[0], ub[1], ub[2], ub[3]);
-        c.hw[q] = fix_nan4(c.hw[q], hb[0], hb[1], hb[2], hb[3]);
+        c.gw[q] = fix_nan4(pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], c.inv1, c.bnd1), gb[0], gb[1], gb[2], gb[3]);
+        c.uw[q] = fix_nan4(pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], c.inv1, c.bnd1), ub[0], ub[1], ub[2], ub[3]);
+        c.hw[q] = fix_nan4(pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], c.inv2, c.bnd2), hb[0], hb[1], hb[2], hb[3]);
       }
     }
-    c.nan = false;
+    c.bad = false;
     const int row = 128 * wm + 32 * TB + fr;
     const int col = 32 * wn + 16 * g;
     const int64_t t = c.pm0 + row;
     if (c.prev) {
-      if (t < c.T) {
-        uint8_t* gp = c.gu8 + t * 2 * c.I + c.pn0 + col;
-        store16(gp, c.gw);
-        store16(gp + c.I, c.uw);
-      }
-      // h8 is a K-slab [I/64][ldt][64]: the tile's 64 columns are one block
-      // (rows past T hold the zeros computed from x8's zero padding)
+      // gu8 is a K-slab [2I/64][ldt][64], h8 one of [I/64][ldt][64]: the
+      // tile's 64 gate, 64 up and 64 h columns are one block each (rows past
+      // T hold the zeros computed from x8's zero padding)
+      store16(c.gu8 + (c.pn0 >> 6) * c.ldt * 64 + t * 64 + col, c.gw);
+      store16(c.gu8 + ((c.I + c.pn0) >> 6) * c.ldt * 64 + t * 64 + col, c.uw);
       store16(c.h8 + (c.pn0 >> 6) * c.ldt * 64 + t * 64 + col, c.hw);
     }
     store16(c.hbuf + row * kPipeHStride + col, c.hw);
@@ -381,11 +375,14 @@ struct SwigluPipe {
     constexpr int cur = KT & 1, nxt = cur ^ 1;
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (kSt - 3)) : "memory");
     __builtin_amdgcn_sched_barrier(0);
+    // the fences come before the stage's memory operations: an asm statement
+    // with side effects stays ordered after every load issued before it, and
+    // the units' arithmetic after the fences
+    fences<ubeg(KT), ubeg(KT + 1)>(c);
     constexpr int ld = KT + kSt - 1 < NK - 1 ? KT + kSt - 1 : NK - 1;
     ML::load_stage(c.lds, (KT + kSt - 1) % kSt, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
     ML::read_frags(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
     ML::template mfma_range<0, ML::kMfma>(c.f[cur], c.acc);
-    fences<ubeg(KT), ubeg(KT + 1)>(c);
     units<ubeg(KT), ubeg(KT + 1)>(c);
     // 8 MFMAs, 12 LDS reads, 6 DMAs, the units' vector ALU work spread
     // after every MFMA (about 90 instructions per unit)
@@ -450,24 +447,6 @@ struct SwigluPipe {
   }
 };
 
-// Token-contiguous (K-slab) copy of a finished LDS h tile (256 tokens x 64
-// features): 16-lane group q of wave w turns a 16 x 16 byte block into 16
-// feature runs of 16 tokens; a wave's stores are 16 whole 64-byte slab rows.
-SFP8_DEV void pipe_h_slab(const uint8_t* hb, int64_t pm0, int64_t pn0, uint8_t* h8t, int64_t rpad) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, li = lane & 15;
-  const int cb = 16 * wave;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int rb = 16 * (4 * p + q);
-    const uint8_t* src = hb + (rb + (li >> 1)) * kPipeHStride + cb + 8 * (li & 1);
-    const intx2 t0 = lds_read_tr8(src);
-    const intx2 t1 = lds_read_tr8(src + 8 * kPipeHStride);
-    const int64_t t = pm0 + rb;
-    *reinterpret_cast<intx4*>(h8t + (t >> 6) * rpad * 64 + (pn0 + cb + li) * 64 + (t & 63)) =
-        intx4{t0[0], t0[1], t1[0], t1[1]};
-  }
-}
-
 template <int NK>
 __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
@@ -495,7 +474,9 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   c.h8 = h8;
   c.m_gu = 0.f;
   c.m_h = 0.f;
-  c.nan = false;
+  c.bad = false;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) c.gw[q] = c.uw[q] = c.hw[q] = 0u;
   c.prev = false;
   c.pm0 = 0;
   c.pn0 = 0;
@@ -549,7 +530,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     P::template stages<0>(c, a_ss, b_ss);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     // the previous tile's h tile is complete: its K-slab copy
-    if (c.prev) pipe_h_slab(c.hbuf, c.pm0, c.pn0, h8t, rpad);
+    if (c.prev) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
     // this tile's g, u (bf16, unscaled) become the next epilogue's input
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
@@ -563,7 +544,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   if (c.prev) {
     P::template tail_units<0>(c);
     __syncthreads();
-    pipe_h_slab(c.hbuf, c.pm0, c.pn0, h8t, rpad);
+    lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
   }
   float* red = reinterpret_cast<float*>(lds + kPipeRing + 2 * kPipeHBytes);
   float mg = wave_max(c.m_gu * deq), mh = wave_max(c.m_h * (deq * deq));
@@ -697,7 +678,7 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
 // (a9) bf16 down dgrad + SwiGLU backward (spark-gpt train.py:1049-1094):
 //   dh = bf16(dy @ Wd); g, u = gu8 / s1; sig = sigmoid(g)
 //   d_gate = dh*u*(sig*(1+g*(1-sig))), d_up = dh*g*sig
-//   dgu8 = e5m2(d * s3) row-major and transposed (ldt), amax slot 3.
+//   dgu8 = e5m2(d * s3) as K-slabs of [T, 2I] and of [2I, ldt], amax slot 3.
 // B = Wd^T (bf16, [I, D]).  Tile 256 tokens x 256 intermediate columns.
 constexpr int kEpiStride2 = 272;
 constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 16;  // after Gt, Ut and the reduction slots
@@ -753,12 +734,13 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
       lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
       kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * kStage, ldb * ip - n0 * kStage,
       [=](int r) { return plain_col(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
-  // gu8 rows of this tile through a range-checked descriptor: rows past T
-  // read as zero (and their dh is zero: dy rows past T read as zero).  All
-  // 32 words of this lane are requested at once, so one memory latency covers
-  // the whole epilogue; blocks past column I get an out-of-range offset and
-  // read zeros (g = u = 0 gives zero gradients, and nothing there is stored).
-  const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 2 * I, (T - m0) * 2 * I);
+  // gu8 is a K-slab [2I/64][ldt][64]: each lane's 64 gate (and 64 up)
+  // columns of a row are one 64-byte slab row.  Rows past T hold zeros (and
+  // their dh is zero: dy rows past T read as zero).  All 32 words of this
+  // lane are requested at once, so one memory latency covers the whole
+  // epilogue; blocks past column I get an out-of-range offset and read zeros
+  // (g = u = 0 gives zero gradients, and nothing there is stored).
+  const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 64, 2 * I * ldt - m0 * 64);
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 128 * wn + 64 * g;
   intx4 wg[4][4], wu[4][4];
@@ -768,9 +750,9 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     for (int nb = 0; nb < 4; ++nb) {
       const int row = 128 * wm + 32 * tb + fr;
       const int64_t j = n0 + cb + 16 * nb;
-      const uint32_t jo = j < I ? (uint32_t)(row * 2 * I + j) : 0x80000000u;
+      const uint32_t jo = j < I ? (uint32_t)((j >> 6) * ldt * 64 + row * 64 + (j & 63)) : 0x80000000u;
       wg[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
-      wu[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)I, 0, 0);
+      wu[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)(I * ldt), 0, 0);
     }
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
@@ -822,7 +804,6 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     }
   }
   __syncthreads();
-  const int rows_valid = (int)((T - m0) < kTile ? (T - m0) : kTile);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
   // dgu8 is a K-slab [2I/64][ldt][64] (the gate/up dgrad's A operand): the
   // tile's gate and up columns are 64-column blocks of every tile row (rows
@@ -834,8 +815,14 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     lds_rows_to_kslab<2>(Gt, kTile, kEpiStride2, dgu8, ldt, m0, n0);
     lds_rows_to_kslab<2>(Ut, kTile, kEpiStride2, dgu8, ldt, m0, I + n0);
   }
-  lds_tile_store_slab<256>(Gt, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0, rows_valid);
-  lds_tile_store_slab<256>(Ut, kTile, cols, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0, rows_valid);
+  // the token-contiguous dgu8t (rows past T hold zero codes)
+  if (cols == kTile) {
+    lds_tile_store_slab_tr<16>(Gt, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0);
+    lds_tile_store_slab_tr<16>(Ut, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0);
+  } else {
+    lds_tile_store_slab_tr<8>(Gt, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0);
+    lds_tile_store_slab_tr<8>(Ut, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0);
+  }
   __syncthreads();  // the next tile's DMA overwrites the staging tiles
   }
   m3 *= s_gu;

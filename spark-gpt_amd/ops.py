@@ -151,7 +151,7 @@ def _kslab(name: str, t: torch.Tensor, dtype, R: int, L: int) -> None:
 
 
 def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T: int, I: int):
-    """(gu8 [T, 2I] row-major, h8 K-slab of [T, I], h8t K-slab of [I, ldt]);
+    """(gu8 K-slab of [T, 2I], h8 K-slab of [T, I], h8t K-slab of [I, ldt]);
     x8 is the K-slab of [T, D], w8 that of [2I, D]; amax[1], amax[2]
     max-accumulated."""
     _need(x8.dim() == 3, "x8 must be a K-slab")
@@ -161,7 +161,7 @@ def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T: int, I: int):
     _kslab("w8", w8, E4M3, 2 * I, D)
     _need(D % 128 == 0 and I % 128 == 0, "D and I must be multiples of 128")
     dev = x8.device
-    gu8 = torch.empty(T, 2 * I, dtype=E4M3, device=dev)
+    gu8 = kslab_empty(ldt, 2 * I, E4M3, dev)
     h8 = kslab_empty(ldt, I, E4M3, dev)
     h8t = slab_empty(I, T, E4M3, dev)
     _lib.call("sfp8_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), T, D, I, scale.data_ptr(),
@@ -189,15 +189,16 @@ def down_fwd(h8, wd8, res, scale, wscale):
 
 def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
     """(dgu8 K-slab of [T, 2I] e5m2, dgu8t K-slab of [2I, ldt] e5m2); wdt is
-    the bf16 K-slab of W_down^T [I, D]; amax[3] max-accumulated."""
+    the bf16 K-slab of W_down^T [I, D], gu8 the e4m3 K-slab of [T, 2I] the
+    forward wrote; amax[3] max-accumulated."""
     _cuda_contig("dy", dy, torch.bfloat16, 2)
-    _cuda_contig("gu8", gu8, E4M3, 2)
     T, D = dy.shape
-    I = gu8.shape[1] // 2
-    _need(gu8.shape == (T, 2 * I), "shape mismatch in down_dgrad_swiglu")
+    _need(gu8.dim() == 3, "gu8 must be a K-slab")
+    I = gu8.shape[0] * SLAB // 2
+    ldt = ldt_of(T)
+    _kslab("gu8", gu8, E4M3, ldt, 2 * I)
     _kslab("wdt", wdt, torch.bfloat16, I, D)
     _need(D % 64 == 0 and I % 128 == 0, "D must be a multiple of 64 and I of 128")
-    ldt = ldt_of(T)
     dgu8 = kslab_empty(ldt, 2 * I, E5M2, dy.device)
     dgu8t = slab_empty(2 * I, T, E5M2, dy.device)
     _lib.call("sfp8_gemm_down_dgrad_swiglu", dy.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), T, D, I,

@@ -40,7 +40,7 @@ def _master(w: Tensor) -> Tensor:
 def block_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Tensor, amax: Tensor,
               eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """y, then for the backward: wdt (bf16 K-slab of W_down^T), x8t, rstd,
-    w8t (K-slab of W8^T), wscale [q_gu, q_d], gu8, h8t."""
+    w8t (K-slab of W8^T), wscale [q_gu, q_d], gu8 (K-slab of [T, 2I]), h8t."""
     I = w_down.shape[1]
     h = h.contiguous()
     x8, x8t, rstd = ops.norm_quant(h, _master(norm_w), scale, amax, eps)
@@ -64,7 +64,7 @@ def _block_fwd_fake(h, norm_w, w_gu, w_down, scale, amax, eps):
             h.new_empty((T,), dtype=torch.float32),
             h.new_empty((2 * I // 64, sr(D), 64), dtype=E4M3),
             h.new_empty((2,), dtype=torch.float32),
-            h.new_empty((T, 2 * I), dtype=E4M3),
+            h.new_empty((2 * I // 64, ldt, 64), dtype=E4M3),
             h.new_empty((ldt // 64, sr(I), 64), dtype=E4M3))
 
 
@@ -78,7 +78,7 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, wdt: Tensor, x8t: Tensor, r
         dy = dy.to(torch.bfloat16)
     h = h.contiguous()
     T, D = h.shape
-    I = gu8.shape[1] // 2
+    I = gu8.shape[0] * ops.SLAB // 2
     dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
     del dgu8
@@ -92,7 +92,7 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, wdt: Tensor, x8t: Tensor, r
 @block_bwd.register_fake
 def _block_bwd_fake(dy, h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax):
     T, D = h.shape
-    I = gu8.shape[1] // 2
+    I = gu8.shape[0] * ops.SLAB // 2
     return (h.new_empty((T, D), dtype=torch.bfloat16),
             h.new_empty((D,), dtype=torch.float32),
             h.new_empty((2 * I, D), dtype=torch.float32),

@@ -57,10 +57,12 @@ def test_swiglu_fwd_integer_operands(dev, T, D, I):
     s = torch.tensor([0.5, 2.0 ** -6, 4.0, 1, 1])
     ws = torch.tensor([2.0 ** -3, 1.0])
     amax = torch.zeros(5, device=dev)
-    gu8, h8s, h8t = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
+    gu8s, h8s, h8t = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
     rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8, w8, s, ws, I)
-    assert torch.equal(u8(gu8), u8(rgu8))
     ldt = sg.ops.ldt_of(T)
+    assert gu8s.shape == (2 * I // 64, ldt, 64)
+    assert torch.equal(u8(sg.ops.unslab(gu8s, T)), u8(rgu8))
+    assert torch.all(u8(sg.ops.unslab(gu8s, ldt))[T:] == 0)
     assert h8s.shape == (I // 64, ldt, 64)
     h8 = sg.ops.unslab(h8s, T)
     assert torch.all(u8(sg.ops.unslab(h8s, ldt))[T:] == 0)
@@ -70,6 +72,34 @@ def test_swiglu_fwd_integer_operands(dev, T, D, I):
     ht = u8(sg.ops.unslab(h8t, I))
     assert torch.equal(ht[:, :T], u8(h8).t())
     assert torch.all(ht[:, T:] == 0)
+    assert amax[1].item() == ra1.item()
+    torch.testing.assert_close(amax[2].cpu(), ra2, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("T,D,I", [(300, 256, 256), (300, 1024, 256)])
+def test_swiglu_fwd_nan_rows(dev, T, D, I):
+    """A NaN code in a token's x8 row makes that token's gate, up and h all
+    NaN: they must carry NaN codes, the other rows must be unaffected, and
+    NaN values do not enter the amax slots."""
+    g = torch.Generator().manual_seed(21 + D)
+    x8 = int_fp8((T, D), E4, g)
+    w8 = int_fp8((2 * I, D), E4, g)
+    bad = torch.tensor([0, 77, T - 1])
+    xb = x8.view(torch.uint8).clone()
+    xb[bad, 5] = 0x7F
+    x8n = xb.view(E4)
+    s = torch.tensor([1.0, 2.0 ** -8, 2.0 ** -12, 1, 1])
+    ws = torch.tensor([1.0, 1.0])
+    amax = torch.zeros(5, device=dev)
+    gu8s, h8s, _ = sg.ops.gateup_swiglu_fwd(slab(x8n, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
+    h8 = u8(sg.ops.unslab(h8s, T))
+    gu = u8(sg.ops.unslab(gu8s, T))
+    assert torch.all((gu[bad] & 0x7F) == 0x7F) and torch.all((h8[bad] & 0x7F) == 0x7F)
+    keep = torch.ones(T, dtype=torch.bool)
+    keep[bad] = False
+    rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8[keep], w8, s, ws, I)
+    assert torch.equal(gu[keep], u8(rgu8))
+    assert int(code_dist(h8[keep].view(E4), rh8).max()) <= 1
     assert amax[1].item() == ra1.item()
     torch.testing.assert_close(amax[2].cpu(), ra2, rtol=1e-5, atol=0)
 
@@ -84,8 +114,8 @@ def test_swiglu_fwd_random(dev, T, D, I):
     w8, q = O.quantize_weight(torch.randn(2 * I, D, generator=g) * D ** -0.5)
     ws = torch.stack([q, torch.tensor(1.0)])
     amax = torch.zeros(5, device=dev)
-    gu8, h8s, _ = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
-    h8 = sg.ops.unslab(h8s, T)
+    gu8s, h8s, _ = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax, T, I)
+    gu8, h8 = sg.ops.unslab(gu8s, T), sg.ops.unslab(h8s, T)
     rgu8, rh8, ra1, ra2 = O.swiglu_fwd(x8, w8, s, ws, I)
     for got, ref in ((gu8, rgu8), (h8, rh8)):
         d = code_dist(got, ref)
@@ -120,7 +150,7 @@ def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     gu8 = O.e4m3(torch.randn(T, 2 * I, generator=g) * 64)
     s = torch.tensor([1, 64.0, 1, 2.0 ** -12, 1])
     amax = torch.zeros(5, device=dev)
-    dgu8s, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), gu8.to(dev), s.to(dev), amax)
+    dgu8s, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), slab(gu8, dev), s.to(dev), amax)
     dgu8 = sg.ops.unslab(dgu8s, T)
     assert torch.all(u8(sg.ops.unslab(dgu8s, sg.ops.ldt_of(T)))[T:] == 0)
     rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
@@ -148,7 +178,7 @@ def test_down_dgrad_swiglu_every_gate_code(dev):
     gu8 = torch.cat([gate, up], dim=1).view(E4)
     s = torch.tensor([1, 64.0, 1, 2.0 ** -6, 1])
     amax = torch.zeros(5, device=dev)
-    dgu8s, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), gu8.to(dev), s.to(dev), amax)
+    dgu8s, dgu8t = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), slab(gu8, dev), s.to(dev), amax)
     dgu8 = sg.ops.unslab(dgu8s, T)
     rdgu8, _, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     nan = torch.isnan(rdgu8.float())
@@ -169,7 +199,7 @@ def test_down_dgrad_swiglu_random(dev, T, D, I):
     gu8 = O.e4m3(torch.randn(T, 2 * I, generator=g) * 64)
     s = torch.tensor([1, 64.0, 1, 2.0 ** 18, 1])
     amax = torch.zeros(5, device=dev)
-    dgu8s, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), gu8.to(dev), s.to(dev), amax)
+    dgu8s, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), slab(gu8, dev), s.to(dev), amax)
     dgu8 = sg.ops.unslab(dgu8s, T)
     rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     d = code_dist(dgu8, rdgu8)

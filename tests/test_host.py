@@ -199,7 +199,7 @@ def test_custom_op_fake_shapes_match_allocations():
             torch.empty(T, device=meta),
             ops.kslab_empty(D, 2 * I, ops.E4M3, meta),
             torch.empty(2, device=meta),
-            torch.empty(T, 2 * I, dtype=ops.E4M3, device=meta),
+            ops.kslab_empty(ops.ldt_of(T), 2 * I, ops.E4M3, meta),
             ops.slab_empty(I, T, ops.E4M3, meta)]
     for got, w in zip(out, want):
         assert got.shape == w.shape and got.dtype == w.dtype
