@@ -252,21 +252,6 @@ SFP8_DEV void block_amax_atomic(float v, float* red, float* dst) {
   }
 }
 
-// 4x4 byte transpose across four dwords: in[r] holds bytes (r,0..3) of a
-// row-major 4x4 byte block; out[c] holds bytes (0..3,c).
-SFP8_DEV void transpose4x4_bytes(const uint32_t in[4], uint32_t out[4]) {
-  // stage 1: interleave bytes of row pairs
-  uint32_t a01lo = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // r0c0 r1c0 r0c1 r1c1
-  uint32_t a01hi = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // r0c2 r1c2 r0c3 r1c3
-  uint32_t a23lo = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
-  uint32_t a23hi = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
-  // stage 2: combine half-words
-  out[0] = __builtin_amdgcn_perm(a23lo, a01lo, 0x05040100u);
-  out[1] = __builtin_amdgcn_perm(a23lo, a01lo, 0x07060302u);
-  out[2] = __builtin_amdgcn_perm(a23hi, a01hi, 0x05040100u);
-  out[3] = __builtin_amdgcn_perm(a23hi, a01hi, 0x07060302u);
-}
-
 // K-slab layout of a token-contiguous FP8 copy of an R-row operand (the weight
 // gradients' operands x8t, h8t, d_gu8t, dy8t): [ldt / 64][slab_rows(R)][64]
 // bytes, element (r, t) at
@@ -276,44 +261,8 @@ SFP8_DEV void transpose4x4_bytes(const uint32_t in[4], uint32_t out[4]) {
 // stays inside the buffer; padding rows only feed discarded output rows.
 __host__ __device__ inline int64_t slab_rows(int64_t R) { return (R + 255) / 256 * 256; }
 
-// Writes an LDS tile of tokens x columns into a K-slab copy:
-//   out(c0 + c, t0 + t) = tile[t][c]  for t < ntok, c < ncols,
-// with tokens t >= tvalid written as zeros.  ntok % 16 == 0, ncols % 4 == 0,
-// t0 % 16 == 0 (a 16-token block never straddles two slabs).  Consecutive
-// threads take consecutive 16-token blocks of the same 4 columns, so the
-// stores of a wave fill whole 64-byte slab rows.
-template <int NT>
-SFP8_DEV void lds_tile_store_slab(const uint8_t* lds, int ntok, int ncols, int stride, uint8_t* out,
-                                  int64_t rpad, int64_t t0, int64_t c0, int tvalid) {
-  const int na = ntok >> 4;
-  const int nblocks = na * (ncols >> 2);
-  for (int idx = threadIdx.x; idx < nblocks; idx += NT) {
-    const int a = idx % na, b = idx / na;
-    uint32_t w[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = a * 16 + i;
-      w[i] = (r < tvalid) ? *reinterpret_cast<const uint32_t*>(lds + r * stride + b * 4) : 0u;
-    }
-    uint32_t t4[4][4];  // t4[c][q]: column 4b+c, tokens 4q..4q+3 of the block
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t o[4];
-      transpose4x4_bytes(&w[4 * q], o);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) t4[c][q] = o[c];
-    }
-    const int64_t t = t0 + 16 * a;
-    uint8_t* base = out + (t >> 6) * rpad * 64 + (t & 63) + (c0 + 4 * b) * 64;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<intx4*>(base + c * 64) =
-          intx4{(int)t4[c][0], (int)t4[c][1], (int)t4[c][2], (int)t4[c][3]};
-  }
-}
-
-// The same for a 256-token LDS tile of NC16 * 16 columns (row stride
-// `stride` bytes) through transposing LDS reads:
+// Writes a 256-token LDS tile of NC16 * 16 columns (row stride `stride`
+// bytes) into a K-slab copy through transposing LDS reads:
 //   out(c0 + c, t0 + t) = tile[t][c]  for t < 256, c < NC16 * 16.
 // Every tile row is copied (callers keep zero codes in rows past the last
 // token); t0 % 64 == 0.  The 16-lane group q of a wave turns a 16 x 16 byte
@@ -335,6 +284,30 @@ SFP8_DEV void lds_tile_store_slab_tr(const uint8_t* lds, int stride, uint8_t* ou
     const int64_t t = t0 + r;
     *reinterpret_cast<intx4*>(out + (t >> 6) * rpad * 64 + (c0 + c + li) * 64 + (t & 63)) =
         intx4{a[0], a[1], b[0], b[1]};
+  }
+}
+
+// The same for an LDS tile of NTOK = 16, 32 or 64 tokens and ncols columns
+// (ncols % 64 == 0, t0 % NTOK == 0): NTOK / 16 lane groups take the token
+// blocks of one 16-column block, so a wave store covers 64 / NTOK * 16 slab
+// rows of NTOK bytes each (whole 64-byte rows when NTOK = 64).
+template <int NTOK>
+SFP8_DEV void lds_rows_store_slab_tr(const uint8_t* lds, int ncols, int stride, uint8_t* out, int64_t rpad,
+                                     int64_t t0, int64_t c0) {
+  static_assert(NTOK == 16 || NTOK == 32 || NTOK == 64, "16, 32 or 64 tokens");
+  constexpr int G = NTOK / 16;  // 16-token blocks per column block
+  constexpr int CB = 4 / G;     // column blocks per wave pass
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, li = lane & 15;
+  const int r = 16 * (q % G);
+  const int64_t t = t0 + r;
+  uint8_t* dst = out + (t >> 6) * rpad * 64 + (t & 63);
+  const int passes = ncols / (16 * CB);
+  for (int u = wave; u < passes; u += 4) {
+    const int c = 16 * (u * CB + q / G);
+    const uint8_t* src = lds + (r + (li >> 1)) * stride + c + 8 * (li & 1);
+    const intx2 a = lds_read_tr8(src);
+    const intx2 b = lds_read_tr8(src + 8 * stride);
+    *reinterpret_cast<intx4*>(dst + (c0 + c + li) * 64) = intx4{a[0], a[1], b[0], b[1]};
   }
 }
 

@@ -142,8 +142,10 @@ struct NormCfg {
   static constexpr int LPR = (D / 8) < 64 ? (D / 8) : 64;  // lanes per row
   static constexpr int RPW = 64 / LPR;                       // rows per wave pass
   static constexpr int CPL = D / (8 * LPR);                  // chunks per lane
-  static constexpr int RT = (65536 / D) < 32 ? (65536 / D) : 32;  // rows per WG
-  static constexpr int STRIDE = D + 8;                             // LDS row stride
+  static constexpr int RT = (65536 / D) < 64 ? (65536 / D) : 64;  // rows per WG
+  // LDS row stride: D + 16 bytes puts the 8 rows of a transposing read on
+  // distinct bank pairs
+  static constexpr int STRIDE = D + 16;
   static constexpr int PASSES = RT / (4 * RPW);                    // row passes per wave
   // passes whose loads are issued together (about 8 chunks of 16 bytes per lane)
   static constexpr int PB = (8 / CPL) < PASSES ? ((8 / CPL) > 0 ? 8 / CPL : 1) : PASSES;
@@ -234,8 +236,8 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
     }
   }
   __syncthreads();
-  const int rows_valid = (int)((T - t0) < Cfg::RT ? (T - t0) : Cfg::RT);
-  lds_tile_store_slab<256>(tile, Cfg::RT, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0, rows_valid);
+  // rows past T hold zero codes
+  lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0);
   block_amax_atomic<4>(m, red, amax);
 }
 
@@ -471,8 +473,8 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   for (int d = threadIdx.x; d < D; d += 256)
     dnw_part[(int64_t)blk * D + d] =
         ((dnw_red[d] + dnw_red[D + d]) + dnw_red[2 * D + d]) + dnw_red[3 * D + d];
-  const int rows_valid = (int)((T - t0) < Cfg::RT ? (T - t0) : Cfg::RT);
-  lds_tile_store_slab<256>(tile, Cfg::RT, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0, rows_valid);
+  // rows past T hold zero codes
+  lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
   block_amax_atomic<4>(m, red, amax + 4);
 }
 

@@ -46,10 +46,12 @@ def test_header_argument_counts_match_binding():
 
 
 def test_size_queries_need_no_gpu():
-    # one partial row per norm work-group, then up to 32 group sums
-    assert _lib.query("sfp8_norm_bwd_partials", 1024, 65536) == 65536 // 32 + 32
+    # one partial row per norm work-group (64 tokens each, 65536 / D when
+    # fewer), then up to 32 group sums
+    assert _lib.query("sfp8_norm_bwd_partials", 1024, 65536) == 65536 // 64 + 32
+    assert _lib.query("sfp8_norm_bwd_partials", 2048, 65536) == 65536 // 32 + 32
     assert _lib.query("sfp8_norm_bwd_partials", 4096, 16384) == 16384 // 16 + 32
-    assert _lib.query("sfp8_norm_bwd_partials", 128, 256) == 8 + 8  # fewer than 32 rows: one group each
+    assert _lib.query("sfp8_norm_bwd_partials", 128, 256) == 4 + 4  # fewer than 32 rows: one group each
     assert _lib.query("sfp8_norm_bwd_partials", 96, 256) == -1
     s = _lib.query("sfp8_wgrad_splits", 6144, 1024, 65536)
     assert s >= 1 and 65536 % s == 0 and (65536 // s) % 128 == 0
