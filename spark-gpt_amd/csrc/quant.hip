@@ -371,7 +371,9 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[4];
   uint8_t* tile = smem;
-  float* dnw_red = reinterpret_cast<float*>(smem + Cfg::RT * Cfg::STRIDE);  // [4 waves][D]
+  // [4 waves][D] floats, in the tile's LDS after the dy8t copy has read it
+  float* dnw_red = reinterpret_cast<float*>(smem);
+  static_assert(4 * D * sizeof(float) <= Cfg::RT * Cfg::STRIDE, "dnw reduction fits in the tile");
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
   const int blk = xcd_row_block(blockIdx.x, gridDim.x);
@@ -454,6 +456,9 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
       }
     }
   }
+  __syncthreads();
+  // rows past T hold zero codes
+  lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
   // fold this lane's dnw accumulators over the rows sharing its columns
 #pragma unroll
   for (int c = 0; c < Cfg::CPL; ++c)
@@ -463,6 +468,7 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
       for (int o = Cfg::LPR; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
       acc[c][j] = v;
     }
+  __syncthreads();  // every wave has read the tile
   if (sr == 0) {
 #pragma unroll
     for (int c = 0; c < Cfg::CPL; ++c)
@@ -473,8 +479,6 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   for (int d = threadIdx.x; d < D; d += 256)
     dnw_part[(int64_t)blk * D + d] =
         ((dnw_red[d] + dnw_red[D + d]) + dnw_red[2 * D + d]) + dnw_red[3 * D + d];
-  // rows past T hold zero codes
-  lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
   block_amax_atomic<4>(m, red, amax + 4);
 }
 
@@ -545,7 +549,7 @@ static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, co
                            const float* nw, int64_t T, const float* scale, float* amax, void* dh,
                            float* dnw, float* part, void* dy8t, int64_t ldt, hipStream_t st) {
   using Cfg = NormCfg<D>;
-  const size_t lds = (size_t)Cfg::RT * Cfg::STRIDE + 4 * D * sizeof(float);
+  const size_t lds = (size_t)Cfg::RT * Cfg::STRIDE;
   const unsigned nblk = (unsigned)(ldt / Cfg::RT);
   const int rc = allow_lds(norm_bwd_kernel<D>, lds);
   if (rc) return rc;
