@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--quant-rows", type=int, default=65536)
     p.add_argument("--quant-cols", type=int, default=4096)
     p.add_argument("--probe", action="store_true", help="one launch of each kernel, for counter passes")
+    p.add_argument("--dist", choices=("normal", "student-t"), default="normal",
+                   help="activations: N(0,1), or Student-t with 3 degrees of freedom (heavy tails)")
     return p.parse_args()
 
 
@@ -152,7 +154,13 @@ def main() -> None:
     dev = torch.device("cuda:0")
     T, D, I = args.tokens, args.d_model, args.ffn
     g = torch.Generator(device=dev).manual_seed(1)
-    h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    if args.dist == "normal":
+        h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    else:  # Student-t, 3 degrees of freedom: z / sqrt(chi2_3 / 3)
+        z = torch.randn(T, D, device=dev, generator=g)
+        chi = sum(torch.randn(T, D, device=dev, generator=g) ** 2 for _ in range(3))
+        h = (z / torch.sqrt(chi / 3)).to(torch.bfloat16)
+        del z, chi
     nw = torch.ones(D, device=dev, requires_grad=True)
     wgu = (torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5).requires_grad_(True)
     wd = (torch.randn(D, I, device=dev, generator=g) * I ** -0.5).requires_grad_(True)
@@ -182,6 +190,13 @@ def main() -> None:
     dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
     dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax)
+    # saturation per fp8 site after the scale roll: codes at the format's
+    # largest magnitude (e4m3 448 = 0x7E, e5m2 57344 = 0x7B, either sign)
+    def at_max(t, code):
+        return int(((t.view(torch.uint8) & 0x7F) == code).sum())
+    saturation = {"x": at_max(x8, 0x7E), "gu": at_max(gu8, 0x7E), "h": at_max(h8, 0x7E),
+                  "d_gu": at_max(dgu8, 0x7B), "dy": at_max(dy8t, 0x7B),
+                  "elements": {"x": T * D, "gu": 2 * T * I, "h": T * I, "d_gu": 2 * T * I, "dy": T * D}}
     # name -> (call, C-ABI symbol, predicate on the symbol's arguments, FLOP, algorithmic bytes)
     kern = {
         "norm_quant": (lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6), "sfp8_norm_quant", None,
@@ -310,12 +325,14 @@ def main() -> None:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8-e4m3/e5m2 (bf16 down dgrad)",
-        "data": "synthetic: seed-fixed N(0,1) bf16 activations, N(0,1/fan_in) fp32 weights, N(0,1e-3) bf16 grads",
+        "data": ("synthetic: seed-fixed " + ("N(0,1)" if args.dist == "normal" else "Student-t(3)")
+                 + " bf16 activations, N(0,1/fan_in) fp32 weights, N(0,1e-3) bf16 grads"),
         "config": {"workload": "fp8_swiglu_mlp_block_fwd_bwd", "tokens": T, "d_model": D, "ffn": I,
                    "flop_per_step": flop, "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4)},
         "roofline": roofline,
         "quantizer": quant,
         "kernels": kernels,
+        "saturation": saturation,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens, D, I)
