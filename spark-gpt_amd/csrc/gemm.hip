@@ -964,6 +964,12 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   }
 }
 
+// out[0, n) = 0: four floats per thread (n % 4 == 0, out 16-byte aligned).
+__global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ out, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i < n) *reinterpret_cast<floatx4*>(out + i) = floatx4{0.f, 0.f, 0.f, 0.f};
+}
+
 // Split-K reduction of the accumulator-order partials of wgrad_kernel:
 // out[m, n] = (sum over s ascending of ws[s]) / (sa * sb).  Thread q owns the
 // q-th float4 of one split's partials; its (m, n) follows from the MFMA
@@ -1045,7 +1051,8 @@ extern "C" {
 int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
                                 void* h8t, int64_t ldt, void* stream) {
-  if (!x8 || !w8 || !scale || !wscale || !amax || !gu8 || !h8 || !h8t) return kErrNullPointer;
+  // token-sized buffers may be null when there are no tokens
+  if (!w8 || !scale || !wscale || !amax || (T > 0 && (!x8 || !gu8 || !h8 || !h8t))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || D % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
   if (!fits32(ldt, D) || !fits32(2 * I, D) || !fits32(ldt, I) || !fits32(ldt, 2 * I)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
@@ -1076,7 +1083,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
 
 int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t T, int64_t D, int64_t I,
                        const float* scale, const float* wscale, void* y, int64_t ldt, void* stream) {
-  if (!h8 || !wd8 || !res || !scale || !wscale || !y) return kErrNullPointer;
+  if (!wd8 || !scale || !wscale || (T > 0 && (!h8 || !res || !y))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 16 || ldt < T || ldt % kTile) return kErrBadShape;
   if (!fits32(ldt, I) || !fits32(slab_rows(D), I)) return kErrBadShape;
   if (!al16(h8) || !al16(wd8) || !al16(res) || !al16(y)) return kErrBadAlignment;
@@ -1093,7 +1100,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream) {
-  if (!dy || !wdt || !gu8 || !scale || !amax || !dgu8 || !dgu8t) return kErrNullPointer;
+  if (!wdt || !scale || !amax || (T > 0 && (!dy || !gu8 || !dgu8 || !dgu8t))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
   if (!fits32(kTile, 2 * D) || !fits32(slab_rows(I), 2 * D) || !fits32(ldt, 2 * I)) return kErrBadShape;
   if (!al16(dy) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
@@ -1117,7 +1124,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
 
 int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t D, int64_t I,
                            const float* scale, const float* wscale, void* dxn, int64_t ldt, void* stream) {
-  if (!dgu8 || !w8t || !scale || !wscale || !dxn) return kErrNullPointer;
+  if (!w8t || !scale || !wscale || (T > 0 && (!dgu8 || !dxn))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 16 || ldt < T || ldt % kTile) return kErrBadShape;
   if (!fits32(ldt, 2 * I) || !fits32(slab_rows(D), 2 * I)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
@@ -1164,7 +1171,7 @@ int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
 
 int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
                     const float* sa, const float* sb, float* out, float* ws, int64_t ws_floats, void* stream) {
-  if (!at || !bt || !sa || !sb || !out) return kErrNullPointer;
+  if (!sa || !sb || !out || (ldt > 0 && (!at || !bt))) return kErrNullPointer;
   if (M <= 0 || N <= 0 || ldt < 0 || ldt % kTile || N % 4) return kErrBadShape;
   if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3) return kErrBadShape;
   // every K-slab offset (stage * rows * 64 + row * 64) is 32-bit
@@ -1174,7 +1181,11 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   const int64_t splits = sfp8_wgrad_splits(M, N, ldt);
   if (splits > 1 && (!ws || ws_floats < sfp8_wgrad_workspace_floats(M, N, ldt))) return kErrWorkspaceTooSmall;
   if (ldt == 0) {
-    return hipMemsetAsync(out, 0, (size_t)(M * N * 4), st) == hipSuccess ? kOk : status();
+    // no tokens: the gradient is zero (a fill kernel, not a memset node, so
+    // that a captured graph replays it correctly)
+    const int64_t n = M * N;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, out, n);
+    return status();
   }
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
   int rc = prep(wgrad_kernel<kFmtE5M2, kFmtE4M3>, kMainLds);

@@ -490,6 +490,11 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
 // order depends only on nb.
 constexpr int kColsumGroups = 32;
 
+__global__ __launch_bounds__(256) void zero_f32_kernel(float* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = 0.0f;
+}
+
 __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, int64_t nb,
                                                      int64_t rpg, int64_t D, float* __restrict__ out) {
   __shared__ float red[4][64];
@@ -571,7 +576,8 @@ extern "C" {
 
 int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const float* scale, float* amax,
                            void* x8, void* x8t, int64_t ldt, void* stream) {
-  if (!x || !scale || !amax || !x8 || !x8t) return kErrNullPointer;
+  // row- and token-sized buffers may be null when there are no rows
+  if (!scale || !amax || (rows > 0 && cols > 0 && (!x || !x8 || !x8t))) return kErrNullPointer;
   if (rows < 0 || cols < 0 || (cols % QR_TILE) != 0 || ldt < rows) return kErrBadShape;
   if (!aligned16(x) || !aligned16(x8)) return kErrBadAlignment;
   if (rows == 0 || cols == 0) return kOk;
@@ -584,7 +590,8 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
 int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
                     const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
                     void* stream) {
-  if (!h || !norm_w || !scale || !amax || !x8 || !x8t || !rstd) return kErrNullPointer;
+  // token-sized buffers may be null when there are no tokens
+  if (!norm_w || !scale || !amax || (T > 0 && (!h || !x8 || !x8t || !rstd))) return kErrNullPointer;
   if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
   if (!aligned16(h) || !aligned16(norm_w) || !aligned16(x8) || !aligned16(x8t)) return kErrBadAlignment;
   if (ldt == 0) return kOk;
@@ -650,7 +657,9 @@ int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
 int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
                   int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
                   float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream) {
-  if (!h || !rstd || !dxn || !dy || !norm_w || !scale || !amax || !dh || !dnw || !partials || !dy8t)
+  // token-sized buffers (and the partials) may be null when there are no tokens
+  if (!norm_w || !scale || !amax || !dnw ||
+      (T > 0 && (!h || !rstd || !dxn || !dy || !dh || !partials || !dy8t)))
     return kErrNullPointer;
   if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
   const int64_t nb = sfp8_norm_bwd_partials(D, ldt);
@@ -659,8 +668,12 @@ int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void*
   if (!aligned16(h) || !aligned16(dxn) || !aligned16(dy) || !aligned16(dh) || !aligned16(norm_w) ||
       !aligned16(dy8t))
     return kErrBadAlignment;
-  if (ldt == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
+  if (ldt == 0) {
+    // no tokens: d_norm_w is an empty sum (zero); nothing else is written
+    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, dnw, D);
+    return launch_status();
+  }
   switch (D) {
     case 128: return launch_norm_bwd<128>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
     case 256: return launch_norm_bwd<256>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);

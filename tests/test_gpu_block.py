@@ -102,6 +102,23 @@ def test_block_matches_oracle(dev, T, D, I):
     assert torch.all(m == 0.5)
 
 
+def test_block_zero_tokens(dev):
+    """No tokens: empty y and dh, zero weight and norm gradients, amax
+    untouched (the reference's sums over zero rows)."""
+    D, I = 256, 384
+    norm, mlp = _setup(dev, 0, D, I, 3)
+    mlp.fp8_amax.fill_(0.5)
+    h = torch.empty(0, D, dtype=torch.bfloat16, device=dev)
+    probe = torch.empty(0, D, device=dev)
+    y, dh, dnw, dwgu, dwd = _step(h, probe, norm, mlp)
+    assert y.shape == (0, D) and y.dtype == torch.bfloat16
+    assert dh.shape == (0, D) and dh.dtype == torch.bfloat16
+    for g, shape in ((dnw, (D,)), (dwgu, (2 * I, D)), (dwd, (D, I))):
+        assert g.shape == shape and g.dtype == torch.float32
+        assert bool((g == 0).all())
+    assert bool((mlp.fp8_amax == 0.5).all())
+
+
 def test_block_deterministic(dev):
     T, D, I = 1000, 256, 768
     norm, mlp = _setup(dev, T, D, I, 5)

@@ -33,7 +33,7 @@ def u8(t: torch.Tensor) -> np.ndarray:
 
 
 def rel_l2(a: torch.Tensor, r: torch.Tensor) -> float:
-    a, r = a.double().cpu(), r.double().cpu()
+    a, r = a.detach().double().cpu(), r.detach().double().cpu()
     return float((a - r).norm() / r.norm().clamp(min=1e-300))
 
 
