@@ -52,6 +52,11 @@ extern "C" {
 #define SFP8_ERR_BAD_ALIGNMENT (-3)
 #define SFP8_ERR_WORKSPACE_TOO_SMALL (-4)
 
+/* Pointer arguments are device pointers and must not be NULL, except that
+ * buffers sized by the token (or row) count may be NULL when that count is
+ * 0: such a call does no work beyond writing the outputs that are not sized
+ * by tokens (d_norm_w and the weight gradients come out zero). */
+
 /* ---- quantizers -------------------------------------------------------- */
 
 /* Standalone quantizer: x8 = e4m3(clamp(x * scale[0], +-448)) row-major
