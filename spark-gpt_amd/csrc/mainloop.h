@@ -38,7 +38,6 @@ constexpr int kStage = 64;                   // bytes of K per stage
 constexpr int kStages = 4;                   // LDS ring depth (>= 3)
 constexpr int kStageA = kTile * kStage;      // 16 KiB
 constexpr int kMainLds = 2 * kStages * kStageA;  // 128 KiB: the 256 x 256 tile's ring
-constexpr bool kDmaFirst = false;  // stage order: DMA issues before the fragment reads
 constexpr int kFmtE4M3 = 0;
 constexpr int kFmtE5M2 = 1;
 
@@ -93,10 +92,8 @@ SFP8_DEV void sched_interleave_valu() {
   }
 }
 
-template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0,
-          bool A_TR = false>
+template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0>
 struct MainLoop {
-  static_assert(!(A_TR && BF16), "token-slab A operands are fp8");
   static_assert(NB == 2 || NB == 4, "2 or 4 B blocks per wave");
   static_assert(STAGES >= 3, "at least three LDS stages");
   static constexpr int kTileN = 64 * NB;                  // B rows per tile
@@ -140,14 +137,7 @@ struct MainLoop {
   template <int I>
   static SFP8_DEV void read_frag(const uint8_t* lds, int buf, const uint32_t (&aoff)[2], const uint32_t (&boff)[2],
                                  Frag& f) {
-    if constexpr (I < 4 && A_TR) {
-      // token-slab A: block tb of 32 tokens is half (tb & 1) of 64-token
-      // block tb >> 1; four transposing reads give 8 K bytes each
-      const uint8_t* p = lds + buf * kStageA + (I >> 1) * 4096 + aoff[I & 1];
-      const intx2 q0 = lds_read_tr8(p), q1 = lds_read_tr8(p + 512), q2 = lds_read_tr8(p + 1024),
-                  q3 = lds_read_tr8(p + 1536);
-      f.a[I] = intx8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
-    } else if constexpr (I < 4) {
+    if constexpr (I < 4) {
       const uint8_t* p = lds + buf * kStageA + I * 32 * kStage;
       const intx4 lo = *reinterpret_cast<const intx4*>(p + aoff[0]);
       const intx4 hi = *reinterpret_cast<const intx4*>(p + aoff[1]);
@@ -232,13 +222,16 @@ struct MainLoop {
   //   kSchedPre MFMAs of stage kt (registers only: they keep the matrix pipe busy
   //   while the waves meet at the barrier);
   //   wait for stage kt+1 to land, barrier;
-  //   4+NB MFMAs, each followed by one fragment (two 16-byte reads) of stage
-  //   kt+1 from `rd_buf`: all reads are issued early in the stage, so they
-  //   have landed long before stage kt+1 starts;
-  //   (4+NB)/2 MFMAs, each followed by two DMA instructions of stage `ld` into
-  //   `dma_buf` (the buffer stage kt-1 used: every wave finished reading it
-  //   before this barrier);
+  //   MFMAs, each followed by a group of the 4+NB fragments (two 16-byte
+  //   reads each) of stage kt+1 from `rd_buf` or of the 4+NB DMA
+  //   instructions of stage `ld` into `dma_buf` (the buffer stage kt-1 used:
+  //   every wave finished reading it before this barrier), all within the
+  //   first 10-16 MFMAs so the reads land long before stage kt+1 starts;
   //   the remaining MFMAs.
+  // The grouping depends on the MFMA length: fp8 256 x 256 alternates
+  // fragments and DMA over 10 MFMAs of 64 cycles, bf16 alternates one
+  // fragment and one DMA over 16 MFMAs of 32 cycles, NB = 2 issues the
+  // fragments over 3 MFMAs and then the DMA over 3.
   static constexpr int kSchedPre = 2;
   static_assert(kMfma >= kSchedPre + (4 + NB) / 2 + (4 + NB) / 2, "stage too short for the schedule");
   static SFP8_DEV void stage(uint8_t* lds, const Frag& cur, Frag& nxt, Acc& acc, int dma_buf, int ld, int rd_buf,
@@ -277,32 +270,35 @@ struct MainLoop {
       __builtin_amdgcn_sched_barrier(0);
       return;
     }
-    if constexpr (kDmaFirst) {
-      mfma_then_dma<P + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      mfma_then_dma<P + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      mfma_then_dma<P + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      if constexpr (NB == 4) mfma_then_dma<P + 3, 6, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      mfma_then_reads<P + H + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      mfma_then_reads<P + H + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      mfma_then_reads<P + H + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      if constexpr (NB == 4) mfma_then_reads<P + H + 3, 6, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-    } else {
-      mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      mfma_then_reads<P + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      mfma_then_reads<P + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      if constexpr (NB == 4) mfma_then_reads<P + 3, 6, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
-      mfma_then_dma<P + H + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      mfma_then_dma<P + H + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      mfma_then_dma<P + H + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
-      if constexpr (NB == 4) mfma_then_dma<P + H + 3, 6, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    if constexpr (!BF16 && NB == 4) {
+      // fp8, 256 x 256: fragments and DMA issues alternate over 10 MFMAs
+      // (2-3 % faster than 4 MFMAs of reads followed by 4 of DMA)
+      mfma_then_reads<P + 0, 0, 1>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 1, 0, 1>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 2, 1, 3>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 3, 1, 3>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 4, 3, 5>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 5, 3, 5>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 6, 5, 7>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 7, 5, 7>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 8, 7, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 9, 7, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_range<P + 10, kMfma>(cur, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      return;
     }
+    // NB = 2: two fragments after each of 3 MFMAs, then two DMA issues after
+    // each of 3
+    mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    mfma_then_reads<P + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    mfma_then_reads<P + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+    mfma_then_dma<P + H + 0, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    mfma_then_dma<P + H + 1, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+    mfma_then_dma<P + H + 2, 4, 6>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
     mfma_range<P + 2 * H, kMfma>(cur, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // A_TR: A is a token slab (64-token blocks of K rows of 64 bytes, tokens
-  // contiguous); a_rowoff(w) is the byte offset of the tile's 64-token block
-  // w and a_sstride is 64 * 64 (one stage = 64 K rows of every block).
   // a_bytes/b_bytes: bytes available from a_base/b_base (range-checked);
   // a_rowoff(r)/b_rowoff(r): byte offset of tile row r from the base within
   // one K stage; a_sstride/b_sstride: bytes from one 64-byte K stage to the
@@ -320,16 +316,8 @@ struct MainLoop {
     // <- logical chunk (lane%4) ^ ((row >> 2) & 3)
     uint32_t voff_a[4], voff_b[NB];
     const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
-    if constexpr (A_TR) {
-      // wave w copies 64-token block w: K rows 16j + lane/4, 16-byte chunk
-      // (lane & 3) ^ (((row >> 2) & 1) << 1) of the row's 64 tokens
-      const uint32_t chunk_tr = (uint32_t)(((lane & 3) ^ (((lane >> 4) & 1) << 1)) << 4);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(wave) + (uint32_t)((16 * j + (lane >> 2)) * 64) + chunk_tr;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + chunk;
-    }
+    for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + chunk;
 #pragma unroll
     for (int j = 0; j < NB; ++j) voff_b[j] = (uint32_t)b_rowoff(16 * NB * wave + 16 * j + (lane >> 2)) + chunk;
     // fragment read offsets (lane half g reads logical chunks 2g, 2g+1)
@@ -338,16 +326,7 @@ struct MainLoop {
     uint32_t aoff[2], boff[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      if constexpr (A_TR) {
-        // transposing reads (index h = block parity): group lane j = lane % 16
-        // points at K row 32*(lane/32) + j/2 (+ 8 per read) and tokens
-        // 32h + 16*((lane/16) & 1) + 8*(j & 1) of the wave's 64-token block
-        const int kl = 32 * (lane >> 5) + ((lane & 15) >> 1);
-        const int cl = (2 * h + ((lane >> 4) & 1)) ^ (((lane >> 3) & 1) << 1);
-        aoff[h] = (uint32_t)(2 * wm * 4096 + kl * 64 + 16 * cl + 8 * (lane & 1));
-      } else {
-        aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
-      }
+      aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
       boff[h] = (uint32_t)(kLdsB + (BLayout<PAIRED, NB>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
     }
 #pragma unroll
