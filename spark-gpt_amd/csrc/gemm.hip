@@ -163,46 +163,70 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   float m_gu = 0.f, m_h = 0.f;
   const int fr = lane & 31, g = lane >> 5;
   const int cb = 64 * wn + 32 * g;  // first of this lane's 32 columns
+  // g, u (bf16-rounded, unscaled) and h of unit (tb, nb, q): 4 columns
+  auto unit = [&](int tb, int nb, int q, float (&gb)[4], float (&ub)[4], float (&hb)[4]) {
+    // g, u rounded to bf16 as in the bf16 path (train.py:1006-1007)
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      const uint32_t pg = pack2_bf16(acc[tb][nb][4 * q + e], acc[tb][nb][4 * q + e + 1]);
+      const uint32_t pu = pack2_bf16(acc[tb][nb + 2][4 * q + e], acc[tb][nb + 2][4 * q + e + 1]);
+      gb[e] = __uint_as_float(pg << 16);
+      gb[e + 1] = __uint_as_float(pg & 0xffff0000u);
+      ub[e] = __uint_as_float(pu << 16);
+      ub[e + 1] = __uint_as_float(pu & 0xffff0000u);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c_exp));
+      hb[e] = gb[e] * sg * ub[e];
+    }
+  };
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;  // token within the tile
     uint32_t gw[8], uw[8], hw[8];
+    bool bad = false;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float gb[4], ub[4], hb[4];
-        // g, u rounded to bf16 as in the bf16 path (train.py:1006-1007)
+        unit(tb, nb, q, gb, ub, hb);
+        // NaN-propagating maxima: inside the e4m3 range (after scaling) the
+        // unclamped conversions are exact; otherwise the row block is redone
+        float a = max3_nan(fabsf(gb[0]), fabsf(ub[0]), fabsf(gb[1]));
+        a = max3_nan(a, fabsf(ub[1]), fabsf(gb[2]));
+        a = max3_nan(a, fabsf(ub[2]), fabsf(gb[3]));
+        a = __builtin_elementwise_maximum(a, fabsf(ub[3]));
+        float b = max3_nan(fabsf(hb[0]), fabsf(hb[1]), fabsf(hb[2]));
+        b = __builtin_elementwise_maximum(b, fabsf(hb[3]));
+        bad |= !(a <= bnd1) | !(b <= bnd2);
+        m_gu = fmaxf(m_gu, a);  // a NaN here is redone by the exact path
+        m_h = fmaxf(m_h, b);
+        const int k = 4 * nb + q;
+        gw[k] = pack4_e4m3_scaled_noclamp(gb[0], gb[1], gb[2], gb[3], inv1, 0u);
+        uw[k] = pack4_e4m3_scaled_noclamp(ub[0], ub[1], ub[2], ub[3], inv1, 0u);
+        hw[k] = pack4_e4m3_scaled_noclamp(hb[0], hb[1], hb[2], hb[3], inv2, 0u);
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(bad)) {  // wave-uniform; NaN or out-of-range data only
+      asm volatile("" ::: "memory");
 #pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          const uint32_t pg = pack2_bf16(acc[tb][nb][4 * q + e], acc[tb][nb][4 * q + e + 1]);
-          const uint32_t pu = pack2_bf16(acc[tb][nb + 2][4 * q + e], acc[tb][nb + 2][4 * q + e + 1]);
-          gb[e] = __uint_as_float(pg << 16);
-          gb[e + 1] = __uint_as_float(pg & 0xffff0000u);
-          ub[e] = __uint_as_float(pu << 16);
-          ub[e + 1] = __uint_as_float(pu & 0xffff0000u);
-        }
-        bool nan = false;
+      for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c_exp));
-          hb[e] = gb[e] * sg * ub[e];
-          m_gu = fmaxf(m_gu, fmaxf(fabsf(gb[e]), fabsf(ub[e])));
-          nan |= hb[e] != hb[e];  // a NaN g or u always reaches h
+        for (int q = 0; q < 4; ++q) {
+          float gb[4], ub[4], hb[4];
+          unit(tb, nb, q, gb, ub, hb);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {  // amax over the non-NaN values
+            m_gu = fmaxf(m_gu, fmaxf(fabsf(gb[e]), fabsf(ub[e])));
+            m_h = fmaxf(m_h, fabsf(hb[e]));
+          }
+          const int k = 4 * nb + q;
+          gw[k] = fix_nan4(pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], inv1, bnd1), gb[0], gb[1], gb[2], gb[3]);
+          uw[k] = fix_nan4(pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], inv1, bnd1), ub[0], ub[1], ub[2], ub[3]);
+          hw[k] = fix_nan4(pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], inv2, bnd2), hb[0], hb[1], hb[2], hb[3]);
         }
-        m_h = fmaxf(fmaxf(m_h, fmaxf(fabsf(hb[0]), fabsf(hb[1]))), fmaxf(fabsf(hb[2]), fabsf(hb[3])));
-        uint32_t pg = pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], inv1, bnd1);
-        uint32_t pu = pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], inv1, bnd1);
-        uint32_t ph = pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], inv2, bnd2);
-        if (__builtin_amdgcn_ballot_w64(nan)) {  // wave-uniform, taken only with NaN data
-          asm volatile("" ::: "memory");
-          pg = fix_nan4(pg, gb[0], gb[1], gb[2], gb[3]);
-          pu = fix_nan4(pu, ub[0], ub[1], ub[2], ub[3]);
-          ph = fix_nan4(ph, hb[0], hb[1], hb[2], hb[3]);
-        }
-        gw[4 * nb + q] = pg;
-        uw[4 * nb + q] = pu;
-        hw[4 * nb + q] = ph;
       }
     }
     store16(Gt + row * kEpiStride + cb, {gw[0], gw[1], gw[2], gw[3]});
