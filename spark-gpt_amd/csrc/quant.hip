@@ -36,11 +36,13 @@ SFP8_DEV int xcd_row_block(int pid, int nblk) {
 // 16-lane group turns a 16 x 16 byte block into 16 column runs of 16 rows.
 constexpr int QR_TILE = 128;
 constexpr int QR_STRIDE = QR_TILE + 8;
+constexpr int QR_CSTRIDE = QR_TILE + 16;  // 16-byte aligned rows; 16-lane writes land on distinct banks
 
 __global__ __launch_bounds__(256) void quant_rowcol_kernel(
     const uint16_t* __restrict__ x, int64_t R, int64_t C, const float* __restrict__ scale,
     float* __restrict__ amax, uint8_t* __restrict__ x8, uint8_t* __restrict__ x8t, int64_t ldt) {
   __shared__ __align__(16) uint8_t tile[QR_TILE * QR_STRIDE];
+  __shared__ __align__(16) uint8_t tcol[QR_TILE * QR_CSTRIDE];  // the tile transposed: [column][128 rows]
   __shared__ float red[4];
   // consecutive work-groups take consecutive column blocks of the same rows,
   // so each input row is read while its DRAM page is open
@@ -101,9 +103,11 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
     *reinterpret_cast<intx2*>(tile + r * QR_STRIDE + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};  // zeros past R
   }
   __syncthreads();
-  // Transposed copy: wave w, pass p covers columns 16*(2w + p/2) .. +15 and
-  // rows 64*(p%2) .. +63; its 16-lane group q takes rows 16q .. 16q+15 of
-  // those, so a wave's stores are 64 contiguous bytes of each of 16 columns.
+  // Transposed copy, in two LDS passes so that every global store covers
+  // whole 128-byte lines of x8t.  Pass 1: wave w, pass p covers columns
+  // 16*(2w + p/2) .. +15 and rows 64*(p%2) .. +63; its 16-lane group q takes
+  // rows 16q .. 16q+15 of those (two transposing reads) into the column-major
+  // tile.  Pass 2: 8 lanes copy one column's 128 rows to x8t.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, li = lane & 15;
 #pragma unroll
@@ -114,15 +118,22 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
     const uint8_t* src = tile + (rb + (li >> 1)) * QR_STRIDE + cb + 8 * (li & 1);
     const intx2 t0 = lds_read_tr8(src);
     const intx2 t1 = lds_read_tr8(src + 8 * QR_STRIDE);
-    const int64_t rbase = r0 + rb;
+    *reinterpret_cast<intx4*>(tcol + (cb + li) * QR_CSTRIDE + rb) = intx4{t0[0], t0[1], t1[0], t1[1]};
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = k * 256 + threadIdx.x;
+    const int col = idx >> 3, ch = idx & 7;  // 8 lanes per column, 16 rows each
+    const int64_t rbase = r0 + 16 * ch;
     if (rbase >= ldt) continue;
-    uint8_t* dst = x8t + (c0 + cb + li) * ldt + rbase;
-    const intx4 w = {t0[0], t0[1], t1[0], t1[1]};
+    const intx4 w = *reinterpret_cast<const intx4*>(tcol + col * QR_CSTRIDE + 16 * ch);
+    uint8_t* dst = x8t + (c0 + col) * ldt + rbase;
     if (rbase + 16 <= ldt && ((((uintptr_t)dst) & 15u) == 0)) {
       *reinterpret_cast<intx4*>(dst) = w;
     } else {
       const int nv = (int)((ldt - rbase) < 16 ? (ldt - rbase) : 16);
-      for (int k = 0; k < nv; ++k) dst[k] = (uint8_t)((uint32_t)w[k >> 2] >> (8 * (k & 3)));
+      for (int b = 0; b < nv; ++b) dst[b] = (uint8_t)((uint32_t)w[b >> 2] >> (8 * (b & 3)));
     }
   }
   block_amax_atomic<4>(m, red, amax);
@@ -581,7 +592,8 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
   if (rows < 0 || cols < 0 || (cols % QR_TILE) != 0 || ldt < rows) return kErrBadShape;
   if (!aligned16(x) || !aligned16(x8)) return kErrBadAlignment;
   if (rows == 0 || cols == 0) return kOk;
-  dim3 grid((unsigned)(cols / QR_TILE), (unsigned)((rows + QR_TILE - 1) / QR_TILE));
+  // row blocks cover ldt, so that x8t columns rows..ldt-1 are written (zeros)
+  dim3 grid((unsigned)(cols / QR_TILE), (unsigned)((ldt + QR_TILE - 1) / QR_TILE));
   hipLaunchKernelGGL(quant_rowcol_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x, rows, cols, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt);
   return launch_status();

@@ -77,6 +77,27 @@ def test_quant_rowcol_ragged(dev, R, C):
     assert torch.all(amax[1:].cpu() == 0)
 
 
+@pytest.mark.parametrize("R,ldt", [(100, 100), (100, 300), (257, 1024), (1, 129)])
+def test_quant_rowcol_ldt_padding(dev, R, ldt):
+    """Through the C ABI with ldt > rows: x8t columns rows..ldt-1 are zeros."""
+    from spark_gpt_amd import _lib
+    C = 256
+    g = torch.Generator().manual_seed(R + ldt)
+    x = torch.randn(R, C, generator=g).to(torch.bfloat16)
+    s = torch.tensor([4.0, 1, 1, 1, 1])
+    amax = torch.zeros(5, device=dev)
+    x8 = torch.empty(R, C, dtype=torch.uint8, device=dev)
+    x8t = torch.full((C, ldt), 0x55, dtype=torch.uint8, device=dev)
+    xd, sd = x.to(dev), s.to(dev)
+    _lib.call("sfp8_quant_e4m3_rowcol", xd.data_ptr(), R, C, sd.data_ptr(), amax.data_ptr(), x8.data_ptr(),
+              x8t.data_ptr(), ldt, _lib.stream_of(xd))
+    r8, r8t, ra = O.quant_rowcol(x, s[0])
+    assert torch.equal(x8.cpu(), u8(r8))
+    assert torch.equal(x8t[:, :R].cpu(), u8(r8t))
+    assert torch.all(x8t[:, R:] == 0)
+    assert amax[0].item() == ra.item()
+
+
 def test_quant_rowcol_north_star_size(dev):
     """65536 x 4096 bf16 with 0.1% outlier columns x50, delayed scale from a
     prewarm pass; bytes, transpose, amax and next scale bit-exact."""
