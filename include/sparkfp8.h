@@ -28,7 +28,7 @@
  *    The token-contiguous copies for the weight gradients (x8t, h8t, dgu8t,
  *    dy8t) are K-slabs of the transposed activation over ldt tokens
  *    (R = features, L = ldt); producers write zeros for tokens T..ldt-1.
- *    The standalone quantizer's outputs are plain row-major x8 and [cols, ldt]
+ *    The standalone quantizer writes a plain row-major x8 and the same K-slab
  *    x8t.
  *  - `stream` is a hipStream_t; every call is asynchronous on it, never
  *    synchronises the device and never allocates device memory.  Callers
@@ -60,10 +60,12 @@ extern "C" {
 /* ---- quantizers -------------------------------------------------------- */
 
 /* Standalone quantizer: x8 = e4m3(clamp(x * scale[0], +-448)) row-major
- * [rows, cols], x8t = x8^T with leading dimension ldt (>= rows; columns
- * rows..ldt-1 zero), amax[0] = max(amax[0], max|x|).
- * The norm-free core of _fp8_norm_quant_kernel (train.py:966-972).
- * cols % 128 == 0; x, x8 16-byte aligned. */
+ * [rows, cols], x8t = K-slab of x8^T over ldt tokens ([ldt/64][slab_rows(cols)]
+ * [64]: the token-contiguous copy the weight gradient reads; tokens
+ * rows..ldt-1 and padding rows cols.. are zeros), amax[0] = max(amax[0],
+ * max|x|).  The norm-free core of _fp8_norm_quant_kernel (train.py:966-972),
+ * whose X8T store (train.py:970) writes the plain [cols, T] transpose.
+ * cols % 128 == 0; ldt >= rows, ldt % 64 == 0; x, x8, x8t 16-byte aligned. */
 int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const float* scale, float* amax,
                            void* x8, void* x8t, int64_t ldt, void* stream);
 

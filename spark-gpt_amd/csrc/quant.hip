@@ -28,34 +28,47 @@ SFP8_DEV int xcd_row_block(int pid, int nblk) {
 
 
 // --------------------------------------------------------------------------
-// Standalone quantizer: x8 = e4m3(x * s), x8t = x8^T, amax = max|x|.
-// Tile 128 rows x 128 cols, 256 threads.  Every thread issues its eight
-// 16-byte row loads before converting any of them; NaN lanes are patched on a
-// wave-uniform path taken only when the wave saw a NaN.  The transposed copy
-// is read out of the LDS tile with the transpose read (lds_read_tr8): a
-// 16-lane group turns a 16 x 16 byte block into 16 column runs of 16 rows.
-constexpr int QR_TILE = 128;
-constexpr int QR_STRIDE = QR_TILE + 8;
-constexpr int QR_CSTRIDE = QR_TILE + 16;  // 16-byte aligned rows; 16-lane writes land on distinct banks
+// Standalone quantizer: x8 = e4m3(x * s) row-major, x8t = the K-slab of
+// x8^T over ldt tokens ([ldt/64][slab_rows(C)][64]), amax = max|x|.
+// A work-group of 256 threads takes COLS columns of 16384 / COLS rows (64 x
+// 256, or 128 x 128 when C is not a multiple of 256).  Every thread issues
+// its eight 16-byte row loads before converting any of them; NaN lanes are
+// patched on a wave-uniform path taken only when the wave saw a NaN.  The
+// tile goes to LDS, is read back transposed with lds_read_tr8 (a 16-lane
+// group turns a 16 x 16 byte block into 16 column runs of 16 rows) into a
+// column-major LDS tile, and leaves as 64-byte slab rows: each 64-token slab
+// of the tile is one contiguous block of COLS * 64 bytes of x8t.  Work-groups
+// past column C write the slab's zero padding rows.
+template <int COLS>
+struct QuantRowcolCfg {
+  static constexpr int kRows = 16384 / COLS;
+  static constexpr int kRowsPerPass = 256 / (COLS / 8);
+  static constexpr int kTileStride = COLS + 16;   // = 4 (mod 8) dwords: conflict-free transposing reads
+  static constexpr int kColStride = kRows + 16;   // = 4 (mod 16) dwords: a group's 16 writes hit distinct banks
+};
 
+template <int COLS>
 __global__ __launch_bounds__(256) void quant_rowcol_kernel(
     const uint16_t* __restrict__ x, int64_t R, int64_t C, const float* __restrict__ scale,
     float* __restrict__ amax, uint8_t* __restrict__ x8, uint8_t* __restrict__ x8t, int64_t ldt) {
-  __shared__ __align__(16) uint8_t tile[QR_TILE * QR_STRIDE];
-  __shared__ __align__(16) uint8_t tcol[QR_TILE * QR_CSTRIDE];  // the tile transposed: [column][128 rows]
+  using Cfg = QuantRowcolCfg<COLS>;
+  constexpr int ROWS = Cfg::kRows, TS = Cfg::kTileStride, CS = Cfg::kColStride;
+  __shared__ __align__(16) uint8_t tile[ROWS * TS];
+  __shared__ __align__(16) uint8_t tcol[COLS * CS];  // [column][ROWS rows]
   __shared__ float red[4];
   // consecutive work-groups take consecutive column blocks of the same rows,
   // so each input row is read while its DRAM page is open
-  const int64_t r0 = (int64_t)blockIdx.y * QR_TILE;
-  const int64_t c0 = (int64_t)blockIdx.x * QR_TILE;
+  const int64_t r0 = (int64_t)blockIdx.y * ROWS;
+  const int64_t c0 = (int64_t)blockIdx.x * COLS;
+  const bool live = c0 < C;  // work-group uniform; false: slab padding only
   const float s = scale[0];
-  const int c8 = threadIdx.x & 15;   // 8-element chunk within the tile row
-  const int rr = threadIdx.x >> 4;   // row within a 16-row pass
+  const int c8 = threadIdx.x % (COLS / 8);  // 8-element chunk within the tile row
+  const int rr = threadIdx.x / (COLS / 8);  // row within a pass
   intx4 v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int64_t gr = r0 + rr + 16 * i;
-    v[i] = gr < R ? *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8) : intx4{0, 0, 0, 0};
+    const int64_t gr = r0 + rr + Cfg::kRowsPerPass * i;
+    v[i] = live && gr < R ? *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8) : intx4{0, 0, 0, 0};
   }
   float m = 0.0f;
   bool nan = false;
@@ -82,7 +95,7 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       // re-read the row chunk (keeps the loaded vectors dead after the cast)
-      const int64_t gr = r0 + rr + 16 * i;
+      const int64_t gr = r0 + rr + Cfg::kRowsPerPass * i;
       const intx4 w = gr < R ? *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8) : intx4{0, 0, 0, 0};
       float f[8];
 #pragma unroll
@@ -97,44 +110,38 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int r = rr + 16 * i;
+    const int r = rr + Cfg::kRowsPerPass * i;
     const int64_t gr = r0 + r;
-    if (gr < R) *reinterpret_cast<intx2*>(x8 + gr * C + c0 + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};
-    *reinterpret_cast<intx2*>(tile + r * QR_STRIDE + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};  // zeros past R
+    if (live && gr < R) *reinterpret_cast<intx2*>(x8 + gr * C + c0 + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};
+    *reinterpret_cast<intx2*>(tile + r * TS + c8 * 8) = intx2{(int)lo[i], (int)hi[i]};  // zeros past R
   }
   __syncthreads();
-  // Transposed copy, in two LDS passes so that every global store covers
-  // whole 128-byte lines of x8t.  Pass 1: wave w, pass p covers columns
-  // 16*(2w + p/2) .. +15 and rows 64*(p%2) .. +63; its 16-lane group q takes
-  // rows 16q .. 16q+15 of those (two transposing reads) into the column-major
-  // tile.  Pass 2: 8 lanes copy one column's 128 rows to x8t.
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane >> 4, li = lane & 15;
+  // 16 x 16 byte blocks: (ROWS / 16) x (COLS / 16) = 64 of them, four per
+  // 16-lane group; group g takes column block (g + 16 p) % (COLS / 16) ...
+  const int lane = threadIdx.x & 63;
+  const int g = threadIdx.x >> 4, li = lane & 15;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const int cb = 16 * (2 * wave + (p >> 1));
-    const int rb = 64 * (p & 1) + 16 * q;
+    const int blk = 16 * p + g;
+    const int cb = 16 * (blk % (COLS / 16)), rb = 16 * (blk / (COLS / 16));
     // source lane li = 2b + h points at tile row rb + b (+8), columns cb + 8h ..
-    const uint8_t* src = tile + (rb + (li >> 1)) * QR_STRIDE + cb + 8 * (li & 1);
+    const uint8_t* src = tile + (rb + (li >> 1)) * TS + cb + 8 * (li & 1);
     const intx2 t0 = lds_read_tr8(src);
-    const intx2 t1 = lds_read_tr8(src + 8 * QR_STRIDE);
-    *reinterpret_cast<intx4*>(tcol + (cb + li) * QR_CSTRIDE + rb) = intx4{t0[0], t0[1], t1[0], t1[1]};
+    const intx2 t1 = lds_read_tr8(src + 8 * TS);
+    *reinterpret_cast<intx4*>(tcol + (cb + li) * CS + rb) = intx4{t0[0], t0[1], t1[0], t1[1]};
   }
   __syncthreads();
+  // slab rows: 4 lanes per 64-token column run, consecutive columns in
+  // consecutive lanes, so a wave store covers 16 whole slab rows (1 KiB)
+  const int64_t cp = slab_rows(C);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int idx = k * 256 + threadIdx.x;
-    const int col = idx >> 3, ch = idx & 7;  // 8 lanes per column, 16 rows each
-    const int64_t rbase = r0 + 16 * ch;
-    if (rbase >= ldt) continue;
-    const intx4 w = *reinterpret_cast<const intx4*>(tcol + col * QR_CSTRIDE + 16 * ch);
-    uint8_t* dst = x8t + (c0 + col) * ldt + rbase;
-    if (rbase + 16 <= ldt && ((((uintptr_t)dst) & 15u) == 0)) {
-      *reinterpret_cast<intx4*>(dst) = w;
-    } else {
-      const int nv = (int)((ldt - rbase) < 16 ? (ldt - rbase) : 16);
-      for (int b = 0; b < nv; ++b) dst[b] = (uint8_t)((uint32_t)w[b >> 2] >> (8 * (b & 3)));
-    }
+    const int sl = idx / (4 * COLS), col = (idx % (4 * COLS)) >> 2, ch = idx & 3;
+    const int64_t t = r0 + 64 * sl;
+    if (t >= ldt) continue;  // ldt % 64 == 0
+    const intx4 w = *reinterpret_cast<const intx4*>(tcol + col * CS + 64 * sl + 16 * ch);
+    *reinterpret_cast<intx4*>(x8t + (t >> 6) * cp * 64 + (c0 + col) * 64 + 16 * ch) = w;
   }
   block_amax_atomic<4>(m, red, amax);
 }
@@ -589,13 +596,24 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
                            void* x8, void* x8t, int64_t ldt, void* stream) {
   // row- and token-sized buffers may be null when there are no rows
   if (!scale || !amax || (rows > 0 && cols > 0 && (!x || !x8 || !x8t))) return kErrNullPointer;
-  if (rows < 0 || cols < 0 || (cols % QR_TILE) != 0 || ldt < rows) return kErrBadShape;
-  if (!aligned16(x) || !aligned16(x8)) return kErrBadAlignment;
+  if (rows < 0 || cols < 0 || (cols % 128) != 0 || ldt < rows || (ldt % 64) != 0) return kErrBadShape;
+  if (!aligned16(x) || !aligned16(x8) || !aligned16(x8t)) return kErrBadAlignment;
   if (rows == 0 || cols == 0) return kOk;
-  // row blocks cover ldt, so that x8t columns rows..ldt-1 are written (zeros)
-  dim3 grid((unsigned)(cols / QR_TILE), (unsigned)((ldt + QR_TILE - 1) / QR_TILE));
-  hipLaunchKernelGGL(quant_rowcol_kernel, grid, dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, rows, cols, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt);
+  // the grid covers the slab's padded columns and all ldt tokens, so that
+  // every byte of x8t is written (zeros past rows and cols)
+  const int64_t cp = slab_rows(cols);
+  hipStream_t st = (hipStream_t)stream;
+  if (cols % 256 == 0) {
+    constexpr int COLS = 256, ROWS = QuantRowcolCfg<COLS>::kRows;
+    dim3 grid((unsigned)(cp / COLS), (unsigned)((ldt + ROWS - 1) / ROWS));
+    hipLaunchKernelGGL(quant_rowcol_kernel<COLS>, grid, dim3(256), 0, st, (const uint16_t*)x, rows, cols, scale,
+                       amax, (uint8_t*)x8, (uint8_t*)x8t, ldt);
+  } else {
+    constexpr int COLS = 128, ROWS = QuantRowcolCfg<COLS>::kRows;
+    dim3 grid((unsigned)(cp / COLS), (unsigned)((ldt + ROWS - 1) / ROWS));
+    hipLaunchKernelGGL(quant_rowcol_kernel<COLS>, grid, dim3(256), 0, st, (const uint16_t*)x, rows, cols, scale,
+                       amax, (uint8_t*)x8, (uint8_t*)x8t, ldt);
+  }
   return launch_status();
 }
 

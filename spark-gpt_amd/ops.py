@@ -86,14 +86,17 @@ def _state(scale: torch.Tensor, amax: torch.Tensor) -> None:
 
 # ------------------------------------------------------------------ quantizers
 def quant_e4m3_rowcol(x: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor):
-    """x8 = e4m3(x * scale[0]), x8t = x8^T ([cols, rows]), amax[0] max|x|."""
+    """x8 = e4m3(x * scale[0]) row-major [rows, cols]; x8t = the token-contiguous
+    K-slab copy of x8^T over ldt_of(rows) tokens ([ldt / 64, slab_rows(cols),
+    64], zeros past rows and cols); amax[0] max|x|."""
     _cuda_contig("x", x, torch.bfloat16, 2)
     R, C = x.shape
     _need(C % 128 == 0, "cols must be a multiple of 128")
+    ldt = ldt_of(R)
     x8 = torch.empty(R, C, dtype=E4M3, device=x.device)
-    x8t = torch.empty(C, R, dtype=E4M3, device=x.device)
+    x8t = slab_empty(C, R, E4M3, x.device)
     _lib.call("sfp8_quant_e4m3_rowcol", x.data_ptr(), R, C, scale.data_ptr(), amax.data_ptr(),
-              x8.data_ptr(), x8t.data_ptr(), R, _lib.stream_of(x))
+              x8.data_ptr(), x8t.data_ptr(), ldt, _lib.stream_of(x))
     return x8, x8t
 
 

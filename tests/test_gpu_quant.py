@@ -33,7 +33,7 @@ def test_e4m3_cast_exhaustive(dev, log2s):
     x8, x8t = sg.ops.quant_e4m3_rowcol(x.to(dev), s.to(dev), torch.zeros(5, device=dev))
     ref = O.e4m3(x.float() * s[0])
     assert torch.equal(u8(x8), u8(ref))
-    assert torch.equal(u8(x8t), u8(ref).t())
+    assert torch.equal(u8(sg.ops.unslab(x8t, x.shape[1])), u8(ref).t())
 
 
 def test_e5m2_cast_exhaustive_via_norm_bwd(dev):
@@ -72,29 +72,35 @@ def test_quant_rowcol_ragged(dev, R, C):
     x8, x8t = sg.ops.quant_e4m3_rowcol(x.to(dev), s.to(dev), amax)
     r8, r8t, ra = O.quant_rowcol(x, s[0])
     assert torch.equal(u8(x8), u8(r8))
-    assert torch.equal(u8(x8t), u8(r8t))
+    xt = u8(sg.ops.unslab(x8t, C))
+    assert torch.equal(xt[:, :R], u8(r8t))
+    assert torch.all(xt[:, R:] == 0)
+    assert torch.all(u8(x8t)[:, C:, :] == 0)  # slab padding rows
     assert amax[0].item() == ra.item()
     assert torch.all(amax[1:].cpu() == 0)
 
 
-@pytest.mark.parametrize("R,ldt", [(100, 100), (100, 300), (257, 1024), (1, 129)])
-def test_quant_rowcol_ldt_padding(dev, R, ldt):
-    """Through the C ABI with ldt > rows: x8t columns rows..ldt-1 are zeros."""
+@pytest.mark.parametrize("R,C,ldt", [(100, 256, 128), (100, 384, 320), (257, 128, 1024), (1, 256, 64),
+                                     (64, 512, 64)])
+def test_quant_rowcol_ldt_padding(dev, R, C, ldt):
+    """Through the C ABI with ldt > rows: x8t tokens rows..ldt-1 and the slab's
+    padding rows are written as zeros over a buffer prefilled with 0x55."""
     from spark_gpt_amd import _lib
-    C = 256
     g = torch.Generator().manual_seed(R + ldt)
     x = torch.randn(R, C, generator=g).to(torch.bfloat16)
     s = torch.tensor([4.0, 1, 1, 1, 1])
     amax = torch.zeros(5, device=dev)
     x8 = torch.empty(R, C, dtype=torch.uint8, device=dev)
-    x8t = torch.full((C, ldt), 0x55, dtype=torch.uint8, device=dev)
+    x8t = torch.full((ldt // 64, sg.ops.slab_rows(C), 64), 0x55, dtype=torch.uint8, device=dev)
     xd, sd = x.to(dev), s.to(dev)
     _lib.call("sfp8_quant_e4m3_rowcol", xd.data_ptr(), R, C, sd.data_ptr(), amax.data_ptr(), x8.data_ptr(),
               x8t.data_ptr(), ldt, _lib.stream_of(xd))
     r8, r8t, ra = O.quant_rowcol(x, s[0])
     assert torch.equal(x8.cpu(), u8(r8))
-    assert torch.equal(x8t[:, :R].cpu(), u8(r8t))
-    assert torch.all(x8t[:, R:] == 0)
+    xt = sg.ops.unslab(x8t, C).cpu()
+    assert torch.equal(xt[:, :R], u8(r8t))
+    assert torch.all(xt[:, R:] == 0)
+    assert torch.all(x8t[:, C:, :] == 0)
     assert amax[0].item() == ra.item()
 
 
@@ -120,7 +126,7 @@ def test_quant_rowcol_north_star_size(dev):
     x8, x8t = sg.ops.quant_e4m3_rowcol(xd, scale, amax)
     r8 = O.e4m3(x.float() * s_ref[0])
     assert torch.equal(u8(x8), u8(r8))
-    assert torch.equal(x8t.view(torch.uint8), x8.view(torch.uint8).t())
+    assert torch.equal(sg.ops.unslab(x8t, C).view(torch.uint8)[:, :R], x8.view(torch.uint8).t())
     assert amax[0].item() == x.float().abs().max().item()
 
 

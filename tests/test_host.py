@@ -67,6 +67,10 @@ def test_invalid_arguments_rejected_before_launch():
     # null pointers and bad shapes return negative codes without touching the device
     assert lib.sfp8_update_scales(None, None, 1, None) == -1
     assert lib.sfp8_quant_e4m3_rowcol(None, 4, 100, None, None, None, None, 4, None) == -1
+    # x8t is a K-slab over ldt tokens: ldt must be a multiple of 64 and cover the rows
+    assert lib.sfp8_quant_e4m3_rowcol(16, 4, 128, 16, 16, 16, 16, 100, None) == -2
+    assert lib.sfp8_quant_e4m3_rowcol(16, 100, 128, 16, 16, 16, 16, 64, None) == -2
+    assert lib.sfp8_quant_e4m3_rowcol(16, 4, 100, 16, 16, 16, 16, 64, None) == -2
     assert lib.sfp8_gemm_wgrad(16, 0, 16, 0, 256, 256, 256, 16, 16, 16, 16, 0, None) == -2  # A must be e5m2
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.check(-1, "x")
