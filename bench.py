@@ -19,8 +19,12 @@ Also reported on the same JSON line:
                 algorithmic traffic / mean duration vs 8 TB/s HBM
   kernels       per-kernel mean durations (each kernel alone, 10 launches),
                 with TFLOP/s or algorithmic GB/s
+  other_workloads  the muP base block (T=8192, D=256, I=1024) on the GPU: wall
+                clock over 20 steps after 5 warm-up steps
   cpu_baseline  the same FP8 recipe emulated in torch on the host cores (the
-                CPU oracle) on a bounded token sample, in TFLOP/s
+                CPU oracle) on a bounded token sample, in TFLOP/s; under
+                `other_workloads` the oracle on the muP base block and on an
+                8192-row sample of the quantizer input
 
 ``--probe`` runs, instead of the benchmark, one calibration copy (fp32 negate
 of 256 Mi elements: 1 GiB read + 1 GiB written) and then every kernel of the
@@ -137,6 +141,93 @@ def cpu_baseline(T: int, D: int, I: int) -> dict:
                   f"d_model={D}, ffn={I}; median of 3 steps after 1 warm-up; {med:.2f} s/step; "
                   f"cpu={cpu_model}",
     }
+
+
+def cpu_extra(quant_rows: int, quant_cols: int) -> dict:
+    """The CPU oracle on the other two measured workloads: the muP base block
+    (T=8192, D=256, I=1024, full size) and the standalone quantizer on a
+    bounded row sample of its 65536 x 4096 input."""
+    import torch
+
+    from oracle import fp8_mlp as O
+
+    out = {}
+    T, D, I = 8192, 256, 1024
+    g = torch.Generator().manual_seed(1)
+    h = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    nw = torch.ones(D)
+    wgu = torch.randn(2 * I, D, generator=g) * D ** -0.5
+    wd = torch.randn(D, I, generator=g) * I ** -0.5
+    dy = (torch.randn(T, D, generator=g) * 1e-3).to(torch.bfloat16)
+    scale, amax = torch.ones(5), torch.zeros(5)
+
+    def step():
+        _, saved = O.block_forward(h, nw, wgu, wd, scale, amax, 1e-6)
+        O.block_backward(dy, saved, scale, amax)
+
+    step()
+    O.update_scales(scale, amax)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    out["muP_base_T8192_D256_I1024"] = {"TFLOP/s": round(18.0 * T * D * I / med / 1e12, 4),
+                                        "s_per_step": round(med, 4)}
+    R = min(quant_rows, 8192)
+    x = torch.randn(R, quant_cols, generator=g)
+    x[:, : max(1, quant_cols // 1000)] *= 50.0
+    x = x.to(torch.bfloat16)
+    s0 = torch.tensor(1.0)
+    O.quant_rowcol(x, s0)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.quant_rowcol(x, s0)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    out["quantizer"] = {"GB/s": round(4.0 * R * quant_cols / med / 1e9, 2), "s_per_call": round(med, 4),
+                        "sample": f"{R} x {quant_cols} rows of the quantizer input (4 B/elem)"}
+    return out
+
+
+def time_block(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
+    """GPU fwd+bwd step time of the block at another shape (prewarm step and
+    scale roll first, as for the headline workload)."""
+    import torch
+
+    import spark_gpt_amd as sg
+    from spark_gpt_amd import ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1)
+    h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    params = [torch.ones(D, device=dev, requires_grad=True),
+              (torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5).requires_grad_(True),
+              (torch.randn(D, I, device=dev, generator=g) * I ** -0.5).requires_grad_(True)]
+    dy = (torch.randn(T, D, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    scale, amax = torch.ones(5, device=dev), torch.zeros(5, device=dev)
+
+    def step():
+        x = h.detach().requires_grad_(True)
+        y = sg._FP8MLPBlock.apply(x, *params, scale, amax, 1e-6)
+        torch.autograd.backward(y, dy, inputs=[x] + params)
+        for p in params:
+            p.grad = None
+
+    step()
+    ops.update_scales(scale, amax)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"tokens": T, "d_model": D, "ffn": I, "ms_per_step": round(ms, 4),
+            "TFLOP/s": round(18.0 * T * D * I / (ms * 1e-3) / 1e12, 2)}
 
 
 def main() -> None:
@@ -334,8 +425,11 @@ def main() -> None:
         "kernels": kernels,
         "saturation": saturation,
     }
+    # the muP base block (T=8192, D=256, I=1024): timed, not targeted
+    out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5)}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens, D, I)
+        out["cpu_baseline"]["other_workloads"] = cpu_extra(args.quant_rows, args.quant_cols)
     print(json.dumps(out), flush=True)
 
 
