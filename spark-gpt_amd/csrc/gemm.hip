@@ -287,16 +287,19 @@ struct SwigluPipe {
   static constexpr int kUnits = 16;  // 4 pairs each: unit u = row block u/4, pairs 4*(u%4) ..
   static constexpr int kSt = 4;      // LDS ring stages
   static constexpr int kDma = ML::kDma;
-  static_assert(NK >= 2 && NK % 2 == 0, "even K stages");
+  static_assert(NK >= kSt && NK % kSt == 0, "whole rings of K stages: a tile's stage s sits in slot s % kSt");
 
   // units run in stage kt: [ubeg(kt), ubeg(kt+1))
   static constexpr int ubeg(int kt) { return (kt * kUnits + NK - 1) / NK; }
 
   struct Ctx {
-    // main loop
+    // main loop; the last kSt - 1 stages of a tile load the first stages of
+    // the next tile (nra, nvoff_b), or repeat this tile's last stage when
+    // there is none (has_next false: nra, nvoff_b = ra, voff_b)
     uint8_t* lds;
-    __amdgpu_buffer_rsrc_t ra, rb;
-    uint32_t voff_a[4], voff_b[2], aoff[2], boff[2];
+    __amdgpu_buffer_rsrc_t ra, rb, nra;
+    uint32_t voff_a[4], voff_b[2], nvoff_b[2], aoff[2], boff[2];
+    bool has_next;
     int wave;
     typename ML::Frag f[2];
     floatx16 acc[4][2];
@@ -389,11 +392,12 @@ struct SwigluPipe {
     store16(c.hbuf + row * kPipeHStride + col, c.hw);
   }
 
-  // Stage KT: wait for stage KT+1 (vector stores count in vmcnt too; they
-  // complete in order after the DMA issued before them, so this wait is at
-  // worst slightly conservative after a stage that stored), barrier, DMA of
-  // stage KT+3, fragments of stage KT+1, the MFMAs of stage KT with this
-  // stage's epilogue units, then the row-block stores the units completed.
+  // Stage KT: wait for stage KT+1, barrier, DMA of stage KT+3 (of the next
+  // tile past the last stage), fragments of stage KT+1, the MFMAs of stage
+  // KT with this stage's epilogue units, then the row-block stores the units
+  // completed.  Vector stores count in vmcnt too and may complete after
+  // later loads, so the wait allows only the kDma loads issued after stage
+  // KT+1's; stores still in flight can make it wait for those as well.
   template <int KT>
   static SFP8_DEV void stage(Ctx& c, int a_ss, int b_ss) {
     constexpr int cur = KT & 1, nxt = cur ^ 1;
@@ -403,8 +407,14 @@ struct SwigluPipe {
     // with side effects stays ordered after every load issued before it, and
     // the units' arithmetic after the fences
     fences<ubeg(KT), ubeg(KT + 1)>(c);
-    constexpr int ld = KT + kSt - 1 < NK - 1 ? KT + kSt - 1 : NK - 1;
-    ML::load_stage(c.lds, (KT + kSt - 1) % kSt, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
+    constexpr int slot = (KT + kSt - 1) % kSt;
+    if constexpr (KT + kSt - 1 < NK) {
+      constexpr int ld = KT + kSt - 1;
+      ML::load_stage(c.lds, slot, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
+    } else {
+      const int ld = c.has_next ? KT + kSt - 1 - NK : NK - 1;
+      ML::load_stage(c.lds, slot, c.nra, c.rb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
+    }
     ML::read_frags(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
     ML::template mfma_range<0, ML::kMfma>(c.f[cur], c.acc);
     units<ubeg(KT), ubeg(KT + 1)>(c);
@@ -522,37 +532,55 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   }
   const int64_t rpad = slab_rows(I);
   const int ntiles = tiles_m * tiles_n;
-  int it = 0;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x, ++it) {
+  const int a_ss = (int)(ldt * kStage), b_ss = (int)(2 * I * kStage);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * kStage) + chunk;
+  c.rb = make_rsrc(w8, D * 2 * I);
+  // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64]; tile origin
+  // (m0, n0) -> A descriptor and B lane offsets
+  auto tile_operands = [&](int tile, int64_t& m0, int64_t& n0, __amdgpu_buffer_rsrc_t& ra, uint32_t (&voff_b)[2]) {
     int tm, tn;
     tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
-    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 64;
-    // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64]
-    c.ra = make_rsrc(x8 + m0 * kStage, D * ldt - m0 * kStage);
-    c.rb = make_rsrc(w8, D * 2 * I);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * kStage) + chunk;
+    m0 = (int64_t)tm * kTile;
+    n0 = (int64_t)tn * 64;
+    ra = make_rsrc(x8 + m0 * kStage, D * ldt - m0 * kStage);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = 32 * c.wave + 16 * j + (lane >> 2);
-      c.voff_b[j] = (uint32_t)(((r >> 6) * (int)I + (int)n0 + paired_col64(r)) * kStage) + chunk;
+      voff_b[j] = (uint32_t)(((r >> 6) * (int)I + (int)n0 + paired_col64(r)) * kStage) + chunk;
+    }
+  };
+  int it = 0;
+  int64_t m0 = 0, n0 = 0;
+  if (blockIdx.x < ntiles) {
+    // prologue, once per work-group: the first tile's stages 0..2 in flight,
+    // stage 0 landed, its fragments read.  Later tiles' first stages are
+    // loaded by the last stages of the tile before.
+    tile_operands(blockIdx.x, m0, n0, c.ra, c.voff_b);
+#pragma unroll
+    for (int s = 0; s < 3; ++s) ML::load_stage(lds, s, c.ra, c.rb, c.voff_a, c.voff_b, s * a_ss, s * b_ss, c.wave);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * ML::kDma) : "memory");
+    ML::read_frags(lds, 0, c.aoff, c.boff, c.f[0]);
+  }
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x, ++it) {
+    int64_t nm0 = m0, nn0 = n0;
+    c.has_next = tile + (int)gridDim.x < ntiles;
+    if (c.has_next) {
+      tile_operands(tile + (int)gridDim.x, nm0, nn0, c.nra, c.nvoff_b);
+    } else {
+      c.nra = c.ra;
+      c.nvoff_b[0] = c.voff_b[0];
+      c.nvoff_b[1] = c.voff_b[1];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) c.acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                                           0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // prologue: stages 0..2 in flight, stage 0 landed, its fragments read
-    const int a_ss = (int)(ldt * kStage), b_ss = (int)(2 * I * kStage);
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-      const int ld = s < NK - 1 ? s : NK - 1;
-      ML::load_stage(lds, s, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
-    }
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * ML::kDma) : "memory");
-    ML::read_frags(lds, 0, c.aoff, c.boff, c.f[0]);
     P::template stages<0>(c, a_ss, b_ss);
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // every wave's h-tile writes are done (the next tile's first stages stay
+    // in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // the previous tile's h tile is complete: its K-slab copy
     if (c.prev) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
     // this tile's g, u (bf16, unscaled) become the next epilogue's input
@@ -564,7 +592,14 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     c.pm0 = m0;
     c.pn0 = n0;
     c.hbuf = lds + kPipeRing + (it & 1) * kPipeHBytes;
+    m0 = nm0;
+    n0 = nn0;
+    c.ra = c.nra;
+    c.voff_b[0] = c.nvoff_b[0];
+    c.voff_b[1] = c.nvoff_b[1];
   }
+  // the last tile's repeated loads of its last stage are still in flight
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if (c.prev) {
     P::template tail_units<0>(c);
     __syncthreads();
