@@ -335,11 +335,17 @@ struct MainLoop {
       for (int j = 0; j < NB; ++j) acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                                         0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int last = nk - 1;
+    // Stages past the last keep their DMA instructions (the waits count
+    // them) but read through descriptors of zero records: every lane is out
+    // of range, so no memory is read and the unused ring slot gets zeros.
+    const __amdgpu_buffer_rsrc_t ra0 = make_rsrc(a_base, 0);
+    const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(b_base, 0);
     // prologue: stages 0 .. STAGES-2 in flight; stage 0 landed; its fragments read
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) {
-      const int ld = s < last ? s : last;
-      load_stage(lds, s, ra, rb, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
+      const bool live = s <= last;
+      const int ld = live ? s : last;
+      load_stage(lds, s, live ? ra : ra0, live ? rb : rb0, voff_a, voff_b, ld * a_sstride, ld * b_sstride, wave);
     }
     // kDma DMA instructions per wave per stage: stages 1 .. STAGES-2 may still fly
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (STAGES - 2)) : "memory");
@@ -351,18 +357,20 @@ struct MainLoop {
     for (int kt = 0; kt < nk; kt += 2) {
       // stage kt on f0, prefetch stage kt+1 into f1; stages kt+2 .. kt+STAGES-2 may fly
       {
-        const int ld = kt + STAGES - 1 < last ? kt + STAGES - 1 : last;
-        stage(lds, f0, f1, acc, (kt + STAGES - 1) % STAGES, ld, (kt + 1) % STAGES, ra, rb, voff_a, voff_b,
-              a_sstride, b_sstride, aoff, boff, wave);
+        const bool live = kt + STAGES - 1 <= last;
+        const int ld = live ? kt + STAGES - 1 : last;
+        stage(lds, f0, f1, acc, (kt + STAGES - 1) % STAGES, ld, (kt + 1) % STAGES, live ? ra : ra0,
+              live ? rb : rb0, voff_a, voff_b, a_sstride, b_sstride, aoff, boff, wave);
       }
       // stage kt+1 on f1, prefetch stage kt+2 into f0
       {
-        const int ld = kt + STAGES < last ? kt + STAGES : last;
-        stage(lds, f1, f0, acc, kt % STAGES, ld, (kt + 2) % STAGES, ra, rb, voff_a, voff_b, a_sstride, b_sstride,
-              aoff, boff, wave);
+        const bool live = kt + STAGES <= last;
+        const int ld = live ? kt + STAGES : last;
+        stage(lds, f1, f0, acc, kt % STAGES, ld, (kt + 2) % STAGES, live ? ra : ra0, live ? rb : rb0, voff_a,
+              voff_b, a_sstride, b_sstride, aoff, boff, wave);
       }
     }
-    // drain the DMA still in flight before the LDS is reused
+    // drain the (empty) DMA still in flight before the LDS is reused
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   }
 };
