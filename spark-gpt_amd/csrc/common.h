@@ -290,8 +290,9 @@ SFP8_DEV void lds_tile_store_slab_tr(const uint8_t* lds, int stride, uint8_t* ou
 // The same for an LDS tile of NTOK = 16, 32 or 64 tokens and ncols columns
 // (ncols % 64 == 0, t0 % NTOK == 0): NTOK / 16 lane groups take the token
 // blocks of one 16-column block, so a wave store covers 64 / NTOK * 16 slab
-// rows of NTOK bytes each (whole 64-byte rows when NTOK = 64).
-template <int NTOK>
+// rows of NTOK bytes each (whole 64-byte rows when NTOK = 64).  NW = waves
+// in the work-group.
+template <int NTOK, int NW = 4>
 SFP8_DEV void lds_rows_store_slab_tr(const uint8_t* lds, int ncols, int stride, uint8_t* out, int64_t rpad,
                                      int64_t t0, int64_t c0) {
   static_assert(NTOK == 16 || NTOK == 32 || NTOK == 64, "16, 32 or 64 tokens");
@@ -302,7 +303,7 @@ SFP8_DEV void lds_rows_store_slab_tr(const uint8_t* lds, int ncols, int stride, 
   const int64_t t = t0 + r;
   uint8_t* dst = out + (t >> 6) * rpad * 64 + (t & 63);
   const int passes = ncols / (16 * CB);
-  for (int u = wave; u < passes; u += 4) {
+  for (int u = wave; u < passes; u += NW) {
     const int c = 16 * (u * CB + q / G);
     const uint8_t* src = lds + (r + (li >> 1)) * stride + c + 8 * (li & 1);
     const intx2 a = lds_read_tr8(src);

@@ -164,21 +164,28 @@ struct NormCfg {
   // LDS row stride: D + 16 bytes puts the 8 rows of a transposing read on
   // distinct bank pairs
   static constexpr int STRIDE = D + 16;
-  static constexpr int PASSES = RT / (4 * RPW);                    // row passes per wave
-  // passes whose loads are issued together (about 8 chunks of 16 bytes per lane)
-  static constexpr int PB = (8 / CPL) < PASSES ? ((8 / CPL) > 0 ? 8 / CPL : 1) : PASSES;
+  // norm_quant: 8 waves per work-group up to D = 1024 (two work-groups per
+  // CU fit the LDS, so 4 waves per SIMD), 4 beyond (whose registers need 2
+  // waves per SIMD); QPASSES row passes per wave, PB of them with their loads
+  // issued together (about 8 chunks of 16 bytes per lane)
+  static constexpr int QW = D <= 1024 ? 8 : 4;
+  static constexpr int QPASSES = RT / (QW * RPW);
+  static constexpr int PB = (8 / CPL) < QPASSES ? ((8 / CPL) > 0 ? 8 / CPL : 1) : QPASSES;
+  // norm_bwd: 4 waves per work-group, PASSES row passes per wave, PB_BWD per batch
+  static constexpr int PASSES = RT / (4 * RPW);
   static constexpr int PB_BWD = (4 / CPL) < PASSES ? ((4 / CPL) > 0 ? 4 / CPL : 1) : PASSES;
-  static_assert(PASSES % PB == 0 && PASSES % PB_BWD == 0, "whole load batches");
+  static_assert(QPASSES % PB == 0 && PASSES % PB_BWD == 0, "whole load batches");
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void norm_quant_kernel(
+__global__ __launch_bounds__(64 * NormCfg<D>::QW) __attribute__((amdgpu_waves_per_eu(NormCfg<D>::QW / 2)))
+void norm_quant_kernel(
     const uint16_t* __restrict__ h, const float* __restrict__ nw, int64_t T, float eps,
     const float* __restrict__ scale, float* __restrict__ amax, uint8_t* __restrict__ x8,
     uint8_t* __restrict__ x8t, int64_t ldt, float* __restrict__ rstd) {
   using Cfg = NormCfg<D>;
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float red[4];
+  __shared__ float red[Cfg::QW];
   uint8_t* tile = smem;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
@@ -196,13 +203,14 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; }
   }
-  // wave wid takes row passes wid, wid + 4, ...; PB passes' loads are issued
-  // before any of them is reduced
-  for (int pb = 0; pb < Cfg::PASSES; pb += Cfg::PB) {
+  // wave wid takes row passes wid, wid + QW, ...; PB passes' loads are
+  // issued before any of them is reduced
+#pragma unroll 1
+  for (int pb = 0; pb < Cfg::QPASSES; pb += Cfg::PB) {
     intx4 v[Cfg::PB][Cfg::CPL];
 #pragma unroll
     for (int q = 0; q < Cfg::PB; ++q) {
-      const int64_t t = t0 + (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const int64_t t = t0 + (wid + Cfg::QW * (pb + q)) * Cfg::RPW + sr;
 #pragma unroll
       for (int c = 0; c < Cfg::CPL; ++c) {
         const int d = (c * Cfg::LPR + li) * 8;
@@ -211,7 +219,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
     }
 #pragma unroll
     for (int q = 0; q < Cfg::PB; ++q) {
-      const int r = (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const int r = (wid + Cfg::QW * (pb + q)) * Cfg::RPW + sr;
       const int64_t t = t0 + r;
       const bool valid = t < T;
       double ss = 0.0;
@@ -255,8 +263,8 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(
   }
   __syncthreads();
   // rows past T hold zero codes
-  lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0);
-  block_amax_atomic<4>(m, red, amax);
+  lds_rows_store_slab_tr<Cfg::RT, Cfg::QW>(tile, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0);
+  block_amax_atomic<Cfg::QW>(m, red, amax);
 }
 
 // --------------------------------------------------------------------------
@@ -562,7 +570,7 @@ static int launch_norm_quant(const void* h, const float* nw, int64_t T, float ep
   const unsigned nblk = (unsigned)(ldt / Cfg::RT);
   const int rc = allow_lds(norm_quant_kernel<D>, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(norm_quant_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, nw, T,
+  hipLaunchKernelGGL(norm_quant_kernel<D>, dim3(nblk), dim3(64 * Cfg::QW), lds, st, (const uint16_t*)h, nw, T,
                      eps, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt, rstd);
   return launch_status();
 }
