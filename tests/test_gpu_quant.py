@@ -16,19 +16,21 @@ def u8(t):
     return t.contiguous().view(torch.uint8).cpu()
 
 
-def all_bf16(nan: bool = True) -> torch.Tensor:
+def all_bf16(nan: bool = True, cols: int = 128) -> torch.Tensor:
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
     if not nan:
         f = bits.float()
         bits = bits[~torch.isnan(f)]
-        bits = bits[: (bits.numel() // 128) * 128]
-    return bits.reshape(-1, 128).contiguous()
+        bits = bits[: (bits.numel() // cols) * cols]
+    return bits.reshape(-1, cols).contiguous()
 
 
+@pytest.mark.parametrize("cols", [128, 256])
 @pytest.mark.parametrize("log2s", [-12, -3, 0, 1, 5, 12])
-def test_e4m3_cast_exhaustive(dev, log2s):
-    """Every bf16 bit pattern x scale: bytes equal torch's clamp+cast (NaN incl.)."""
-    x = all_bf16()
+def test_e4m3_cast_exhaustive(dev, log2s, cols):
+    """Every bf16 bit pattern x scale: bytes equal torch's clamp+cast (NaN
+    incl.), through the 128 x 128 tile (128 columns) and the 64 x 256 tile."""
+    x = all_bf16(cols=cols)
     s = torch.tensor([2.0 ** log2s, 1, 1, 1, 1])
     x8, x8t = sg.ops.quant_e4m3_rowcol(x.to(dev), s.to(dev), torch.zeros(5, device=dev))
     ref = O.e4m3(x.float() * s[0])
