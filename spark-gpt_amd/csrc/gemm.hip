@@ -268,7 +268,9 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
 // ALU does the epilogue).  The h bytes of a tile also go to one of two LDS
 // tiles; its token-contiguous (K-slab) copy is written at the next tile
 // boundary with LDS transpose reads.  The last tile's epilogue runs alone.
-// NK = D / 64 K stages, fully unrolled so each unit has a fixed stage.
+// NK = D / 64 K stages, fully unrolled so each unit has a fixed stage; the K
+// stream runs on across tiles (the last three stages of a tile load the next
+// tile's first three), so a tile boundary waits for no DMA.
 constexpr int kPipeHStride = 80;                    // 64 h bytes + 16 per LDS row
 constexpr int kPipeHBytes = kTile * kPipeHStride;   // one h tile
 constexpr int kPipeRing = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4>::kLds;  // 96 KiB
