@@ -672,6 +672,38 @@ SFP8_DEV void write_bf16_half(const uint8_t* lds, int p, int64_t m0, int64_t n0,
   }
 }
 
+// Residual words of staged half p, in write_bf16_half's order (16 per
+// thread); rows past T read as zero through the descriptor.
+SFP8_DEV void load_res_half(__amdgpu_buffer_rsrc_t rres, int p, int64_t n0, int64_t D, intx4 (&rv)[16]) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int idx = (int)threadIdx.x + 256 * k;
+    const int lr = idx >> 5, c = idx & 31;
+    const uint32_t off = (uint32_t)((half_tile_row(lr, p) * D + n0 + 8 * c) * 2);
+    rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0);
+  }
+}
+
+// write_bf16_half with the residual already in registers.
+SFP8_DEV void write_bf16_half_res(const uint8_t* lds, int p, int64_t m0, int64_t n0, int64_t T, int64_t D,
+                                  const intx4 (&rv)[16], uint16_t* __restrict__ out) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int idx = (int)threadIdx.x + 256 * k;
+    const int lr = idx >> 5, c = idx & 31;
+    const int64_t t = m0 + half_tile_row(lr, p), n = n0 + 8 * c;
+    if (t >= T || n >= D) continue;
+    intx4 o = *reinterpret_cast<const intx4*>(lds + lr * kBf16Stride + c * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a = (uint32_t)rv[k][i], b = (uint32_t)o[i];
+      o[i] = (int)pack2_bf16(__uint_as_float(b << 16) + __uint_as_float(a << 16),
+                             __uint_as_float(b & 0xffff0000u) + __uint_as_float(a & 0xffff0000u));
+    }
+    *reinterpret_cast<intx4*>(out + t * D + n) = o;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // (a7) down forward + residual (spark-gpt train.py:1019-1046):
 //   y = bf16(res + bf16(acc / (s2 * q_d)))
@@ -691,48 +723,22 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
       wd8 + n0 * kStage, I * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
       (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[1]);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int fr = lane & 31, g = lane >> 5;
-  const int cb = 128 * wn + 64 * g;
-  // every residual word of this lane is requested at once (one memory
-  // latency for the epilogue); rows past T read as zero through the
-  // descriptor's range check and are not stored
   const __amdgpu_buffer_rsrc_t rres = make_rsrc(res + m0 * D, (T - m0) * D * 2);
-  intx4 rv[4][4][2];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const uint32_t off = (uint32_t)(((128 * wm + 32 * tb + fr) * D + n0 + cb + 16 * nb) * 2);
-      rv[tb][nb][0] = __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0);
-      rv[tb][nb][1] = __builtin_amdgcn_raw_buffer_load_b128(rres, off + 16, 0, 0);
-    }
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int64_t t = m0 + 128 * wm + 32 * tb + fr;
-    if (t >= T) continue;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int64_t n = n0 + cb + 16 * nb;
-      if (n >= D) continue;
-      float o[16];
-      // out rounded to bf16 before the residual add (train.py:1043)
-      round16_bf16(acc[tb][nb], deq, o);
-      const intx4 r0 = rv[tb][nb][0];
-      const intx4 r1 = rv[tb][nb][1];
-      uint32_t w0[4], w1[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t a = (uint32_t)r0[i], b = (uint32_t)r1[i];
-        w0[i] = pack2_bf16(o[2 * i] + __uint_as_float(a << 16), o[2 * i + 1] + __uint_as_float(a & 0xffff0000u));
-        w1[i] = pack2_bf16(o[8 + 2 * i] + __uint_as_float(b << 16),
-                           o[8 + 2 * i + 1] + __uint_as_float(b & 0xffff0000u));
-      }
-      store16(y + t * D + n, w0);
-      store16(y + t * D + n + 8, w1);
-    }
-  }
+  // Every residual word the two staged halves add is requested at once (one
+  // memory latency), in the order the staged rows are written, so both the
+  // residual reads and the y writes are whole rows; rows past T read as zero
+  // through the descriptor's range check and are not stored.
+  intx4 rv0[16], rv1[16];
+  load_res_half(rres, 0, n0, D, rv0);
+  load_res_half(rres, 1, n0, D, rv1);
+  // out rounded to bf16 before the residual add (train.py:1043)
+  stage_bf16_half<0>(lds, acc, deq);
+  __syncthreads();
+  write_bf16_half_res(lds, 0, m0, n0, T, D, rv0, y);
+  __syncthreads();
+  stage_bf16_half<1>(lds, acc, deq);
+  __syncthreads();
+  write_bf16_half_res(lds, 1, m0, n0, T, D, rv1, y);
 }
 
 // ---------------------------------------------------------------------------
