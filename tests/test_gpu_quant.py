@@ -106,6 +106,25 @@ def test_quant_rowcol_ldt_padding(dev, R, C, ldt):
     assert amax[0].item() == ra.item()
 
 
+@pytest.mark.parametrize("C", [128, 256])
+def test_quant_rowcol_amax_ignores_nan(dev, C):
+    """NaN elements get torch's NaN codes; amax is the maximum over the finite
+    magnitudes (a NaN activation does not poison the next delayed scale)."""
+    g = torch.Generator().manual_seed(11 + C)
+    x = torch.randn(300, C, generator=g)
+    x[7, 5] = float("nan")
+    x[250, C - 1] = float("nan")
+    x[100, 3] = -37.5  # the largest finite magnitude
+    x = x.to(torch.bfloat16)
+    s = torch.tensor([2.0, 1, 1, 1, 1])
+    amax = torch.zeros(5, device=dev)
+    x8, x8t = sg.ops.quant_e4m3_rowcol(x.to(dev), s.to(dev), amax)
+    ref = O.e4m3(x.float() * s[0])
+    assert torch.equal(u8(x8), u8(ref))
+    assert torch.equal(u8(sg.ops.unslab(x8t, C))[:, :300], u8(ref).t())
+    assert amax[0].item() == 37.5
+
+
 def test_quant_rowcol_north_star_size(dev):
     """65536 x 4096 bf16 with 0.1% outlier columns x50, delayed scale from a
     prewarm pass; bytes, transpose, amax and next scale bit-exact."""
