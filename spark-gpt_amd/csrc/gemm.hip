@@ -801,55 +801,61 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
       lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
       kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * kStage, ldb * ip - n0 * kStage,
       [=](int r) { return plain_col(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
-  // gu8 is a K-slab [2I/64][ldt][64]: each lane's 64 gate (and 64 up)
-  // columns of a row are one 64-byte slab row.  Rows past T hold zeros (and
-  // their dh is zero: dy rows past T read as zero).  All 32 words of this
-  // lane are requested at once, so one memory latency covers the whole
-  // epilogue; blocks past column I get an out-of-range offset and read zeros
-  // (g = u = 0 gives zero gradients, and nothing there is stored).
+  // Row-order epilogue, in two passes of 128 tile rows (the rows of
+  // stage_bf16_half<P>): dh staged in LDS as bf16, then each thread takes
+  // 16-column chunks of one row, reading gu8 and writing dgu8 as whole K-slab
+  // rows; the codes also go to LDS for the token-contiguous dgu8t.
   const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 64, 2 * I * ldt - m0 * 64);
-  const int fr = lane & 31, g = lane >> 5;
-  const int cb = 128 * wn + 64 * g;
-  intx4 wg[4][4], wu[4][4];
+  const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
+  uint8_t* DH = lds;
+  uint8_t* G2 = lds + 128 * kBf16Stride;
+  uint8_t* U2 = G2 + 128 * kEpiStride2;
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
+  for (int P = 0; P < 2; ++P) {
+    // gu8 words of this thread's 8 chunks, requested at once
+    intx4 wg[8], wu[8];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int row = 128 * wm + 32 * tb + fr;
-      const int64_t j = n0 + cb + 16 * nb;
+    for (int k = 0; k < 8; ++k) {
+      const int item = 4 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
+      const int c = 64 * slab + 16 * (lane & 3);
+      const int row = half_tile_row(lr, P);
+      const int64_t j = n0 + c;
       const uint32_t jo = j < I ? (uint32_t)((j >> 6) * ldt * 64 + row * 64 + (j & 63)) : 0x80000000u;
-      wg[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
-      wu[tb][nb] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)(I * ldt), 0, 0);
+      wg[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
+      wu[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)(I * ldt), 0, 0);
     }
+    if (P == 1) __syncthreads();  // pass 0's dgu8t copy has read the LDS
+    // dh rounded to bf16 (train.py:1082)
+    if (P == 0) stage_bf16_half<0>(DH, acc, 1.0f);
+    else stage_bf16_half<1>(DH, acc, 1.0f);
+    __syncthreads();
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int row = 128 * wm + 32 * tb + fr;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int col = cb + 16 * nb;
+    for (int k = 0; k < 8; ++k) {
+      const int item = 4 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
+      const int c = 64 * slab + 16 * (lane & 3);
+      const int64_t t = m0 + half_tile_row(lr, P);
+      const intx4 h0 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c);
+      const intx4 h1 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c + 16);
       uint32_t pg[4], pu[4];
-      float dh[16];
-      // dh rounded to bf16 (train.py:1082)
-      round16_bf16(acc[tb][nb], 1.0f, dh);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t gw = (uint32_t)wg[tb][nb][w];
+        const uint32_t hw0 = (uint32_t)(w < 2 ? h0[2 * w] : h1[2 * w - 4]);
+        const uint32_t hw1 = (uint32_t)(w < 2 ? h0[2 * w + 1] : h1[2 * w - 3]);
+        const float dhv[4] = {__uint_as_float(hw0 << 16), __uint_as_float(hw0 & 0xffff0000u),
+                              __uint_as_float(hw1 << 16), __uint_as_float(hw1 & 0xffff0000u)};
+        const uint32_t gw = (uint32_t)wg[k][w];
         const floatx2 g01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, false);
         const floatx2 g23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, true);
-        const floatx2 u01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[tb][nb][w], 1.0f, false);
-        const floatx2 u23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[tb][nb][w], 1.0f, true);
+        const floatx2 u01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[k][w], 1.0f, false);
+        const floatx2 u23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[k][w], 1.0f, true);
         const float g8v[4] = {g01.x, g01.y, g23.x, g23.y}, u8v[4] = {u01.x, u01.y, u23.x, u23.y};
         float dg[4], du[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const floatx2 f = lut[(gw >> (8 * e)) & 0xFFu];  // (sig, sig * (1 + g * (1 - sig)))
-          const float d = dh[4 * w + e];
-          dg[e] = (d * u8v[e]) * f.y;
-          du[e] = (d * g8v[e]) * f.x;
+          dg[e] = (dhv[e] * u8v[e]) * f.y;
+          du[e] = (dhv[e] * g8v[e]) * f.x;
         }
-        // NaN-propagating maximum of the eight magnitudes: one compare tells
-        // whether every value is finite and inside the e5m2 range (then the
-        // clamp is a no-op and no NaN needs patching)
         float mw = max3_nan(fabsf(dg[0]), fabsf(du[0]), fabsf(dg[1]));
         mw = max3_nan(mw, fabsf(du[1]), fabsf(dg[2]));
         mw = max3_nan(mw, fabsf(du[2]), fabsf(dg[3]));
@@ -866,29 +872,23 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
         }
         m3 = fmaxf(m3, mw);
       }
-      store16(Gt + row * kEpiStride2 + col, pg);
-      store16(Ut + row * kEpiStride2 + col, pu);
+      store16(G2 + lr * kEpiStride2 + c, pg);
+      store16(U2 + lr * kEpiStride2 + c, pu);
+      // dgu8 is a K-slab [2I/64][ldt][64]; four lanes write one 64-byte row
+      if (c < cols) {
+        const int64_t j = n0 + c;
+        store16(dgu8 + (j >> 6) * ldt * 64 + t * 64 + (j & 63), pg);
+        store16(dgu8 + ((I + j) >> 6) * ldt * 64 + t * 64 + (j & 63), pu);
+      }
     }
-  }
-  __syncthreads();
-  const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
-  // dgu8 is a K-slab [2I/64][ldt][64] (the gate/up dgrad's A operand): the
-  // tile's gate and up columns are 64-column blocks of every tile row (rows
-  // past T hold zeros: their dh is zero)
-  if (cols == kTile) {
-    lds_rows_to_kslab<4>(Gt, kTile, kEpiStride2, dgu8, ldt, m0, n0);
-    lds_rows_to_kslab<4>(Ut, kTile, kEpiStride2, dgu8, ldt, m0, I + n0);
-  } else {
-    lds_rows_to_kslab<2>(Gt, kTile, kEpiStride2, dgu8, ldt, m0, n0);
-    lds_rows_to_kslab<2>(Ut, kTile, kEpiStride2, dgu8, ldt, m0, I + n0);
-  }
-  // the token-contiguous dgu8t (rows past T hold zero codes)
-  if (cols == kTile) {
-    lds_tile_store_slab_tr<16>(Gt, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0);
-    lds_tile_store_slab_tr<16>(Ut, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0);
-  } else {
-    lds_tile_store_slab_tr<8>(Gt, kEpiStride2, dgu8t, slab_rows(2 * I), m0, n0);
-    lds_tile_store_slab_tr<8>(Ut, kEpiStride2, dgu8t, slab_rows(2 * I), m0, I + n0);
+    __syncthreads();
+    // the token-contiguous dgu8t: local rows 0-63 are tile rows 64P.., rows
+    // 64-127 tile rows 128 + 64P.. (rows past T hold zero codes)
+    const int64_t rp2 = slab_rows(2 * I);
+    lds_rows_store_slab_tr<64>(G2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, n0);
+    lds_rows_store_slab_tr<64>(G2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, n0);
+    lds_rows_store_slab_tr<64>(U2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, I + n0);
+    lds_rows_store_slab_tr<64>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, I + n0);
   }
   __syncthreads();  // the next tile's DMA overwrites the staging tiles
   }
