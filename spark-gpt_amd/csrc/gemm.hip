@@ -283,6 +283,16 @@ SFP8_DEV int paired_col64(int r) {
   return 32 * wn + 16 * ((w >> 2) & 1) + 4 * (w >> 3) + (w & 3);
 }
 
+// The h tile's 256 rows of 64 bytes to 256 consecutive K-slab rows.
+SFP8_DEV void pipe_h8_rows(const uint8_t* hbuf, uint8_t* dst) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = 256 * k + (int)threadIdx.x, r = idx >> 2, ch = idx & 3;
+    *reinterpret_cast<intx4*>(dst + r * 64 + 16 * ch) =
+        *reinterpret_cast<const intx4*>(hbuf + r * kPipeHStride + 16 * ch);
+  }
+}
+
 template <int NK>
 struct SwigluPipe {
   using ML = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4>;
@@ -389,7 +399,6 @@ struct SwigluPipe {
       // T hold the zeros computed from x8's zero padding)
       store16(c.gu8 + (c.pn0 >> 6) * c.ldt * 64 + t * 64 + col, c.gw);
       store16(c.gu8 + ((c.I + c.pn0) >> 6) * c.ldt * 64 + t * 64 + col, c.uw);
-      store16(c.h8 + (c.pn0 >> 6) * c.ldt * 64 + t * 64 + col, c.hw);
     }
     store16(c.hbuf + row * kPipeHStride + col, c.hw);
   }
@@ -583,8 +592,12 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     // every wave's h-tile writes are done (the next tile's first stages stay
     // in flight)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    // the previous tile's h tile is complete: its K-slab copy
-    if (c.prev) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
+    // the previous tile's h tile is complete: its K-slab copies (h8: 256
+    // token rows of 64 bytes, one contiguous block; h8t transposed)
+    if (c.prev) {
+      pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
+      lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
+    }
     // this tile's g, u (bf16, unscaled) become the next epilogue's input
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
@@ -605,6 +618,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   if (c.prev) {
     P::template tail_units<0>(c);
     __syncthreads();
+    pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
     lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
   }
   float* red = reinterpret_cast<float*>(lds + kPipeRing + 2 * kPipeHBytes);
