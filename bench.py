@@ -2,16 +2,21 @@
 
 Workload (default): tokens=65536, d_model=1024, ffn=3072 (Qwen3-0.6B width),
 bf16 inputs ~N(0,1), weights ~N(0,1/fan_in), upstream grads ~N(0,1e-3),
-seed-fixed, after one prewarm step + scale roll.  A step is one forward and
-backward of the block (7-argument autograd Function, all kernels on the
-current stream).  Value = 18*T*D*I FLOP / step time, in TFLOP/s.
+seed-fixed, after one prewarm step + scale roll.  A step is one training
+step of the block: forward and backward through the 7-argument autograd
+Function, then the post-step hook ``fp8_update_scales`` (the delayed-scale
+roll and the once-per-optimizer-step re-quantization of the fp32 masters),
+all on the current stream.  Value = 18*T*D*I FLOP / step time, in TFLOP/s.
 
 Also reported on the same JSON line:
-  roofline      the kernel taking the most time per step: HIP events recorded
-                on its stream around each of its launches inside the timed
-                steps; algorithmic FLOP per launch / mean duration vs the dense
-                MFMA peak of its input type; `traffic` = HBM bytes per launch
-                from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+  kernels_in_step  per-kernel mean duration inside the step: a second pass of
+                the same steps with HIP events recorded on the launch stream
+                around every C-ABI launch
+  roofline      the kernel taking the most time per step (from that pass):
+                algorithmic FLOP (or bytes) per launch / mean in-step duration
+                vs the dense MFMA peak of its input type (or HBM); `traffic` =
+                HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+                WRITE_SIZE summary
                 (profiles/traffic_fwd_bwd_T65536_D1024_I3072.md), null for
                 other workloads
   quantizer     the standalone quantizer (bf16 65536x4096 with 0.1% x50 outlier
@@ -25,6 +30,10 @@ Also reported on the same JSON line:
                 CPU oracle) on a bounded token sample, in TFLOP/s; under
                 `other_workloads` the oracle on the muP base block and on an
                 8192-row sample of the quantizer input
+
+``--trace`` runs only the headline steps (prewarm, warm-up, timed and
+instrumented passes), so that a ``rocprofv3 --kernel-trace --stats`` summary
+of it averages in-step launches of the headline shape only.
 
 ``--probe`` runs, instead of the benchmark, one calibration copy (fp32 negate
 of 256 Mi elements: 1 GiB read + 1 GiB written) and then every kernel of the
@@ -61,6 +70,8 @@ def parse():
     p.add_argument("--quant-rows", type=int, default=65536)
     p.add_argument("--quant-cols", type=int, default=4096)
     p.add_argument("--probe", action="store_true", help="one launch of each kernel, for counter passes")
+    p.add_argument("--trace", action="store_true",
+                   help="headline steps only (no standalone kernels, quantizer, other shapes or CPU leg)")
     p.add_argument("--dist", choices=("normal", "student-t"), default="normal",
                    help="activations: N(0,1), or Student-t with 3 degrees of freedom (heavy tails)")
     return p.parse_args()
@@ -192,32 +203,56 @@ def cpu_extra(quant_rows: int, quant_cols: int) -> dict:
     return out
 
 
-def time_block(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
-    """GPU fwd+bwd step time of the block at another shape (prewarm step and
-    scale roll first, as for the headline workload)."""
+class _Norm:
+    """The RMSNorm parameters the block reads (weight, eps)."""
+
+    def __init__(self, weight, eps=1e-6):
+        self.weight, self.eps = weight, eps
+
+
+def make_block(T: int, D: int, I: int, dist: str = "normal", seed: int = 1):
+    """(h, dy, norm, mlp, step): synthetic inputs of the workload and one
+    training step of the block (forward, backward, post-step hook)."""
     import torch
 
     import spark_gpt_amd as sg
-    from spark_gpt_amd import ops
 
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(1)
-    h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
-    params = [torch.ones(D, device=dev, requires_grad=True),
-              (torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5).requires_grad_(True),
-              (torch.randn(D, I, device=dev, generator=g) * I ** -0.5).requires_grad_(True)]
+    g = torch.Generator(device=dev).manual_seed(seed)
+    if dist == "normal":
+        h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    else:  # Student-t, 3 degrees of freedom: z / sqrt(chi2_3 / 3)
+        z = torch.randn(T, D, device=dev, generator=g)
+        chi = sum(torch.randn(T, D, device=dev, generator=g) ** 2 for _ in range(3))
+        h = (z / torch.sqrt(chi / 3)).to(torch.bfloat16)
+        del z, chi
+    mlp = sg.MLP(D, I).to(dev).train()
+    with torch.no_grad():
+        mlp.gate_up_proj.weight.copy_(torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5)
+        mlp.down_proj.weight.copy_(torch.randn(D, I, device=dev, generator=g) * I ** -0.5)
+    norm = _Norm(torch.ones(D, device=dev, requires_grad=True))
     dy = (torch.randn(T, D, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
-    scale, amax = torch.ones(5, device=dev), torch.zeros(5, device=dev)
+    params = [norm.weight, mlp.gate_up_proj.weight, mlp.down_proj.weight]
 
     def step():
         x = h.detach().requires_grad_(True)
-        y = sg._FP8MLPBlock.apply(x, *params, scale, amax, 1e-6)
+        y = sg.fp8_mlp_block(x, norm, mlp)
         torch.autograd.backward(y, dy, inputs=[x] + params)
         for p in params:
             p.grad = None
+        # post-step hook (train.py:4049-4050): scale roll + weight re-quantization
+        sg.fp8_update_scales(mlp)
 
+    return h, dy, norm, mlp, step
+
+
+def time_block(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
+    """GPU training-step time of the block at another shape (prewarm step and
+    scale roll first, as for the headline workload)."""
+    import torch
+
+    _h, _dy, _norm, _mlp, step = make_block(T, D, I)
     step()
-    ops.update_scales(scale, amax)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -230,6 +265,18 @@ def time_block(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
             "TFLOP/s": round(18.0 * T * D * I / (ms * 1e-3) / 1e12, 2)}
 
 
+def launch_name(sym: str, a, D: int, I: int) -> str:
+    """Kernel name of a C-ABI launch (symbol, its arguments)."""
+    if sym == "sfp8_weight_quant":
+        return "weight_quant_gu" if a[1] == 2 * I else "weight_quant_down"
+    if sym == "sfp8_gemm_wgrad":
+        return "wgrad_down" if a[4] == D else "wgrad_gateup"
+    return {"sfp8_norm_quant": "norm_quant", "sfp8_gemm_gateup_swiglu_fwd": "gateup_swiglu_fwd",
+            "sfp8_gemm_down_fwd": "down_fwd", "sfp8_gemm_down_dgrad_swiglu": "down_dgrad_swiglu_bf16",
+            "sfp8_gemm_gateup_dgrad": "gateup_dgrad", "sfp8_norm_bwd": "norm_bwd",
+            "sfp8_update_scales": "update_scales"}.get(sym, sym)
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -239,170 +286,147 @@ def main() -> None:
 
     import torch
 
-    import spark_gpt_amd as sg
     from spark_gpt_amd import _lib, ops
 
     dev = torch.device("cuda:0")
     T, D, I = args.tokens, args.d_model, args.ffn
-    g = torch.Generator(device=dev).manual_seed(1)
-    if args.dist == "normal":
-        h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
-    else:  # Student-t, 3 degrees of freedom: z / sqrt(chi2_3 / 3)
-        z = torch.randn(T, D, device=dev, generator=g)
-        chi = sum(torch.randn(T, D, device=dev, generator=g) ** 2 for _ in range(3))
-        h = (z / torch.sqrt(chi / 3)).to(torch.bfloat16)
-        del z, chi
-    nw = torch.ones(D, device=dev, requires_grad=True)
-    wgu = (torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5).requires_grad_(True)
-    wd = (torch.randn(D, I, device=dev, generator=g) * I ** -0.5).requires_grad_(True)
-    dy = (torch.randn(T, D, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
-    scale = torch.ones(5, device=dev)
-    amax = torch.zeros(5, device=dev)
-    params = [nw, wgu, wd]
-
-    def step():
-        x = h.detach().requires_grad_(True)
-        y = sg._FP8MLPBlock.apply(x, *params, scale, amax, 1e-6)
-        torch.autograd.backward(y, dy, inputs=[x] + params)
-        for p in params:
-            p.grad = None
-
-    step()                            # prewarm: records amax under scale 1
-    ops.update_scales(scale, amax)    # roll, as the trainer does after the prewarm step
-
-    # ---- every kernel of the step, alone (HIP events on the current stream) ----
+    h, dy, norm, mlp, step = make_block(T, D, I, args.dist)
+    scale, amax = mlp.fp8_scale, mlp.fp8_amax
+    step()  # prewarm: records amax under scale 1, then the roll (as the trainer does)
     stream = torch.cuda.current_stream(dev)
-    nwd = nw.detach()
-    x8, x8t, rstd = ops.norm_quant(h, nwd, scale, amax, 1e-6)
-    wscale = torch.empty(2, device=dev)
-    w8, w8t, _ = ops.weight_quant(wgu.detach(), wscale[0:1], w8=True, w8t=True)
-    wd8, _, wdt = ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True)
-    gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I)
-    dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
-    dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
-    dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax)
-    # saturation per fp8 site after the scale roll: codes at the format's
-    # largest magnitude (e4m3 448 = 0x7E, e5m2 57344 = 0x7B, either sign)
-    def at_max(t, code):
-        return int(((t.view(torch.uint8) & 0x7F) == code).sum())
-    saturation = {"x": at_max(x8, 0x7E), "gu": at_max(gu8, 0x7E), "h": at_max(h8, 0x7E),
-                  "d_gu": at_max(dgu8, 0x7B), "dy": at_max(dy8t, 0x7B),
-                  "elements": {"x": T * D, "gu": 2 * T * I, "h": T * I, "d_gu": 2 * T * I, "dy": T * D}}
-    # name -> (call, C-ABI symbol, predicate on the symbol's arguments, FLOP, algorithmic bytes)
-    kern = {
-        "norm_quant": (lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6), "sfp8_norm_quant", None,
-                       None, T * (4.0 * D + 4)),
-        "weight_quant_gu": (lambda: ops.weight_quant(wgu.detach(), wscale[0:1], w8=True, w8t=True),
-                            "sfp8_weight_quant", None, None, 10.0 * 2 * I * D),
-        "weight_quant_down": (lambda: ops.weight_quant(wd.detach(), wscale[1:2], w8=True, bf16t=True),
-                              "sfp8_weight_quant", None, None, 11.0 * D * I),
-        "gateup_swiglu_fwd": (lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I),
-                              "sfp8_gemm_gateup_swiglu_fwd", None, 4.0 * T * D * I, None),
-        "down_fwd": (lambda: ops.down_fwd(h8, wd8, h, scale, wscale), "sfp8_gemm_down_fwd", None,
-                     2.0 * T * D * I, None),
-        "down_dgrad_swiglu_bf16": (lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax),
-                                   "sfp8_gemm_down_dgrad_swiglu", None, 2.0 * T * D * I, None),
-        "gateup_dgrad": (lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D), "sfp8_gemm_gateup_dgrad", None,
-                         4.0 * T * D * I, None),
-        "norm_bwd": (lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax), "sfp8_norm_bwd", None,
-                     None, T * (9.0 * D + 4)),
-        "wgrad_down": (lambda: ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3]), "sfp8_gemm_wgrad",
-                       lambda a: a[4] == D, 2.0 * T * D * I, None),
-        "wgrad_gateup": (lambda: ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1]), "sfp8_gemm_wgrad",
-                         lambda a: a[4] == 2 * I, 4.0 * T * D * I, None),
+
+    # FLOP or algorithmic bytes per launch of each kernel
+    work = {
+        "norm_quant": (None, T * (4.0 * D + 4)),
+        "weight_quant_gu": (None, 10.0 * 2 * I * D),
+        "weight_quant_down": (None, 11.0 * D * I),
+        "gateup_swiglu_fwd": (4.0 * T * D * I, None),
+        "down_fwd": (2.0 * T * D * I, None),
+        "down_dgrad_swiglu_bf16": (2.0 * T * D * I, None),
+        "gateup_dgrad": (4.0 * T * D * I, None),
+        "norm_bwd": (None, T * (9.0 * D + 4)),
+        "wgrad_down": (2.0 * T * D * I, None),
+        "wgrad_gateup": (4.0 * T * D * I, None),
+        "update_scales": (None, 40.0),
     }
 
-    if args.probe:
-        # calibration copy of known size, then one launch of each kernel
-        src = torch.ones(256 << 20, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
-        for name, (fn, *_rest) in kern.items():
-            fn()
-            torch.cuda.synchronize()
-            print(f"probe {name} done", flush=True)
-        xq = torch.randn(args.quant_rows, args.quant_cols, device=dev).to(torch.bfloat16)
-        torch.cuda.synchronize()
-        ops.quant_e4m3_rowcol(xq, scale, amax)
-        torch.cuda.synchronize()
-        print("probe quantizer done", flush=True)
-        print(json.dumps({"probe": list(kern) + ["quantizer"], "copy_bytes_read": 1 << 30,
-                          "copy_bytes_written": 1 << 30}))
-        return
-
-    kernels = {}
-    for name, (fn, _sym, _pred, fl, by) in kern.items():
-        kms = timed_launches(fn, 10, stream)
-        rec = {"ms": round(kms, 4)}
+    def rates(name, ms):
+        fl, by = work.get(name, (None, None))
+        rec = {"ms": round(ms, 4)}
         if fl:
-            rec["tflops"] = round(fl / (kms * 1e-3) / 1e12, 1)
+            rec["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
         if by:
-            rec["GB/s"] = round(by / (kms * 1e-3) / 1e9, 1)
-        kernels[name] = rec
-    dom = max(kernels, key=lambda k: kernels[k]["ms"])
-    _fn, dom_sym, dom_pred, dom_flop, dom_bytes = kern[dom]
+            rec["GB/s"] = round(by / (ms * 1e-3) / 1e9, 1)
+        return rec
 
-    # ---- timed steps; events around each launch of the dominant kernel ----
+    out_extra = {}
+    if args.probe or not args.trace:
+        # every kernel of the step alone (HIP events on the current stream)
+        nwd = norm.weight.detach()
+        x8, x8t, rstd = ops.norm_quant(h, nwd, scale, amax, 1e-6)
+        wscale = torch.empty(2, device=dev)
+        w8, w8t, _ = ops.weight_quant(mlp.gate_up_proj.weight.detach(), wscale[0:1], w8=True, w8t=True)
+        wd8, _, wdt = ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True, bf16t=True)
+        gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I)
+        dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
+        dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
+        dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax)
+
+        # saturation per fp8 site after the scale roll: codes at the format's
+        # largest magnitude (e4m3 448 = 0x7E, e5m2 57344 = 0x7B, either sign)
+        def at_max(t, code):
+            return int(((t.view(torch.uint8) & 0x7F) == code).sum())
+
+        out_extra["saturation"] = {
+            "x": at_max(x8, 0x7E), "gu": at_max(gu8, 0x7E), "h": at_max(h8, 0x7E), "d_gu": at_max(dgu8, 0x7B),
+            "dy": at_max(dy8t, 0x7B),
+            "elements": {"x": T * D, "gu": 2 * T * I, "h": T * I, "d_gu": 2 * T * I, "dy": T * D}}
+        kern = {
+            "norm_quant": lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6),
+            "weight_quant_gu": lambda: ops.weight_quant(mlp.gate_up_proj.weight.detach(), wscale[0:1], w8=True,
+                                                        w8t=True),
+            "weight_quant_down": lambda: ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True,
+                                                          bf16t=True),
+            "gateup_swiglu_fwd": lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I),
+            "down_fwd": lambda: ops.down_fwd(h8, wd8, h, scale, wscale),
+            "down_dgrad_swiglu_bf16": lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax),
+            "gateup_dgrad": lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D),
+            "norm_bwd": lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax),
+            "wgrad_down": lambda: ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3]),
+            "wgrad_gateup": lambda: ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1]),
+        }
+        if args.probe:
+            # calibration copy of known size, then one launch of each kernel
+            src = torch.ones(256 << 20, device=dev)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            torch.neg(src, out=dst)
+            torch.cuda.synchronize()
+            del src, dst
+            for name, fn in kern.items():
+                fn()
+                torch.cuda.synchronize()
+                print(f"probe {name} done", flush=True)
+            xq = torch.randn(args.quant_rows, args.quant_cols, device=dev).to(torch.bfloat16)
+            torch.cuda.synchronize()
+            ops.quant_e4m3_rowcol(xq, scale, amax)
+            torch.cuda.synchronize()
+            print("probe quantizer done", flush=True)
+            print(json.dumps({"probe": list(kern) + ["quantizer"], "copy_bytes_read": 1 << 30,
+                              "copy_bytes_written": 1 << 30}))
+            return
+        out_extra["kernels"] = {name: rates(name, timed_launches(fn, 10, stream)) for name, fn in kern.items()}
+        del x8, x8t, rstd, w8, w8t, wd8, wdt, gu8, h8, h8t, dgu8, dgu8t, dxn, dh, dnw, dy8t
+
+    # ---- timed steps (clean: nothing but the step's own launches) ----
     for _ in range(args.warmup):
         step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    flop = 18.0 * T * D * I
+    tflops = flop / (ms * 1e-3) / 1e12
+
+    # ---- the same steps again, HIP events around every C-ABI launch ----
     marks = []
     plain_call = _lib.call
 
     def traced_call(name, *a):
-        if name != dom_sym or (dom_pred is not None and not dom_pred(a)):
-            return plain_call(name, *a)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         plain_call(name, *a)
         e1.record(stream)
-        marks.append((e0, e1))
+        marks.append((launch_name(name, a, D, I), e0, e1))
 
-    torch.cuda.synchronize()
     _lib.call = traced_call
     try:
-        t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / args.steps
     finally:
         _lib.call = plain_call
-    flop = 18.0 * T * D * I
-    tflops = flop / (ms * 1e-3) / 1e12
-    dom_ms = sum(a.elapsed_time(b) for a, b in marks) / max(1, len(marks))
-
+    per = {}
+    for name, e0, e1 in marks:
+        per.setdefault(name, []).append(e0.elapsed_time(e1))
+    in_step = {n: dict(rates(n, sum(v) / len(v)), launches_per_step=len(v) / args.steps) for n, v in per.items()}
+    dom = max(in_step, key=lambda n: in_step[n]["ms"] * in_step[n]["launches_per_step"])
+    dom_ms = in_step[dom]["ms"]
+    dom_flop, dom_bytes = work[dom]
     traffic = read_traffic(dom) if (T, D, I) == TRAFFIC_WORKLOAD else None
     if dom_flop:
         achieved = dom_flop / (dom_ms * 1e-3) / 1e12
         peak = BF16_PEAK_TFLOPS if "bf16" in dom else FP8_PEAK_TFLOPS
         roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": peak,
                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
-                    "flop_per_launch": dom_flop, "launches_timed": len(marks), "ms_per_launch": round(dom_ms, 4)}
+                    "flop_per_launch": dom_flop, "launches_timed": len(per[dom]), "ms_per_launch": round(dom_ms, 4)}
     else:
         achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                    "bytes_per_launch": dom_bytes, "launches_timed": len(marks), "ms_per_launch": round(dom_ms, 4)}
-
-    # ---- standalone quantizer (HBM-bound) ----
-    R, C = args.quant_rows, args.quant_cols
-    gq = torch.Generator(device=dev).manual_seed(3)
-    xq = torch.randn(R, C, device=dev, generator=gq)
-    cols = torch.randperm(C, device=dev, generator=gq)[: max(1, C // 1000)]
-    xq[:, cols] *= 50.0
-    xq = xq.to(torch.bfloat16)
-    qs, qa = torch.ones(5, device=dev), torch.zeros(5, device=dev)
-    ops.quant_e4m3_rowcol(xq, qs, qa)
-    ops.update_scales(qs, qa)
-    qms = timed_launches(lambda: ops.quant_e4m3_rowcol(xq, qs, qa), 20, stream)
-    qbytes = 4.0 * R * C
-    qgbps = qbytes / (qms * 1e-3) / 1e9
-    quant = {"rows": R, "cols": C, "ms": round(qms, 4), "GB/s": round(qgbps, 1),
-             "frac_hbm": round(qgbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": qbytes}
-    del xq
+                    "bytes_per_launch": dom_bytes, "launches_timed": len(per[dom]), "ms_per_launch": round(dom_ms, 4)}
 
     out = {
         "metric": "FP8 MLP fwd+bwd TFLOP/s (% FP8 MFMA peak); quantize GB/s (% HBM peak)",
@@ -421,15 +445,31 @@ def main() -> None:
         "config": {"workload": "fp8_swiglu_mlp_block_fwd_bwd", "tokens": T, "d_model": D, "ffn": I,
                    "flop_per_step": flop, "frac_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4)},
         "roofline": roofline,
-        "quantizer": quant,
-        "kernels": kernels,
-        "saturation": saturation,
+        "kernels_in_step": in_step,
     }
-    # the muP base block (T=8192, D=256, I=1024): timed, not targeted
-    out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5)}
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_tokens, D, I)
-        out["cpu_baseline"]["other_workloads"] = cpu_extra(args.quant_rows, args.quant_cols)
+    out.update(out_extra)
+    if not args.trace:
+        # ---- standalone quantizer (HBM-bound) ----
+        R, C = args.quant_rows, args.quant_cols
+        gq = torch.Generator(device=dev).manual_seed(3)
+        xq = torch.randn(R, C, device=dev, generator=gq)
+        cols = torch.randperm(C, device=dev, generator=gq)[: max(1, C // 1000)]
+        xq[:, cols] *= 50.0
+        xq = xq.to(torch.bfloat16)
+        qs, qa = torch.ones(5, device=dev), torch.zeros(5, device=dev)
+        ops.quant_e4m3_rowcol(xq, qs, qa)
+        ops.update_scales(qs, qa)
+        qms = timed_launches(lambda: ops.quant_e4m3_rowcol(xq, qs, qa), 20, stream)
+        qbytes = 4.0 * R * C
+        qgbps = qbytes / (qms * 1e-3) / 1e9
+        out["quantizer"] = {"rows": R, "cols": C, "ms": round(qms, 4), "GB/s": round(qgbps, 1),
+                            "frac_hbm": round(qgbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": qbytes}
+        del xq
+        # the muP base block (T=8192, D=256, I=1024): timed, not targeted
+        out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5)}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline(args.cpu_tokens, D, I)
+            out["cpu_baseline"]["other_workloads"] = cpu_extra(args.quant_rows, args.quant_cols)
     print(json.dumps(out), flush=True)
 
 

@@ -105,7 +105,9 @@ int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
  * -> gu8 (K-slab of [T, 2I], gate columns first, rpad = ldt) e4m3, h8
  * (K-slab of [T, I]) e4m3, h8t (K-slab of [I, ldt]: token-contiguous copy
  * of h8 for the down wgrad) e4m3; rows T..ldt of gu8 and h8 are zeros;
- * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0. */
+ * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0, and
+ * ldt == T rounded up to 256 (the outputs' padding tokens are written then;
+ * any other ldt is SFP8_ERR_BAD_SHAPE). */
 int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
                                 void* h8t, int64_t ldt, void* stream);
@@ -123,7 +125,8 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
  * rpad = ldt, as the forward wrote it) e4m3 -> dgu8 (K-slab of [T, 2I]) e5m2,
  * dgu8t (K-slab of [2I, ldt])
  * e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is recorded by
- * sfp8_norm_bwd.)  D % 64 == 0, I % 128 == 0. */
+ * sfp8_norm_bwd.)  D % 64 == 0, I % 128 == 0, ldt == T rounded up to 256
+ * (as for sfp8_gemm_gateup_swiglu_fwd: every padding token is written). */
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream);
@@ -141,6 +144,7 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
  * out[m, n] = sum_t at[m, t] * bt[n, t] / (sa[0] * sb[0]), fp32 [M, N].
  * at: K-slab copy of M rows over ldt tokens, e5m2 (fmt_a = 1); bt: K-slab
  * copy of N rows, e4m3 (fmt_b = 0).
+ * M > 0, N > 0, N % 4 == 0, ldt % 256 == 0.
  * ws: fp32 workspace of sfp8_wgrad_workspace_floats(M, N, ldt) floats (may be
  * NULL when that is 0).  Deterministic: split-K partials are summed in split
  * order by a second kernel on the same stream. */

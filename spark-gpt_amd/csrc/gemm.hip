@@ -913,69 +913,32 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
 // ---------------------------------------------------------------------------
 // (a10) gate/up dgrad (spark-gpt train.py:1239-1241):
 //   dxn = bf16(acc * (1/s3) * (1/q_gu)), A = d_gu8 (e5m2, [T, 2I]), B = W8^T (e4m3, [D, 2I]).
-// Persistent form for NB == 2: gridDim.x = 2 work-groups per CU, each looping
-// over tiles pid, pid + gridDim.x, ...  Work-groups [n_cu, 2*n_cu) are the
-// second on their CU; they start after a bounded sleep of about half a tile
-// so that the two work-groups of a CU alternate main loop and epilogue.
-SFP8_DEV void stagger_second_wg(int n_cu, int sleep_iters) {
-  if ((int)blockIdx.x >= n_cu)
-    for (int i = 0; i < sleep_iters; ++i) __builtin_amdgcn_s_sleep(127);
-}
-
-template <int NB>
-__global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gateup_dgrad_kernel(
+// One work-group per 256 x 256 tile; the bf16 tile is staged in LDS in two
+// passes of 128 rows and written as whole rows.
+__global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
     const uint8_t* __restrict__ dgu8, const uint8_t* __restrict__ w8t, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, uint16_t* __restrict__ dxn,
-    int64_t ldt, int tiles_m, int tiles_n, int n_cu, int sleep_iters) {
-  using ML = MainLoop<false, kFmtE5M2, kFmtE4M3, false, NB, NB == 2 ? 3 : kStages>;
+    int64_t ldt, int tiles_m, int tiles_n) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int64_t K = 2 * I;
   const int64_t dp = slab_rows(D);
   const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
-  const int ntiles = tiles_m * tiles_n;
-  if constexpr (NB == 2) stagger_second_wg(n_cu, sleep_iters);
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    int tm, tn;
-    tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
-    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * ML::kTileN;
-    floatx16 acc[4][NB];
-    // K-slab operands: dgu8 [2I/64][ldt][64], w8t [2I/64][slab_rows(D)][64]
-    ML::run(lds, dgu8 + m0 * kStage, K * ldt - m0 * kStage, [=](int r) { return r * kStage; },
-            (int)(ldt * kStage), w8t + n0 * kStage, K * dp - n0 * kStage,
-            [=](int r) { return plain_col_nb<NB>(r) * kStage; }, (int)(dp * kStage), (int)(K / kStage), acc);
-    if constexpr (NB == 4) {
-      stage_bf16_half<0>(lds, acc, sab);
-      __syncthreads();
-      write_bf16_half(lds, 0, m0, n0, T, D, D, nullptr, dxn);
-      __syncthreads();
-      stage_bf16_half<1>(lds, acc, sab);
-      __syncthreads();
-      write_bf16_half(lds, 1, m0, n0, T, D, D, nullptr, dxn);
-    } else {
-      // each lane: 32 consecutive columns of one row per tb
-      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
-      const int fr = lane & 31, g = lane >> 5;
-      const int64_t n = n0 + 32 * NB * wn + 16 * NB * g;
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const int64_t t = m0 + 128 * wm + 32 * tb + fr;
-        if (t >= T) continue;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          if (n + 16 * nb >= D) continue;  // D % 16 == 0
-          uint32_t w0[4], w1[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            w0[i] = pack2_bf16(acc[tb][nb][2 * i] * sab, acc[tb][nb][2 * i + 1] * sab);
-            w1[i] = pack2_bf16(acc[tb][nb][8 + 2 * i] * sab, acc[tb][nb][8 + 2 * i + 1] * sab);
-          }
-          store16(dxn + t * D + n + 16 * nb, w0);
-          store16(dxn + t * D + n + 16 * nb + 8, w1);
-        }
-      }
-    }
-    __syncthreads();  // the next tile's DMA overwrites the LDS
-  }
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+  floatx16 acc[4][4];
+  // K-slab operands: dgu8 [2I/64][ldt][64], w8t [2I/64][slab_rows(D)][64]
+  MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
+      lds, dgu8 + m0 * kStage, K * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage),
+      w8t + n0 * kStage, K * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
+      (int)(K / kStage), acc);
+  stage_bf16_half<0>(lds, acc, sab);
+  __syncthreads();
+  write_bf16_half(lds, 0, m0, n0, T, D, D, nullptr, dxn);
+  __syncthreads();
+  stage_bf16_half<1>(lds, acc, sab);
+  __syncthreads();
+  write_bf16_half(lds, 1, m0, n0, T, D, D, nullptr, dxn);
 }
 
 // ---------------------------------------------------------------------------
@@ -1035,12 +998,13 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       const int64_t n = n0 + cb + 16 * nb;
-      if (n >= N) continue;
       floatx4* p = reinterpret_cast<floatx4*>(dst + m * N + n);
+      // N % 4 == 0: each float4 is wholly inside the row or wholly past it
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        p[i] = floatx4{acc[tb][nb][4 * i] * deq, acc[tb][nb][4 * i + 1] * deq, acc[tb][nb][4 * i + 2] * deq,
-                       acc[tb][nb][4 * i + 3] * deq};
+        if (n + 4 * i < N)
+          p[i] = floatx4{acc[tb][nb][4 * i] * deq, acc[tb][nb][4 * i + 1] * deq, acc[tb][nb][4 * i + 2] * deq,
+                         acc[tb][nb][4 * i + 3] * deq};
     }
   }
 }
@@ -1079,9 +1043,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 }  // namespace sfp8
 
-// B blocks per wave of the gate/up dgrad (4: 256 x 256 tiles, one work-group
-// per CU; 2: 256 x 128 tiles, two per CU)
-constexpr int kGateupDgradNB = 4;
 static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
 static_assert(sfp8::kPipeLds <= 160 * 1024, "deferred-epilogue SwiGLU fits the 160 KiB LDS");
 static_assert(128 * sfp8::kBf16Stride <= sfp8::kMainLds, "bf16 epilogue staging fits the main loop's LDS");
@@ -1134,7 +1095,10 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
                                 void* h8t, int64_t ldt, void* stream) {
   // token-sized buffers may be null when there are no tokens
   if (!w8 || !scale || !wscale || !amax || (T > 0 && (!x8 || !gu8 || !h8 || !h8t))) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || D % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
+  // the grid covers ceil(T / 256) token tiles, which write every padding
+  // token of the outputs only when ldt is T rounded up to 256
+  if (T < 0 || D <= 0 || I <= 0 || D % (2 * kStage) || I % 128 || ldt != (int64_t)cdiv(T, kTile) * kTile)
+    return kErrBadShape;
   if (!fits32(ldt, D) || !fits32(2 * I, D) || !fits32(ldt, I) || !fits32(ldt, 2 * I)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -1182,7 +1146,8 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream) {
   if (!wdt || !scale || !amax || (T > 0 && (!dy || !gu8 || !dgu8 || !dgu8t))) return kErrNullPointer;
-  if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 128 || ldt < T || ldt % kTile) return kErrBadShape;
+  if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 128 || ldt != (int64_t)cdiv(T, kTile) * kTile)
+    return kErrBadShape;  // ldt = T rounded up to 256: the grid writes every padding token
   if (!fits32(kTile, 2 * D) || !fits32(slab_rows(I), 2 * D) || !fits32(ldt, 2 * I)) return kErrBadShape;
   if (!al16(dy) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
   if (T == 0) return kOk;
@@ -1210,21 +1175,12 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
   if (!fits32(ldt, 2 * I) || !fits32(slab_rows(D), 2 * I)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
   if (T == 0) return kOk;
-  using ML = MainLoop<false, kFmtE5M2, kFmtE4M3, false, kGateupDgradNB, kGateupDgradNB == 2 ? 3 : kStages>;
-  const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, ML::kTileN);
-  const int ntiles = tiles_m * tiles_n;
-  int n_cu = 0;
-  int rc = cu_count(&n_cu);
+  const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
+  int rc = prep(gateup_dgrad_kernel, kMainLds);
   if (rc) return rc;
-  // NB == 2: persistent, two work-groups per CU; NB == 4: one work-group per tile
-  const int grid = kGateupDgradNB == 2 ? (ntiles < 2 * n_cu ? ntiles : 2 * n_cu) : ntiles;
-  // about half a tile of main loop: (K / 64) stages of ~1.2k cycles, s_sleep 127 ~ 8k cycles
-  const int sleep_iters = (int)((2 * I / kStage) * 1200 / 2 / 8128);
-  rc = prep(gateup_dgrad_kernel<kGateupDgradNB>, ML::kLds);
-  if (rc) return rc;
-  hipLaunchKernelGGL(gateup_dgrad_kernel<kGateupDgradNB>, dim3(grid), dim3(256), ML::kLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)dgu8, (const uint8_t*)w8t, T, D, I, scale, wscale, (uint16_t*)dxn, ldt,
-                     tiles_m, tiles_n, n_cu, sleep_iters);
+                     tiles_m, tiles_n);
   return status();
 }
 

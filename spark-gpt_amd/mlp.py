@@ -4,6 +4,8 @@ Mirrors the reference's interface for this path (N8python/spark-gpt train.py):
 
 * ``FP8_MLP``, ``FP8_SITE_MAX``, ``FP8_HEADROOM_BINADES`` -- train.py:914-924
 * ``_use_fp8_mlp(block, h)``                            -- train.py:927-934
+  (``make_fp8_mlp_guard(flag)`` builds the same guard over a trainer's own
+  flag, ``set_fp8_mlp(flag)`` sets this module's)
 * ``fp8_update_scales(model)``                          -- train.py:937-946
 * ``MLP(dim, hidden_dim)`` (same parameter/buffer names) -- train.py:247-262
 * ``_FP8MLPBlock.apply(h, norm_w, w_gu, w_down, scale, amax, eps)``
@@ -14,6 +16,13 @@ y = h + down(SwiGLU(gate_up(rmsnorm(h)))) with x, gu, h stored e4m3 and d_gu
 scales, fp32 master weights quantized just in time, fp32 weight/norm grads,
 bf16 dh.  There is no CPU or eager-torch fallback: without the HIP library the
 block raises.
+
+Weight quantization is cached per optimizer step: the e4m3 copies of the two
+fp32 masters are made once and reused by every forward until the weights
+change, instead of in every forward as train.py:1211-1212 does.  The copy is
+refreshed by ``fp8_update_scales`` (which the trainer calls right after
+``optimizer.step()``, train.py:4049-4050) and whenever a master's version
+counter moves; the bytes are those a per-forward quantization gives.
 """
 from __future__ import annotations
 
@@ -22,7 +31,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from . import torch_ops  # noqa: F401  (registers the sparkfp8:: operators)
+from . import torch_ops  # registers the sparkfp8:: operators; holds the weight cache
 
 FP8_MLP = False  # set True to route dense MLP sub-blocks through _FP8MLPBlock while training
 
@@ -33,27 +42,62 @@ FP8_HEADROOM_BINADES = 1
 MAX_HIDDEN = 4096  # largest hidden size the norm kernels tile (a whole row per wave)
 
 
-def _use_fp8_mlp(block, h: torch.Tensor) -> bool:
-    """Same predicate as the reference guard (train.py:927-934), with the
-    Triton clause replaced by the HIP build and the norm kernels' hidden-size
-    cap (128 <= D <= 4096)."""
-    if not (FP8_MLP and block.training and not getattr(block, "is_sparse", False)
-            and h.is_cuda and h.dtype == torch.bfloat16):
-        return False  # checked first: sparse blocks' mlp has no down_proj
-    d, inter = h.shape[1], block.mlp.down_proj.weight.shape[1]
-    return d % 128 == 0 and d & (d - 1) == 0 and d <= MAX_HIDDEN and inter % 128 == 0
+def set_fp8_mlp(flag: bool) -> None:
+    """Sets ``FP8_MLP``, the switch ``_use_fp8_mlp`` reads (``--fp8-mlp``)."""
+    global FP8_MLP
+    FP8_MLP = bool(flag)
+
+
+def make_fp8_mlp_guard(flag):
+    """The guard of train.py:927-934 over a flag read at call time: ``flag``
+    is a zero-argument callable returning the trainer's switch (spark-gpt's
+    ``main()`` rebinds its module global ``FP8_MLP``, train.py:3642, so the
+    guard must read that global, not a copy taken at import).  The Triton
+    clause of the reference becomes "the HIP build", which importing this
+    package already requires, plus the norm kernels' hidden-size cap."""
+
+    def _use_fp8_mlp(block, h: torch.Tensor) -> bool:
+        if not (flag() and block.training and not getattr(block, "is_sparse", False)
+                and h.is_cuda and h.dtype == torch.bfloat16):
+            return False  # checked first: sparse blocks' mlp has no down_proj
+        d, inter = h.shape[1], block.mlp.down_proj.weight.shape[1]
+        return d % 128 == 0 and d & (d - 1) == 0 and d <= MAX_HIDDEN and inter % 128 == 0
+
+    return _use_fp8_mlp
+
+
+# this module's own switch
+_use_fp8_mlp = make_fp8_mlp_guard(lambda: FP8_MLP)
 
 
 @torch.no_grad()
 def fp8_update_scales(model: nn.Module) -> None:
     """Roll every fp8 block's recorded amax into next step's scales (device-side,
     no host sync).  Applies to every module carrying ``fp8_scale``/``fp8_amax``
-    5-slot buffers (this module's ``MLP`` and the reference's MLP/Experts)."""
+    5-slot buffers (this module's ``MLP`` and the reference's MLP/Experts).
+
+    The trainer calls this right after ``optimizer.step()``, so it is also where
+    the cached e4m3 weight copies of each dense MLP are re-quantized from the
+    updated fp32 masters (the optimizer may write them through raw pointers,
+    train.py:2955, which no version counter sees)."""
     for m in model.modules():
         scale = getattr(m, "fp8_scale", None)
         amax = getattr(m, "fp8_amax", None)
         if isinstance(scale, torch.Tensor) and isinstance(amax, torch.Tensor) and scale.numel() == 5:
             ops.update_scales(scale, amax)
+            w_gu, w_down = _dense_weights(m)
+            if w_gu is not None:
+                torch_ops.refresh_weight_cache(w_gu, w_down)
+
+
+def _dense_weights(m: nn.Module):
+    """(gate_up, down) fp32 master weights of a dense MLP module, else (None, None)."""
+    gu, dn = getattr(m, "gate_up_proj", None), getattr(m, "down_proj", None)
+    w_gu, w_down = getattr(gu, "weight", None), getattr(dn, "weight", None)
+    if isinstance(w_gu, torch.Tensor) and isinstance(w_down, torch.Tensor) and w_gu.dim() == 2 \
+            and w_down.dim() == 2:
+        return w_gu, w_down
+    return None, None
 
 
 class MLP(nn.Module):
@@ -87,17 +131,17 @@ class _FP8MLPBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, norm_w, w_gu, w_down, scale, amax, eps):
-        y, wdt, x8t, rstd, w8t, wscale, gu8, h8t = torch.ops.sparkfp8.block_fwd(
-            h, norm_w, w_gu, w_down, scale, amax, eps)
+        y, x8t, rstd, gu8, h8t = torch.ops.sparkfp8.block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)
         # backward needs the token-contiguous x8t / h8t (weight grads), gu8
-        # (SwiGLU backward), W8^T (gate/up dgrad) and bf16 Wd^T (down dgrad)
-        ctx.save_for_backward(h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax)
+        # (SwiGLU backward) and the masters, whose quantized copies (W8^T for
+        # the gate/up dgrad, bf16 Wd^T for the down dgrad) it finds cached
+        ctx.save_for_backward(h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t, scale, amax)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax = ctx.saved_tensors
-        dh, dnw, dwgu, dwd = torch.ops.sparkfp8.block_bwd(dy, h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t,
+        h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t, scale, amax = ctx.saved_tensors
+        dh, dnw, dwgu, dwd = torch.ops.sparkfp8.block_bwd(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t,
                                                           scale, amax)
         return dh, dnw, dwgu, dwd, None, None, None
 

@@ -9,15 +9,21 @@ buffer in place (``mutates_args``), as the reference's kernels do with their
 atomic max (train.py:1015-1016, 1094).
 
 * ``sparkfp8::block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)`` returns
-  y and the tensors the backward needs (train.py:1200-1226).
-* ``sparkfp8::block_bwd(dy, h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t,
+  y and the activations the backward needs (train.py:1200-1226).
+* ``sparkfp8::block_bwd(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t,
   scale, amax)`` returns (dh, d_norm_w, dW_gate_up, dW_down)
   (train.py:1228-1252).
 * ``sparkfp8::update_scales(scale, amax)`` is the delayed-scale roll
   (train.py:937-946).
+
+The forward's e4m3 weight copies come from a cache keyed on the fp32
+masters (``cached_weights``), so the two just-in-time quantizations of
+train.py:1211-1212 run once per optimizer step rather than once per forward.
 """
 from __future__ import annotations
 
+import threading
+import weakref
 from typing import Tuple
 
 import torch
@@ -36,20 +42,95 @@ def _master(w: Tensor) -> Tensor:
     return w.contiguous()
 
 
+# ------------------------------------------------------------ weight cache
+FP8_WEIGHT_CACHE = True  # False: quantize the masters in every forward, as train.py:1211-1212
+
+# id(w_gu) -> (weakref(w_gu), weakref(w_down), key, (w8, w8t, wd8, wdt, wscale)).
+# Entries hold device memory only while their gate/up master is alive.
+_WCACHE: dict = {}
+_WLOCK = threading.Lock()
+
+
+def _wkey(w_gu: Tensor, w_down: Tensor):
+    return (w_gu._version, w_gu.data_ptr(), tuple(w_gu.shape), w_down._version, w_down.data_ptr(),
+            tuple(w_down.shape))
+
+
+def quantize_weights(w_gu: Tensor, w_down: Tensor):
+    """(w8, w8t, wd8, wdt, wscale): e4m3 K-slabs of W_gu and its transpose,
+    of W_down, the bf16 K-slab of W_down^T and [q_gu, q_d] (train.py:949-952,
+    1211-1213, 1224-1225)."""
+    wscale = torch.empty(2, dtype=torch.float32, device=w_gu.device)
+    w8, w8t, _ = ops.weight_quant(_master(w_gu), wscale[0:1], w8=True, w8t=True)
+    wd8, _, wdt = ops.weight_quant(_master(w_down), wscale[1:2], w8=True, bf16t=True)
+    return w8, w8t, wd8, wdt, wscale
+
+
+def _drop_entry(i: int, ref) -> None:
+    with _WLOCK:
+        ent = _WCACHE.get(i)
+        if ent is not None and ent[0] is ref:
+            del _WCACHE[i]
+
+
+def _store(w_gu: Tensor, w_down: Tensor, q) -> None:
+    i = id(w_gu)
+    ref = weakref.ref(w_gu, lambda r, i=i: _drop_entry(i, r))
+    with _WLOCK:
+        _WCACHE[i] = (ref, weakref.ref(w_down), _wkey(w_gu, w_down), q)
+
+
+def cached_weights(w_gu: Tensor, w_down: Tensor):
+    """The forward's quantized weights: the cached copies while the same two
+    masters are unchanged since they were quantized (same objects, storage
+    and version counters), else a fresh quantization, which is cached.
+    Cached tensors are never written again: a refresh allocates new ones, so
+    a pending backward keeps the copies its forward used."""
+    if not FP8_WEIGHT_CACHE:
+        return quantize_weights(w_gu, w_down)
+    with _WLOCK:
+        ent = _WCACHE.get(id(w_gu))
+    if ent is not None and ent[0]() is w_gu and ent[1]() is w_down and ent[2] == _wkey(w_gu, w_down):
+        return ent[3]
+    q = quantize_weights(w_gu, w_down)
+    _store(w_gu, w_down, q)
+    return q
+
+
+@torch.no_grad()
+def refresh_weight_cache(w_gu: Tensor, w_down: Tensor) -> None:
+    """Re-quantize the cached copies of (w_gu, w_down), if there are any:
+    called after the optimizer has written the masters (which it may do
+    without moving their version counters)."""
+    with _WLOCK:
+        ent = _WCACHE.get(id(w_gu))
+    if ent is None or ent[0]() is not w_gu:
+        return
+    if not FP8_WEIGHT_CACHE or not w_gu.is_cuda:
+        _drop_entry(id(w_gu), ent[0])
+        return
+    _store(w_gu, w_down, quantize_weights(w_gu, w_down))
+
+
+def clear_weight_cache() -> None:
+    with _WLOCK:
+        _WCACHE.clear()
+
+
 @torch.library.custom_op("sparkfp8::block_fwd", mutates_args={"amax"})
 def block_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Tensor, amax: Tensor,
-              eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """y, then for the backward: wdt (bf16 K-slab of W_down^T), x8t, rstd,
-    w8t (K-slab of W8^T), wscale [q_gu, q_d], gu8 (K-slab of [T, 2I]), h8t."""
+              eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """y, then for the backward: x8t, rstd, gu8 (K-slab of [T, 2I]), h8t.
+    The quantized weights stay in the weight cache: they are never an output
+    (a compiled graph may recycle the memory of the tensors it saves for
+    backward), and the backward looks them up from the same masters."""
     I = w_down.shape[1]
     h = h.contiguous()
     x8, x8t, rstd = ops.norm_quant(h, _master(norm_w), scale, amax, eps)
-    wscale = torch.empty(2, dtype=torch.float32, device=h.device)
-    w8, w8t, _ = ops.weight_quant(_master(w_gu), wscale[0:1], w8=True, w8t=True)
-    wd8, _, wdt = ops.weight_quant(_master(w_down), wscale[1:2], w8=True, bf16t=True)
+    w8, _w8t, wd8, _wdt, wscale = cached_weights(w_gu, w_down)
     gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, h.shape[0], I)
     y = ops.down_fwd(h8, wd8, h, scale, wscale)
-    return y, wdt, x8t, rstd, w8t, wscale, gu8, h8t
+    return y, x8t, rstd, gu8, h8t
 
 
 @block_fwd.register_fake
@@ -59,26 +140,25 @@ def _block_fwd_fake(h, norm_w, w_gu, w_down, scale, amax, eps):
     ldt = ops.ldt_of(T)
     sr = ops.slab_rows
     return (h.new_empty((T, D), dtype=torch.bfloat16),
-            h.new_empty((D // 32, sr(I), 32), dtype=torch.bfloat16),
             h.new_empty((ldt // 64, sr(D), 64), dtype=E4M3),
             h.new_empty((T,), dtype=torch.float32),
-            h.new_empty((2 * I // 64, sr(D), 64), dtype=E4M3),
-            h.new_empty((2,), dtype=torch.float32),
             h.new_empty((2 * I // 64, ldt, 64), dtype=E4M3),
             h.new_empty((ldt // 64, sr(I), 64), dtype=E4M3))
 
 
 @torch.library.custom_op("sparkfp8::block_bwd", mutates_args={"amax"})
-def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, wdt: Tensor, x8t: Tensor, rstd: Tensor, w8t: Tensor,
-              wscale: Tensor, gu8: Tensor, h8t: Tensor, scale: Tensor,
-              amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
-    """(dh bf16, d_norm_w fp32, dW_gate_up fp32, dW_down fp32)."""
+def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, x8t: Tensor, rstd: Tensor,
+              gu8: Tensor, h8t: Tensor, scale: Tensor, amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dh bf16, d_norm_w fp32, dW_gate_up fp32, dW_down fp32).  W8^T, the
+    bf16 W_down^T and the weight scales are the forward's (the cache entry of
+    the same, unchanged masters; train.py:1224-1225 saves them instead)."""
     dy = dy.contiguous()
     if dy.dtype != torch.bfloat16:
         dy = dy.to(torch.bfloat16)
     h = h.contiguous()
     T, D = h.shape
     I = gu8.shape[0] * ops.SLAB // 2
+    _w8, w8t, _wd8, wdt, wscale = cached_weights(w_gu, w_down)
     dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
     del dgu8
@@ -90,7 +170,7 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, wdt: Tensor, x8t: Tensor, r
 
 
 @block_bwd.register_fake
-def _block_bwd_fake(dy, h, norm_w, wdt, x8t, rstd, w8t, wscale, gu8, h8t, scale, amax):
+def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t, scale, amax):
     T, D = h.shape
     I = gu8.shape[0] * ops.SLAB // 2
     return (h.new_empty((T, D), dtype=torch.bfloat16),

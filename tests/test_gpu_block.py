@@ -64,7 +64,7 @@ def test_fp8_mlp_block_tracks_fp32_reference(dev):
         assert err < 0.12, f"{name}: rel err {err:.3e}"
 
 
-@pytest.mark.parametrize("T,D,I", [(1000, 256, 768), (257, 128, 384), (2048, 1024, 3072)])
+@pytest.mark.parametrize("T,D,I", [(1000, 256, 768), (257, 128, 384), (2048, 1024, 3072), (8192, 256, 1024)])
 def test_block_matches_oracle(dev, T, D, I):
     """Same inputs, same delayed scales: every output and grad within rel-L2
     1e-2 of the CPU emulation of the recipe; bit-exact amax slots 0 and 4."""
@@ -151,7 +151,7 @@ def test_custom_ops_opcheck(dev):
     utils = ("test_faketensor",)
     torch.library.opcheck(torch.ops.sparkfp8.block_fwd.default, args, test_utils=utils)
     out = torch.ops.sparkfp8.block_fwd(*args)
-    bargs = (dy, h, norm.weight.detach()) + tuple(out[1:]) + (mlp.fp8_scale, mlp.fp8_amax)
+    bargs = (dy, h, norm.weight.detach(), args[2], args[3]) + tuple(out[1:]) + (mlp.fp8_scale, mlp.fp8_amax)
     torch.library.opcheck(torch.ops.sparkfp8.block_bwd.default, bargs, test_utils=utils)
 
 
@@ -164,10 +164,11 @@ class _Block(nn.Module):
         return sg.fp8_mlp_block(h, self.norm, self.mlp)
 
 
-def test_compiled_block_matches_eager(dev):
-    """torch.compile (train.py:3787) traces the block as the two custom
-    operators: no graph break, and the same bytes as eager for y, every
-    gradient and the amax slots."""
+@pytest.mark.parametrize("backend", ["inductor", "aot_eager"])
+def test_compiled_block_matches_eager(dev, backend):
+    """torch.compile (train.py:3787, mode="default": the inductor backend)
+    traces the block as the two custom operators: no graph break, and the
+    same bytes as eager for y, every gradient and the amax slots."""
     T, D, I = 300, 256, 384
     norm, mlp = _setup(dev, T, D, I, 22)
     blk = _Block(norm, mlp)
@@ -188,6 +189,77 @@ def test_compiled_block_matches_eager(dev):
     explain = torch._dynamo.explain(blk)(h.clone().requires_grad_(True))
     assert explain.graph_break_count == 0, explain.break_reasons
     torch._dynamo.reset()
-    got = run(torch.compile(blk, backend="aot_eager", dynamic=False))
-    for a, b in zip(got, ref):
-        assert torch.equal(a, b)
+    cblk = torch.compile(blk, backend=backend, mode="default" if backend == "inductor" else None, dynamic=False)
+    for _ in range(2):  # the second call runs the cached compiled graphs
+        got = run(cblk)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+    torch._dynamo.reset()
+
+
+def _count_weight_quant(monkeypatch):
+    calls = []
+    real = sg.ops.weight_quant
+
+    def counted(*a, **k):
+        calls.append(a[0].shape)
+        return real(*a, **k)
+
+    monkeypatch.setattr(sg.ops, "weight_quant", counted)
+    return calls
+
+
+def test_weight_cache_reuses_quantization(dev, monkeypatch):
+    """Forwards after the first launch no weight quantization while the
+    masters are unchanged; the block's outputs and gradients are the bytes of
+    the per-forward quantization (the reference's behaviour, cache off); an
+    optimizer write that moves no version counter is picked up by
+    fp8_update_scales, one that does by the next forward."""
+    from spark_gpt_amd import torch_ops as TO
+
+    T, D, I = 1000, 256, 768
+    norm, mlp = _setup(dev, T, D, I, 31)
+    h = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    probe = torch.randn(T, D, device=dev)
+    TO.clear_weight_cache()
+    calls = _count_weight_quant(monkeypatch)
+    _step(h, probe, norm, mlp)
+    assert len(calls) == 2
+    sg.fp8_update_scales(mlp)  # re-quantizes the cached masters (2 launches)
+    assert len(calls) == 4
+    s0 = mlp.fp8_scale.clone()
+
+    def fresh_run(cache):
+        mlp.fp8_amax.zero_()
+        mlp.fp8_scale.copy_(s0)
+        monkeypatch.setattr(TO, "FP8_WEIGHT_CACHE", cache)
+        out = _step(h, probe, norm, mlp)
+        return out, mlp.fp8_amax.clone()
+
+    n = len(calls)
+    cached, a1 = fresh_run(True)
+    cached2, _ = fresh_run(True)
+    assert len(calls) == n  # neither forward nor backward quantized
+    per_fwd, a2 = fresh_run(False)
+    assert len(calls) == n + 4  # forward 2, backward 2
+    for x, y, z in zip(cached, cached2, per_fwd):
+        assert torch.equal(x, y) and torch.equal(x, z)
+    assert torch.equal(a1, a2)
+    monkeypatch.setattr(TO, "FP8_WEIGHT_CACHE", True)
+    # an in-place update moves the version counter: the next forward re-quantizes
+    w = mlp.gate_up_proj.weight
+    with torch.no_grad():
+        w.mul_(0.5)
+    n = len(calls)
+    halved, _ = fresh_run(True)
+    assert len(calls) == n + 2
+    assert not torch.equal(halved[0], cached[0])
+    # a write that bypasses the version counter (as an optimizer writing
+    # through raw pointers): fp8_update_scales re-quantizes
+    w.data.mul_(2.0)
+    sg.fp8_update_scales(mlp)
+    back, a3 = fresh_run(True)
+    for x, y in zip(back, cached):
+        assert torch.equal(x, y)
+    assert torch.equal(a3, a1)
+    TO.clear_weight_cache()

@@ -113,6 +113,40 @@ def test_wide_full_size_row_local(dev):
     assert torch.equal(part[1], full[1][:R])  # dh
 
 
+def test_headline_full_size_row_local(dev):
+    """tokens=65536, d_model=1024, ffn=3072 (the persistent SwiGLU forward at
+    48 tiles per work-group, carrying one K stream and a deferred epilogue
+    across tiles): with fixed scales, y and dh of the first 512 tokens equal
+    a run on those tokens alone, bit for bit; two runs are identical; all five
+    amax slots are recorded."""
+    T, D, I, R = 65536, 1024, 3072, 512
+    norm, mlp = make_layer(dev, D, I, 6)
+    gen = torch.Generator(device=dev).manual_seed(55)
+    h = torch.randn(T, D, generator=gen, device=dev).to(torch.bfloat16)
+    dy = (torch.randn(T, D, generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
+    block_step(h, dy, norm, mlp)
+    sg.fp8_update_scales(mlp)
+    s0 = mlp.fp8_scale.clone()
+    full = block_step(h, dy, norm, mlp)
+    amax_full = mlp.fp8_amax.clone()
+    assert bool((amax_full > 0).all())
+    for t in full:
+        assert torch.isfinite(t.float()).all()
+    mlp.fp8_amax.zero_()
+    again = block_step(h, dy, norm, mlp)
+    for a, b in zip(full, again):
+        assert torch.equal(a, b)
+    assert torch.equal(mlp.fp8_amax, amax_full)
+    mlp.fp8_scale.copy_(s0)
+    part = block_step(h[:R].contiguous(), dy[:R].contiguous(), norm, mlp)
+    assert torch.equal(part[0], full[0][:R])  # y
+    assert torch.equal(part[1], full[1][:R])  # dh
+    # and the last 512 tokens (the tiles the persistent work-groups reach last)
+    tail = block_step(h[T - R:].contiguous(), dy[T - R:].contiguous(), norm, mlp)
+    assert torch.equal(tail[0], full[0][T - R:])
+    assert torch.equal(tail[1], full[1][T - R:])
+
+
 def test_wide_full_size_wgrad_gemm(dev):
     """The down-proj weight gradient at tokens=65536 (split-K over the whole
     token range) against a float32 matmul of the same e5m2 / e4m3 operands."""

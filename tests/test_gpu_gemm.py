@@ -265,3 +265,33 @@ def test_wgrad_matches_oracle_forms(dev):
     for got, ref in ((dwd, O.down_wgrad(dy, h8, s)), (dwgu, O.gateup_wgrad(dgu8, x8, s))):
         torch.testing.assert_close(got.cpu(), ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()))
         assert O.rel_l2(got.cpu(), ref) < 1e-4
+
+
+@pytest.mark.parametrize("M,N", [(256, 100), (300, 36), (64, 4)])
+def test_wgrad_ragged_columns_stay_in_bounds(dev, M, N):
+    """N % 16 != 0 with one K split (the kernel's own epilogue writes [M, N]):
+    every float4 past column N is skipped, so a guard region right after the
+    output is untouched and the output equals a float32 matmul."""
+    from spark_gpt_amd import _lib
+
+    T = 200
+    ldt = sg.ops.ldt_of(T)
+    assert _lib.query("sfp8_wgrad_splits", M, N, ldt) == 1
+    g = torch.Generator().manual_seed(M + N)
+    a = int_fp8((T, M), E5, g, -4, 4)
+    b = int_fp8((T, N), E4, g, -4, 4)
+    at = torch.zeros(M, ldt, dtype=torch.uint8)
+    bt = torch.zeros(N, ldt, dtype=torch.uint8)
+    at[:, :T] = u8(a).t()
+    bt[:, :T] = u8(b).t()
+    at_s = sg.ops.to_slab(at.view(E5)).to(dev)
+    bt_s = sg.ops.to_slab(bt.view(E4)).to(dev)
+    sa, sb = torch.tensor([1.0], device=dev), torch.tensor([1.0], device=dev)
+    guard = 1 << 16
+    buf = torch.full((M * N + guard,), 12345.0, device=dev)
+    _lib.call("sfp8_gemm_wgrad", at_s.data_ptr(), 1, bt_s.data_ptr(), 0, M, N, ldt, sa.data_ptr(), sb.data_ptr(),
+              buf.data_ptr(), None, 0, _lib.stream_of(buf))
+    torch.cuda.synchronize()
+    ref = a.float().t() @ b.float()
+    assert torch.equal(buf[: M * N].view(M, N).cpu(), ref)
+    assert bool((buf[M * N:] == 12345.0).all())

@@ -72,6 +72,11 @@ def test_invalid_arguments_rejected_before_launch():
     assert lib.sfp8_quant_e4m3_rowcol(16, 100, 128, 16, 16, 16, 16, 64, None) == -2
     assert lib.sfp8_quant_e4m3_rowcol(16, 4, 100, 16, 16, 16, 16, 64, None) == -2
     assert lib.sfp8_gemm_wgrad(16, 0, 16, 0, 256, 256, 256, 16, 16, 16, 16, 0, None) == -2  # A must be e5m2
+    # producers of padded K-slabs write every padding token only for ldt = T rounded up to 256
+    assert lib.sfp8_gemm_gateup_swiglu_fwd(16, 16, 100, 256, 384, 16, 16, 16, 16, 16, 16, 512, None) == -2
+    assert lib.sfp8_gemm_gateup_swiglu_fwd(16, 16, 100, 256, 384, 16, 16, 16, 16, 16, 16, 100, None) == -2
+    assert lib.sfp8_gemm_down_dgrad_swiglu(16, 16, 16, 300, 256, 384, 16, 16, 16, 16, 768, None) == -2
+    assert lib.sfp8_gemm_wgrad(16, 1, 16, 0, 256, 102, 256, 16, 16, 16, 16, 0, None) == -2  # N % 4
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.check(-1, "x")
     with pytest.raises(RuntimeError, match="HIP error 1"):
@@ -196,18 +201,139 @@ def test_custom_op_fake_shapes_match_allocations():
         nw, wgu, wd = torch.empty(D, device=dev), torch.empty(2 * I, D, device=dev), torch.empty(D, I, device=dev)
         s, a = torch.empty(5, device=dev), torch.empty(5, device=dev)
         out = torch.ops.sparkfp8.block_fwd(h, nw, wgu, wd, s, a, 1e-6)
-        grads = torch.ops.sparkfp8.block_bwd(torch.empty(T, D, dtype=torch.bfloat16, device=dev), h, nw,
+        grads = torch.ops.sparkfp8.block_bwd(torch.empty(T, D, dtype=torch.bfloat16, device=dev), h, nw, wgu, wd,
                                              *out[1:], s, a)
     meta = "meta"
     want = [torch.empty(T, D, dtype=torch.bfloat16, device=meta),
-            ops.kslab_empty(I, D, torch.bfloat16, meta),
             ops.slab_empty(D, T, ops.E4M3, meta),
             torch.empty(T, device=meta),
-            ops.kslab_empty(D, 2 * I, ops.E4M3, meta),
-            torch.empty(2, device=meta),
             ops.kslab_empty(ops.ldt_of(T), 2 * I, ops.E4M3, meta),
             ops.slab_empty(I, T, ops.E4M3, meta)]
+    assert len(out) == len(want)
     for got, w in zip(out, want):
         assert got.shape == w.shape and got.dtype == w.dtype
     assert [tuple(g.shape) for g in grads] == [(T, D), (D,), (2 * I, D), (D, I)]
     assert [g.dtype for g in grads] == [torch.bfloat16] + [torch.float32] * 3
+
+
+def _integration_snippet():
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    tail = text[text.index("<!-- trainer-binding -->"):]
+    return tail[tail.index("```python") + len("```python"):tail.index("```", tail.index("```python") + 9)]
+
+
+# The parts of spark-gpt's train.py this path touches, reduced to what the
+# binding needs: the switch (train.py:914), main()'s rebinding of it
+# (train.py:3635-3642) and Block.forward's dispatch (train.py:2359-2365).
+_STUB_TRAINER_HEAD = """
+FP8_MLP = False
+"""
+_STUB_TRAINER_TAIL = """
+def main(fp8_mlp):
+    global FP8_MLP
+    FP8_MLP = fp8_mlp
+
+class Block:
+    def __init__(self, block):
+        self.block = block
+
+    def forward(self, h):
+        b = self.block
+        if _use_fp8_mlp(b, h):
+            return _FP8MLPBlock.apply(h, b.norm_w, b.mlp.gate_up_proj.weight, b.mlp.down_proj.weight,
+                                      b.mlp.fp8_scale, b.mlp.fp8_amax, 1e-6)
+        return "bf16"
+"""
+
+
+def test_documented_trainer_binding(monkeypatch):
+    """INTEGRATION.md's substitution, run in a stub of train.py: after main()
+    sets the trainer's own FP8_MLP, a dense training block goes to
+    _FP8MLPBlock; before it, and for eval or sparse blocks, it does not."""
+    import types
+
+    train = types.ModuleType("train_stub")
+    exec(_STUB_TRAINER_HEAD + _integration_snippet() + _STUB_TRAINER_TAIL, train.__dict__)
+    assert train._FP8MLPBlock is sg._FP8MLPBlock
+    calls = []
+
+    class _Recorder:
+        @staticmethod
+        def apply(*args):
+            calls.append(args)
+            return "fp8"
+
+    monkeypatch.setattr(train, "_FP8MLPBlock", _Recorder)
+    dense = _FakeBlock(1024, 3072).train()
+    dense.norm_w = torch.ones(1024)
+    blk = train.Block(dense)
+    h = _FakeCudaTensor((10, 1024))
+    assert blk.forward(h) == "bf16" and not calls  # --fp8-mlp not given
+    train.main(True)
+    assert sg.mlp.FP8_MLP is False  # the package's own switch is not involved
+    assert blk.forward(h) == "fp8" and len(calls) == 1
+    assert calls[0][2] is dense.mlp.gate_up_proj.weight
+    dense.eval()
+    assert blk.forward(h) == "bf16"
+    sparse = _FakeBlock(1024, 3072, sparse=True).train()
+    assert train._use_fp8_mlp(sparse, h) is False
+    train.main(False)
+    dense.train()
+    assert blk.forward(h) == "bf16"
+
+
+def test_set_fp8_mlp_switches_package_guard(monkeypatch):
+    from spark_gpt_amd import mlp as M
+
+    monkeypatch.setattr(M, "FP8_MLP", False)
+    b = _FakeBlock(256, 768).train()
+    h = _FakeCudaTensor((10, 256))
+    assert sg._use_fp8_mlp(b, h) is False
+    sg.set_fp8_mlp(True)
+    assert sg.FP8_MLP is True and sg._use_fp8_mlp(b, h) is True
+    sg.set_fp8_mlp(False)
+    assert sg._use_fp8_mlp(b, h) is False
+
+
+def test_weight_cache_keys(monkeypatch):
+    """The cache reuses a quantization while the same masters are unchanged,
+    re-quantizes when a version counter moves, and fp8_update_scales
+    re-quantizes entries whose masters the optimizer may have rewritten
+    (quantization replaced by a counter: no GPU)."""
+    from spark_gpt_amd import torch_ops as TO
+
+    n = []
+    monkeypatch.setattr(TO, "quantize_weights", lambda a, b: n.append(1) or ("q", len(n)))
+    TO.clear_weight_cache()
+    wgu, wd = torch.zeros(8, 4), torch.zeros(4, 4)
+    q1 = TO.cached_weights(wgu, wd)
+    assert TO.cached_weights(wgu, wd) is q1 and len(n) == 1
+    with torch.no_grad():
+        wgu.add_(1)  # in-place update: version counter moves
+    q2 = TO.cached_weights(wgu, wd)
+    assert q2 is not q1 and len(n) == 2
+    other = torch.zeros(4, 4)
+    assert TO.cached_weights(wgu, other) is not q2 and len(n) == 3  # another down master
+    # a refresh re-quantizes (entries on CPU masters are dropped instead)
+    TO.refresh_weight_cache(wgu, other)
+    assert TO.cached_weights(wgu, other)[1] == 4
+    monkeypatch.setattr(TO, "FP8_WEIGHT_CACHE", False)
+    TO.cached_weights(wgu, other)
+    TO.cached_weights(wgu, other)
+    assert len(n) == 6
+    TO.clear_weight_cache()
+
+
+def test_weight_cache_entry_dies_with_master(monkeypatch):
+    import gc
+
+    from spark_gpt_amd import torch_ops as TO
+
+    monkeypatch.setattr(TO, "quantize_weights", lambda a, b: ("q",))
+    TO.clear_weight_cache()
+    wgu, wd = torch.zeros(8, 4), torch.zeros(4, 4)
+    TO.cached_weights(wgu, wd)
+    assert len(TO._WCACHE) == 1
+    del wgu
+    gc.collect()
+    assert len(TO._WCACHE) == 0
