@@ -35,7 +35,9 @@
  *    provide every output and workspace buffer.
  *  - Return value: 0 on success; a negative SFP8_ERR_* code for invalid
  *    arguments (nothing is launched); a positive hipError_t from the launch.
- *  - Calls are re-entrant: the library has no mutable global state.
+ *  - Calls are re-entrant: the library has no mutable global state, except
+ *    the per-device address of the fixed scratch that sfp8_norm_bwd_noalloc
+ *    looks up once per device (under a lock).
  */
 #ifndef SPARKFP8_H
 #define SPARKFP8_H
@@ -51,6 +53,7 @@ extern "C" {
 #define SFP8_ERR_BAD_SHAPE (-2)
 #define SFP8_ERR_BAD_ALIGNMENT (-3)
 #define SFP8_ERR_WORKSPACE_TOO_SMALL (-4)
+#define SFP8_ERR_SCRATCH_LIMIT (-5) /* beyond sfp8_norm_bwd_noalloc's fixed scratch */
 
 /* Pointer arguments are device pointers and must not be NULL, except that
  * buffers sized by the token (or row) count may be NULL when that count is
@@ -170,6 +173,24 @@ int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void*
                   int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
                   float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream);
 int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt);
+
+/* Allocation-free RMSNorm backward.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as sfp8_norm_bwd without the partials workspace:
+ * the dnw partials live in a fixed file-scope device array of
+ * SFP8_NOALLOC_SCRATCH_FLOATS floats (32 MiB), one per GPU, held until the
+ * process ends.  Shapes whose sfp8_norm_bwd_partials(D, ldt) * D exceeds it
+ * return SFP8_ERR_SCRATCH_LIMIT before anything is launched (ldt up to
+ * 522240 tokens at D=1024, 130048 at D=2048, 32256 at D=4096).  The call allocates
+ * nothing; the first call on a device looks up that device's address of the
+ * array.  Every call on one GPU shares its array: calls that overlap on one
+ * GPU (concurrent streams, threads) race and must be serialised by the
+ * caller; nothing in it needs to start at zero. */
+#define SFP8_NOALLOC_SCRATCH_FLOATS (8LL << 20)
+int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
+                          int64_t ldt, void* stream);
 
 #ifdef __cplusplus
 }

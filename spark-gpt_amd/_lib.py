@@ -36,6 +36,7 @@ SIGNATURES = {
     "sfp8_slab_bytes": (_I64, [_I64, _I64]),
     "sfp8_norm_bwd": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "sfp8_norm_bwd_partials": (_I64, [_I64, _I64]),
+    "sfp8_norm_bwd_noalloc": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
 }
 
 ERRORS = {
@@ -43,6 +44,7 @@ ERRORS = {
     -2: "unsupported shape",
     -3: "misaligned pointer (16-byte alignment required)",
     -4: "workspace too small",
+    -5: "shape beyond the allocation-free entry point's fixed scratch",
 }
 
 _lock = threading.Lock()

@@ -34,6 +34,7 @@ enum Status : int {
   kErrBadShape = -2,
   kErrBadAlignment = -3,
   kErrWorkspaceTooSmall = -4,
+  kErrScratchLimit = -5,  // the allocation-free entry point's fixed scratch is too small
 };
 
 SFP8_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }

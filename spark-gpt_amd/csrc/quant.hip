@@ -10,6 +10,8 @@
 // tile into LDS, then each thread gathers a 16(row) x 4(col) byte block with
 // dword reads, transposes it in registers (v_perm) and writes 16-byte runs of
 // the transposed output.
+#include <mutex>
+
 #include "common.h"
 #include "scale.h"
 
@@ -542,6 +544,41 @@ static inline int64_t colsum_groups(int64_t nb) { return nb < kColsumGroups ? nb
 }  // namespace sfp8
 
 // ============================================================================
+// Fixed scratch of the allocation-free norm backward (sfp8_norm_bwd_noalloc).
+// Every GPU the library runs on holds its own copy of this array until the
+// process ends.  In host code `scratch` names a host-side stand-in, not a
+// device address: the device address comes from hipGetSymbolAddress, once
+// per device, and only that address is passed to kernels.
+// ============================================================================
+constexpr int64_t kNoAllocScratchFloats = int64_t(8) << 20;  // 32 MiB of fp32 partials (SFP8_NOALLOC_SCRATCH_FLOATS)
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call on
+// that device, with that device current).
+int scratch_address(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return sfp8::kErrBadShape;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return sfp8::kErrNullPointer;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return sfp8::kOk;
+}
+}  // namespace
+
+// ============================================================================
 // C ABI
 // ============================================================================
 using namespace sfp8;
@@ -692,21 +729,11 @@ int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
   return nb < 0 ? -1 : nb + colsum_groups(nb);
 }
 
-int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
-                  int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
-                  float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream) {
-  // token-sized buffers (and the partials) may be null when there are no tokens
-  if (!norm_w || !scale || !amax || !dnw ||
-      (T > 0 && (!h || !rstd || !dxn || !dy || !dh || !partials || !dy8t)))
-    return kErrNullPointer;
-  if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
-  const int64_t nb = sfp8_norm_bwd_partials(D, ldt);
-  if (nb < 0) return kErrBadShape;
-  if (partials_cap < nb * D) return kErrWorkspaceTooSmall;
-  if (!aligned16(h) || !aligned16(dxn) || !aligned16(dy) || !aligned16(dh) || !aligned16(norm_w) ||
-      !aligned16(dy8t))
-    return kErrBadAlignment;
-  hipStream_t st = (hipStream_t)stream;
+// Shared by sfp8_norm_bwd (caller's workspace) and sfp8_norm_bwd_noalloc
+// (the fixed scratch); the arguments are checked by the callers.
+static int norm_bwd_launch(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                           int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
+                           float* partials, void* dy8t, int64_t ldt, hipStream_t st) {
   if (ldt == 0) {
     // no tokens: d_norm_w is an empty sum (zero); nothing else is written
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, dnw, D);
@@ -723,5 +750,45 @@ int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void*
   }
 }
 
+// Argument checks common to both norm backward entry points.
+static int norm_bwd_check(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
+                          int64_t ldt) {
+  if (!norm_w || !scale || !amax || !dnw || (T > 0 && (!h || !rstd || !dxn || !dy || !dh || !dy8t)))
+    return kErrNullPointer;
+  if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
+  if (sfp8_norm_bwd_partials(D, ldt) < 0) return kErrBadShape;
+  if (!aligned16(h) || !aligned16(dxn) || !aligned16(dy) || !aligned16(dh) || !aligned16(norm_w) ||
+      !aligned16(dy8t))
+    return kErrBadAlignment;
+  return kOk;
+}
+
+int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                  int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
+                  float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream) {
+  // token-sized buffers (and the partials) may be null when there are no tokens
+  int rc = norm_bwd_check(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, dy8t, ldt);
+  if (rc) return rc;
+  if (T > 0 && !partials) return kErrNullPointer;
+  if (partials_cap < sfp8_norm_bwd_partials(D, ldt) * D) return kErrWorkspaceTooSmall;
+  return norm_bwd_launch(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials, dy8t, ldt,
+                         (hipStream_t)stream);
+}
+
+int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
+                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
+                          int64_t ldt, void* stream) {
+  int rc = norm_bwd_check(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, dy8t, ldt);
+  if (rc) return rc;
+  // the dnw partials (every row of which the kernels write before reading:
+  // nothing has to start at zero) must fit the fixed scratch
+  if (sfp8_norm_bwd_partials(D, ldt) * D > kNoAllocScratchFloats) return kErrScratchLimit;
+  float* partials = nullptr;
+  rc = scratch_address(&partials);
+  if (rc) return rc;
+  return norm_bwd_launch(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials, dy8t, ldt,
+                         (hipStream_t)stream);
+}
 
 }  // extern "C"

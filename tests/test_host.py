@@ -77,6 +77,9 @@ def test_invalid_arguments_rejected_before_launch():
     assert lib.sfp8_gemm_gateup_swiglu_fwd(16, 16, 100, 256, 384, 16, 16, 16, 16, 16, 16, 100, None) == -2
     assert lib.sfp8_gemm_down_dgrad_swiglu(16, 16, 16, 300, 256, 384, 16, 16, 16, 16, 768, None) == -2
     assert lib.sfp8_gemm_wgrad(16, 1, 16, 0, 256, 102, 256, 16, 16, 16, 16, 0, None) == -2  # N % 4
+    # the allocation-free norm backward refuses shapes beyond its fixed scratch on the host
+    assert lib.sfp8_norm_bwd_noalloc(16, 16, 16, 16, 16, 65536, 4096, 16, 16, 16, 16, 16, 65536, None) == -5
+    assert lib.sfp8_norm_bwd_noalloc(None, 16, 16, 16, 16, 256, 1024, 16, 16, 16, 16, 16, 256, None) == -1
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.check(-1, "x")
     with pytest.raises(RuntimeError, match="HIP error 1"):
