@@ -142,7 +142,12 @@ def test_down_fwd_integer_operands(dev, T, D, I):
     assert torch.equal(y.cpu(), ry)
 
 
-@pytest.mark.parametrize("T,D,I", SHAPES)
+# The headline width D = 1024: the persistent dgrad with fewer tiles than CUs
+# and with three tiles per work-group (T = 16384); ragged T.
+SHAPES_DGRAD_PIPE = [(1000, 1024, 768), (1, 1024, 128), (4099, 1024, 3072), (16384, 1024, 3072)]
+
+
+@pytest.mark.parametrize("T,D,I", SHAPES + SHAPES_DGRAD_PIPE)
 def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     g = torch.Generator().manual_seed(3 + T + D + I)
     dy = torch.randint(-8, 9, (T, D), generator=g).float().to(torch.bfloat16)
@@ -162,13 +167,13 @@ def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-5, atol=0)
 
 
-def test_down_dgrad_swiglu_every_gate_code(dev):
+@pytest.mark.parametrize("T,D,I", [(512, 256, 256), (8192, 1024, 3072)])
+def test_down_dgrad_swiglu_every_gate_code(dev, T, D, I):
     """Every e4m3 code as gate and as up value, the two NaN codes included.
     The kernel takes sigmoid(g) and sig*(1 + g*(1 - sig)) from a table over
     the 256 gate codes and multiplies in the reference's order, so only a
     sigmoid that differs from torch's by an ulp can move a byte.  NaN outputs
     must carry a NaN code (the sign of a NaN is not specified)."""
-    T, D, I = 512, 256, 256
     g = torch.Generator().manual_seed(11)
     dy = torch.randint(-8, 9, (T, D), generator=g).float().to(torch.bfloat16)
     wd = torch.randint(-8, 9, (D, I), generator=g).float().to(torch.bfloat16)
@@ -191,7 +196,7 @@ def test_down_dgrad_swiglu_every_gate_code(dev):
     assert torch.equal(dt[:, :T], got.t())
 
 
-@pytest.mark.parametrize("T,D,I", SHAPES[:3])
+@pytest.mark.parametrize("T,D,I", SHAPES[:3] + SHAPES_DGRAD_PIPE[2:])
 def test_down_dgrad_swiglu_random(dev, T, D, I):
     g = torch.Generator().manual_seed(4 + T + D + I)
     dy = (torch.randn(T, D, generator=g) * 1e-3).to(torch.bfloat16)
@@ -203,7 +208,15 @@ def test_down_dgrad_swiglu_random(dev, T, D, I):
     dgu8 = sg.ops.unslab(dgu8s, T)
     rdgu8, ra3, _ = O.down_dgrad_swiglu(dy, wd, gu8, s, I)
     d = code_dist(dgu8, rdgu8)
-    assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 0.02
+    # Where dh = dy @ Wd cancels, the oracle's own fp32 sum can be more than
+    # half a bf16 ulp from the exact (fp64) value; its byte there is not
+    # pinned (any fp32 order, the kernel's included, may round elsewhere).
+    # Such elements must be rare; every other byte is within one code.
+    dh32, dh64 = dy.float() @ wd.float(), dy.double() @ wd.double()
+    unpinned = (dh32.double() - dh64).abs() > dh64.abs() * 2.0 ** -9
+    unpinned = torch.cat([unpinned, unpinned], dim=1)
+    assert float(unpinned.float().mean()) < 1e-3
+    assert int(d[~unpinned].max()) <= 1 and float((d > 0).float().mean()) < 0.02
     torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-2, atol=0)
 
 
