@@ -3,12 +3,12 @@
 Import as ``spark_gpt_amd`` (the repository-root module of that name loads
 this directory as the package).
 """
-from .mlp import (FP8_HEADROOM_BINADES, FP8_SITE_MAX, MAX_HIDDEN, MLP, _FP8MLPBlock, _use_fp8_mlp,
+from .mlp import (FP8_HEADROOM_BINADES, FP8_SITE_MAX, MLP, _FP8MLPBlock, _use_fp8_mlp,
                   fp8_mlp_block, fp8_update_scales, make_fp8_mlp_guard, set_fp8_mlp)
 from . import mlp, ops, torch_ops
 
 __all__ = [
-    "FP8_HEADROOM_BINADES", "FP8_SITE_MAX", "MAX_HIDDEN", "MLP", "_FP8MLPBlock", "_use_fp8_mlp",
+    "FP8_HEADROOM_BINADES", "FP8_SITE_MAX", "MLP", "_FP8MLPBlock", "_use_fp8_mlp",
     "fp8_mlp_block", "fp8_update_scales", "make_fp8_mlp_guard", "mlp", "ops", "set_fp8_mlp", "torch_ops",
 ]
 

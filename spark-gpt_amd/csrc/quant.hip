@@ -270,6 +270,121 @@ void norm_quant_kernel(
 }
 
 // --------------------------------------------------------------------------
+// Norm-fused quantizer for wide rows (D >= 8192, D % 4096 == 0), same
+// results as norm_quant_kernel: a row no longer fits a wave's registers, so
+// a work-group of 64 tokens makes two passes.  Pass 1: each wave reduces
+// sum h^2 of 16 rows (fp64, exact) into rstd.  Pass 2, per 1024-column
+// chunk: each wave normalises and quantizes its 16 rows' chunk into the x8
+// K-slab and an LDS tile, and the 64 x 1024 tile leaves as whole 64-byte
+// rows of the token-contiguous x8t (transposing LDS reads).  The chunk's
+// second read of h mostly hits the caches.
+constexpr int kWideRows = 64;
+constexpr int kWideChunk = 1024;
+constexpr int kWideStride = kWideChunk + 16;  // LDS tile row stride (conflict-free transposing reads)
+constexpr int kWideLdsTile = kWideRows * kWideStride;
+
+__host__ __device__ inline bool wide_hidden(int64_t D) { return D >= 8192 && D % 4096 == 0; }
+
+__global__ __launch_bounds__(256) void norm_quant_wide_kernel(
+    const uint16_t* __restrict__ h, const float* __restrict__ nw, int64_t T, int64_t D, float eps,
+    const float* __restrict__ scale, float* __restrict__ amax, uint8_t* __restrict__ x8,
+    uint8_t* __restrict__ x8t, int64_t ldt, float* __restrict__ rstd) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[4];
+  __shared__ float rs_sh[kWideRows];
+  uint8_t* tile = smem;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int blk = xcd_row_block(blockIdx.x, gridDim.x);
+  const int64_t t0 = (int64_t)blk * kWideRows;
+  const float s0 = scale[0];
+  // pass 1: sum of squares, 8 loads of 16 bytes per lane in flight
+  for (int rr = 0; rr < 16; ++rr) {
+    const int r = 16 * wid + rr;
+    const int64_t t = t0 + r;
+    double ss = 0.0;
+    if (t < T) {
+      const uint16_t* row = h + t * D;
+      for (int64_t c0 = 0; c0 < D; c0 += 8 * 512) {
+        intx4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const intx4*>(row + c0 + 512 * k + 8 * lane);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float a = bf16_bits_to_f32((uint32_t)v[k][j] & 0xffffu), b = bf16_bits_to_f32((uint32_t)v[k][j] >> 16);
+            ss = __builtin_fma((double)a, (double)a, ss);  // squares of bf16 values are exact in fp64
+            ss = __builtin_fma((double)b, (double)b, ss);
+          }
+      }
+    }
+    ss = wave_sum_f64(ss);
+    const float var = (float)ss / (float)D + eps;
+    const float r_ = (float)(1.0 / __builtin_sqrt((double)var));
+    if (lane == 0) {
+      rs_sh[r] = r_;
+      if (t < T) rstd[t] = r_;
+    }
+  }
+  __syncthreads();
+  float m = 0.0f;
+  const int64_t cp = slab_rows(D);
+  for (int64_t cc = 0; cc < D; cc += kWideChunk) {
+    // the lane's 8 columns of each 512-column half of the chunk
+    float w[2][8];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(nw + cc + 512 * hf + 8 * lane);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(nw + cc + 512 * hf + 8 * lane + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { w[hf][j] = a[j]; w[hf][4 + j] = b[j]; }
+    }
+#pragma unroll 1
+    for (int rb = 0; rb < 16; rb += 4) {
+      intx4 v[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t t = t0 + 16 * wid + rb + q;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          v[q][hf] = t < T ? *reinterpret_cast<const intx4*>(h + t * D + cc + 512 * hf + 8 * lane) : intx4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 16 * wid + rb + q;
+        const int64_t t = t0 + r;
+        const bool valid = t < T;
+        const float r_ = rs_sh[r];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          float n[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            n[2 * j] = (bf16_bits_to_f32((uint32_t)v[q][hf][j] & 0xffffu) * r_) * w[hf][2 * j];
+            n[2 * j + 1] = (bf16_bits_to_f32((uint32_t)v[q][hf][j] >> 16) * r_) * w[hf][2 * j + 1];
+          }
+          uint32_t lo = 0u, hi = 0u;
+          if (valid) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(n[j]));
+            lo = pack4_e4m3(n[0] * s0, n[1] * s0, n[2] * s0, n[3] * s0);
+            hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
+          }
+          const int64_t d = cc + 512 * hf + 8 * lane;
+          // x8 is a K-slab [D/64][ldt][64], zeros for tokens T..ldt-1
+          *reinterpret_cast<intx2*>(x8 + (d >> 6) * ldt * 64 + t * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
+          *reinterpret_cast<intx2*>(tile + r * kWideStride + 512 * hf + 8 * lane) = intx2{(int)lo, (int)hi};
+        }
+      }
+    }
+    __syncthreads();
+    lds_rows_store_slab_tr<kWideRows>(tile, kWideChunk, kWideStride, x8t, cp, t0, cc);
+    __syncthreads();  // the next chunk overwrites the tile
+  }
+  block_amax_atomic<4>(m, red, amax);
+}
+
+// --------------------------------------------------------------------------
 // Weight quantization (spark-gpt train.py:949-952), two launches:
 //   weight_amax_kernel:  per-block max|w| partials (no zero-init needed)
 //   weight_quant_kernel: every block folds the partials into amax and
@@ -510,6 +625,141 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   block_amax_atomic<4>(m, red, amax + 4);
 }
 
+// RMSNorm backward for wide rows (D >= 8192, D % 4096 == 0), the same
+// computation as norm_bwd_kernel in two passes over a work-group of 64
+// tokens: pass 1 reduces S = sum (g*w)*h per row; pass 2, per 1024-column
+// chunk, writes dh, accumulates the chunk's dnw partial (each wave over its
+// 16 rows in order, then the 4 waves in order) and stages e5m2(dy*s4) for
+// the token-contiguous dy8t, written as whole 64-byte rows.
+__global__ __launch_bounds__(256) void norm_bwd_wide_kernel(
+    const uint16_t* __restrict__ h, const float* __restrict__ rstd, const uint16_t* __restrict__ dxn,
+    const uint16_t* __restrict__ dy, const float* __restrict__ nw, int64_t T, int64_t D,
+    const float* __restrict__ scale, float* __restrict__ amax, uint16_t* __restrict__ dh,
+    float* __restrict__ dnw_part, uint8_t* __restrict__ dy8t, int64_t ldt) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float red[4];
+  __shared__ float coef_sh[kWideRows], rs_sh[kWideRows];
+  uint8_t* tile = smem;
+  float* dnw_red = reinterpret_cast<float*>(smem + kWideLdsTile);  // [4 waves][1024]
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int blk = xcd_row_block(blockIdx.x, gridDim.x);
+  const int64_t t0 = (int64_t)blk * kWideRows;
+  const float s4 = scale[4];
+  // pass 1: S per row
+  for (int rr = 0; rr < 16; ++rr) {
+    const int r = 16 * wid + rr;
+    const int64_t t = t0 + r;
+    float S = 0.0f, rs = 0.0f;
+    if (t < T) {
+      rs = rstd[t];
+      for (int64_t c0 = 0; c0 < D; c0 += 4 * 512) {
+        intx4 vh[4], vg[4];
+        floatx4 wa[4], wb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int64_t d = c0 + 512 * k + 8 * lane;
+          vh[k] = *reinterpret_cast<const intx4*>(h + t * D + d);
+          vg[k] = *reinterpret_cast<const intx4*>(dxn + t * D + d);
+          wa[k] = *reinterpret_cast<const floatx4*>(nw + d);
+          wb[k] = *reinterpret_cast<const floatx4*>(nw + d + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t uh = (uint32_t)vh[k][j >> 1], ug = (uint32_t)vg[k][j >> 1];
+            const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
+            const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
+            const float wv = j < 4 ? wa[k][j] : wb[k][j - 4];
+            S += (g * wv) * hf;
+          }
+      }
+    }
+    S = wave_sum_f32(S);
+    if (lane == 0) {
+      coef_sh[r] = S * rs * rs * rs * (1.0f / (float)D);
+      rs_sh[r] = rs;
+    }
+  }
+  __syncthreads();
+  float m = 0.0f;
+  const int64_t cp = slab_rows(D);
+  for (int64_t cc = 0; cc < D; cc += kWideChunk) {
+    float w[2][8], acc[2][8];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(nw + cc + 512 * hf + 8 * lane);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(nw + cc + 512 * hf + 8 * lane + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { w[hf][j] = a[j]; w[hf][4 + j] = b[j]; }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[hf][j] = 0.0f;
+    }
+#pragma unroll 1
+    for (int rb = 0; rb < 16; rb += 2) {
+      intx4 vh[2][2], vg[2][2], vd[2][2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int64_t t = t0 + 16 * wid + rb + q;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int64_t o = t * D + cc + 512 * hf + 8 * lane;
+          const intx4 z = {0, 0, 0, 0};
+          vh[q][hf] = t < T ? *reinterpret_cast<const intx4*>(h + o) : z;
+          vg[q][hf] = t < T ? *reinterpret_cast<const intx4*>(dxn + o) : z;
+          vd[q][hf] = t < T ? *reinterpret_cast<const intx4*>(dy + o) : z;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int r = 16 * wid + rb + q;
+        const int64_t t = t0 + r;
+        const bool valid = t < T;
+        const float rs = rs_sh[r], coef = coef_sh[r];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          float o[8], dyf[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t uh = (uint32_t)vh[q][hf][j >> 1], ug = (uint32_t)vg[q][hf][j >> 1];
+            const uint32_t ud = (uint32_t)vd[q][hf][j >> 1];
+            const float hv = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
+            const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
+            dyf[j] = bf16_bits_to_f32((j & 1) ? (ud >> 16) : (ud & 0xffffu));
+            const float gw = g * w[hf][j];
+            o[j] = (gw * rs - hv * coef) + dyf[j];
+            acc[hf][j] += g * (hv * rs);
+            m = fmaxf(m, fabsf(dyf[j]));
+          }
+          const int64_t d = cc + 512 * hf + 8 * lane;
+          uint32_t lo = 0u, hi = 0u;
+          if (valid) {
+            intx4 ov;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ov[j] = (int)pack2_bf16(o[2 * j], o[2 * j + 1]);
+            *reinterpret_cast<intx4*>(dh + t * D + d) = ov;
+            lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
+            hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
+          }
+          *reinterpret_cast<intx2*>(tile + r * kWideStride + 512 * hf + 8 * lane) = intx2{(int)lo, (int)hi};
+        }
+      }
+    }
+    // this wave's dnw partial of the chunk (its 16 rows, in order)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dnw_red[wid * kWideChunk + 512 * hf + 8 * lane + j] = acc[hf][j];
+    __syncthreads();
+    lds_rows_store_slab_tr<kWideRows>(tile, kWideChunk, kWideStride, dy8t, cp, t0, cc);
+    for (int d = threadIdx.x; d < kWideChunk; d += 256)
+      dnw_part[(int64_t)blk * D + cc + d] =
+          ((dnw_red[d] + dnw_red[kWideChunk + d]) + dnw_red[2 * kWideChunk + d]) + dnw_red[3 * kWideChunk + d];
+    __syncthreads();  // the next chunk overwrites the tile and the reduction rows
+  }
+  block_amax_atomic<4>(m, red, amax + 4);
+}
+
 // Fixed-order column sums over row groups: out[y][d] = sum of part[b][d] for
 // b in [y*rpg, min(nb, (y+1)*rpg)).  Work-group (x, y) owns 64 columns of
 // group y; thread (r, c) sums rows r, r+4, r+8, ... of the group in ascending
@@ -635,6 +885,30 @@ static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, co
   return launch_status();
 }
 
+static int colsum_launch(float* part, int64_t nb, int64_t D, float* dnw, hipStream_t st) {
+  // partial rows: nb from the norm kernel, then the group sums after them
+  const int64_t G = colsum_groups(nb), rpg = (nb + G - 1) / G;
+  float* group_sums = part + nb * D;
+  const unsigned cblk = (unsigned)((D + 63) / 64);
+  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, (unsigned)G), dim3(256), 0, st, part, nb, rpg, D, group_sums);
+  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, 1), dim3(256), 0, st, (const float*)group_sums, G, G, D, dnw);
+  return launch_status();
+}
+
+static int launch_norm_bwd_wide(const void* h, const float* rstd, const void* dxn, const void* dy, const float* nw,
+                                int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
+                                float* part, void* dy8t, int64_t ldt, hipStream_t st) {
+  const size_t lds = (size_t)kWideLdsTile + 4 * kWideChunk * sizeof(float);
+  const int rc = allow_lds(norm_bwd_wide_kernel, lds);
+  if (rc) return rc;
+  const int64_t nb = ldt / kWideRows;
+  hipLaunchKernelGGL(norm_bwd_wide_kernel, dim3((unsigned)nb), dim3(256), lds, st, (const uint16_t*)h, rstd,
+                     (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, D, scale, amax, (uint16_t*)dh, part,
+                     (uint8_t*)dy8t, ldt);
+  const int e = launch_status();
+  return e ? e : colsum_launch(part, nb, D, dnw, st);
+}
+
 extern "C" {
 
 int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const float* scale, float* amax,
@@ -662,6 +936,16 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
   return launch_status();
 }
 
+static int launch_norm_quant_wide(const void* h, const float* nw, int64_t T, int64_t D, float eps,
+                                  const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
+                                  hipStream_t st) {
+  const int rc = allow_lds(norm_quant_wide_kernel, kWideLdsTile);
+  if (rc) return rc;
+  hipLaunchKernelGGL(norm_quant_wide_kernel, dim3((unsigned)(ldt / kWideRows)), dim3(256), kWideLdsTile, st,
+                     (const uint16_t*)h, nw, T, D, eps, scale, amax, (uint8_t*)x8, (uint8_t*)x8t, ldt, rstd);
+  return launch_status();
+}
+
 int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
                     const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
                     void* stream) {
@@ -678,7 +962,9 @@ int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, fl
     case 1024: return launch_norm_quant<1024>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
     case 2048: return launch_norm_quant<2048>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
     case 4096: return launch_norm_quant<4096>(h, norm_w, T, eps, scale, amax, x8, x8t, ldt, rstd, st);
-    default: return kErrBadShape;
+    default:
+      if (wide_hidden(D)) return launch_norm_quant_wide(h, norm_w, T, D, eps, scale, amax, x8, x8t, ldt, rstd, st);
+      return kErrBadShape;
   }
 }
 
@@ -720,7 +1006,7 @@ static int64_t norm_bwd_blocks(int64_t D, int64_t ldt) {
     case 1024: return ldt / NormCfg<1024>::RT;
     case 2048: return ldt / NormCfg<2048>::RT;
     case 4096: return ldt / NormCfg<4096>::RT;
-    default: return -1;
+    default: return wide_hidden(D) ? ldt / kWideRows : -1;
   }
 }
 
@@ -746,7 +1032,10 @@ static int norm_bwd_launch(const void* h, const float* rstd, const void* dxn, co
     case 1024: return launch_norm_bwd<1024>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
     case 2048: return launch_norm_bwd<2048>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
     case 4096: return launch_norm_bwd<4096>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
-    default: return kErrBadShape;
+    default:
+      if (wide_hidden(D)) return launch_norm_bwd_wide(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials,
+                                                     dy8t, ldt, st);
+      return kErrBadShape;
   }
 }
 

@@ -39,8 +39,6 @@ FP8_MLP = False  # set True to route dense MLP sub-blocks through _FP8MLPBlock w
 # 2 = h (SwiGLU output, e4m3), 3 = d_gu (its gradient, e5m2), 4 = dy (e5m2)
 FP8_SITE_MAX = (448.0, 448.0, 448.0, 57344.0, 57344.0)
 FP8_HEADROOM_BINADES = 1
-MAX_HIDDEN = 4096  # largest hidden size the norm kernels tile (a whole row per wave)
-
 
 def set_fp8_mlp(flag: bool) -> None:
     """Sets ``FP8_MLP``, the switch ``_use_fp8_mlp`` reads (``--fp8-mlp``)."""
@@ -54,14 +52,14 @@ def make_fp8_mlp_guard(flag):
     ``main()`` rebinds its module global ``FP8_MLP``, train.py:3642, so the
     guard must read that global, not a copy taken at import).  The Triton
     clause of the reference becomes "the HIP build", which importing this
-    package already requires, plus the norm kernels' hidden-size cap."""
+    package already requires; the shape predicate is the reference's."""
 
     def _use_fp8_mlp(block, h: torch.Tensor) -> bool:
         if not (flag() and block.training and not getattr(block, "is_sparse", False)
                 and h.is_cuda and h.dtype == torch.bfloat16):
             return False  # checked first: sparse blocks' mlp has no down_proj
         d, inter = h.shape[1], block.mlp.down_proj.weight.shape[1]
-        return d % 128 == 0 and d & (d - 1) == 0 and d <= MAX_HIDDEN and inter % 128 == 0
+        return d % 128 == 0 and d & (d - 1) == 0 and inter % 128 == 0
 
     return _use_fp8_mlp
 

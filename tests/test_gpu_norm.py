@@ -13,7 +13,7 @@ def u8(t):
 
 
 CASES = [(1, 128), (257, 256), (1000, 256), (333, 512), (1000, 1024), (4099, 1024), (300, 2048),
-         (200, 4096)]
+         (200, 4096), (300, 8192), (1, 8192), (129, 16384)]
 
 
 @pytest.mark.parametrize("T,D", CASES)
@@ -56,7 +56,8 @@ def test_norm_quant_heavy_tails(dev):
     assert (u8(r8) & 0x7F).eq(0x7E).any()  # some saturate
 
 
-@pytest.mark.parametrize("T,D", [(1000, 256), (257, 1024), (4099, 1024), (300, 4096)])
+@pytest.mark.parametrize("T,D", [(1000, 256), (257, 1024), (4099, 1024), (300, 4096), (300, 8192),
+                                 (65, 16384)])
 def test_norm_bwd(dev, T, D):
     g = torch.Generator().manual_seed(T * D)
     h = torch.randn(T, D, generator=g).to(torch.bfloat16)

@@ -53,6 +53,11 @@ def test_size_queries_need_no_gpu():
     assert _lib.query("sfp8_norm_bwd_partials", 4096, 16384) == 16384 // 16 + 32
     assert _lib.query("sfp8_norm_bwd_partials", 128, 256) == 4 + 4  # fewer than 32 rows: one group each
     assert _lib.query("sfp8_norm_bwd_partials", 96, 256) == -1
+    # rows of 8192 and more: 64 tokens per work-group
+    assert _lib.query("sfp8_norm_bwd_partials", 8192, 65536) == 65536 // 64 + 32
+    assert _lib.query("sfp8_norm_bwd_partials", 32768, 256) == 4 + 4
+    assert _lib.query("sfp8_norm_bwd_partials", 12288, 256) == 4 + 4  # any multiple of 4096 from 8192
+    assert _lib.query("sfp8_norm_bwd_partials", 10240, 256) == -1
     s = _lib.query("sfp8_wgrad_splits", 6144, 1024, 65536)
     assert s >= 1 and 65536 % s == 0 and (65536 // s) % 128 == 0
     assert _lib.query("sfp8_wgrad_workspace_floats", 6144, 1024, 65536) == (s * 6144 * 1024 if s > 1 else 0)
@@ -158,7 +163,8 @@ class _FakeCudaTensor:
 
 
 @pytest.mark.parametrize("d,inter,ok", [(1024, 3072, True), (256, 768, True), (384, 768, False),
-                                        (1024, 3000, False), (8192, 1024, False), (128, 128, True)])
+                                        (1024, 3000, False), (8192, 1024, True), (16384, 3072, True),
+                                        (12288, 3072, False), (128, 128, True), (64, 128, False)])
 def test_guard_predicate(monkeypatch, d, inter, ok):
     from spark_gpt_amd import mlp as M
 
