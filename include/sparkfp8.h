@@ -192,6 +192,91 @@ int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, con
                           int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
                           int64_t ldt, void* stream);
 
+/* ---- FP8 MoE experts (grouped) ----------------------------------------- */
+/* The grouped twin of the block (_FP8Experts, train.py:1543-1605).  The R
+ * expert-order rows (token/expert pairs sorted by expert; expert e owns rows
+ * offsets[e-1] .. offsets[e]-1, offsets = inclusive prefix sums of the
+ * per-expert counts, int32 [E]) are laid out in "padded expert order":
+ * every expert's rows start on a 256-row boundary, so a GEMM tile never
+ * straddles two experts, and padding rows are zeros.  ldp =
+ * sfp8_moe_padded_rows(R, E) rows hold the worst case.  The plan (int32,
+ * sfp8_moe_plan_ints(R, E) entries) maps 256-row tiles to (expert, first
+ * expert-order row, valid rows); it is built on the device, so nothing is
+ * read back to the host.  Expert weights: E stacked K-slabs (each as the
+ * dense entry point's), per-expert scales q[E]. */
+int64_t sfp8_moe_plan_ints(int64_t R, int64_t E);
+int64_t sfp8_moe_padded_rows(int64_t R, int64_t E);
+
+/* Builds the plan from offsets (replaces _expert_tile's per-program scan,
+ * train.py:1266-1297, with one table per layer).  1 <= E <= 1024. */
+int sfp8_moe_plan(const int* offsets, int64_t E, int64_t R, int* plan, int64_t plan_ints, void* stream);
+
+/* Gathered rows -> fp8 in padded expert order.  Padded row p of tile t takes
+ * source row map[u] (map != NULL: the token index of expert-order row u) or u
+ * (map == NULL), u = first row of t + p % 256, while p % 256 < the tile's
+ * valid rows; else zeros (and out-of-range indices read as zeros).
+ *   fmt = e4m3 (0): replaces _fp8_moe_gather_quant_kernel (train.py:1300-1314):
+ *     xs = K-slab of e4m3(clamp(x * scale[sslot])) over [ldp, D] (the gate/up
+ *     GEMM's A), xt = its token-contiguous K-slab [D, ldp];
+ *   fmt = e5m2 (1), xs = NULL: the e5m2 dout copy the down weight gradient
+ *     quantizes in registers (train.py:1520-1521), token-contiguous.
+ * amax[aslot] = max |src| over the gathered rows.  D % 128 == 0, and a
+ * multiple of 1024 above 1024. */
+int sfp8_moe_rows_quant(const void* src, int64_t nsrc, int64_t D, const int64_t* map, int64_t nmap,
+                        const int* plan, int64_t ldp, const float* scale, int sslot, float* amax, int aslot,
+                        int fmt, void* xs, void* xt, void* stream);
+
+/* Per-expert weight quantization, replaces _fp8_quantize_experts
+ * (train.py:1535-1540): E matrices [rows, cols] fp32 -> q_out[e], and
+ * optionally per expert w8 / w8t / bf16 W^T K-slabs as sfp8_weight_quant
+ * (stacked, one whole K-slab per expert).  partials: 512 * E floats. */
+int sfp8_weight_quant_experts(const float* w, int64_t E, int64_t rows, int64_t cols, float* partials,
+                              int64_t nparts_cap, float* q_out, void* w8, void* w8t, void* wbf16t, void* stream);
+
+/* Grouped gate/up forward + SwiGLU, replaces _fp8_moe_swiglu_fwd_kernel
+ * (train.py:1317-1352): as sfp8_gemm_gateup_swiglu_fwd over padded expert
+ * order, expert e's W8 at w8 + e * D * slab_rows(2I) and q_gu[e]. */
+int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, int64_t D, int64_t I, const int* plan,
+                                    int64_t ldp, const float* scale, const float* q_gu, float* amax, void* gu8,
+                                    void* h8, void* h8t, void* stream);
+
+/* Grouped down forward, replaces _fp8_moe_down_fwd_kernel
+ * (train.py:1355-1377): out [R, D] bf16 expert-order rows (no residual). */
+int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D, int64_t I, const int* plan,
+                           int64_t ldp, const float* scale, const float* q_d, void* out, int64_t R, void* stream);
+
+/* Grouped bf16 down dgrad + SwiGLU backward, replaces
+ * _fp8_moe_down_dgrad_swiglu_kernel (train.py:1380-1420): dout [R, D] bf16
+ * expert-order rows, wdt per expert (bf16 K-slab of W_down[e]^T) ->
+ * dgu8 / dgu8t over padded expert order; amax[3].  (amax[4] = max|dout| is
+ * recorded by the e5m2 dout copy, sfp8_moe_rows_quant.) */
+int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const void* gu8, int64_t E, int64_t D,
+                                    int64_t I, int64_t R, const int* plan, int64_t ldp, const float* scale,
+                                    float* amax, void* dgu8, void* dgu8t, void* stream);
+
+/* Grouped gate/up dgrad, replaces _fp8_moe_dgrad_kernel (train.py:1423-1443):
+ * dx [R, D] bf16 expert-order rows. */
+int sfp8_moe_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t E, int64_t D, int64_t I, const int* plan,
+                               int64_t ldp, const float* scale, const float* q_gu, void* dx, int64_t R, void* stream);
+
+/* Grouped weight gradient, replaces _fp8_moe_wgrad_kernel (train.py:1446-1477)
+ * and _fp8_moe_wgrad_rows_kernel (train.py:1503-1529, whose fp32 atomics are
+ * replaced by split partials summed in order: deterministic):
+ * out[e] = sum over expert e's rows of at[:, t] bt[:, t]^T / (sa * sb),
+ * fp32 [E, M, N]; experts without rows get zeros.  ws: fp32 workspace of
+ * sfp8_moe_wgrad_workspace_floats(M, N, E) floats (may be NULL when 0). */
+int64_t sfp8_moe_wgrad_splits(int64_t M, int64_t N, int64_t E);
+int64_t sfp8_moe_wgrad_workspace_floats(int64_t M, int64_t N, int64_t E);
+int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t E,
+                        const int* plan, int64_t ldp, const float* sa, const float* sb, float* out, float* ws,
+                        int64_t ws_floats, void* stream);
+
+/* out[t] = bf16(sum over slots j < k of dx[inv[t*k + j]]), fp32 sum in slot
+ * order: replaces _sum_topk_rows (train.py:2213-2217) in the experts'
+ * backward (train.py:1604).  inv int64 [T*k]; out-of-range entries add 0. */
+int sfp8_moe_topk_sum(const void* dx, int64_t R, int64_t D, const int64_t* inv, int64_t T, int64_t k, void* out,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

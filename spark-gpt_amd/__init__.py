@@ -5,11 +5,13 @@ this directory as the package).
 """
 from .mlp import (FP8_HEADROOM_BINADES, FP8_SITE_MAX, MLP, _FP8MLPBlock, _use_fp8_mlp,
                   fp8_mlp_block, fp8_update_scales, make_fp8_mlp_guard, set_fp8_mlp)
-from . import mlp, ops, torch_ops
+from .moe import _FP8Experts, _use_fp8_moe, make_fp8_moe_guard
+from . import mlp, moe, ops, torch_ops
 
 __all__ = [
     "FP8_HEADROOM_BINADES", "FP8_SITE_MAX", "MLP", "_FP8MLPBlock", "_use_fp8_mlp",
     "fp8_mlp_block", "fp8_update_scales", "make_fp8_mlp_guard", "mlp", "ops", "set_fp8_mlp", "torch_ops",
+    "_FP8Experts", "_use_fp8_moe", "make_fp8_moe_guard", "moe",
 ]
 
 

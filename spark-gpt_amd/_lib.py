@@ -37,6 +37,19 @@ SIGNATURES = {
     "sfp8_norm_bwd": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "sfp8_norm_bwd_partials": (_I64, [_I64, _I64]),
     "sfp8_norm_bwd_noalloc": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
+    "sfp8_moe_plan_ints": (_I64, [_I64, _I64]),
+    "sfp8_moe_padded_rows": (_I64, [_I64, _I64]),
+    "sfp8_moe_plan": (_INT, [_P, _I64, _I64, _P, _I64, _P]),
+    "sfp8_moe_rows_quant": (_INT, [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _INT, _P, _INT, _INT, _P, _P, _P]),
+    "sfp8_weight_quant_experts": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P]),
+    "sfp8_moe_gemm_gateup_swiglu_fwd": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "sfp8_moe_gemm_down_fwd": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
+    "sfp8_moe_gemm_down_dgrad_swiglu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P]),
+    "sfp8_moe_gemm_gateup_dgrad": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
+    "sfp8_moe_wgrad_splits": (_I64, [_I64, _I64, _I64]),
+    "sfp8_moe_wgrad_workspace_floats": (_I64, [_I64, _I64, _I64]),
+    "sfp8_moe_gemm_wgrad": (_INT, [_P, _INT, _P, _INT, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _P]),
+    "sfp8_moe_topk_sum": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _P]),
 }
 
 ERRORS = {

@@ -25,6 +25,9 @@ namespace sfp8 {
 
 constexpr float kE4M3Max = 448.0f;
 constexpr float kE5M2Max = 57344.0f;
+// fp8 format selectors (the f8f6f4 MFMA's operand format fields use the same codes)
+constexpr int kFmtE4M3 = 0;
+constexpr int kFmtE5M2 = 1;
 
 // Library status codes (hipError_t values are passed through unchanged and are
 // all positive; ours are negative).
@@ -312,5 +315,33 @@ SFP8_DEV void lds_rows_store_slab_tr(const uint8_t* lds, int ncols, int stride, 
     *reinterpret_cast<intx4*>(dst + (c0 + c + li) * 64) = intx4{a[0], a[1], b[0], b[1]};
   }
 }
+
+// ---------------------------------------------------------------------------
+// MoE plan: the expert-order rows of a grouped (MoE) layer in "padded expert
+// order", every expert's rows starting on a 256-row boundary, so that each
+// 256-row GEMM tile belongs to one expert.  Tile t covers padded rows
+// 256t .. 256t + 255.  The plan is an int32 array written on the device
+// from the experts' inclusive row-count prefix sums (no host sync):
+//   [0] NT, the number of tiles; [1] E
+//   [kPlanHdr + e]          padded start row of expert e (a multiple of 256)
+//   [kPlanHdr + E + e]      padded row count of expert e (a multiple of 256)
+//   [kPlanHdr + 2E + 3t]    tile t: expert, first unpadded row, valid rows
+constexpr int kPlanHdr = 8;
+
+__host__ __device__ inline int64_t moe_max_tiles(int64_t R, int64_t E) { return (R + 255) / 256 + E; }
+__host__ __device__ inline int64_t moe_plan_ints(int64_t R, int64_t E) {
+  return kPlanHdr + 2 * E + 3 * moe_max_tiles(R, E);
+}
+
+struct MoePlan {
+  const int* p;
+  SFP8_DEV int ntiles() const { return p[0]; }
+  SFP8_DEV int experts() const { return p[1]; }
+  SFP8_DEV int pstart(int e) const { return p[kPlanHdr + e]; }
+  SFP8_DEV int pcount(int e) const { return p[kPlanHdr + experts() + e]; }
+  SFP8_DEV int expert(int t) const { return p[kPlanHdr + 2 * experts() + 3 * t]; }
+  SFP8_DEV int urow(int t) const { return p[kPlanHdr + 2 * experts() + 3 * t + 1]; }
+  SFP8_DEV int rows(int t) const { return p[kPlanHdr + 2 * experts() + 3 * t + 2]; }
+};
 
 }  // namespace sfp8

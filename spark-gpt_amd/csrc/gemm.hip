@@ -125,14 +125,24 @@ SFP8_DEV void round16_bf16(const floatx16& a, float s, float (&o)[16]) {
 // u of the same 32 consecutive columns.
 constexpr int kEpiStride = 144;
 
+// With a MoE plan (grouped experts): tile row tm of padded expert order,
+// its expert's W8 at w8 + e * w_estride and weight scale wscale[e]; tile
+// rows past the plan's count exit.
 __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
     const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, float* __restrict__ amax,
     uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int64_t ldt,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, const int* __restrict__ plan, int64_t w_estride) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  if (plan) {
+    const MoePlan P{plan};
+    if (tm >= P.ntiles()) return;  // work-group uniform
+    const int e = P.expert(tm);
+    w8 += e * w_estride;
+    wscale += e;
+  }
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -721,13 +731,28 @@ SFP8_DEV void write_bf16_half_res(const uint8_t* lds, int p, int64_t m0, int64_t
 // ---------------------------------------------------------------------------
 // (a7) down forward + residual (spark-gpt train.py:1019-1046):
 //   y = bf16(res + bf16(acc / (s2 * q_d)))
+// With a MoE plan: no residual; tile row tm of padded expert order writes
+// its rows(tm) valid rows to y rows urow(tm).. (expert order, unpadded);
+// W_down8 of expert e at wd8 + e * w_estride, its scale wscale[e] (the dense
+// call passes wscale + 1: [q_gu, q_d]).
 __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
     const uint8_t* __restrict__ h8, const uint8_t* __restrict__ wd8, const uint16_t* __restrict__ res,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, const float* __restrict__ wscale,
-    uint16_t* __restrict__ y, int64_t ldt, int tiles_m, int tiles_n) {
+    uint16_t* __restrict__ y, int64_t ldt, int tiles_m, int tiles_n, const int* __restrict__ plan,
+    int64_t w_estride) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  int64_t u0 = 0, urows = 0;
+  if (plan) {
+    const MoePlan P{plan};
+    if (tm >= P.ntiles()) return;  // work-group uniform
+    const int e = P.expert(tm);
+    wd8 += e * w_estride;
+    wscale += e;
+    u0 = P.urow(tm);
+    urows = P.rows(tm);
+  }
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   floatx16 acc[4][4];
   // K-slab operands: h8 [I/64][ldt][64], wd8 [I/64][slab_rows(D)][64]
@@ -736,7 +761,18 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
       lds, h8 + m0 * kStage, I * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage),
       wd8 + n0 * kStage, I * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
       (int)(I / kStage), acc);
-  const float deq = 1.0f / (scale[2] * wscale[1]);
+  const float deq = 1.0f / (scale[2] * wscale[0]);
+  if (plan) {
+    // expert rows, no residual: out rounded to bf16 (train.py:1439-1441 stores acc / (s2 q_d) as bf16)
+    stage_bf16_half<0>(lds, acc, deq);
+    __syncthreads();
+    write_bf16_half(lds, 0, u0, n0, u0 + urows, D, D, nullptr, y);
+    __syncthreads();
+    stage_bf16_half<1>(lds, acc, deq);
+    __syncthreads();
+    write_bf16_half(lds, 1, u0, n0, u0 + urows, D, D, nullptr, y);
+    return;
+  }
   const __amdgpu_buffer_rsrc_t rres = make_rsrc(res + m0 * D, (T - m0) * D * 2);
   // Every residual word the two staged halves add is requested at once (one
   // memory latency), in the order the staged rows are written, so both the
@@ -764,11 +800,15 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
 constexpr int kEpiStride2 = 272;
 constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 16;  // after Gt, Ut and the reduction slots
 
+// With a MoE plan: tile rows are padded expert order (gu8, dgu8, dgu8t over
+// ldt padded rows); dy is the row-major upstream gradient of the expert-order
+// rows (its rows urow(tm).. for tile row tm), W_down^T of expert e at
+// wdt + e * w_estride (bytes); the tile count comes from the plan.
 __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ wdt, const uint8_t* __restrict__ gu8,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, float* __restrict__ amax,
     uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n,
-    int stagger_iters) {
+    int stagger_iters, const int* __restrict__ plan, int64_t w_estride) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -803,17 +843,27 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   // start a quarter of a tile apart (a bounded sleep) so that their bursts
   // do not coincide.
   for (int i = 0; i < ((int)(blockIdx.x >> 3) & 3) * stagger_iters; ++i) __builtin_amdgcn_s_sleep(127);
+  if (plan) tiles_m = MoePlan{plan}.ntiles();
   const int ntiles = tiles_m * tiles_n;
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
   int tm, tn;
   tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+  // dy rows of this tile: rows m0.. (dense) or the expert rows urow(tm).. (MoE)
+  int64_t a_row = m0, a_rows = T - m0;
+  const uint8_t* wb = reinterpret_cast<const uint8_t*>(wdt);
+  if (plan) {
+    const MoePlan P{plan};
+    a_row = P.urow(tm);
+    a_rows = P.rows(tm);
+    wb += P.expert(tm) * w_estride;
+  }
   floatx16 acc[4][4];
-  // A = dy row-major (rows past T read as zero through the range check);
-  // B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
+  // A = dy row-major (rows past the tile's last read as zero through the
+  // range check); B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
   MainLoop<true, 0, 0, false>::run(
-      lds, reinterpret_cast<const uint8_t*>(dy) + m0 * ldb, (T - m0) * ldb, [=](int r) { return r * (int)ldb; },
-      kStage, reinterpret_cast<const uint8_t*>(wdt) + n0 * kStage, ldb * ip - n0 * kStage,
+      lds, reinterpret_cast<const uint8_t*>(dy) + a_row * ldb, a_rows * ldb, [=](int r) { return r * (int)ldb; },
+      kStage, wb + n0 * kStage, ldb * ip - n0 * kStage,
       [=](int r) { return plain_col(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
   // Row-order epilogue, in two passes of 128 tile rows (the rows of
   // stage_bf16_half<P>): dh staged in LDS as bf16, then each thread takes
@@ -915,16 +965,29 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
 //   dxn = bf16(acc * (1/s3) * (1/q_gu)), A = d_gu8 (e5m2, [T, 2I]), B = W8^T (e4m3, [D, 2I]).
 // One work-group per 256 x 256 tile; the bf16 tile is staged in LDS in two
 // passes of 128 rows and written as whole rows.
+// With a MoE plan: tile row tm of padded expert order writes its rows(tm)
+// valid rows to dxn rows urow(tm).. (expert order, unpadded); W8^T of
+// expert e at w8t + e * w_estride, its scale wscale[e].
 __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
     const uint8_t* __restrict__ dgu8, const uint8_t* __restrict__ w8t, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, uint16_t* __restrict__ dxn,
-    int64_t ldt, int tiles_m, int tiles_n) {
+    int64_t ldt, int tiles_m, int tiles_n, const int* __restrict__ plan, int64_t w_estride) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int64_t K = 2 * I;
   const int64_t dp = slab_rows(D);
-  const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  int64_t u0 = (int64_t)tm * kTile, uend = T;  // output rows of this tile
+  if (plan) {
+    const MoePlan P{plan};
+    if (tm >= P.ntiles()) return;  // work-group uniform
+    const int e = P.expert(tm);
+    w8t += e * w_estride;
+    wscale += e;
+    u0 = P.urow(tm);
+    uend = u0 + P.rows(tm);
+  }
+  const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   floatx16 acc[4][4];
   // K-slab operands: dgu8 [2I/64][ldt][64], w8t [2I/64][slab_rows(D)][64]
@@ -934,11 +997,11 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
       (int)(K / kStage), acc);
   stage_bf16_half<0>(lds, acc, sab);
   __syncthreads();
-  write_bf16_half(lds, 0, m0, n0, T, D, D, nullptr, dxn);
+  write_bf16_half(lds, 0, u0, n0, uend, D, D, nullptr, dxn);
   __syncthreads();
   stage_bf16_half<1>(lds, acc, sab);
   __syncthreads();
-  write_bf16_half(lds, 1, m0, n0, T, D, D, nullptr, dxn);
+  write_bf16_half(lds, 1, u0, n0, uend, D, D, nullptr, dxn);
 }
 
 // ---------------------------------------------------------------------------
@@ -1009,6 +1072,76 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   }
 }
 
+// Grouped (MoE) weight gradient: out[e, m, n] = sum over expert e's padded
+// rows t of A[m, t] * B[n, t] / (sa * sb), A and B token-contiguous K-slab
+// copies over the padded expert order (zeros in padding rows).  Work-group
+// (tile, split, expert) = (blockIdx.x, blockIdx.y, blockIdx.z) takes split
+// sp of the expert's 64-token stages (an even number of them; none for an
+// expert without rows, whose gradient comes out zero).  With one split it
+// writes out[e] itself; otherwise its raw partial in accumulator order to
+// ws[e][sp][tile], summed in split order by splitk_reduce_kernel.
+template <int FMT_A, int FMT_B>
+__global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
+    const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldp,
+    const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out, float* __restrict__ ws,
+    const int* __restrict__ plan, int tiles_m, int tiles_n, int splits) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const MoePlan P{plan};
+  const int e = blockIdx.z, sp = blockIdx.y;
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int64_t nst = P.pcount(e) / kStage;  // a multiple of 4
+  int64_t q = (nst + splits - 1) / splits;
+  q = (q + 1) & ~(int64_t)1;
+  const int64_t k0 = (int64_t)sp * q;
+  const int64_t nk = nst - k0 < 0 ? 0 : (nst - k0 < q ? nst - k0 : q);
+  const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
+  const int64_t s0 = P.pstart(e) / kStage + k0;  // first 64-token stage
+  const uint8_t* a0 = at + s0 * rpa * kStage + m0 * kStage;
+  const uint8_t* b0 = bt + s0 * rpb * kStage + n0 * kStage;
+  const int64_t a_bytes = nk > 0 ? at + ldp * rpa - a0 : 0, b_bytes = nk > 0 ? bt + ldp * rpb - b0 : 0;
+  floatx16 acc[4][4];
+  MainLoop<false, FMT_A, FMT_B, false>::run(
+      lds, a0, a_bytes, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_bytes,
+      [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)nk, acc);
+  if (splits > 1) {
+    // accumulator order: [expert][split][tile][wave][tb][nb][i][lane][4]
+    float* frag = ws + (((int64_t)e * splits + sp) * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
+                  wave * (kTile * kTile / 4);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          reinterpret_cast<floatx4*>(frag + (tb * 4 + nb) * 1024 + i * 256)[lane] =
+              floatx4{acc[tb][nb][4 * i], acc[tb][nb][4 * i + 1], acc[tb][nb][4 * i + 2], acc[tb][nb][4 * i + 3]};
+    return;
+  }
+  const float deq = 1.0f / (sa[0] * sb[0]);
+  float* dst = out + (int64_t)e * M * N;
+  const int fr = lane & 31, g = lane >> 5;
+  const int cb = 128 * wn + 64 * g;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int64_t m = m0 + 128 * wm + 32 * tb + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int64_t n = n0 + cb + 16 * nb;
+      floatx4* p = reinterpret_cast<floatx4*>(dst + m * N + n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + 4 * i < N)
+          p[i] = floatx4{acc[tb][nb][4 * i] * deq, acc[tb][nb][4 * i + 1] * deq, acc[tb][nb][4 * i + 2] * deq,
+                         acc[tb][nb][4 * i + 3] * deq};
+    }
+  }
+}
+
 // out[0, n) = 0: four floats per thread (n % 4 == 0, out 16-byte aligned).
 __global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ out, int64_t n) {
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -1026,6 +1159,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                                                             const float* __restrict__ sb, float* __restrict__ out) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (q >= n4) return;
+  // expert blockIdx.y of a grouped gradient: its splits' partials, its [M, N]
+  ws += (int64_t)blockIdx.y * splits * n4 * 4;
+  out += (int64_t)blockIdx.y * M * N;
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
   floatx4 acc = w4[q];
   for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
@@ -1122,7 +1258,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
   if (rc) return rc;
   hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)x8, (const uint8_t*)w8, T, D, I, scale, wscale, amax, (uint8_t*)gu8,
-                     (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n);
+                     (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
 }
 
@@ -1137,8 +1273,8 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
   int rc = prep(down_fwd_kernel, kMainLds);
   if (rc) return rc;
   hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
-                     (const uint8_t*)h8, (const uint8_t*)wd8, (const uint16_t*)res, T, D, I, scale, wscale,
-                     (uint16_t*)y, ldt, tiles_m, tiles_n);
+                     (const uint8_t*)h8, (const uint8_t*)wd8, (const uint16_t*)res, T, D, I, scale, wscale + 1,
+                     (uint16_t*)y, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
 }
 
@@ -1164,7 +1300,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
   if (rc) return rc;
   hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(grid), dim3(256), kDgradLds, (hipStream_t)stream,
                      (const uint16_t*)dy, (const uint16_t*)wdt, (const uint8_t*)gu8, T, D, I, scale, amax,
-                     (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, stagger);
+                     (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, stagger, (const int*)nullptr, (int64_t)0);
   return status();
 }
 
@@ -1180,7 +1316,7 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
   if (rc) return rc;
   hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)dgu8, (const uint8_t*)w8t, T, D, I, scale, wscale, (uint16_t*)dxn, ldt,
-                     tiles_m, tiles_n);
+                     tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
 }
 
@@ -1233,7 +1369,119 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws,
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+                     (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  return status();
+}
+
+// ---- grouped (MoE expert) GEMMs over padded expert order (common.h) ----
+// ldp = padded rows (256 * sfp8_moe_padded_rows); plan from sfp8_moe_plan.
+namespace {
+inline bool moe_shape(int64_t E, int64_t D, int64_t I, int64_t ldp) {
+  return E > 0 && D > 0 && I > 0 && D % 128 == 0 && I % 128 == 0 && ldp > 0 && ldp % kTile == 0;
+}
+}  // namespace
+
+int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, int64_t D, int64_t I, const int* plan,
+                                    int64_t ldp, const float* scale, const float* q_gu, float* amax, void* gu8,
+                                    void* h8, void* h8t, void* stream) {
+  if (!x8 || !w8 || !plan || !scale || !q_gu || !amax || !gu8 || !h8 || !h8t) return kErrNullPointer;
+  if (!moe_shape(E, D, I, ldp) || !fits32(ldp, D) || !fits32(2 * I, D) || !fits32(ldp, 2 * I)) return kErrBadShape;
+  if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
+  const int tiles_m = (int)(ldp / kTile), tiles_n = (int)(I / 128);
+  int rc = prep(swiglu_fwd_kernel, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+                     (const uint8_t*)x8, (const uint8_t*)w8, ldp, D, I, scale, q_gu, amax, (uint8_t*)gu8,
+                     (uint8_t*)h8, (uint8_t*)h8t, ldp, tiles_m, tiles_n, plan, D * slab_rows(2 * I));
+  return status();
+}
+
+int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D, int64_t I, const int* plan,
+                           int64_t ldp, const float* scale, const float* q_d, void* out, int64_t R, void* stream) {
+  if (!h8 || !wd8 || !plan || !scale || !q_d || (R > 0 && !out)) return kErrNullPointer;
+  if (!moe_shape(E, D, I, ldp) || R < 0 || !fits32(ldp, I) || !fits32(slab_rows(D), I)) return kErrBadShape;
+  if (!al16(h8) || !al16(wd8) || !al16(out)) return kErrBadAlignment;
+  const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(D, kTile);
+  int rc = prep(down_fwd_kernel, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+                     (const uint8_t*)h8, (const uint8_t*)wd8, (const uint16_t*)nullptr, R, D, I, scale, q_d,
+                     (uint16_t*)out, ldp, tiles_m, tiles_n, plan, I * slab_rows(D));
+  return status();
+}
+
+int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const void* gu8, int64_t E, int64_t D,
+                                    int64_t I, int64_t R, const int* plan, int64_t ldp, const float* scale,
+                                    float* amax, void* dgu8, void* dgu8t, void* stream) {
+  if (!wdt || !gu8 || !plan || !scale || !amax || !dgu8 || !dgu8t || (R > 0 && !dout)) return kErrNullPointer;
+  if (!moe_shape(E, D, I, ldp) || R < 0) return kErrBadShape;
+  if (!fits32(kTile, 2 * D) || !fits32(slab_rows(I), 2 * D) || !fits32(ldp, 2 * I)) return kErrBadShape;
+  if (!al16(dout) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
+  int n_cu = 0;
+  int rc = cu_count(&n_cu);
+  if (rc) return rc;
+  const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(I, kTile);
+  const int ntiles = tiles_m * tiles_n;  // an upper bound: the kernel reads the plan's count
+  rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kDgradLds,
+                     (hipStream_t)stream, (const uint16_t*)dout, (const uint16_t*)wdt, (const uint8_t*)gu8, R, D, I,
+                     scale, amax, (uint8_t*)dgu8, (uint8_t*)dgu8t, ldp, tiles_m, tiles_n, 0, plan,
+                     2 * D * slab_rows(I));
+  return status();
+}
+
+int sfp8_moe_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t E, int64_t D, int64_t I, const int* plan,
+                               int64_t ldp, const float* scale, const float* q_gu, void* dx, int64_t R, void* stream) {
+  if (!dgu8 || !w8t || !plan || !scale || !q_gu || (R > 0 && !dx)) return kErrNullPointer;
+  if (!moe_shape(E, D, I, ldp) || R < 0 || !fits32(ldp, 2 * I) || !fits32(slab_rows(D), 2 * I)) return kErrBadShape;
+  if (!al16(dgu8) || !al16(w8t) || !al16(dx)) return kErrBadAlignment;
+  const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(D, kTile);
+  int rc = prep(gateup_dgrad_kernel, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+                     (const uint8_t*)dgu8, (const uint8_t*)w8t, R, D, I, scale, q_gu, (uint16_t*)dx, ldp, tiles_m,
+                     tiles_n, plan, 2 * I * slab_rows(D));
+  return status();
+}
+
+// K splits of a grouped weight gradient: enough work-groups to fill the GPU
+// (about 512) when there are few experts and tiles.
+int64_t sfp8_moe_wgrad_splits(int64_t M, int64_t N, int64_t E) {
+  const int64_t wgs = (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * E;
+  int64_t s = 1;
+  while (s < 8 && wgs * s < 512) s *= 2;
+  return s;
+}
+
+int64_t sfp8_moe_wgrad_workspace_floats(int64_t M, int64_t N, int64_t E) {
+  const int64_t s = sfp8_moe_wgrad_splits(M, N, E);
+  return s > 1 ? E * s * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile : 0;
+}
+
+int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t E,
+                        const int* plan, int64_t ldp, const float* sa, const float* sb, float* out, float* ws,
+                        int64_t ws_floats, void* stream) {
+  if (!at || !bt || !plan || !sa || !sb || !out) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || E <= 0 || N % 4 || ldp <= 0 || ldp % kTile) return kErrBadShape;
+  if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3) return kErrBadShape;
+  if (!fits32(slab_rows(M), ldp) || !fits32(slab_rows(N), ldp)) return kErrBadShape;
+  if (!al16(at) || !al16(bt) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  const int64_t splits = sfp8_moe_wgrad_splits(M, N, E);
+  if (splits > 1 && (!ws || ws_floats < sfp8_moe_wgrad_workspace_floats(M, N, E))) return kErrWorkspaceTooSmall;
+  hipStream_t st = (hipStream_t)stream;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  int rc = prep(moe_wgrad_kernel<kFmtE5M2, kFmtE4M3>, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((moe_wgrad_kernel<kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)splits,
+                                                                  (unsigned)E),
+                     dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldp, sa, sb, out, ws, plan,
+                     tiles_m, tiles_n, (int)splits);
+  rc = status();
+  if (rc || splits == 1) return rc;
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }

@@ -38,8 +38,6 @@ constexpr int kStage = 64;                   // bytes of K per stage
 constexpr int kStages = 4;                   // LDS ring depth (>= 3)
 constexpr int kStageA = kTile * kStage;      // 16 KiB
 constexpr int kMainLds = 2 * kStages * kStageA;  // 128 KiB: the 256 x 256 tile's ring
-constexpr int kFmtE4M3 = 0;
-constexpr int kFmtE5M2 = 1;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 

@@ -394,9 +394,13 @@ __global__ __launch_bounds__(256) void norm_quant_wide_kernel(
 //     a bf16 K-slab of W^T.  Block 0 stores q.
 constexpr int WQ_PARTS = 512;
 
+// Expert e = blockIdx.y of a batch (E matrices of n elements, partials
+// gridDim.x per expert); a dense weight is the batch of one.
 __global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restrict__ w, int64_t n,
                                                            float* __restrict__ partials) {
   __shared__ float red[4];
+  w += (int64_t)blockIdx.y * n;
+  partials += (int64_t)blockIdx.y * gridDim.x;
   float m = 0.0f;
   const int64_t n4 = n >> 2;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
@@ -422,6 +426,18 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
   __shared__ float qs;
   __shared__ __align__(16) uint8_t t8[WQ_TILE * (WQ_TILE + 8)];
   __shared__ __align__(16) uint16_t t16[WQ_TILE * (WQ_TILE + 2)];
+  {
+    // expert e = blockIdx.z of a batch: its matrix, partials, scale and the
+    // three K-slab copies (each a whole K-slab per expert)
+    const int64_t e = blockIdx.z;
+    const int64_t rp_ = (R + 255) / 256 * 256, cp_ = (C + 255) / 256 * 256;
+    w += e * R * C;
+    partials += e * nparts;
+    q_out += e;
+    if (w8) w8 += e * C * rp_;
+    if (w8t) w8t += e * R * cp_;
+    if (wbt) wbt += e * R * cp_;
+  }
   float m = 0.0f;
   for (int i = threadIdx.x; i < nparts; i += 256) m = fmaxf(m, partials[i]);
   m = wave_max(m);
@@ -968,24 +984,35 @@ int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, fl
   }
 }
 
-int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partials, int64_t nparts_cap,
-                      float* q_out, void* w8, void* w8t, void* wbf16t, void* stream) {
+static int weight_quant_batch(const float* w, int64_t E, int64_t rows, int64_t cols, float* partials,
+                              int64_t nparts_cap, float* q_out, void* w8, void* w8t, void* wbf16t, hipStream_t st) {
   if (!w || !partials || !q_out) return kErrNullPointer;
-  if (rows <= 0 || cols <= 0 || (cols % 64) != 0 || (w8t && rows % 64) || (wbf16t && rows % 32))
+  if (E <= 0 || E > 65535 || rows <= 0 || cols <= 0 || (cols % 64) != 0 || (w8t && rows % 64) ||
+      (wbf16t && rows % 32))
     return kErrBadShape;
-  if (nparts_cap < WQ_PARTS) return kErrWorkspaceTooSmall;
+  if (nparts_cap < WQ_PARTS * E) return kErrWorkspaceTooSmall;
   if (!aligned16(w)) return kErrBadAlignment;
-  hipStream_t st = (hipStream_t)stream;
   const int64_t n = rows * cols;
+  if (n % 4) return kErrBadShape;  // every expert's matrix starts 16-byte aligned
   int nparts = (int)((n / 4 + 255) / 256);
   if (nparts > WQ_PARTS) nparts = WQ_PARTS;
   if (nparts < 1) nparts = 1;
-  hipLaunchKernelGGL(weight_amax_kernel, dim3(nparts), dim3(256), 0, st, w, n, partials);
-  // 64 x 64 tiles over rows and columns rounded up to 256 (K-slab padding)
-  dim3 grid((unsigned)((rows + 255) / 256 * 4), (unsigned)((cols + 255) / 256 * 4));
+  hipLaunchKernelGGL(weight_amax_kernel, dim3(nparts, (unsigned)E), dim3(256), 0, st, w, n, partials);
+  // 64 x 64 tiles over rows and columns rounded up to 256 (K-slab padding), one z-plane per expert
+  dim3 grid((unsigned)((rows + 255) / 256 * 4), (unsigned)((cols + 255) / 256 * 4), (unsigned)E);
   hipLaunchKernelGGL(weight_quant_kernel, grid, dim3(256), 0, st, w, rows, cols, partials, nparts, q_out,
                      (uint8_t*)w8, (uint8_t*)w8t, (uint16_t*)wbf16t);
   return launch_status();
+}
+
+int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partials, int64_t nparts_cap,
+                      float* q_out, void* w8, void* w8t, void* wbf16t, void* stream) {
+  return weight_quant_batch(w, 1, rows, cols, partials, nparts_cap, q_out, w8, w8t, wbf16t, (hipStream_t)stream);
+}
+
+int sfp8_weight_quant_experts(const float* w, int64_t E, int64_t rows, int64_t cols, float* partials,
+                              int64_t nparts_cap, float* q_out, void* w8, void* w8t, void* wbf16t, void* stream) {
+  return weight_quant_batch(w, E, rows, cols, partials, nparts_cap, q_out, w8, w8t, wbf16t, (hipStream_t)stream);
 }
 
 int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream) {

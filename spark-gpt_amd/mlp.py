@@ -89,8 +89,12 @@ def fp8_update_scales(model: nn.Module) -> None:
 
 
 def _dense_weights(m: nn.Module):
-    """(gate_up, down) fp32 master weights of a dense MLP module, else (None, None)."""
+    """(gate_up, down) fp32 master weights of an fp8 module: a dense MLP's two
+    Linear weights (2-D), or the packed expert Parameters of the reference's
+    Experts (3-D [E, 2I, D], [E, D, I], train.py:2252-2257); else (None, None)."""
     gu, dn = getattr(m, "gate_up_proj", None), getattr(m, "down_proj", None)
+    if isinstance(gu, torch.Tensor) and isinstance(dn, torch.Tensor) and gu.dim() == 3 and dn.dim() == 3:
+        return gu, dn
     w_gu, w_down = getattr(gu, "weight", None), getattr(dn, "weight", None)
     if isinstance(w_gu, torch.Tensor) and isinstance(w_down, torch.Tensor) and w_gu.dim() == 2 \
             and w_down.dim() == 2:

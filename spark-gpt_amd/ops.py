@@ -43,6 +43,13 @@ def kslab_empty(R: int, L: int, dtype, device) -> torch.Tensor:
     return torch.empty(L // n, slab_rows(R), n, dtype=dtype, device=device)
 
 
+def kslab_shape(R: int, L: int, dtype) -> tuple:
+    """Shape of kslab_empty(R, L, dtype)."""
+    n = SLAB // torch.empty((), dtype=dtype).element_size()
+    _need(L % n == 0, f"K extent {L} must be a multiple of {n}")
+    return (L // n, slab_rows(R), n)
+
+
 def slab_empty(R: int, T: int, dtype, device) -> torch.Tensor:
     """A token-contiguous K-slab copy of R feature rows over ldt_of(T) tokens
     (the weight gradients' operands): [ldt / 64, slab_rows(R), 64]; element
@@ -262,3 +269,135 @@ def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
               T, D, scale.data_ptr(), amax.data_ptr(), dh.data_ptr(), dnw.data_ptr(), parts.data_ptr(),
               parts.numel(), dy8t.data_ptr(), ldt, _lib.stream_of(h))
     return dh, dnw, dy8t
+
+
+# ------------------------------------------------------------------ MoE experts (grouped)
+def moe_padded_rows(R: int, E: int) -> int:
+    """Rows of the padded expert order (every expert's rows from a 256-row
+    boundary): the worst case for R rows over E experts."""
+    return _lib.query("sfp8_moe_padded_rows", R, E)
+
+
+def moe_plan(offsets: torch.Tensor, R: int) -> torch.Tensor:
+    """The tile table of padded expert order, built on the device from the
+    experts' inclusive row-count prefix sums (int32 [E]); no host sync."""
+    _need(offsets.is_cuda and offsets.dim() == 1, "offsets must be a 1-D device tensor")
+    offsets = offsets.to(torch.int32).contiguous()
+    E = offsets.numel()
+    n = _lib.query("sfp8_moe_plan_ints", R, E)
+    _need(n > 0, f"unsupported expert count {E}")
+    plan = torch.empty(n, dtype=torch.int32, device=offsets.device)
+    _lib.call("sfp8_moe_plan", offsets.data_ptr(), E, R, plan.data_ptr(), n, _lib.stream_of(offsets))
+    return plan
+
+
+def moe_rows_quant(src: torch.Tensor, index, plan: torch.Tensor, ldp: int, scale, sslot: int, amax, aslot: int,
+                   fmt: int, with_rows: bool):
+    """fp8 copies of gathered rows in padded expert order: (xs, xt) = (K-slab of
+    [ldp, D] or None, token-contiguous K-slab of [D, ldp]); row u of the expert
+    order is src[index[u]] (or src[u] without index)."""
+    _cuda_contig("src", src, torch.bfloat16, 2)
+    n, D = src.shape
+    dt = E4M3 if fmt == FMT_E4M3 else E5M2
+    xs = kslab_empty(ldp, D, E4M3, src.device) if with_rows else None
+    xt = kslab_empty(D, ldp, dt, src.device)
+    idx = None
+    if index is not None:
+        _need(index.is_cuda and index.dtype == torch.int64, "row index must be an int64 device tensor")
+        idx = index.contiguous()
+    _lib.call("sfp8_moe_rows_quant", src.data_ptr(), n, D, _lib.ptr(idx), 0 if idx is None else idx.numel(),
+              plan.data_ptr(), ldp, scale.data_ptr(), sslot, amax.data_ptr(), aslot, fmt, _lib.ptr(xs), xt.data_ptr(),
+              _lib.stream_of(src))
+    return xs, xt
+
+
+def weight_quant_experts(w: torch.Tensor, q_out: torch.Tensor, *, w8: bool = True, w8t: bool = False,
+                         bf16t: bool = False):
+    """Per-expert e4m3 copies of fp32 masters [E, R, C] (stacked K-slabs, as
+    weight_quant per expert); the pow2 scales land in q_out[0:E]."""
+    _cuda_contig("w", w, torch.float32, 3)
+    E, R, C = w.shape
+    _need(q_out.numel() >= E and q_out.is_contiguous(), "q_out must hold E scales")
+    dev = w.device
+    o8 = torch.empty((E,) + kslab_shape(R, C, E4M3), dtype=E4M3, device=dev) if w8 else None
+    o8t = torch.empty((E,) + kslab_shape(C, R, E4M3), dtype=E4M3, device=dev) if w8t else None
+    obt = torch.empty((E,) + kslab_shape(C, R, torch.bfloat16), dtype=torch.bfloat16, device=dev) if bf16t else None
+    parts = torch.empty(512 * E, dtype=torch.float32, device=dev)
+    _lib.call("sfp8_weight_quant_experts", w.data_ptr(), E, R, C, parts.data_ptr(), parts.numel(), q_out.data_ptr(),
+              _lib.ptr(o8), _lib.ptr(o8t), _lib.ptr(obt), _lib.stream_of(w))
+    return o8, o8t, obt
+
+
+def moe_gateup_swiglu_fwd(x8, w8, plan, scale, q_gu, amax, I: int):
+    """(gu8, h8, h8t) over padded expert order; x8 the K-slab of [ldp, D], w8
+    the stacked per-expert K-slabs of [2I, D]."""
+    D, ldp = x8.shape[0] * SLAB, x8.shape[1]
+    E = w8.shape[0]
+    dev = x8.device
+    gu8 = kslab_empty(ldp, 2 * I, E4M3, dev)
+    h8 = kslab_empty(ldp, I, E4M3, dev)
+    h8t = kslab_empty(I, ldp, E4M3, dev)
+    _lib.call("sfp8_moe_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), E, D, I, plan.data_ptr(), ldp,
+              scale.data_ptr(), q_gu.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr(),
+              _lib.stream_of(x8))
+    return gu8, h8, h8t
+
+
+def moe_down_fwd(h8, wd8, plan, scale, q_d, R: int, D: int):
+    """out [R, D] bf16 expert-order rows (no residual)."""
+    I, ldp = h8.shape[0] * SLAB, h8.shape[1]
+    E = wd8.shape[0]
+    out = torch.empty(R, D, dtype=torch.bfloat16, device=h8.device)
+    _lib.call("sfp8_moe_gemm_down_fwd", h8.data_ptr(), wd8.data_ptr(), E, D, I, plan.data_ptr(), ldp,
+              scale.data_ptr(), q_d.data_ptr(), out.data_ptr(), R, _lib.stream_of(h8))
+    return out
+
+
+def moe_down_dgrad_swiglu(dout, wdt, gu8, plan, scale, amax):
+    """(dgu8, dgu8t) e5m2 over padded expert order; dout [R, D] bf16 expert-order
+    rows, wdt the stacked bf16 K-slabs of W_down[e]^T."""
+    _cuda_contig("dout", dout, torch.bfloat16, 2)
+    R, D = dout.shape
+    I2, ldp = gu8.shape[0] * SLAB, gu8.shape[1]
+    E = wdt.shape[0]
+    dev = dout.device
+    dgu8 = kslab_empty(ldp, I2, E5M2, dev)
+    dgu8t = kslab_empty(I2, ldp, E5M2, dev)
+    _lib.call("sfp8_moe_gemm_down_dgrad_swiglu", dout.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), E, D, I2 // 2, R,
+              plan.data_ptr(), ldp, scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr(),
+              _lib.stream_of(dout))
+    return dgu8, dgu8t
+
+
+def moe_gateup_dgrad(dgu8, w8t, plan, scale, q_gu, R: int, D: int):
+    """dx [R, D] bf16 expert-order rows."""
+    I2, ldp = dgu8.shape[0] * SLAB, dgu8.shape[1]
+    E = w8t.shape[0]
+    dx = torch.empty(R, D, dtype=torch.bfloat16, device=dgu8.device)
+    _lib.call("sfp8_moe_gemm_gateup_dgrad", dgu8.data_ptr(), w8t.data_ptr(), E, D, I2 // 2, plan.data_ptr(), ldp,
+              scale.data_ptr(), q_gu.data_ptr(), dx.data_ptr(), R, _lib.stream_of(dgu8))
+    return dx
+
+
+def moe_wgrad(at, bt, M: int, N: int, E: int, plan, sa, sb):
+    """out[e] = sum over expert e's rows of at^T bt / (sa * sb), fp32 [E, M, N];
+    at (e5m2) and bt (e4m3) token-contiguous K-slab copies over padded expert order."""
+    _cuda_contig("at", at, E5M2, 3)
+    _cuda_contig("bt", bt, E4M3, 3)
+    ldp = at.shape[0] * SLAB
+    out = torch.empty(E, M, N, dtype=torch.float32, device=at.device)
+    nws = _lib.query("sfp8_moe_wgrad_workspace_floats", M, N, E)
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=at.device)
+    _lib.call("sfp8_moe_gemm_wgrad", at.data_ptr(), FMT_E5M2, bt.data_ptr(), FMT_E4M3, M, N, E, plan.data_ptr(), ldp,
+              sa.data_ptr(), sb.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(at))
+    return out
+
+
+def moe_topk_sum(dx, inverse_permutation, T: int, top_k: int):
+    """out[t] = sum of the top_k expert-order rows of token t (bf16 [T, D])."""
+    _cuda_contig("dx", dx, torch.bfloat16, 2)
+    inv = inverse_permutation.to(torch.int64).contiguous()
+    R, D = dx.shape
+    out = torch.empty(T, D, dtype=torch.bfloat16, device=dx.device)
+    _lib.call("sfp8_moe_topk_sum", dx.data_ptr(), R, D, inv.data_ptr(), T, top_k, out.data_ptr(), _lib.stream_of(dx))
+    return out

@@ -58,8 +58,16 @@ def _wkey(w_gu: Tensor, w_down: Tensor):
 
 def quantize_weights(w_gu: Tensor, w_down: Tensor):
     """(w8, w8t, wd8, wdt, wscale): e4m3 K-slabs of W_gu and its transpose,
-    of W_down, the bf16 K-slab of W_down^T and [q_gu, q_d] (train.py:949-952,
-    1211-1213, 1224-1225)."""
+    of W_down, the bf16 K-slab of W_down^T and the pow2 weight scales.
+    Dense masters (2-D): wscale = [q_gu, q_d] (train.py:949-952, 1211-1213,
+    1224-1225).  Expert masters (3-D, [E, 2I, D] and [E, D, I]): every copy
+    stacked per expert and wscale [2, E] (train.py:1535-1540, 1564-1565,
+    1567-1569)."""
+    if w_gu.dim() == 3:
+        wscale = torch.empty(2, w_gu.shape[0], dtype=torch.float32, device=w_gu.device)
+        w8, w8t, _ = ops.weight_quant_experts(_master(w_gu), wscale[0], w8=True, w8t=True)
+        wd8, _, wdt = ops.weight_quant_experts(_master(w_down), wscale[1], w8=True, bf16t=True)
+        return w8, w8t, wd8, wdt, wscale
     wscale = torch.empty(2, dtype=torch.float32, device=w_gu.device)
     w8, w8t, _ = ops.weight_quant(_master(w_gu), wscale[0:1], w8=True, w8t=True)
     wd8, _, wdt = ops.weight_quant(_master(w_down), wscale[1:2], w8=True, bf16t=True)
@@ -177,6 +185,69 @@ def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t, scale, ama
             h.new_empty((D,), dtype=torch.float32),
             h.new_empty((2 * I, D), dtype=torch.float32),
             h.new_empty((D, I), dtype=torch.float32))
+
+
+# ------------------------------------------------------------ MoE experts
+@torch.library.custom_op("sparkfp8::moe_fwd", mutates_args={"amax"})
+def moe_fwd(x: Tensor, w_gu: Tensor, w_d: Tensor, token_index: Tensor, offsets: Tensor, scale: Tensor,
+            amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """_FP8Experts.forward (train.py:1552-1587): out [R, D] bf16 expert-order
+    rows (unweighted), then for the backward the plan, x8t, gu8 and h8t (over
+    padded expert order).  Quantized expert weights stay in the weight cache."""
+    x = x.contiguous()
+    R = token_index.numel()
+    E, I2, D = w_gu.shape
+    plan = ops.moe_plan(offsets, R)
+    ldp = ops.moe_padded_rows(R, E)
+    x8, x8t = ops.moe_rows_quant(x, token_index, plan, ldp, scale, 0, amax, 0, ops.FMT_E4M3, True)
+    w8, _w8t, wd8, _wdt, wscale = cached_weights(w_gu, w_d)
+    gu8, h8, h8t = ops.moe_gateup_swiglu_fwd(x8, w8, plan, scale, wscale[0], amax, I2 // 2)
+    out = ops.moe_down_fwd(h8, wd8, plan, scale, wscale[1], R, D)
+    return out, plan, x8t, gu8, h8t
+
+
+@moe_fwd.register_fake
+def _moe_fwd_fake(x, w_gu, w_d, token_index, offsets, scale, amax):
+    R = token_index.numel()
+    E, I2, D = w_gu.shape
+    ldp = 256 * ((R + 255) // 256 + E)
+    return (x.new_empty((R, D), dtype=torch.bfloat16),
+            x.new_empty((8 + 2 * E + 3 * (ldp // 256),), dtype=torch.int32),
+            x.new_empty(ops.kslab_shape(D, ldp, E4M3), dtype=E4M3),
+            x.new_empty(ops.kslab_shape(ldp, I2, E4M3), dtype=E4M3),
+            x.new_empty(ops.kslab_shape(I2 // 2, ldp, E4M3), dtype=E4M3))
+
+
+@torch.library.custom_op("sparkfp8::moe_bwd", mutates_args={"amax"})
+def moe_bwd(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8t: Tensor, gu8: Tensor, h8t: Tensor,
+            inverse_permutation: Tensor, T: int, top_k: int, scale: Tensor,
+            amax: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """_FP8Experts.backward (train.py:1589-1605): (dx [T, D] bf16 summed over
+    each token's top_k rows, dW_gate_up fp32 [E, 2I, D], dW_down fp32 [E, D, I])."""
+    dout = dout.contiguous()
+    if dout.dtype != torch.bfloat16:
+        dout = dout.to(torch.bfloat16)
+    R, D = dout.shape
+    E, I2, _ = w_gu.shape
+    ldp = gu8.shape[1]
+    _w8, w8t, _wd8, wdt, wscale = cached_weights(w_gu, w_d)
+    # e5m2 dout over padded expert order (the down wgrad's operand) and amax[4]
+    _, dout8t = ops.moe_rows_quant(dout, None, plan, ldp, scale, 4, amax, 4, ops.FMT_E5M2, False)
+    dgu8, dgu8t = ops.moe_down_dgrad_swiglu(dout, wdt, gu8, plan, scale, amax)
+    dx = ops.moe_gateup_dgrad(dgu8, w8t, plan, scale, wscale[0], R, D)
+    del dgu8
+    dw_gu = ops.moe_wgrad(dgu8t, x8t, I2, D, E, plan, scale[3:4], scale[0:1])
+    dw_d = ops.moe_wgrad(dout8t, h8t, D, I2 // 2, E, plan, scale[4:5], scale[2:3])
+    dxn = ops.moe_topk_sum(dx, inverse_permutation, T, top_k)
+    return dxn, dw_gu, dw_d
+
+
+@moe_bwd.register_fake
+def _moe_bwd_fake(dout, w_gu, w_d, plan, x8t, gu8, h8t, inverse_permutation, T, top_k, scale, amax):
+    E, I2, D = w_gu.shape
+    return (dout.new_empty((T, D), dtype=torch.bfloat16),
+            dout.new_empty((E, I2, D), dtype=torch.float32),
+            dout.new_empty((E, D, I2 // 2), dtype=torch.float32))
 
 
 @torch.library.custom_op("sparkfp8::update_scales", mutates_args={"scale", "amax"})

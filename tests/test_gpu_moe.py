@@ -1,0 +1,237 @@
+"""GPU parity of the FP8 MoE experts (_FP8Experts, train.py:1543-1605): the
+device-built plan, the gather + e4m3 quantization (bit-exact), the grouped
+layer against the oracle (oracle/fp8_moe.py) on the same scales, the mirror of
+the reference's own test (tests/test_fp8_mlp.py:57-109: vs an fp32 autograd of
+the routed experts, an expert without tokens gets exactly zero gradients),
+determinism and the expert weight cache."""
+import pytest
+import torch
+import torch.nn as nn
+
+import spark_gpt_amd as sg
+from oracle import fp8_mlp as O
+from oracle import fp8_moe as M
+
+pytestmark = pytest.mark.gpu
+E4 = torch.float8_e4m3fn
+
+
+class _Experts(nn.Module):
+    """The reference's packed experts (train.py:2244-2260): parameters and fp8
+    buffers, and the FP8 branch of its forward (train.py:2268-2299)."""
+
+    def __init__(self, E, D, I):
+        super().__init__()
+        self.num_experts, self.hidden_dim, self.intermediate_dim = E, D, I
+        self.gate_up_proj = nn.Parameter(torch.empty(E, 2 * I, D))
+        self.down_proj = nn.Parameter(torch.empty(E, D, I))
+        self.register_buffer("fp8_scale", torch.ones(5), persistent=False)
+        self.register_buffer("fp8_amax", torch.zeros(5), persistent=False)
+
+    def forward(self, x, selected, weights):
+        T, k = x.shape[0], selected.shape[-1]
+        tok, inv, offsets, perm = M.route(selected, self.num_experts)
+        sw = weights.reshape(-1)[perm]
+        rows = sg._FP8Experts.apply(x, self.gate_up_proj, self.down_proj, tok, inv, offsets, k, self.fp8_scale,
+                                    self.fp8_amax)
+        return M.combine_topk(rows, sw, inv, k)
+
+
+def _u8(t):
+    return t.contiguous().view(torch.uint8).cpu()
+
+
+def _padded_rows(offsets, ldp):
+    """expert-order row of each padded row (-1: padding), as the plan lays them out."""
+    out = torch.full((ldp,), -1, dtype=torch.int64)
+    p = 0
+    for e, (r0, r1) in enumerate(M.expert_ranges(offsets.cpu())):
+        n = r1 - r0
+        out[p:p + n] = torch.arange(r0, r1)
+        p += -(-n // 256) * 256
+    return out
+
+
+def test_plan_matches_routing(dev):
+    E, R = 6, 1000
+    counts = torch.tensor([300, 0, 513, 1, 0, 186])
+    offsets = torch.cumsum(counts, 0).to(torch.int32)
+    plan = sg.ops.moe_plan(offsets.to(dev), R).cpu()
+    tiles = []
+    ps = 0
+    for e, c in enumerate(counts.tolist()):
+        assert plan[8 + e] == ps and plan[8 + E + e] == -(-c // 256) * 256
+        u0 = int(offsets[e]) - c
+        for j in range(-(-c // 256)):
+            tiles.append((e, u0 + 256 * j, min(256, c - 256 * j)))
+        ps += -(-c // 256) * 256
+    assert int(plan[0]) == len(tiles) and int(plan[1]) == E
+    got = plan[8 + 2 * E: 8 + 2 * E + 3 * len(tiles)].view(-1, 3)
+    assert got.tolist() == [list(t) for t in tiles]
+
+
+def test_gather_quant_bit_exact(dev):
+    T, D, E, k = 700, 1024, 5, 2
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(T, D, generator=g) * 3).to(torch.bfloat16)
+    x[7, 5] = float("nan")
+    selected = torch.stack([torch.randint(0, E, (T,), generator=g), torch.randint(0, E, (T,), generator=g)], 1)
+    tok, inv, offsets, _ = M.route(selected, E)
+    R = tok.numel()
+    plan = sg.ops.moe_plan(offsets.to(dev), R)
+    ldp = sg.ops.moe_padded_rows(R, E)
+    scale = torch.tensor([16.0, 1, 1, 1, 1], device=dev)
+    amax = torch.zeros(5, device=dev)
+    x8, x8t = sg.ops.moe_rows_quant(x.to(dev), tok.to(dev), plan, ldp, scale, 0, amax, 0, sg.ops.FMT_E4M3, True)
+    ref = _u8(O.e4m3(x[tok].float() * 16.0))
+    rows = _padded_rows(offsets, ldp)
+    got = _u8(sg.ops.unslab(x8, ldp))
+    gt = _u8(sg.ops.unslab(x8t, D))
+    valid = rows >= 0
+    assert torch.equal(got[valid], ref[rows[valid]])
+    assert torch.all(got[~valid] == 0) and torch.all(gt[:, ~valid] == 0)
+    assert torch.equal(gt.t(), got)
+    finite = x[tok].float().abs()
+    assert amax[0].item() == finite[~torch.isnan(finite)].max().item()
+
+
+def _make(dev, E, D, I, seed, std=None):
+    ex = _Experts(E, D, I)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        ex.gate_up_proj.copy_(torch.randn(E, 2 * I, D, generator=g) * (std or D ** -0.5))
+        ex.down_proj.copy_(torch.randn(E, D, I, generator=g) * (std or I ** -0.5))
+    return ex.to(dev).train()
+
+
+def _gpu_step(ex, x, selected, weights, probe):
+    xx = x.clone().requires_grad_(True)
+    out = ex(xx, selected, weights)
+    grads = torch.autograd.grad((out.float() * probe).sum(), [xx, ex.gate_up_proj, ex.down_proj])
+    return [out.detach()] + list(grads)
+
+
+def test_fp8_experts_track_fp32_reference(dev):
+    """Mirror of spark-gpt tests/test_fp8_mlp.py:57-109 (same shapes, init,
+    routing, protocol and bound), plus exactly-zero gradients of the expert
+    that gets no tokens."""
+    torch.manual_seed(0)
+    E, D, I, T, k = 4, 256, 128, 500, 2
+    ex = _make(dev, E, D, I, 0, std=0.05)
+    x = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    choices = torch.tensor([[0, 1], [1, 3], [0, 3]], device=dev)  # expert 2 gets no tokens
+    selected = choices[torch.randint(0, 3, (T,), device=dev)]
+    weights = torch.softmax(torch.randn(T, k, device=dev), -1).to(torch.bfloat16)
+    probe = torch.randn(T, D, device=dev)
+    _gpu_step(ex, x, selected, weights, probe)
+    assert bool((ex.fp8_amax > 0).all()), ex.fp8_amax
+    sg.fp8_update_scales(ex)
+    assert bool((ex.fp8_amax == 0).all())
+    out = _gpu_step(ex, x, selected, weights, probe)
+    ref = M.fp32_experts_reference(x.cpu(), selected.cpu(), weights.cpu(), ex.gate_up_proj.cpu(),
+                                   ex.down_proj.cpu(), probe.cpu())
+    for name, a, r in zip(("out", "dx", "dW_gate_up", "dW_down"), out, ref):
+        a = a.float().cpu()
+        assert torch.isfinite(a).all(), name
+        assert O.rel_l2(a, r) < 0.12, name
+    assert bool((out[2][2] == 0).all()) and bool((out[3][2] == 0).all())  # unused expert
+
+
+@pytest.mark.parametrize("T,D,I,E,k,skew", [(500, 256, 128, 4, 2, False), (4096, 1024, 256, 8, 2, True),
+                                            (300, 128, 384, 3, 1, False)])
+def test_moe_matches_oracle(dev, T, D, I, E, k, skew):
+    """Same inputs and scales: every output and gradient within rel-L2 1e-2 of
+    the oracle; amax slots 0 and 4 bit-exact.  `skew` routes half of the
+    tokens' first slot to expert 0 (the imbalance spark-gpt sees in
+    practice)."""
+    ex = _make(dev, E, D, I, T + E)
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    sel = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    if skew:
+        sel[: T // 2, 0] = 0
+        sel[: T // 2, 1] = torch.randint(1, E, (T // 2,), generator=g)
+    weights = torch.softmax(torch.randn(T, k, generator=g), -1).to(torch.bfloat16)
+    probe = torch.randn(T, D, generator=g) * 1e-2
+    args = (x.to(dev), sel.to(dev), weights.to(dev), probe.to(dev))
+    _gpu_step(ex, *args)
+    sg.fp8_update_scales(ex)
+    s = ex.fp8_scale.cpu().clone()
+    out = [t.cpu() for t in _gpu_step(ex, *args)]
+    a_gpu = ex.fp8_amax.cpu()
+    a_ref = torch.zeros(5)
+    tok, inv, offsets, perm = M.route(sel, E)
+    sw = weights.reshape(-1)[perm]
+    rows, saved = M.moe_forward(x, ex.gate_up_proj.detach().cpu(), ex.down_proj.detach().cpu(), tok, offsets,
+                                s.clone(), a_ref)
+    y = M.combine_topk(rows, sw, inv, k)
+    d_rows = M.combine_topk_backward(probe.to(torch.bfloat16), sw, tok)
+    (dx, dwgu, dwd), _ = M.moe_backward(d_rows, saved, s.clone(), a_ref, inv, k)
+    for name, a, r in zip(("out", "dx", "dW_gate_up", "dW_down"), out, (y, dx, dwgu, dwd)):
+        assert torch.isfinite(a.float()).all(), name
+        assert O.rel_l2(a.float(), r.float()) < 1e-2, name
+    assert a_gpu[0] == a_ref[0] and a_gpu[4] == a_ref[4]
+    torch.testing.assert_close(a_gpu, a_ref, rtol=2e-2, atol=0)
+
+
+def test_moe_deterministic(dev):
+    E, D, I, T, k = 4, 512, 256, 1000, 2
+    ex = _make(dev, E, D, I, 9)
+    x = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    sel = torch.stack([torch.randperm(E)[:k] for _ in range(T)]).to(dev)
+    weights = torch.softmax(torch.randn(T, k, device=dev), -1).to(torch.bfloat16)
+    probe = torch.randn(T, D, device=dev)
+    _gpu_step(ex, x, sel, weights, probe)
+    sg.fp8_update_scales(ex)
+    s0 = ex.fp8_scale.clone()
+    a = _gpu_step(ex, x, sel, weights, probe)
+    am = ex.fp8_amax.clone()
+    ex.fp8_amax.zero_()
+    ex.fp8_scale.copy_(s0)
+    b = _gpu_step(ex, x, sel, weights, probe)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    assert torch.equal(am, ex.fp8_amax)
+
+
+def test_moe_weight_cache_refresh(dev, monkeypatch):
+    """The expert copies are quantized once per optimizer step: forwards after
+    the first launch no weight quantization, fp8_update_scales re-quantizes
+    (an optimizer may write the masters through raw pointers), and the bytes
+    equal a per-forward quantization."""
+    from spark_gpt_amd import torch_ops as TO
+
+    E, D, I, T, k = 4, 256, 128, 300, 2
+    ex = _make(dev, E, D, I, 12)
+    x = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    sel = torch.stack([torch.randperm(E)[:k] for _ in range(T)]).to(dev)
+    weights = torch.softmax(torch.randn(T, k, device=dev), -1).to(torch.bfloat16)
+    probe = torch.randn(T, D, device=dev)
+    calls = []
+    real = sg.ops.weight_quant_experts
+    monkeypatch.setattr(sg.ops, "weight_quant_experts", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    TO.clear_weight_cache()
+    _gpu_step(ex, x, sel, weights, probe)
+    assert len(calls) == 2
+    sg.fp8_update_scales(ex)
+    assert len(calls) == 4
+    s0 = ex.fp8_scale.clone()
+
+    def run(cache):
+        ex.fp8_amax.zero_()
+        ex.fp8_scale.copy_(s0)
+        monkeypatch.setattr(TO, "FP8_WEIGHT_CACHE", cache)
+        return _gpu_step(ex, x, sel, weights, probe)
+
+    n = len(calls)
+    cached = run(True)
+    assert len(calls) == n
+    fresh = run(False)
+    for u, v in zip(cached, fresh):
+        assert torch.equal(u, v)
+    monkeypatch.setattr(TO, "FP8_WEIGHT_CACHE", True)
+    ex.gate_up_proj.data.mul_(0.5)  # bypasses the version counter
+    sg.fp8_update_scales(ex)
+    halved = run(True)
+    assert not torch.equal(halved[0], cached[0])
+    TO.clear_weight_cache()
