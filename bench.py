@@ -24,16 +24,22 @@ Also reported on the same JSON line:
                 algorithmic traffic / mean duration vs 8 TB/s HBM
   kernels       per-kernel mean durations (each kernel alone, 10 launches),
                 with TFLOP/s or algorithmic GB/s
-  other_workloads  the muP base block (T=8192, D=256, I=1024) on the GPU: wall
-                clock over 20 steps after 5 warm-up steps
+  other_workloads  on the GPU, wall clock over 20 steps after 5 warm-up steps:
+                the muP base block (T=8192, D=256, I=1024), and the FP8 MoE
+                experts (``_FP8Experts`` fwd+bwd + post-step hook) on 65536
+                tokens routed top-2 over 8 experts, D=1024, I=1536 (131072
+                expert rows: the dense headline's FLOP), with their in-step
+                kernels and roofline
   cpu_baseline  the same FP8 recipe emulated in torch on the host cores (the
                 CPU oracle) on a bounded token sample, in TFLOP/s; under
-                `other_workloads` the oracle on the muP base block and on an
-                8192-row sample of the quantizer input
+                `other_workloads` the oracle on the muP base block, on a
+                token sample of the MoE workload and on an 8192-row sample of
+                the quantizer input
 
 ``--trace`` runs only the headline steps (prewarm, warm-up, timed and
 instrumented passes), so that a ``rocprofv3 --kernel-trace --stats`` summary
-of it averages in-step launches of the headline shape only.
+of it averages in-step launches of the headline shape only; ``--trace moe``
+does the same for the MoE workload.
 
 ``--probe`` runs, instead of the benchmark, one calibration copy (fp32 negate
 of 256 Mi elements: 1 GiB read + 1 GiB written) and then every kernel of the
@@ -55,6 +61,9 @@ BF16_PEAK_TFLOPS = 2516.5  # MI355X dense bf16 MFMA
 HBM_PEAK_GBPS = 8000.0     # MI355X HBM3E
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_fwd_bwd_T65536_D1024_I3072.md")
 TRAFFIC_WORKLOAD = (65536, 1024, 3072)
+# the compute-matched MoE of the headline width: top-2 of 8 experts at half the
+# dense ffn (the same 18*T*k*D*I FLOP per step as the dense block)
+MOE_WORKLOAD = {"T": 65536, "D": 1024, "I": 1536, "E": 8, "k": 2}
 
 
 def parse():
@@ -70,8 +79,9 @@ def parse():
     p.add_argument("--quant-rows", type=int, default=65536)
     p.add_argument("--quant-cols", type=int, default=4096)
     p.add_argument("--probe", action="store_true", help="one launch of each kernel, for counter passes")
-    p.add_argument("--trace", action="store_true",
-                   help="headline steps only (no standalone kernels, quantizer, other shapes or CPU leg)")
+    p.add_argument("--trace", nargs="?", const="dense", choices=("dense", "moe"), default=None,
+                   help="steps of one workload only (no standalone kernels, quantizer, other shapes or CPU "
+                        "leg): the headline block (default) or the MoE experts")
     p.add_argument("--dist", choices=("normal", "student-t"), default="normal",
                    help="activations: N(0,1), or Student-t with 3 degrees of freedom (heavy tails)")
     return p.parse_args()
@@ -200,7 +210,46 @@ def cpu_extra(quant_rows: int, quant_cols: int) -> dict:
     med = sorted(times)[1]
     out["quantizer"] = {"GB/s": round(4.0 * R * quant_cols / med / 1e9, 2), "s_per_call": round(med, 4),
                         "sample": f"{R} x {quant_cols} rows of the quantizer input (4 B/elem)"}
+    del x
+    out["moe"] = cpu_moe(8192)
     return out
+
+
+def cpu_moe(T: int) -> dict:
+    """The CPU oracle's FP8 experts (fwd+bwd) on T tokens of the MoE workload
+    (top-2 of 8 experts, D=1024, I=1536), median of 3 steps after a prewarm
+    step and scale roll."""
+    import torch
+
+    from oracle import fp8_mlp as O
+    from oracle import fp8_moe as OM
+
+    mw = MOE_WORKLOAD
+    D, I, E, k = mw["D"], mw["I"], mw["E"], mw["k"]
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    wgu = torch.randn(E, 2 * I, D, generator=g) * D ** -0.5
+    wd = torch.randn(E, D, I, generator=g) * I ** -0.5
+    selected = torch.rand(T, E, generator=g).topk(k, dim=-1).indices
+    token_index, inverse_permutation, offsets, _ = OM.route(selected, E)
+    dout = (torch.randn(T * k, D, generator=g) * 1e-3).to(torch.bfloat16)
+    scale, amax = torch.ones(5), torch.zeros(5)
+
+    def step():
+        _, saved = OM.moe_forward(x, wgu, wd, token_index, offsets, scale, amax)
+        OM.moe_backward(dout, saved, scale, amax, inverse_permutation, k)
+
+    step()
+    O.update_scales(scale, amax)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[1]
+    flop = 18.0 * T * k * D * I
+    return {"TFLOP/s": round(flop / med / 1e12, 4), "s_per_step": round(med, 4),
+            "sample": f"{T} tokens top-{k} of {E} experts, d_model={D}, ffn={I}"}
 
 
 class _Norm:
@@ -271,10 +320,172 @@ def launch_name(sym: str, a, D: int, I: int) -> str:
         return "weight_quant_gu" if a[1] == 2 * I else "weight_quant_down"
     if sym == "sfp8_gemm_wgrad":
         return "wgrad_down" if a[4] == D else "wgrad_gateup"
+    if sym == "sfp8_weight_quant_experts":
+        return "weight_quant_gu" if a[2] == 2 * I else "weight_quant_down"
+    if sym == "sfp8_moe_gemm_wgrad":
+        return "moe_wgrad_down" if a[4] == D else "moe_wgrad_gateup"
+    if sym == "sfp8_moe_rows_quant":
+        return "moe_gather_quant_x" if a[11] == 0 else "moe_quant_dout"
     return {"sfp8_norm_quant": "norm_quant", "sfp8_gemm_gateup_swiglu_fwd": "gateup_swiglu_fwd",
             "sfp8_gemm_down_fwd": "down_fwd", "sfp8_gemm_down_dgrad_swiglu": "down_dgrad_swiglu_bf16",
             "sfp8_gemm_gateup_dgrad": "gateup_dgrad", "sfp8_norm_bwd": "norm_bwd",
-            "sfp8_update_scales": "update_scales"}.get(sym, sym)
+            "sfp8_update_scales": "update_scales", "sfp8_moe_plan": "moe_plan",
+            "sfp8_moe_gemm_gateup_swiglu_fwd": "moe_gateup_swiglu_fwd", "sfp8_moe_gemm_down_fwd": "moe_down_fwd",
+            "sfp8_moe_gemm_down_dgrad_swiglu": "moe_down_dgrad_swiglu_bf16",
+            "sfp8_moe_gemm_gateup_dgrad": "moe_gateup_dgrad", "sfp8_moe_topk_sum": "moe_topk_sum"}.get(sym, sym)
+
+
+def rates(work: dict, name: str, ms: float) -> dict:
+    """Mean duration of a kernel with its TFLOP/s or algorithmic GB/s."""
+    fl, by = work.get(name, (None, None))
+    rec = {"ms": round(ms, 4)}
+    if fl:
+        rec["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+    if by:
+        rec["GB/s"] = round(by / (ms * 1e-3) / 1e9, 1)
+    return rec
+
+
+def trace_steps(step, steps: int, stream, namer) -> dict:
+    """`steps` more steps with HIP events recorded on `stream` around every
+    C-ABI launch: {kernel name: [ms per launch, ...]}."""
+    import torch
+
+    from spark_gpt_amd import _lib
+
+    marks = []
+    plain_call = _lib.call
+
+    def traced_call(name, *a):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        plain_call(name, *a)
+        e1.record(stream)
+        marks.append((namer(name, a), e0, e1))
+
+    _lib.call = traced_call
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        _lib.call = plain_call
+    per = {}
+    for name, e0, e1 in marks:
+        per.setdefault(name, []).append(e0.elapsed_time(e1))
+    return per
+
+
+def in_step_summary(per: dict, steps: int, work: dict, traffic_of=lambda k: None):
+    """(per-kernel in-step means, roofline of the kernel taking the most time
+    per step): algorithmic FLOP (or bytes) per launch / mean in-step duration
+    vs the dense MFMA peak of its input type (or HBM)."""
+    in_step = {n: dict(rates(work, n, sum(v) / len(v)), launches_per_step=len(v) / steps) for n, v in per.items()}
+    dom = max(in_step, key=lambda n: in_step[n]["ms"] * in_step[n]["launches_per_step"])
+    dom_ms = in_step[dom]["ms"]
+    dom_flop, dom_bytes = work[dom]
+    if dom_flop:
+        achieved = dom_flop / (dom_ms * 1e-3) / 1e12
+        peak = BF16_PEAK_TFLOPS if "bf16" in dom else FP8_PEAK_TFLOPS
+        roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic_of(dom),
+                    "flop_per_launch": dom_flop, "launches_timed": len(per[dom]), "ms_per_launch": round(dom_ms, 4)}
+    else:
+        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_of(dom),
+                    "bytes_per_launch": dom_bytes, "launches_timed": len(per[dom]), "ms_per_launch": round(dom_ms, 4)}
+    return in_step, roofline
+
+
+def make_moe(T: int, D: int, I: int, E: int, k: int, seed: int = 4):
+    """(step, rows per expert): one training step of the FP8 experts
+    (``_FP8Experts`` forward and backward, then the post-step hook) on T
+    tokens routed to k distinct experts each (random router logits, the
+    expert-order bookkeeping of train.py:2268-2290), seed-fixed."""
+    import torch
+
+    import spark_gpt_amd as sg
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    class _ExpertWeights(torch.nn.Module):
+        """The state the experts read: packed fp32 masters and the 5-slot
+        scale / amax buffers (train.py:2252-2260)."""
+
+        def __init__(self):
+            super().__init__()
+            self.gate_up_proj = torch.nn.Parameter(torch.randn(E, 2 * I, D, device=dev, generator=g) * D ** -0.5)
+            self.down_proj = torch.nn.Parameter(torch.randn(E, D, I, device=dev, generator=g) * I ** -0.5)
+            self.register_buffer("fp8_scale", torch.ones(5, device=dev), persistent=False)
+            self.register_buffer("fp8_amax", torch.zeros(5, device=dev), persistent=False)
+
+    m = _ExpertWeights().train()
+    x = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    selected = torch.rand(T, E, device=dev, generator=g).topk(k, dim=-1).indices
+    sorted_experts, permutation = torch.sort(selected.reshape(-1))
+    token_index = permutation // k
+    inverse_permutation = torch.empty_like(permutation)
+    inverse_permutation[permutation] = torch.arange(permutation.numel(), device=dev)
+    counts = torch.bincount(sorted_experts, minlength=E)
+    offsets = torch.cumsum(counts, dim=0, dtype=torch.int32)
+    dout = (torch.randn(T * k, D, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    params = [m.gate_up_proj, m.down_proj]
+
+    def step():
+        xx = x.detach().requires_grad_(True)
+        out = sg._FP8Experts.apply(xx, m.gate_up_proj, m.down_proj, token_index, inverse_permutation, offsets, k,
+                                   m.fp8_scale, m.fp8_amax)
+        torch.autograd.backward(out, dout, inputs=[xx] + params)
+        for p in params:
+            p.grad = None
+        sg.fp8_update_scales(m)
+
+    return step, counts.tolist()
+
+
+def time_moe(T: int, D: int, I: int, E: int, k: int, steps: int, warmup: int) -> dict:
+    """GPU training-step time of the FP8 experts (prewarm step and scale roll
+    first), its in-step kernels and the roofline of the dominant one.  The
+    routed rows R = T*k carry 18*R*D*I FLOP per step."""
+    import torch
+
+    step, counts = make_moe(T, D, I, E, k)
+    stream = torch.cuda.current_stream()
+    step()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    R = T * k
+    flop = 18.0 * R * D * I
+    work = {
+        "moe_plan": (None, 4.0 * E),
+        "moe_gather_quant_x": (None, 4.0 * R * D),
+        "moe_quant_dout": (None, 3.0 * R * D),
+        "weight_quant_gu": (None, 10.0 * E * 2 * I * D),
+        "weight_quant_down": (None, 11.0 * E * D * I),
+        "moe_gateup_swiglu_fwd": (4.0 * R * D * I, None),
+        "moe_down_fwd": (2.0 * R * D * I, None),
+        "moe_down_dgrad_swiglu_bf16": (2.0 * R * D * I, None),
+        "moe_gateup_dgrad": (4.0 * R * D * I, None),
+        "moe_wgrad_gateup": (4.0 * R * D * I, None),
+        "moe_wgrad_down": (2.0 * R * D * I, None),
+        "moe_topk_sum": (None, 2.0 * R * D + 2.0 * T * D),
+        "update_scales": (None, 40.0),
+    }
+    per = trace_steps(step, steps, stream, lambda sym, a: launch_name(sym, a, D, I))
+    in_step, roofline = in_step_summary(per, steps, work)
+    return {"workload": "fp8_moe_experts_fwd_bwd", "tokens": T, "top_k": k, "experts": E, "d_model": D, "ffn": I,
+            "routed_rows": R, "rows_per_expert": counts, "flop_per_step": flop, "ms_per_step": round(ms, 4),
+            "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+            "frac_fp8_peak": round(flop / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "roofline": roofline, "kernels_in_step": in_step}
 
 
 def main() -> None:
@@ -286,8 +497,13 @@ def main() -> None:
 
     import torch
 
-    from spark_gpt_amd import _lib, ops
+    from spark_gpt_amd import ops
 
+    if args.trace == "moe":
+        mw = MOE_WORKLOAD
+        print(json.dumps({"moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], args.steps, args.warmup)}),
+              flush=True)
+        return
     dev = torch.device("cuda:0")
     T, D, I = args.tokens, args.d_model, args.ffn
     h, dy, norm, mlp, step = make_block(T, D, I, args.dist)
@@ -309,15 +525,6 @@ def main() -> None:
         "wgrad_gateup": (4.0 * T * D * I, None),
         "update_scales": (None, 40.0),
     }
-
-    def rates(name, ms):
-        fl, by = work.get(name, (None, None))
-        rec = {"ms": round(ms, 4)}
-        if fl:
-            rec["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
-        if by:
-            rec["GB/s"] = round(by / (ms * 1e-3) / 1e9, 1)
-        return rec
 
     out_extra = {}
     if args.probe or not args.trace:
@@ -375,7 +582,7 @@ def main() -> None:
             print(json.dumps({"probe": list(kern) + ["quantizer"], "copy_bytes_read": 1 << 30,
                               "copy_bytes_written": 1 << 30}))
             return
-        out_extra["kernels"] = {name: rates(name, timed_launches(fn, 10, stream)) for name, fn in kern.items()}
+        out_extra["kernels"] = {name: rates(work, name, timed_launches(fn, 10, stream)) for name, fn in kern.items()}
         del x8, x8t, rstd, w8, w8t, wd8, wdt, gu8, h8, h8t, dgu8, dgu8t, dxn, dh, dnw, dy8t
 
     # ---- timed steps (clean: nothing but the step's own launches) ----
@@ -391,42 +598,9 @@ def main() -> None:
     tflops = flop / (ms * 1e-3) / 1e12
 
     # ---- the same steps again, HIP events around every C-ABI launch ----
-    marks = []
-    plain_call = _lib.call
-
-    def traced_call(name, *a):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        plain_call(name, *a)
-        e1.record(stream)
-        marks.append((launch_name(name, a, D, I), e0, e1))
-
-    _lib.call = traced_call
-    try:
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-    finally:
-        _lib.call = plain_call
-    per = {}
-    for name, e0, e1 in marks:
-        per.setdefault(name, []).append(e0.elapsed_time(e1))
-    in_step = {n: dict(rates(n, sum(v) / len(v)), launches_per_step=len(v) / args.steps) for n, v in per.items()}
-    dom = max(in_step, key=lambda n: in_step[n]["ms"] * in_step[n]["launches_per_step"])
-    dom_ms = in_step[dom]["ms"]
-    dom_flop, dom_bytes = work[dom]
-    traffic = read_traffic(dom) if (T, D, I) == TRAFFIC_WORKLOAD else None
-    if dom_flop:
-        achieved = dom_flop / (dom_ms * 1e-3) / 1e12
-        peak = BF16_PEAK_TFLOPS if "bf16" in dom else FP8_PEAK_TFLOPS
-        roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1), "peak": peak,
-                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
-                    "flop_per_launch": dom_flop, "launches_timed": len(per[dom]), "ms_per_launch": round(dom_ms, 4)}
-    else:
-        achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-        roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                    "bytes_per_launch": dom_bytes, "launches_timed": len(per[dom]), "ms_per_launch": round(dom_ms, 4)}
+    per = trace_steps(step, args.steps, stream, lambda sym, a: launch_name(sym, a, D, I))
+    in_step, roofline = in_step_summary(
+        per, args.steps, work, lambda k: read_traffic(k) if (T, D, I) == TRAFFIC_WORKLOAD else None)
 
     out = {
         "metric": "FP8 MLP fwd+bwd TFLOP/s (% FP8 MFMA peak); quantize GB/s (% HBM peak)",
@@ -466,7 +640,10 @@ def main() -> None:
                             "frac_hbm": round(qgbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": qbytes}
         del xq
         # the muP base block (T=8192, D=256, I=1024): timed, not targeted
-        out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5)}
+        del h, dy, norm, mlp, step
+        mw = MOE_WORKLOAD
+        out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5),
+                                  "moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], 20, 5)}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline(args.cpu_tokens, D, I)
             out["cpu_baseline"]["other_workloads"] = cpu_extra(args.quant_rows, args.quant_cols)

@@ -227,26 +227,26 @@ int sfp8_moe_rows_quant(const void* src, int64_t nsrc, int64_t D, const int64_t*
                         int fmt, void* xs, void* xt, void* stream);
 
 /* Per-expert weight quantization, replaces _fp8_quantize_experts
- * (train.py:1535-1540): E matrices [rows, cols] fp32 -> q_out[e], and
+ * (train.py:1536-1540): E matrices [rows, cols] fp32 -> q_out[e], and
  * optionally per expert w8 / w8t / bf16 W^T K-slabs as sfp8_weight_quant
  * (stacked, one whole K-slab per expert).  partials: 512 * E floats. */
 int sfp8_weight_quant_experts(const float* w, int64_t E, int64_t rows, int64_t cols, float* partials,
                               int64_t nparts_cap, float* q_out, void* w8, void* w8t, void* wbf16t, void* stream);
 
 /* Grouped gate/up forward + SwiGLU, replaces _fp8_moe_swiglu_fwd_kernel
- * (train.py:1317-1352): as sfp8_gemm_gateup_swiglu_fwd over padded expert
+ * (train.py:1316-1353): as sfp8_gemm_gateup_swiglu_fwd over padded expert
  * order, expert e's W8 at w8 + e * D * slab_rows(2I) and q_gu[e]. */
 int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, int64_t D, int64_t I, const int* plan,
                                     int64_t ldp, const float* scale, const float* q_gu, float* amax, void* gu8,
                                     void* h8, void* h8t, void* stream);
 
 /* Grouped down forward, replaces _fp8_moe_down_fwd_kernel
- * (train.py:1355-1377): out [R, D] bf16 expert-order rows (no residual). */
+ * (train.py:1356-1378): out [R, D] bf16 expert-order rows (no residual). */
 int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D, int64_t I, const int* plan,
                            int64_t ldp, const float* scale, const float* q_d, void* out, int64_t R, void* stream);
 
 /* Grouped bf16 down dgrad + SwiGLU backward, replaces
- * _fp8_moe_down_dgrad_swiglu_kernel (train.py:1380-1420): dout [R, D] bf16
+ * _fp8_moe_down_dgrad_swiglu_kernel (train.py:1381-1423): dout [R, D] bf16
  * expert-order rows, wdt per expert (bf16 K-slab of W_down[e]^T) ->
  * dgu8 / dgu8t over padded expert order; amax[3].  (amax[4] = max|dout| is
  * recorded by the e5m2 dout copy, sfp8_moe_rows_quant.) */
@@ -254,13 +254,13 @@ int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const voi
                                     int64_t I, int64_t R, const int* plan, int64_t ldp, const float* scale,
                                     float* amax, void* dgu8, void* dgu8t, void* stream);
 
-/* Grouped gate/up dgrad, replaces _fp8_moe_dgrad_kernel (train.py:1423-1443):
+/* Grouped gate/up dgrad, replaces _fp8_moe_dgrad_kernel (train.py:1425-1448):
  * dx [R, D] bf16 expert-order rows. */
 int sfp8_moe_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t E, int64_t D, int64_t I, const int* plan,
                                int64_t ldp, const float* scale, const float* q_gu, void* dx, int64_t R, void* stream);
 
-/* Grouped weight gradient, replaces _fp8_moe_wgrad_kernel (train.py:1446-1477)
- * and _fp8_moe_wgrad_rows_kernel (train.py:1503-1529, whose fp32 atomics are
+/* Grouped weight gradient, replaces _fp8_moe_wgrad_kernel (train.py:1450-1478)
+ * and _fp8_moe_wgrad_rows_kernel (train.py:1503-1533, whose fp32 atomics are
  * replaced by split partials summed in order: deterministic):
  * out[e] = sum over expert e's rows of at[:, t] bt[:, t]^T / (sa * sb),
  * fp32 [E, M, N]; experts without rows get zeros.  ws: fp32 workspace of

@@ -4,9 +4,9 @@ TEST INFRASTRUCTURE ONLY (the checker; never shipped).
 Follows ``train.py`` of N8python/spark-gpt, lines 1255-1606, per expert with
 the dense block's pieces (``oracle/fp8_mlp.py``): the expert-order gather and
 e4m3 quantization of x (train.py:1300-1314), per-expert pow2 weight scales
-(train.py:1535-1540), the grouped SwiGLU forward (1317-1352), down forward
-(1355-1377), down dgrad + SwiGLU backward (1380-1420), gate/up dgrad
-(1423-1443), the two weight gradients (1446-1529) and the top-k row sum
+(train.py:1536-1540), the grouped SwiGLU forward (1316-1353), down forward
+(1356-1378), down dgrad + SwiGLU backward (1381-1423), gate/up dgrad
+(1425-1448), the two weight gradients (1450-1533) and the top-k row sum
 (2213-2217).  Expert e owns expert-order rows offsets[e-1] .. offsets[e]-1.
 """
 from __future__ import annotations
@@ -17,7 +17,7 @@ from .fp8_mlp import amax_of, down_dgrad_swiglu, e4m3, e5m2, f, swiglu_fwd
 
 
 def quantize_experts(w: torch.Tensor):
-    """Per-expert e4m3 copies of (E, out, in) fp32 masters, train.py:1535-1540."""
+    """Per-expert e4m3 copies of (E, out, in) fp32 masters, train.py:1536-1540."""
     amax = w.detach().float().abs().amax(dim=(1, 2)).clamp(min=1e-30)
     q = torch.exp2(torch.floor(torch.log2(448.0 / amax)))
     return (w.detach().float() * q[:, None, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn), q

@@ -763,7 +763,7 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
       (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[0]);
   if (plan) {
-    // expert rows, no residual: out rounded to bf16 (train.py:1439-1441 stores acc / (s2 q_d) as bf16)
+    // expert rows, no residual: out rounded to bf16 (train.py:1377-1378 stores acc / (s2 q_d) as bf16)
     stage_bf16_half<0>(lds, acc, deq);
     __syncthreads();
     write_bf16_half(lds, 0, u0, n0, u0 + urows, D, D, nullptr, y);

@@ -61,8 +61,8 @@ def quantize_weights(w_gu: Tensor, w_down: Tensor):
     of W_down, the bf16 K-slab of W_down^T and the pow2 weight scales.
     Dense masters (2-D): wscale = [q_gu, q_d] (train.py:949-952, 1211-1213,
     1224-1225).  Expert masters (3-D, [E, 2I, D] and [E, D, I]): every copy
-    stacked per expert and wscale [2, E] (train.py:1535-1540, 1564-1565,
-    1567-1569)."""
+    stacked per expert and wscale [2, E] (train.py:1536-1540, 1561-1562,
+    1572-1573)."""
     if w_gu.dim() == 3:
         wscale = torch.empty(2, w_gu.shape[0], dtype=torch.float32, device=w_gu.device)
         w8, w8t, _ = ops.weight_quant_experts(_master(w_gu), wscale[0], w8=True, w8t=True)

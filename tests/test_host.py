@@ -233,7 +233,8 @@ def _integration_snippet():
 
 # The parts of spark-gpt's train.py this path touches, reduced to what the
 # binding needs: the switch (train.py:914), main()'s rebinding of it
-# (train.py:3635-3642) and Block.forward's dispatch (train.py:2359-2365).
+# (train.py:3635-3642), Block.forward's dispatch (train.py:2359-2365) and
+# Experts.forward's (train.py:2292-2296).
 _STUB_TRAINER_HEAD = """
 FP8_MLP = False
 """
@@ -251,6 +252,17 @@ class Block:
         if _use_fp8_mlp(b, h):
             return _FP8MLPBlock.apply(h, b.norm_w, b.mlp.gate_up_proj.weight, b.mlp.down_proj.weight,
                                       b.mlp.fp8_scale, b.mlp.fp8_amax, 1e-6)
+        return "bf16"
+
+class Experts:
+    def __init__(self, m):
+        self.m = m
+
+    def forward(self, x, token_index, inverse_permutation, offsets, top_k):
+        m = self.m
+        if _use_fp8_moe(m, x):
+            return _FP8Experts.apply(x, m.gate_up_proj, m.down_proj, token_index, inverse_permutation, offsets,
+                                     top_k, m.fp8_scale, m.fp8_amax)
         return "bf16"
 """
 
@@ -289,6 +301,47 @@ def test_documented_trainer_binding(monkeypatch):
     train.main(False)
     dense.train()
     assert blk.forward(h) == "bf16"
+
+
+def test_documented_trainer_binding_experts(monkeypatch):
+    """The same substitution routes a training Experts module (power-of-two
+    hidden size, 128-divisible expert ffn) to _FP8Experts once main() sets
+    FP8_MLP, and nothing else."""
+    import types
+
+    train = types.ModuleType("train_stub")
+    exec(_STUB_TRAINER_HEAD + _integration_snippet() + _STUB_TRAINER_TAIL, train.__dict__)
+    assert train._FP8Experts is sg._FP8Experts
+    calls = []
+
+    class _Recorder:
+        @staticmethod
+        def apply(*args):
+            calls.append(args)
+            return "fp8"
+
+    monkeypatch.setattr(train, "_FP8Experts", _Recorder)
+    m = torch.nn.Module()
+    m.hidden_dim, m.intermediate_dim = 1024, 768
+    m.gate_up_proj = torch.nn.Parameter(torch.zeros(4, 2 * 768, 1024))
+    m.down_proj = torch.nn.Parameter(torch.zeros(4, 1024, 768))
+    m.fp8_scale, m.fp8_amax = torch.ones(5), torch.zeros(5)
+    m.train()
+    ex = train.Experts(m)
+    x = _FakeCudaTensor((10, 1024))
+    args = (None, None, None, 2)
+    assert ex.forward(x, *args) == "bf16" and not calls
+    train.main(True)
+    assert ex.forward(x, *args) == "fp8" and len(calls) == 1
+    assert calls[0][1] is m.gate_up_proj and calls[0][6] == 2 and calls[0][8] is m.fp8_amax
+    m.eval()
+    assert ex.forward(x, *args) == "bf16"
+    m.train()
+    m.intermediate_dim = 100  # not a multiple of 128
+    assert ex.forward(x, *args) == "bf16"
+    m.intermediate_dim, m.hidden_dim = 768, 768  # not a power of two
+    assert ex.forward(_FakeCudaTensor((10, 768)), *args) == "bf16"
+    train.main(False)
 
 
 def test_set_fp8_mlp_switches_package_guard(monkeypatch):
