@@ -219,9 +219,8 @@ int sfp8_moe_plan(const int* offsets, int64_t E, int64_t R, int* plan, int64_t p
  *     xs = K-slab of e4m3(clamp(x * scale[sslot])) over [ldp, D] (the gate/up
  *     GEMM's A), xt = its token-contiguous K-slab [D, ldp];
  *   fmt = e5m2 (1), xs = NULL: the e5m2 dout copy the down weight gradient
- *     quantizes in registers (train.py:1520-1521), token-contiguous.
- * amax[aslot] = max |src| over the gathered rows.  D % 128 == 0, and a
- * multiple of 1024 above 1024. */
+ *     quantizes in registers (train.py:1525-1526), token-contiguous.
+ * amax[aslot] = max |src| over the gathered rows.  D % 128 == 0. */
 int sfp8_moe_rows_quant(const void* src, int64_t nsrc, int64_t D, const int64_t* map, int64_t nmap,
                         const int* plan, int64_t ldp, const float* scale, int sslot, float* amax, int aslot,
                         int fmt, void* xs, void* xt, void* stream);

@@ -68,10 +68,15 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ o
 //   optional: the gate/up GEMM's A operand) and as the token-contiguous
 //   K-slab of [D, ldp] (xt: the weight gradients' operand),
 //   amax[aslot] = max |src| over the gathered rows.
-// A work-group takes 64 padded rows; columns go in chunks of up to 1024,
-// staged in an LDS tile and written transposed as whole 64-byte rows.
+// A work-group takes 64 padded rows; columns go in chunks of up to 512 (the
+// last one ragged), staged in a 17 KiB LDS tile (eight work-groups per CU)
+// and written transposed as whole 64-byte rows.  Within a chunk, 16-byte
+// source unit f is (slab f >> 9, row (f >> 3) & 63, 8 columns 8 * (f & 7)):
+// a wave reads 128-byte runs of 8 rows and writes 512 contiguous bytes of
+// one xs slab; each thread keeps kRqBatch loads in flight.
 constexpr int kRqRows = 64;
-constexpr int kRqChunk = 1024;
+constexpr int kRqChunk = 256;
+constexpr int kRqBatch = 4;
 
 template <int FMT>
 __global__ __launch_bounds__(256) void moe_rows_quant_kernel(
@@ -98,40 +103,52 @@ __global__ __launch_bounds__(256) void moe_rows_quant_kernel(
   }
   __syncthreads();
   const float s = scale[sslot];
-  const int64_t C = D < kRqChunk ? D : kRqChunk;
-  const int stride = (int)C + 16;  // conflict-free transposing reads
-  const int units = (int)(C / 8);  // 8-column units per row
+  const int stride = (int)(D < kRqChunk ? D : kRqChunk) + 16;  // conflict-free transposing reads
   const int64_t cp = slab_rows(D);
   float m = 0.0f;
-  for (int64_t cc = 0; cc < D; cc += C) {
-    for (int f = threadIdx.x; f < kRqRows * units; f += 256) {
-      const int r = f / units, u = f % units;
-      const int64_t sr = rsrc[r];
-      const int64_t d = cc + 8 * u;
-      intx4 v = {0, 0, 0, 0};
-      if (sr >= 0) v = *reinterpret_cast<const intx4*>(src + sr * D + d);
-      float x[8];
+  for (int64_t cc = 0; cc < D; cc += kRqChunk) {
+    const int C = (int)(D - cc < kRqChunk ? D - cc : kRqChunk);
+    const int units = kRqRows * (C / 8);
+    for (int f0 = threadIdx.x; f0 < units; f0 += kRqBatch * 256) {
+      intx4 v[kRqBatch];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        x[2 * k] = bf16_bits_to_f32((uint32_t)v[k] & 0xffffu);
-        x[2 * k + 1] = bf16_bits_to_f32((uint32_t)v[k] >> 16);
+      for (int i = 0; i < kRqBatch; ++i) {
+        const int f = f0 + 256 * i;
+        const int64_t sr = rsrc[(f >> 3) & 63];
+        v[i] = intx4{0, 0, 0, 0};
+        if (f < units && sr >= 0)
+          v[i] = *reinterpret_cast<const intx4*>(src + sr * D + cc + 64 * (f >> 9) + 8 * (f & 7));
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(x[k]));
-      uint32_t lo, hi;
-      if (FMT == kFmtE4M3) {
-        lo = pack4_e4m3(x[0] * s, x[1] * s, x[2] * s, x[3] * s);
-        hi = pack4_e4m3(x[4] * s, x[5] * s, x[6] * s, x[7] * s);
-      } else {
-        lo = pack4_e5m2(x[0] * s, x[1] * s, x[2] * s, x[3] * s);
-        hi = pack4_e5m2(x[4] * s, x[5] * s, x[6] * s, x[7] * s);
+      for (int i = 0; i < kRqBatch; ++i) {
+        const int f = f0 + 256 * i;
+        if (f < units) {
+          const int k = f & 7, r = (f >> 3) & 63, c = f >> 9;
+          float x[8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            x[2 * q] = bf16_bits_to_f32((uint32_t)v[i][q] & 0xffffu);
+            x[2 * q + 1] = bf16_bits_to_f32((uint32_t)v[i][q] >> 16);
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(x[q]));
+          uint32_t lo, hi;
+          if (FMT == kFmtE4M3) {
+            lo = pack4_e4m3(x[0] * s, x[1] * s, x[2] * s, x[3] * s);
+            hi = pack4_e4m3(x[4] * s, x[5] * s, x[6] * s, x[7] * s);
+          } else {
+            lo = pack4_e5m2(x[0] * s, x[1] * s, x[2] * s, x[3] * s);
+            hi = pack4_e5m2(x[4] * s, x[5] * s, x[6] * s, x[7] * s);
+          }
+          if (xs)
+            *reinterpret_cast<intx2*>(xs + ((cc >> 6) + c) * ldp * 64 + (p0 + r) * 64 + 8 * k) =
+                intx2{(int)lo, (int)hi};
+          *reinterpret_cast<intx2*>(tile + r * stride + 64 * c + 8 * k) = intx2{(int)lo, (int)hi};
+        }
       }
-      const int64_t p = p0 + r;
-      if (xs) *reinterpret_cast<intx2*>(xs + (d >> 6) * ldp * 64 + p * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
-      *reinterpret_cast<intx2*>(tile + r * stride + 8 * u) = intx2{(int)lo, (int)hi};
     }
     __syncthreads();
-    lds_rows_store_slab_tr<kRqRows>(tile, (int)C, stride, xt, cp, p0, cc);
+    lds_rows_store_slab_tr<kRqRows>(tile, C, stride, xt, cp, p0, cc);
     __syncthreads();  // the next chunk overwrites the tile
   }
   block_amax_atomic<4>(m, red, amax + aslot);
@@ -213,8 +230,7 @@ int sfp8_moe_rows_quant(const void* src, int64_t nsrc, int64_t D, const int64_t*
                         const int* plan, int64_t ldp, const float* scale, int sslot, float* amax, int aslot,
                         int fmt, void* xs, void* xt, void* stream) {
   if (!scale || !amax || !plan || (ldp > 0 && !xt) || (nsrc > 0 && !src)) return kErrNullPointer;
-  if (D <= 0 || D % 128 || (D > kRqChunk && D % kRqChunk) || ldp < 0 || ldp % 256 || nsrc < 0 || nmap < 0)
-    return kErrBadShape;
+  if (D <= 0 || D % 128 || ldp < 0 || ldp % 256 || nsrc < 0 || nmap < 0) return kErrBadShape;
   if (sslot < 0 || sslot > 4 || aslot < 0 || aslot > 4 || (fmt != kFmtE4M3 && fmt != kFmtE5M2) ||
       (xs && fmt != kFmtE4M3))
     return kErrBadShape;

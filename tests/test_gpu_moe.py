@@ -70,8 +70,11 @@ def test_plan_matches_routing(dev):
     assert got.tolist() == [list(t) for t in tiles]
 
 
-def test_gather_quant_bit_exact(dev):
-    T, D, E, k = 700, 1024, 5, 2
+@pytest.mark.parametrize("D", [1024, 384, 640, 2560])
+def test_gather_quant_bit_exact(dev, D):
+    """x gathered and quantized: one column chunk (384), whole chunks (1024,
+    2560) and a ragged last chunk (640)."""
+    T, E, k = 700, 5, 2
     g = torch.Generator().manual_seed(3)
     x = (torch.randn(T, D, generator=g) * 3).to(torch.bfloat16)
     x[7, 5] = float("nan")
@@ -93,6 +96,32 @@ def test_gather_quant_bit_exact(dev):
     assert torch.equal(gt.t(), got)
     finite = x[tok].float().abs()
     assert amax[0].item() == finite[~torch.isnan(finite)].max().item()
+
+
+def test_dout_quant_e5m2_bit_exact(dev):
+    """The e5m2 form (no gather, no row copy): dout rows of the caller's expert
+    order to the token-contiguous K-slab over padded expert order, amax of
+    |dout| in slot 4, saturating values clamped to +-57344."""
+    E, D = 3, 512
+    counts = torch.tensor([300, 0, 77])
+    offsets = torch.cumsum(counts, 0).to(torch.int32)
+    R = int(counts.sum())
+    g = torch.Generator().manual_seed(4)
+    dout = (torch.randn(R, D, generator=g) * 1e-3).to(torch.bfloat16)
+    dout[5, :3] = torch.tensor([1.0, -1.0, 0.25]).to(torch.bfloat16)  # x scale 2^16: clamps
+    plan = sg.ops.moe_plan(offsets.to(dev), R)
+    ldp = sg.ops.moe_padded_rows(R, E)
+    scale = torch.tensor([1, 1, 1, 1, 2.0 ** 16], device=dev)
+    amax = torch.zeros(5, device=dev)
+    xs, xt = sg.ops.moe_rows_quant(dout.to(dev), None, plan, ldp, scale, 4, amax, 4, sg.ops.FMT_E5M2, False)
+    assert xs is None
+    ref = _u8(O.e5m2(dout.float() * 2.0 ** 16))
+    rows = _padded_rows(offsets, ldp)
+    gt = _u8(sg.ops.unslab(xt, D))
+    valid = rows >= 0
+    assert torch.equal(gt.t()[valid], ref[rows[valid]])
+    assert torch.all(gt[:, ~valid] == 0)
+    assert amax[4].item() == dout.float().abs().max().item() and amax[:4].sum().item() == 0
 
 
 def _make(dev, E, D, I, seed, std=None):
