@@ -276,6 +276,94 @@ int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, in
 int sfp8_moe_topk_sum(const void* dx, int64_t R, int64_t D, const int64_t* inv, int64_t T, int64_t k, void* out,
                       void* stream);
 
+/* ---------------------------------------------------------------------------
+ * bf16 SwiGLU path (spark-gpt's default, non-FP8 MLP path): _NormSwiGLU
+ * (train.py:2101-2131) and _FusedSwiGLU (train.py:2067-2090), dense or
+ * grouped over MoE experts (rows in padded expert order, a plan from
+ * sfp8_moe_plan).  bf16 K-slab of a row-major X [R, C]: element (r, c) at
+ * byte ((c / 32) * roundup(R, 256) + r) * 64 + (c % 32) * 2.  D % 64 == 0,
+ * I % 64 == 0.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of the bf16 K-slab of [rows, cols] (cols % 32 == 0), else -1. */
+int64_t sfp8_bf16_slab_bytes(int64_t rows, int64_t cols);
+
+/* W [E][R][C] (fp32, times nw[c] when nw != NULL; or bf16 when src_bf16)
+ * -> ws = bf16 K-slabs of W[e] (when ws != NULL) and wt = of W[e]^T (when
+ * wt != NULL), stacked per expert; padding rows zero.  Replaces the weight
+ * casts of train.py:2112 (W' = bf16(w_gu * norm_w)), 259 and 2306, whose
+ * results the reference's kernels read through strides.  R % 64 == 0,
+ * C % 64 == 0. */
+int sfp8_bf16_weight_slabs(const void* w, int src_bf16, const float* nw, int64_t E, int64_t R, int64_t C, void* ws,
+                           void* wt, void* stream);
+
+/* x [nsrc, D] bf16 rows in padded order (plan, or rows 0..nsrc-1 when plan
+ * is NULL) -> xt, the token-contiguous bf16 K-slab of x^T over ldp rows (the
+ * weight gradient's operand; zeros past the rows), and with rstd (plan NULL
+ * only) rstd[t] = 1 / sqrt(sum x^2 / D + eps): the row statistic
+ * _swiglu_gemm_kernel accumulates in its NORM mode (train.py:1689-1700). */
+int sfp8_bf16_rows_prep(const void* x, int64_t nsrc, int64_t D, const int* plan, int64_t ldp, float eps, float* rstd,
+                        void* xt, void* stream);
+
+/* Gate/up GEMM with the SwiGLU epilogue, replaces _swiglu_gemm_kernel
+ * (train.py:1625-1716, launch 1719-1743): x [T, D] bf16, w = bf16 K-slab of
+ * W [2I, D] (gate rows first), rstd [T] or NULL (the folded-norm row scale):
+ * gu = [bf16(acc_g * rs) | bf16(acc_u * rs)] [T, 2I], h = bf16(g sigmoid(g) u)
+ * [T, I]. */
+int sfp8_bf16_gemm_swiglu_fwd(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd,
+                              void* gu, void* h, void* stream);
+
+/* The same grouped (E experts, _FusedSwiGLU with several groups): x, gu, h
+ * in expert order, w the stacked per-expert K-slabs. */
+int sfp8_bf16_moe_gemm_swiglu_fwd(const void* x, const void* w, int64_t E, int64_t D, int64_t I, const int* plan,
+                                  int64_t ldp, void* gu, void* h, void* stream);
+
+/* The SwiGLU gradient of the rows, replaces _swiglu_tiles in the prologues of
+ * _swiglu_dgrad_kernel and _swiglu_wgrad_kernel (train.py:1899-2026), once
+ * for both: G' = [bf16(dh u sig (1 + g (1 - sig))) | bf16(dh g sig)] with
+ * dh = dout * rstd (rstd NULL: 1), written as gs = its bf16 K-slab over ldp
+ * padded rows and gt = the token-contiguous K-slab of G'^T; padding zero. */
+int sfp8_bf16_swiglu_bwd(const void* gu, const void* dout, int64_t nsrc, int64_t I, const float* rstd,
+                         const int* plan, int64_t ldp, void* gs, void* gt, void* stream);
+
+/* out [T, N] = bf16(A B^T): A the bf16 K-slab of [lda rows, K], B of [N, K];
+ * the dgrad of _swiglu_dgrad_kernel (train.py:1907-1980, its d_gu operand
+ * precomputed by sfp8_bf16_swiglu_bwd).  N % 8 == 0, K % 32 == 0. */
+int sfp8_bf16_gemm(const void* a, const void* b, int64_t T, int64_t N, int64_t K, int64_t lda, void* out,
+                   void* stream);
+
+/* The same grouped: A over ldp padded rows, out in expert order. */
+int sfp8_bf16_moe_gemm(const void* a, const void* b, int64_t E, int64_t N, int64_t K, const int* plan, int64_t ldp,
+                       void* out, void* stream);
+
+/* _NormSwiGLU's RMSNorm backward (train.py:2125-2128): dh = bf16(p - rstd^2
+ * sum(h p) / D h) per row, p [T, D] bf16 the dgrad output. */
+int sfp8_bf16_norm_dh(const void* p, const void* h, const float* rstd, int64_t T, int64_t D, void* dh, void* stream);
+
+/* Weight gradient, replaces _swiglu_wgrad_kernel (train.py:1983-2026):
+ * out [M, N] = bf16(sum over ldt tokens of at[:, t] bt[:, t]^T), at / bt the
+ * token-contiguous bf16 K-slabs of [M, ldt] / [N, ldt]; split partials summed
+ * in order (deterministic).  ws: fp32 workspace of
+ * sfp8_bf16_wgrad_workspace_floats(M, N, ldt) floats.  M N % 8 == 0. */
+int64_t sfp8_bf16_wgrad_splits(int64_t M, int64_t N, int64_t ldt);
+int64_t sfp8_bf16_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt);
+int sfp8_bf16_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, int64_t ldt, void* out, float* ws,
+                         int64_t ws_floats, void* stream);
+
+/* The same per expert over its padded rows: out [E, M, N] bf16, zeros for
+ * experts without rows (train.py:2047-2063 with several groups). */
+int64_t sfp8_bf16_moe_wgrad_workspace_floats(int64_t M, int64_t N, int64_t E);
+int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, int64_t E, const int* plan,
+                             int64_t ldp, void* out, float* ws, int64_t ws_floats, void* stream);
+
+/* _NormSwiGLU's fold of the weight gradient (train.py:2129-2131): dw =
+ * f32(dwp) * nw (fp32 [M, N]) and dnw[n] = sum over m of f32(dwp[m, n]) *
+ * w[m, n] (fp32, 64-row blocks in order, then their sum in order); part:
+ * sfp8_bf16_fold_partials(M, N) floats. */
+int64_t sfp8_bf16_fold_partials(int64_t M, int64_t N);
+int sfp8_bf16_fold_grads(const void* dwp, const float* w, const float* nw, int64_t M, int64_t N, float* dw,
+                         float* dnw, float* part, int64_t part_floats, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

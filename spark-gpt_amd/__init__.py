@@ -1,4 +1,5 @@
-"""MI355X-native FP8 SwiGLU MLP block for spark-gpt (gfx950 HIP kernels behind a C ABI).
+"""MI355X-native SwiGLU MLP paths of spark-gpt: the FP8 block and experts, and the
+bf16 fused SwiGLU (gfx950 HIP kernels behind a C ABI).
 
 Import as ``spark_gpt_amd`` (the repository-root module of that name loads
 this directory as the package).
@@ -6,12 +7,16 @@ this directory as the package).
 from .mlp import (FP8_HEADROOM_BINADES, FP8_SITE_MAX, MLP, _FP8MLPBlock, _use_fp8_mlp,
                   fp8_mlp_block, fp8_update_scales, make_fp8_mlp_guard, set_fp8_mlp)
 from .moe import _FP8Experts, _use_fp8_moe, make_fp8_moe_guard
-from . import mlp, moe, ops, torch_ops
+from .swiglu import (_FusedSwiGLU, _NormSwiGLU, _use_fused_norm_mlp, _use_fused_swiglu, make_fused_norm_mlp_guard,
+                     make_fused_swiglu_guard)
+from . import mlp, moe, ops, swiglu, torch_ops
 
 __all__ = [
     "FP8_HEADROOM_BINADES", "FP8_SITE_MAX", "MLP", "_FP8MLPBlock", "_use_fp8_mlp",
     "fp8_mlp_block", "fp8_update_scales", "make_fp8_mlp_guard", "mlp", "ops", "set_fp8_mlp", "torch_ops",
     "_FP8Experts", "_use_fp8_moe", "make_fp8_moe_guard", "moe",
+    "_FusedSwiGLU", "_NormSwiGLU", "_use_fused_norm_mlp", "_use_fused_swiglu", "make_fused_norm_mlp_guard",
+    "make_fused_swiglu_guard", "swiglu",
 ]
 
 

@@ -1014,7 +1014,10 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
 // (frag_offset below: each wave store instruction is one contiguous 1 KiB
 // run) and splitk_reduce_kernel sums them in split order (deterministic) and
 // scatters them to [M, N].
-template <int FMT_A, int FMT_B>
+// BF16: bf16 operands (2 bytes per token: `ldt` and `kchunk` count K bytes),
+// and the partials always go to `out` as the workspace, for the bf16 reduce
+// (bf16_wgrad_reduce_kernel) to round.
+template <bool BF16, int FMT_A, int FMT_B>
 __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldt,
     int64_t kchunk, const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out,
@@ -1033,10 +1036,10 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   const uint8_t* b0 = bt + (kb / kStage) * rpb * kStage + n0 * kStage;
   const uint8_t* a_end = at + ldt * rpa;
   const uint8_t* b_end = bt + ldt * rpb;
-  MainLoop<false, FMT_A, FMT_B, false>::run(
+  MainLoop<BF16, FMT_A, FMT_B, false>::run(
       lds, a0, a_end - a0, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_end - b0,
       [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)(kchunk / kStage), acc);
-  if (splits > 1) {
+  if (BF16 || splits > 1) {
     // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
     float* frag = out + ((int64_t)sp * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
                   wave * (kTile * kTile / 4);
@@ -1080,7 +1083,9 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
 // expert without rows, whose gradient comes out zero).  With one split it
 // writes out[e] itself; otherwise its raw partial in accumulator order to
 // ws[e][sp][tile], summed in split order by splitk_reduce_kernel.
-template <int FMT_A, int FMT_B>
+// BF16: bf16 operands, 2 bytes per padded row (`ldp` counts K bytes), and the
+// partials always go to ws, for bf16_wgrad_reduce_kernel to round.
+template <bool BF16, int FMT_A, int FMT_B>
 __global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldp,
     const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out, float* __restrict__ ws,
@@ -1093,21 +1098,22 @@ __global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int64_t nst = P.pcount(e) / kStage;  // a multiple of 4
+  constexpr int64_t kBpe = BF16 ? 2 : 1;  // K bytes per padded row
+  const int64_t nst = P.pcount(e) * kBpe / kStage;  // a multiple of 4
   int64_t q = (nst + splits - 1) / splits;
   q = (q + 1) & ~(int64_t)1;
   const int64_t k0 = (int64_t)sp * q;
   const int64_t nk = nst - k0 < 0 ? 0 : (nst - k0 < q ? nst - k0 : q);
   const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
-  const int64_t s0 = P.pstart(e) / kStage + k0;  // first 64-token stage
+  const int64_t s0 = P.pstart(e) * kBpe / kStage + k0;  // first 64-byte stage
   const uint8_t* a0 = at + s0 * rpa * kStage + m0 * kStage;
   const uint8_t* b0 = bt + s0 * rpb * kStage + n0 * kStage;
   const int64_t a_bytes = nk > 0 ? at + ldp * rpa - a0 : 0, b_bytes = nk > 0 ? bt + ldp * rpb - b0 : 0;
   floatx16 acc[4][4];
-  MainLoop<false, FMT_A, FMT_B, false>::run(
+  MainLoop<BF16, FMT_A, FMT_B, false>::run(
       lds, a0, a_bytes, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_bytes,
       [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)nk, acc);
-  if (splits > 1) {
+  if (BF16 || splits > 1) {
     // accumulator order: [expert][split][tile][wave][tb][nb][i][lane][4]
     float* frag = ws + (((int64_t)e * splits + sp) * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
                   wave * (kTile * kTile / 4);
@@ -1175,6 +1181,152 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     const float deq = 1.0f / (sa[0] * sb[0]);
     *reinterpret_cast<floatx4*>(out + m * N + n) = acc * deq;
   }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 SwiGLU MLP path (spark-gpt's default, non-FP8 path): the gate/up GEMM
+// with the SwiGLU epilogue of _swiglu_gemm_kernel (train.py:1625-1716), the
+// plain bf16 GEMM of its dgrad and the rounding reduce of its weight
+// gradient.  Operands are bf16 K-slabs (2 bytes per element: a 64-byte
+// stage is 32 elements of K) or, for the forward's A, the caller's
+// row-major x.
+
+// Forward: gate/up = x @ W^T per tile (fp32 accumulate), then
+//   g = bf16(acc_g * rs), u = bf16(acc_u * rs)   (rs = rstd[row] when the
+//   RMSNorm is folded into W, else 1; train.py:1696-1702),
+//   h = bf16(g * sigmoid(g) * u)                (train.py:1709-1715),
+// gu = [g | u] row-major [rows, 2I] (saved for the backward), h row-major
+// [rows, I].  Tile: 256 rows x 128 (gate, up) column pairs; B is the bf16
+// K-slab of W [2D/64][slab_rows(2I)][64] in the paired layout (a lane holds
+// g and u of the same 32 consecutive columns).  A = x row-major [rows, D]
+// (rows past the tile's last read as zero through the range check).
+// With a MoE plan: tile row tm of padded expert order reads and writes the
+// expert-order rows urow(tm) .. + rows(tm); W of expert e at w + e * w_estride
+// (bytes).  Columns from I on (the last tile when I % 128 != 0) are not
+// written.
+__global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, int64_t T, int64_t D, int64_t I,
+    const float* __restrict__ rstd, uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int tiles_m, int tiles_n,
+    const int* __restrict__ plan, int64_t w_estride) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  int64_t r0 = (int64_t)tm * kTile, nrows = T - r0;
+  if (plan) {
+    const MoePlan P{plan};
+    if (tm >= P.ntiles()) return;  // work-group uniform
+    r0 = P.urow(tm);
+    nrows = P.rows(tm);
+    w += P.expert(tm) * w_estride;
+  }
+  const int64_t n0 = (int64_t)tn * 128;
+  const int64_t ldx = D * 2;  // bytes per x row = K bytes
+  const int64_t wr = slab_rows(2 * I);
+  floatx16 acc[4][4];
+  MainLoop<true, 0, 0, true>::run(
+      lds, reinterpret_cast<const uint8_t*>(x) + r0 * ldx, nrows * ldx, [=](int r) { return r * (int)ldx; },
+      kStage, w, ldx * wr, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
+      (int)(wr * kStage), (int)(ldx / kStage), acc);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave & 1, wn = wave >> 1, fr = lane & 31, g = lane >> 5;
+  const int64_t c0 = n0 + 64 * wn + 32 * g;  // first of this lane's 32 columns
+  if (c0 >= I) return;  // no barrier follows
+  const float c_exp = -1.4426950408889634f;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int lr = 128 * wm + 32 * tb + fr;  // row within the tile
+    if (lr >= nrows) continue;
+    const int64_t t = r0 + lr;
+    const float rs = rstd ? rstd[t] : 1.0f;
+    uint32_t gw[16], uw[16], hw[16];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const uint32_t pg = pack2_bf16(acc[tb][nb][v] * rs, acc[tb][nb][v + 1] * rs);
+        const uint32_t pu = pack2_bf16(acc[tb][nb + 2][v] * rs, acc[tb][nb + 2][v + 1] * rs);
+        const float g0 = __uint_as_float(pg << 16), g1 = __uint_as_float(pg & 0xffff0000u);
+        const float u0 = __uint_as_float(pu << 16), u1 = __uint_as_float(pu & 0xffff0000u);
+        const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * c_exp));
+        const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * c_exp));
+        const int k = 8 * nb + v / 2;
+        gw[k] = pg;
+        uw[k] = pu;
+        hw[k] = pack2_bf16(g0 * s0 * u0, g1 * s1 * u1);
+      }
+    }
+    uint16_t* gp = gu + t * 2 * I + c0;
+    uint16_t* hp = h + t * I + c0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (c0 + 8 * j >= I) break;  // I % 8 == 0: whole 16-byte pieces
+      store16(gp + 8 * j, {gw[4 * j], gw[4 * j + 1], gw[4 * j + 2], gw[4 * j + 3]});
+      store16(gp + I + 8 * j, {uw[4 * j], uw[4 * j + 1], uw[4 * j + 2], uw[4 * j + 3]});
+      store16(hp + 8 * j, {hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]});
+    }
+  }
+}
+
+// out[u, n] = bf16(sum_k A[m, k] * B[n, k]) with A a bf16 K-slab over lda
+// rows (Kb bytes of K) and B a bf16 K-slab [Kb/64][slab_rows(N)][64]: the
+// dgrad of the SwiGLU path (_swiglu_dgrad_kernel, train.py:1907-1980, its
+// d_gu operand precomputed).  One work-group per 256 x 256 tile; the bf16
+// tile is staged in LDS in two passes of 128 rows and written as whole rows.
+// With a MoE plan: A in padded expert order, tile row tm writes its rows(tm)
+// valid rows to out rows urow(tm).. (expert order); B of expert e at
+// b + e * b_estride (bytes).
+__global__ __launch_bounds__(256, 1) void bf16_gemm_kernel(
+    const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, int64_t T, int64_t N, int64_t Kb, int64_t lda,
+    uint16_t* __restrict__ out, int tiles_m, int tiles_n, const int* __restrict__ plan, int64_t b_estride) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int64_t bp = slab_rows(N);
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  int64_t u0 = (int64_t)tm * kTile, uend = T;  // output rows of this tile
+  if (plan) {
+    const MoePlan P{plan};
+    if (tm >= P.ntiles()) return;  // work-group uniform
+    b += P.expert(tm) * b_estride;
+    u0 = P.urow(tm);
+    uend = u0 + P.rows(tm);
+  }
+  const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+  floatx16 acc[4][4];
+  MainLoop<true, 0, 0, false>::run(
+      lds, a + m0 * kStage, Kb * lda - m0 * kStage, [=](int r) { return r * kStage; }, (int)(lda * kStage),
+      b + n0 * kStage, Kb * bp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(bp * kStage),
+      (int)(Kb / kStage), acc);
+  stage_bf16_half<0>(lds, acc, 1.0f);
+  __syncthreads();
+  write_bf16_half(lds, 0, u0, n0, uend, N, N, nullptr, out);
+  __syncthreads();
+  stage_bf16_half<1>(lds, acc, 1.0f);
+  __syncthreads();
+  write_bf16_half(lds, 1, u0, n0, uend, N, N, nullptr, out);
+}
+
+// The bf16 weight gradient's reduction: out[m, n] = bf16(sum over s
+// ascending of ws[s]) (the bf16 result of _swiglu_wgrad_kernel,
+// train.py:1983-2026), partials in wgrad_kernel's accumulator order;
+// blockIdx.y = expert of a grouped gradient (out [E, M, N]).
+__global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __restrict__ ws, int splits, int64_t n4,
+                                                                int tiles_n, int64_t M, int64_t N,
+                                                                uint16_t* __restrict__ out) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= n4) return;
+  ws += (int64_t)blockIdx.y * splits * n4 * 4;
+  out += (int64_t)blockIdx.y * M * N;
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
+  floatx4 acc = w4[q];
+  for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  const int lane = (int)(q & 63), i = (int)(q >> 6) & 3, nb = (int)(q >> 8) & 3, tb = (int)(q >> 10) & 3;
+  const int wave = (int)(q >> 12) & 3;
+  const int64_t tile = q >> 14;
+  const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
+  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
+  const int64_t n = tn * kTile + 128 * (wave >> 1) + 64 * (lane >> 5) + 16 * nb + 4 * i;
+  if (m < M && n < N)  // N % 4 == 0: the 4 values are wholly inside or past the row
+    *reinterpret_cast<intx2*>(out + m * N + n) = intx2{(int)pack2_bf16(acc[0], acc[1]), (int)pack2_bf16(acc[2], acc[3])};
 }
 
 }  // namespace sfp8
@@ -1361,9 +1513,9 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
     return status();
   }
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(wgrad_kernel<kFmtE5M2, kFmtE4M3>, kMainLds);
+  int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((wgrad_kernel<kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
+  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
                      kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
                      splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits);
   rc = status();
@@ -1472,9 +1624,9 @@ int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, in
   if (splits > 1 && (!ws || ws_floats < sfp8_moe_wgrad_workspace_floats(M, N, E))) return kErrWorkspaceTooSmall;
   hipStream_t st = (hipStream_t)stream;
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(moe_wgrad_kernel<kFmtE5M2, kFmtE4M3>, kMainLds);
+  int rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((moe_wgrad_kernel<kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)splits,
+  hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)splits,
                                                                   (unsigned)E),
                      dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldp, sa, sb, out, ws, plan,
                      tiles_m, tiles_n, (int)splits);
@@ -1483,6 +1635,137 @@ int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, in
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  return status();
+}
+
+
+// ---- bf16 SwiGLU path (the default, non-FP8 path) ----
+namespace {
+inline bool bf16_shape(int64_t D, int64_t I) { return D > 0 && I > 0 && D % 64 == 0 && I % 64 == 0; }
+
+int bf16_swiglu_launch(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd, void* gu,
+                       void* h, const int* plan, int64_t E, int tiles_m, hipStream_t st) {
+  const int tiles_n = cdiv(I, 128);
+  int rc = prep(bf16_swiglu_fwd_kernel, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(bf16_swiglu_fwd_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), kMainLds, st,
+                     (const uint16_t*)x, (const uint8_t*)w, T, D, I, rstd, (uint16_t*)gu, (uint16_t*)h, tiles_m,
+                     tiles_n, plan, plan ? 2 * D * slab_rows(2 * I) : 0);
+  (void)E;
+  return status();
+}
+
+int bf16_gemm_launch(const void* a, const void* b, int64_t T, int64_t N, int64_t K, int64_t lda, void* out,
+                     const int* plan, int tiles_m, hipStream_t st) {
+  const int tiles_n = cdiv(N, kTile);
+  int rc = prep(bf16_gemm_kernel, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(bf16_gemm_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), kMainLds, st,
+                     (const uint8_t*)a, (const uint8_t*)b, T, N, 2 * K, lda, (uint16_t*)out, tiles_m, tiles_n, plan,
+                     plan ? 2 * K * slab_rows(N) : 0);
+  return status();
+}
+}  // namespace
+
+int sfp8_bf16_gemm_swiglu_fwd(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd,
+                              void* gu, void* h, void* stream) {
+  if (!w || (T > 0 && (!x || !gu || !h))) return kErrNullPointer;
+  if (T < 0 || !bf16_shape(D, I) || !fits32(kTile, 2 * D) || !fits32(slab_rows(2 * I), 2 * D)) return kErrBadShape;
+  if (!al16(x) || !al16(w) || !al16(gu) || !al16(h)) return kErrBadAlignment;
+  if (T == 0) return kOk;
+  return bf16_swiglu_launch(x, w, T, D, I, rstd, gu, h, nullptr, 1, cdiv(T, kTile), (hipStream_t)stream);
+}
+
+int sfp8_bf16_moe_gemm_swiglu_fwd(const void* x, const void* w, int64_t E, int64_t D, int64_t I, const int* plan,
+                                  int64_t ldp, void* gu, void* h, void* stream) {
+  if (!w || !plan || (ldp > 0 && (!x || !gu || !h))) return kErrNullPointer;
+  if (E <= 0 || ldp < 0 || ldp % kTile || !bf16_shape(D, I) || !fits32(kTile, 2 * D) ||
+      !fits32(slab_rows(2 * I), 2 * D))
+    return kErrBadShape;
+  if (!al16(x) || !al16(w) || !al16(gu) || !al16(h)) return kErrBadAlignment;
+  if (ldp == 0) return kOk;
+  return bf16_swiglu_launch(x, w, 0, D, I, nullptr, gu, h, plan, E, (int)(ldp / kTile), (hipStream_t)stream);
+}
+
+int sfp8_bf16_gemm(const void* a, const void* b, int64_t T, int64_t N, int64_t K, int64_t lda, void* out,
+                   void* stream) {
+  if (!b || (T > 0 && (!a || !out))) return kErrNullPointer;
+  if (T < 0 || N <= 0 || N % 8 || K <= 0 || K % 32 || lda < T || lda % kTile) return kErrBadShape;
+  if (!fits32(lda, 2 * K) || !fits32(slab_rows(N), 2 * K)) return kErrBadShape;
+  if (!al16(a) || !al16(b) || !al16(out)) return kErrBadAlignment;
+  if (T == 0) return kOk;
+  return bf16_gemm_launch(a, b, T, N, K, lda, out, nullptr, cdiv(T, kTile), (hipStream_t)stream);
+}
+
+int sfp8_bf16_moe_gemm(const void* a, const void* b, int64_t E, int64_t N, int64_t K, const int* plan, int64_t ldp,
+                       void* out, void* stream) {
+  if (!b || !plan || (ldp > 0 && (!a || !out))) return kErrNullPointer;
+  if (E <= 0 || N <= 0 || N % 8 || K <= 0 || K % 32 || ldp < 0 || ldp % kTile) return kErrBadShape;
+  if (!fits32(ldp, 2 * K) || !fits32(slab_rows(N), 2 * K)) return kErrBadShape;
+  if (!al16(a) || !al16(b) || !al16(out)) return kErrBadAlignment;
+  if (ldp == 0) return kOk;
+  return bf16_gemm_launch(a, b, 0, N, K, ldp, out, plan, (int)(ldp / kTile), (hipStream_t)stream);
+}
+
+int64_t sfp8_bf16_wgrad_splits(int64_t M, int64_t N, int64_t ldt) { return sfp8_wgrad_splits(M, N, 2 * ldt); }
+
+int64_t sfp8_bf16_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
+  return sfp8_bf16_wgrad_splits(M, N, ldt) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
+}
+
+int sfp8_bf16_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, int64_t ldt, void* out, float* ws,
+                         int64_t ws_floats, void* stream) {
+  if (!out || (ldt > 0 && (!at || !bt))) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || ldt < 0 || ldt % kTile || N % 4 || (M * N) % 8) return kErrBadShape;
+  if (!fits32(slab_rows(M), 2 * ldt) || !fits32(slab_rows(N), 2 * ldt)) return kErrBadShape;
+  if (!al16(at) || !al16(bt) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  hipStream_t st = (hipStream_t)stream;
+  if (ldt == 0) {
+    // no tokens: a zero gradient (M * N bf16 = M * N / 2 floats of zero bits)
+    const int64_t n = M * N / 2;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, (float*)out, n);
+    return status();
+  }
+  const int64_t splits = sfp8_bf16_wgrad_splits(M, N, ldt);
+  if (!ws || ws_floats < sfp8_bf16_wgrad_workspace_floats(M, N, ldt)) return kErrWorkspaceTooSmall;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  int rc = prep(wgrad_kernel<true, 0, 0>, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((wgrad_kernel<true, 0, 0>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256), kMainLds,
+                     st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws,
+                     tiles_m, tiles_n, (int)splits);
+  rc = status();
+  if (rc) return rc;
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+                     (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  return status();
+}
+
+int64_t sfp8_bf16_moe_wgrad_workspace_floats(int64_t M, int64_t N, int64_t E) {
+  return E * sfp8_moe_wgrad_splits(M, N, E) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
+}
+
+int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, int64_t E, const int* plan,
+                             int64_t ldp, void* out, float* ws, int64_t ws_floats, void* stream) {
+  if (!at || !bt || !plan || !out) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || E <= 0 || N % 4 || ldp <= 0 || ldp % kTile) return kErrBadShape;
+  if (!fits32(slab_rows(M), 2 * ldp) || !fits32(slab_rows(N), 2 * ldp)) return kErrBadShape;
+  if (!al16(at) || !al16(bt) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  const int64_t splits = sfp8_moe_wgrad_splits(M, N, E);
+  if (!ws || ws_floats < sfp8_bf16_moe_wgrad_workspace_floats(M, N, E)) return kErrWorkspaceTooSmall;
+  hipStream_t st = (hipStream_t)stream;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  int rc = prep(moe_wgrad_kernel<true, 0, 0>, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((moe_wgrad_kernel<true, 0, 0>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)E),
+                     dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldp, nullptr, nullptr,
+                     nullptr, ws, plan, tiles_m, tiles_n, (int)splits);
+  rc = status();
+  if (rc) return rc;
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
+                     (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
 

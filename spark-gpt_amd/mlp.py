@@ -31,6 +31,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
+from . import swiglu as _swiglu
 from . import torch_ops  # registers the sparkfp8:: operators; holds the weight cache
 
 FP8_MLP = False  # set True to route dense MLP sub-blocks through _FP8MLPBlock while training
@@ -103,7 +104,9 @@ def _dense_weights(m: nn.Module):
 
 
 class MLP(nn.Module):
-    """Same parameters and buffers as the reference MLP (train.py:247-262)."""
+    """Same parameters, buffers and forward as the reference MLP
+    (train.py:247-262): the fused bf16 SwiGLU (``_FusedSwiGLU``) when
+    ``_use_fused_swiglu(x)``, else gate/up -> silu * up -> down in torch."""
 
     def __init__(self, dim: int, hidden_dim: int):
         super().__init__()
@@ -114,6 +117,10 @@ class MLP(nn.Module):
         self.register_buffer("fp8_amax", torch.zeros(5), persistent=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _swiglu._use_fused_swiglu(x) and self.gate_up_proj.weight.shape[0] % 128 == 0:
+            weight = self.gate_up_proj.weight.to(dtype=x.dtype).unsqueeze(0)
+            offs = torch.full((1,), x.shape[0], device=x.device, dtype=torch.int32)
+            return self.down_proj(_swiglu._FusedSwiGLU.apply(x, weight, offs))
         gate, up = self.gate_up_proj(x).chunk(2, dim=-1)
         return self.down_proj(F.silu(gate) * up)
 

@@ -401,3 +401,127 @@ def moe_topk_sum(dx, inverse_permutation, T: int, top_k: int):
     out = torch.empty(T, D, dtype=torch.bfloat16, device=dx.device)
     _lib.call("sfp8_moe_topk_sum", dx.data_ptr(), R, D, inv.data_ptr(), T, top_k, out.data_ptr(), _lib.stream_of(dx))
     return out
+
+
+# ----------------------------------------------------- bf16 SwiGLU path
+# The default (non-FP8) MLP path: bf16 K-slabs (32 elements of K per 64-byte
+# row), rows dense (no plan) or in padded expert order (a MoE plan).
+BF16 = torch.bfloat16
+
+
+def bf16_weight_slabs(w: torch.Tensor, norm_w=None, *, rows: bool = True, transposed: bool = True):
+    """bf16 K-slabs of W [E, R, C] (fp32, times norm_w[c] when given, or bf16):
+    (ws: stacked K-slabs of W[e] [R, C] or None, wt: of W[e]^T [C, R] or None)."""
+    _need(w.is_cuda and w.dim() == 3 and w.is_contiguous() and w.dtype in (torch.float32, BF16),
+          "w must be a contiguous [E, R, C] fp32 or bf16 device tensor")
+    E, R, C = w.shape
+    _need(R % 64 == 0 and C % 64 == 0, f"weight dims {R} x {C} must be multiples of 64")
+    if norm_w is not None:
+        _cuda_contig("norm_w", norm_w, torch.float32, 1)
+    dev = w.device
+    ws = torch.empty((E,) + kslab_shape(R, C, BF16), dtype=BF16, device=dev) if rows else None
+    wt = torch.empty((E,) + kslab_shape(C, R, BF16), dtype=BF16, device=dev) if transposed else None
+    _lib.call("sfp8_bf16_weight_slabs", w.data_ptr(), int(w.dtype == BF16), _lib.ptr(norm_w), E, R, C, _lib.ptr(ws),
+              _lib.ptr(wt), _lib.stream_of(w))
+    return ws, wt
+
+
+def bf16_rows_prep(x: torch.Tensor, plan, ldp: int, eps=None):
+    """(rstd [rows] fp32 or None, xt): xt the token-contiguous bf16 K-slab of
+    x^T over ldp padded rows; rstd = 1/sqrt(mean(x^2) + eps) when eps is given
+    (dense rows only)."""
+    _cuda_contig("x", x, BF16, 2)
+    n, D = x.shape
+    xt = kslab_empty(D, ldp, BF16, x.device)
+    rstd = torch.empty(n, dtype=torch.float32, device=x.device) if eps is not None else None
+    _lib.call("sfp8_bf16_rows_prep", x.data_ptr(), n, D, _lib.ptr(plan), ldp, float(eps or 0.0), _lib.ptr(rstd),
+              xt.data_ptr(), _lib.stream_of(x))
+    return rstd, xt
+
+
+def bf16_swiglu_fwd(x: torch.Tensor, ws: torch.Tensor, I: int, rstd=None, plan=None, ldp: int = 0):
+    """(gu [rows, 2I], h [rows, I]) bf16: the gate/up GEMM with the SwiGLU
+    epilogue, rows scaled by rstd when given (dense) or grouped by a plan."""
+    _cuda_contig("x", x, BF16, 2)
+    n, D = x.shape
+    gu = torch.empty(n, 2 * I, dtype=BF16, device=x.device)
+    h = torch.empty(n, I, dtype=BF16, device=x.device)
+    if plan is None:
+        _lib.call("sfp8_bf16_gemm_swiglu_fwd", x.data_ptr(), ws.data_ptr(), n, D, I, _lib.ptr(rstd), gu.data_ptr(),
+                  h.data_ptr(), _lib.stream_of(x))
+    else:
+        _lib.call("sfp8_bf16_moe_gemm_swiglu_fwd", x.data_ptr(), ws.data_ptr(), ws.shape[0], D, I, plan.data_ptr(),
+                  ldp, gu.data_ptr(), h.data_ptr(), _lib.stream_of(x))
+    return gu, h
+
+
+def bf16_swiglu_bwd(gu: torch.Tensor, dout: torch.Tensor, rstd, plan, ldp: int):
+    """(gs, gt): G' = bf16 SwiGLU gradient of the rows (times rstd when given)
+    as the K-slab over ldp padded rows and its token-contiguous transpose."""
+    _cuda_contig("gu", gu, BF16, 2)
+    _cuda_contig("dout", dout, BF16, 2)
+    n, I2 = gu.shape
+    _need(dout.shape == (n, I2 // 2), "dout must be [rows, I]")
+    gs = kslab_empty(ldp, I2, BF16, gu.device)
+    gt = kslab_empty(I2, ldp, BF16, gu.device)
+    _lib.call("sfp8_bf16_swiglu_bwd", gu.data_ptr(), dout.data_ptr(), n, I2 // 2, _lib.ptr(rstd), _lib.ptr(plan), ldp,
+              gs.data_ptr(), gt.data_ptr(), _lib.stream_of(gu))
+    return gs, gt
+
+
+def bf16_gemm(a: torch.Tensor, b: torch.Tensor, rows: int, N: int, K: int, plan=None):
+    """out [rows, N] bf16 = A @ B^T, A a bf16 K-slab over padded rows (dense:
+    the first `rows` rows; a plan: the expert-order rows of each tile), B the
+    (stacked per expert) bf16 K-slab of [N, K]."""
+    lda = a.shape[1]
+    out = torch.empty(rows, N, dtype=BF16, device=a.device)
+    if plan is None:
+        _lib.call("sfp8_bf16_gemm", a.data_ptr(), b.data_ptr(), rows, N, K, lda, out.data_ptr(), _lib.stream_of(a))
+    else:
+        _lib.call("sfp8_bf16_moe_gemm", a.data_ptr(), b.data_ptr(), b.shape[0], N, K, plan.data_ptr(), lda,
+                  out.data_ptr(), _lib.stream_of(a))
+    return out
+
+
+def bf16_norm_dh(p: torch.Tensor, h: torch.Tensor, rstd: torch.Tensor):
+    """dh = bf16(p - rstd^2 * sum(h * p) / D * h) per row."""
+    _cuda_contig("p", p, BF16, 2)
+    _cuda_contig("h", h, BF16, 2)
+    T, D = h.shape
+    dh = torch.empty_like(h)
+    _lib.call("sfp8_bf16_norm_dh", p.data_ptr(), h.data_ptr(), rstd.data_ptr(), T, D, dh.data_ptr(), _lib.stream_of(h))
+    return dh
+
+
+def bf16_wgrad(at: torch.Tensor, bt: torch.Tensor, M: int, N: int, plan=None, E: int = 1):
+    """bf16(A^T B) over the padded rows: [M, N] (dense) or [E, M, N] (per
+    expert, with a plan); at, bt the token-contiguous bf16 K-slabs of [M, ldp]
+    and [N, ldp]."""
+    ldp = at.shape[0] * (SLAB // 2)
+    dev = at.device
+    if plan is None:
+        out = torch.empty(M, N, dtype=BF16, device=dev)
+        nws = _lib.query("sfp8_bf16_wgrad_workspace_floats", M, N, ldp)
+        ws = torch.empty(max(nws, 1), dtype=torch.float32, device=dev)
+        _lib.call("sfp8_bf16_gemm_wgrad", at.data_ptr(), bt.data_ptr(), M, N, ldp, out.data_ptr(), ws.data_ptr(),
+                  ws.numel(), _lib.stream_of(at))
+    else:
+        out = torch.empty(E, M, N, dtype=BF16, device=dev)
+        nws = _lib.query("sfp8_bf16_moe_wgrad_workspace_floats", M, N, E)
+        ws = torch.empty(max(nws, 1), dtype=torch.float32, device=dev)
+        _lib.call("sfp8_bf16_moe_gemm_wgrad", at.data_ptr(), bt.data_ptr(), M, N, E, plan.data_ptr(), ldp,
+                  out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(at))
+    return out
+
+
+def bf16_fold_grads(dwp: torch.Tensor, w: torch.Tensor, norm_w: torch.Tensor):
+    """(dw = f32(dwp) * norm_w, dnorm_w = sum over rows of f32(dwp) * w): the
+    gradients of the fp32 gate/up master and the norm weight from the bf16
+    gradient of the folded weight."""
+    M, N = dwp.shape
+    dw = torch.empty(M, N, dtype=torch.float32, device=dwp.device)
+    dnw = torch.empty(N, dtype=torch.float32, device=dwp.device)
+    part = torch.empty(_lib.query("sfp8_bf16_fold_partials", M, N), dtype=torch.float32, device=dwp.device)
+    _lib.call("sfp8_bf16_fold_grads", dwp.data_ptr(), w.data_ptr(), norm_w.data_ptr(), M, N, dw.data_ptr(),
+              dnw.data_ptr(), part.data_ptr(), part.numel(), _lib.stream_of(dwp))
+    return dw, dnw

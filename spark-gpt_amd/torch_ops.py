@@ -258,3 +258,116 @@ def update_scales(scale: Tensor, amax: Tensor) -> None:
 @update_scales.register_fake
 def _update_scales_fake(scale, amax):
     return None
+
+
+# ----------------------------------------------------- bf16 SwiGLU path
+BF16 = torch.bfloat16
+
+
+@torch.library.custom_op("sparkfp8::norm_swiglu_fwd", mutates_args=())
+def norm_swiglu_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor,
+                                                                                   Tensor]:
+    """_NormSwiGLU.forward (train.py:2111-2121): out = SwiGLU(gate_up(rmsnorm(h)))
+    [T, I] bf16, the norm weight folded into the gate/up weight (W' =
+    bf16(w_gu * norm_w)); then, for the backward, the bf16 K-slab of W'^T, gu
+    [T, 2I], rstd [T] and the token-contiguous bf16 K-slab of h^T."""
+    h = h.contiguous()
+    T, D = h.shape
+    I = w_gu.shape[0] // 2
+    ws, wt = ops.bf16_weight_slabs(w_gu.detach().contiguous().unsqueeze(0), norm_w.detach().contiguous())
+    rstd, xt = ops.bf16_rows_prep(h, None, ops.ldt_of(T), float(eps))
+    gu, out = ops.bf16_swiglu_fwd(h, ws, I, rstd=rstd)
+    return out, wt, gu, rstd, xt
+
+
+@norm_swiglu_fwd.register_fake
+def _norm_swiglu_fwd_fake(h, norm_w, w_gu, eps):
+    T, D = h.shape
+    I2 = w_gu.shape[0]
+    return (h.new_empty((T, I2 // 2), dtype=BF16), h.new_empty((1,) + ops.kslab_shape(D, I2, BF16), dtype=BF16),
+            h.new_empty((T, I2), dtype=BF16), h.new_empty((T,), dtype=torch.float32),
+            h.new_empty(ops.kslab_shape(D, ops.ldt_of(T), BF16), dtype=BF16))
+
+
+@torch.library.custom_op("sparkfp8::norm_swiglu_bwd", mutates_args=())
+def norm_swiglu_bwd(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: Tensor, gu: Tensor, rstd: Tensor,
+                    xt: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """_NormSwiGLU.backward (train.py:2123-2131): (dh bf16 [T, D], dnorm_w fp32
+    [D], dw_gu fp32 [2I, D]).  G' = rstd * d_gu (bf16) once for both GEMMs:
+    p = bf16(G' W'), dh = bf16(p - rstd^2 sum(h p) / D h), dW' = bf16(G'^T h),
+    dw_gu = dW' * norm_w, dnorm_w = sum_rows(dW' * w_gu)."""
+    dout = dout.contiguous()
+    if dout.dtype != BF16:
+        dout = dout.to(BF16)
+    h = h.contiguous()
+    T, D = h.shape
+    I2 = gu.shape[1]
+    ldt = xt.shape[0] * (ops.SLAB // 2)
+    gs, gt = ops.bf16_swiglu_bwd(gu, dout, rstd, None, ldt)
+    p = ops.bf16_gemm(gs, wt, T, D, I2)
+    del gs
+    dh = ops.bf16_norm_dh(p, h, rstd)
+    dwp = ops.bf16_wgrad(gt, xt, I2, D)
+    dw, dnw = ops.bf16_fold_grads(dwp, w_gu.detach().contiguous(), norm_w.detach().contiguous())
+    return dh, dnw, dw
+
+
+@norm_swiglu_bwd.register_fake
+def _norm_swiglu_bwd_fake(dout, h, norm_w, w_gu, wt, gu, rstd, xt):
+    T, D = h.shape
+    return (h.new_empty((T, D), dtype=BF16), h.new_empty((D,), dtype=torch.float32),
+            h.new_empty(tuple(w_gu.shape), dtype=torch.float32))
+
+
+def _plan_ints(R: int, E: int) -> int:
+    return 8 + 2 * E + 3 * ((R + 255) // 256 + E)
+
+
+@torch.library.custom_op("sparkfp8::swiglu_fwd", mutates_args=())
+def swiglu_fwd(x: Tensor, weight: Tensor, offs: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """_FusedSwiGLU.forward (train.py:2077-2081): h = SwiGLU(x W_e^T) [R, I]
+    bf16 for the rows of each group e (offs: inclusive int32 row-count prefix
+    sums), then gu [R, 2I] and the device-built row plan for the backward."""
+    x = x.contiguous()
+    weight = weight.contiguous()
+    R, D = x.shape
+    E, I2, _ = weight.shape
+    plan = ops.moe_plan(offs, R)
+    ldp = ops.moe_padded_rows(R, E)
+    ws, _ = ops.bf16_weight_slabs(weight, rows=True, transposed=False)
+    gu, h = ops.bf16_swiglu_fwd(x, ws, I2 // 2, plan=plan, ldp=ldp)
+    return h, gu, plan
+
+
+@swiglu_fwd.register_fake
+def _swiglu_fwd_fake(x, weight, offs):
+    R, D = x.shape
+    E, I2, _ = weight.shape
+    return (x.new_empty((R, I2 // 2), dtype=BF16), x.new_empty((R, I2), dtype=BF16),
+            x.new_empty((_plan_ints(R, E),), dtype=torch.int32))
+
+
+@torch.library.custom_op("sparkfp8::swiglu_bwd", mutates_args=())
+def swiglu_bwd(dh: Tensor, x: Tensor, weight: Tensor, gu: Tensor, plan: Tensor) -> Tuple[Tensor, Tensor]:
+    """_FusedSwiGLU.backward (train.py:2083-2090): (dx [R, D] bf16, dW [E, 2I, D]
+    bf16), the SwiGLU gradient G' (bf16) computed once for both GEMMs."""
+    dh = dh.contiguous()
+    if dh.dtype != BF16:
+        dh = dh.to(BF16)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    R, D = x.shape
+    E, I2, _ = weight.shape
+    ldp = ops.moe_padded_rows(R, E)
+    _, wt = ops.bf16_weight_slabs(weight, rows=False, transposed=True)
+    _, xt = ops.bf16_rows_prep(x, plan, ldp)
+    gs, gt = ops.bf16_swiglu_bwd(gu, dh, None, plan, ldp)
+    dx = ops.bf16_gemm(gs, wt, R, D, I2, plan=plan)
+    del gs
+    dw = ops.bf16_wgrad(gt, xt, I2, D, plan=plan, E=E)
+    return dx, dw
+
+
+@swiglu_bwd.register_fake
+def _swiglu_bwd_fake(dh, x, weight, gu, plan):
+    return x.new_empty(tuple(x.shape), dtype=BF16), x.new_empty(tuple(weight.shape), dtype=BF16)

@@ -1,0 +1,291 @@
+"""GPU parity of the bf16 SwiGLU MLP path (spark-gpt's default, non-FP8 path):
+_NormSwiGLU (train.py:2101-2131) and _FusedSwiGLU (train.py:2067-2090) on the
+gfx950 kernels, against the oracle (oracle/bf16_swiglu.py) on the same
+inputs, and the mirrors of the reference's own tests (tests/test_moe.py:
+385-423 and 468-517: against an fp32 autograd and the unfused bf16 path)."""
+import pytest
+import torch
+import torch.nn as nn
+
+import spark_gpt_amd as sg
+from oracle import bf16_swiglu as B
+from oracle import fp8_mlp as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulps_bf16(a, b):
+    """|a - b| in units of b's bf16 ulp (elementwise, for finite b)."""
+    a, b = a.float().cpu(), b.float().cpu()
+    ulp = torch.ldexp(torch.ones_like(b), torch.frexp(b)[1] - 8).clamp(min=2.0 ** -133)
+    return (a - b).abs() / ulp
+
+
+def _assert_bf16_close(got, ref, name, ulps=1, frac=2e-3):
+    """Every element within `ulps` bf16 ulps of the oracle except a fraction
+    `frac` (GEMM sums in another order shift the fp32 value before its bf16
+    rounding), and none beyond 4 ulps... unless the oracle value is tiny
+    (cancellation): rel-L2 below 1e-2 covers those."""
+    d = _ulps_bf16(got, ref)
+    big = ref.float().cpu().abs() > 1e-3 * ref.float().abs().max().item()
+    assert (d[big] > ulps).float().mean().item() <= frac, (name, (d[big] > ulps).float().mean().item())
+    assert O.rel_l2(got.float().cpu(), ref.float().cpu()) < 1e-2, name
+
+
+def _norm_case(dev, T, D, I, seed):
+    g = torch.Generator().manual_seed(seed)
+    norm_w = torch.rand(D, generator=g) + 0.5
+    w_gu = torch.randn(2 * I, D, generator=g) * D ** -0.5
+    h = (torch.randn(T, D, generator=g) * 3.0).to(torch.bfloat16)
+    probe = torch.randn(T, I, generator=g)
+    return h, norm_w, w_gu, probe
+
+
+def _gpu_norm_step(dev, h, norm_w, w_gu, probe, eps=1e-6):
+    hh = h.to(dev).requires_grad_(True)
+    nw = norm_w.to(dev).requires_grad_(True)
+    wgu = w_gu.to(dev).requires_grad_(True)
+    out = sg._NormSwiGLU.apply(hh, nw, wgu, eps)
+    grads = torch.autograd.grad(out, [hh, nw, wgu], probe.to(dev).to(torch.bfloat16))
+    return [out.detach()] + list(grads)
+
+
+@pytest.mark.parametrize("T,D,I", [(1000, 512, 768), (1000, 1024, 768), (300, 128, 192), (257, 256, 320)])
+def test_norm_swiglu_matches_oracle(dev, T, D, I):
+    h, norm_w, w_gu, probe = _norm_case(dev, T, D, I, 3)
+    out, dh, dnw, dw = _gpu_norm_step(dev, h, norm_w, w_gu, probe)
+    r_out, saved = B.norm_swiglu_forward(h, norm_w, w_gu, 1e-6)
+    r_dh, r_dnw, r_dw = B.norm_swiglu_backward(probe.to(torch.bfloat16), saved)
+    assert out.dtype == torch.bfloat16 and dh.dtype == torch.bfloat16
+    assert dnw.dtype == torch.float32 and dw.dtype == torch.float32
+    _assert_bf16_close(out, r_out, "out")
+    _assert_bf16_close(dh, r_dh, "dh", ulps=2, frac=1e-2)
+    for name, a, r in (("dnorm_w", dnw, r_dnw), ("dw_gu", dw, r_dw)):
+        assert torch.isfinite(a).all(), name
+        assert O.rel_l2(a.cpu(), r) < 1e-2, (name, O.rel_l2(a.cpu(), r))
+
+
+def test_norm_swiglu_rstd_and_gu(dev):
+    """The saved row statistic and gate/up values of the forward operator:
+    rstd bit-exact to the oracle's spec, gu within one bf16 ulp."""
+    T, D, I = 700, 512, 256
+    h, norm_w, w_gu, _ = _norm_case(dev, T, D, I, 4)
+    out, wt, gu, rstd, xt = torch.ops.sparkfp8.norm_swiglu_fwd(h.to(dev), norm_w.to(dev), w_gu.to(dev), 1e-6)
+    _, saved = B.norm_swiglu_forward(h, norm_w, w_gu, 1e-6)
+    assert torch.equal(rstd.cpu(), saved["rstd"])
+    _assert_bf16_close(gu, saved["gu"], "gu")
+    # W'^T slab and the token-contiguous h^T: exact copies
+    wp = B.fold_weight(w_gu, norm_w).to(torch.bfloat16)
+    assert torch.equal(sg.ops.unslab(wt[0], D).cpu(), wp.t().contiguous())
+    ht = sg.ops.unslab(xt, D).cpu()
+    assert torch.equal(ht[:, :T], h.t()) and torch.all(ht[:, T:] == 0)
+
+
+@pytest.mark.parametrize("hidden", [512, 1024])
+def test_norm_swiglu_tracks_fp32_reference(dev, hidden):
+    """Mirror of spark-gpt tests/test_moe.py:468-517: the fused norm path
+    against an fp32 autograd, no worse than 1.5x the unfused bf16 path (torch
+    RMSNorm, then _FusedSwiGLU under autocast) + 1e-3."""
+    torch.manual_seed(0)
+    rows, inter = 1000, 768
+    norm_w = (torch.rand(hidden, device=dev) + 0.5).requires_grad_(True)
+    w_gu = (torch.randn(2 * inter, hidden, device=dev) * hidden ** -0.5).requires_grad_(True)
+    h0 = (torch.randn(rows, hidden, device=dev) * 3.0).to(torch.bfloat16)
+    probe = torch.randn(rows, inter, device=dev)
+    params = [norm_w, w_gu]
+
+    def run(fn, dtype):
+        h = h0.to(dtype).requires_grad_(True)
+        out = fn(h)
+        g = torch.autograd.grad((out.float() * probe).sum(), [h] + params)
+        return (out.float(),) + tuple(t.float() for t in g)
+
+    def fp32(h):
+        xn = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6) * norm_w
+        gate, up = (xn @ w_gu.t()).chunk(2, dim=-1)
+        return torch.nn.functional.silu(gate) * up
+
+    def unfused(h):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            offs = torch.full((1,), rows, device=dev, dtype=torch.int32)
+            xn = h.float() * torch.rsqrt(h.float().pow(2).mean(dim=-1, keepdim=True) + 1e-6)
+            xn = xn.to(h.dtype) * norm_w.to(h.dtype)
+            return sg._FusedSwiGLU.apply(xn, w_gu.to(torch.bfloat16).unsqueeze(0), offs)
+
+    ref = run(fp32, torch.float32)
+    base = run(unfused, torch.bfloat16)
+    fused = run(lambda h: sg._NormSwiGLU.apply(h, norm_w, w_gu, 1e-6), torch.bfloat16)
+    for name, f_, b_, r in zip(("out", "dh", "dnorm_w", "dW_gu"), fused, base, ref):
+        err_f = ((f_ - r).norm() / r.norm()).item()
+        err_b = ((b_ - r).norm() / r.norm()).item()
+        assert torch.isfinite(f_).all(), name
+        assert err_f < 1.5 * err_b + 1e-3, (hidden, name, err_f, err_b)
+
+
+def _fused_case(counts, rows=1000, dim=128, inter=192, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, dim, generator=g).to(torch.bfloat16)
+    probe = torch.randn(rows, inter, generator=g).to(torch.bfloat16)
+    w = (torch.randn(len(counts), 2 * inter, dim, generator=g) * 0.05).to(torch.bfloat16)
+    offs = torch.cumsum(torch.tensor(counts), 0).to(torch.int32)
+    return x, w, offs, probe
+
+
+def _gpu_fused(dev, x, w, offs, probe):
+    xx = x.to(dev).requires_grad_(True)
+    ww = w.to(dev).requires_grad_(True)
+    h = sg._FusedSwiGLU.apply(xx, ww, offs.to(dev))
+    dx, dw = torch.autograd.grad(h, [xx, ww], probe.to(dev))
+    return h.detach(), dx, dw
+
+
+@pytest.mark.parametrize("counts", [[1000], [300, 0, 700], [1, 511, 0, 256, 232]])
+def test_fused_swiglu_matches_oracle(dev, counts):
+    x, w, offs, probe = _fused_case(counts, dim=256, inter=320, seed=5)
+    h, dx, dw = _gpu_fused(dev, x, w, offs, probe)
+    r_h, r_gu = B.fused_swiglu_forward(x, w, offs)
+    r_dx, r_dw = B.fused_swiglu_backward(probe, x, w, r_gu, offs)
+    assert h.dtype == dx.dtype == dw.dtype == torch.bfloat16
+    _assert_bf16_close(h, r_h, "h")
+    _assert_bf16_close(dx, r_dx, "dx", ulps=2, frac=1e-2)
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert torch.all(dw[e] == 0), e
+        else:
+            assert O.rel_l2(dw[e].float().cpu(), r_dw[e].float()) < 1e-2, e
+
+
+def test_fused_swiglu_matches_unfused_dense_and_grouped(dev):
+    """Mirror of spark-gpt tests/test_moe.py:385-423: dense and grouped (one
+    group without rows), rows 1000, dim 128, inter 192, against an fp32
+    reference (bound 0.05 * scale + 1e-3) and the unfused torch bf16 path
+    (no worse than 1.5x it + 0.01 * scale + 1e-3); the empty group's
+    gradient is exactly zero."""
+    torch.manual_seed(0)
+    rows, dim, inter = 1000, 128, 192
+    x = torch.randn(rows, dim, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    probe = torch.randn(rows, inter, device=dev, dtype=torch.bfloat16)
+
+    def unfused(x_, w_, offs_):
+        parts, start = [], 0
+        for e in range(w_.shape[0]):
+            end = int(offs_[e])
+            gate, up = (x_[start:end] @ w_[e].t()).chunk(2, dim=-1)
+            parts.append(torch.nn.functional.silu(gate) * up)
+            start = end
+        return torch.cat(parts)
+
+    def check(w, offs):
+        x32 = x.detach().float().requires_grad_(True)
+        w32 = w.detach().float().requires_grad_(True)
+        ref = unfused(x32, w32, offs)
+        rx, rw = torch.autograd.grad((ref * probe.float()).sum(), (x32, w32))
+        fused_h = sg._FusedSwiGLU.apply(x, w, offs)
+        fx, fw = torch.autograd.grad((fused_h * probe).sum(), (x, w))
+        unfused_h = unfused(x, w, offs)
+        ux, uw = torch.autograd.grad((unfused_h * probe).sum(), (x, w))
+        for name, f_, u_, r in (("h", fused_h, unfused_h, ref), ("dx", fx, ux, rx), ("dw", fw, uw, rw)):
+            err_f = (f_.float() - r).abs().max().item()
+            err_u = (u_.float() - r).abs().max().item()
+            scale = r.abs().max().item()
+            assert err_f < 0.05 * scale + 1e-3, (name, err_f, scale)
+            assert err_f < 1.5 * err_u + 0.01 * scale + 1e-3, (name, err_f, err_u)
+        return fw
+
+    w = (torch.randn(1, 2 * inter, dim, device=dev) * 0.05).to(torch.bfloat16).requires_grad_(True)
+    check(w, torch.tensor([rows], device=dev, dtype=torch.int32))
+    counts = torch.tensor([300, 0, 700], device=dev)
+    w3 = (torch.randn(3, 2 * inter, dim, device=dev) * 0.05).to(torch.bfloat16).requires_grad_(True)
+    gw3 = check(w3, torch.cumsum(counts, 0).to(torch.int32))
+    assert torch.all(gw3[1] == 0)
+
+
+def test_mlp_forward_takes_the_fused_path(dev, monkeypatch):
+    """MLP.forward (train.py:256-262) routes a 2-D CUDA bf16 input through
+    _FusedSwiGLU when the switch is on, and through torch otherwise; both give
+    the same function."""
+    torch.manual_seed(1)
+    mlp = sg.MLP(256, 384).to(dev)
+    x = torch.randn(500, 256, device=dev).to(torch.bfloat16)
+    calls = []
+    real = sg._FusedSwiGLU.apply
+
+    def counted(*a):
+        calls.append(1)
+        return real(*a)
+
+    monkeypatch.setattr(sg.swiglu._FusedSwiGLU, "apply", counted)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = mlp(x)
+        monkeypatch.setattr(sg.swiglu, "FUSED_SWIGLU", False)
+        y_ref = mlp(x)
+    assert len(calls) == 1
+    assert O.rel_l2(y.float().cpu(), y_ref.float().cpu()) < 1e-2
+
+
+def test_norm_swiglu_deterministic_and_zero_rows(dev):
+    h, norm_w, w_gu, probe = _norm_case(dev, 600, 256, 256, 6)
+    a = _gpu_norm_step(dev, h, norm_w, w_gu, probe)
+    b = _gpu_norm_step(dev, h, norm_w, w_gu, probe)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    out, dh, dnw, dw = _gpu_norm_step(dev, h[:0], norm_w, w_gu, probe[:0])
+    assert out.shape == (0, 256) and dh.shape == (0, 256)
+    assert torch.all(dnw == 0) and torch.all(dw == 0)
+
+
+class _NormMLP(nn.Module):
+    def __init__(self, D, I):
+        super().__init__()
+        self.norm_w = nn.Parameter(torch.rand(D) + 0.5)
+        self.w_gu = nn.Parameter(torch.randn(2 * I, D) * D ** -0.5)
+
+    def forward(self, h):
+        return sg._NormSwiGLU.apply(h, self.norm_w, self.w_gu, 1e-6)
+
+
+def test_compiled_norm_swiglu_matches_eager(dev):
+    """torch.compile (inductor, train.py:3787) traces _NormSwiGLU as its two
+    custom operators, no graph break, same bytes as eager."""
+    torch.manual_seed(2)
+    m = _NormMLP(256, 384).to(dev)
+    h = torch.randn(300, 256, device=dev).to(torch.bfloat16)
+    dy = torch.randn(300, 384, device=dev).to(torch.bfloat16)
+
+    def run(mod):
+        for p in m.parameters():
+            p.grad = None
+        x = h.clone().requires_grad_(True)
+        y = mod(x)
+        y.backward(dy)
+        return [y.detach(), x.grad] + [p.grad.clone() for p in m.parameters()]
+
+    ref = run(m)
+    explain = torch._dynamo.explain(m)(h.clone().requires_grad_(True))
+    assert explain.graph_break_count == 0, explain.break_reasons
+    torch._dynamo.reset()
+    cm = torch.compile(m, mode="default", dynamic=False)
+    for _ in range(2):
+        got = run(cm)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+    torch._dynamo.reset()
+
+
+def test_bf16_ops_opcheck(dev):
+    """Fake implementations of the four bf16 operators against real runs."""
+    utils = ("test_faketensor",)
+    T, D, I = 300, 256, 384
+    h, norm_w, w_gu, _ = _norm_case(dev, T, D, I, 7)
+    args = (h.to(dev), norm_w.to(dev), w_gu.to(dev), 1e-6)
+    torch.library.opcheck(torch.ops.sparkfp8.norm_swiglu_fwd.default, args, test_utils=utils)
+    out, wt, gu, rstd, xt = torch.ops.sparkfp8.norm_swiglu_fwd(*args)
+    dout = torch.randn(T, I, device=dev).to(torch.bfloat16)
+    bargs = (dout, args[0], args[1], args[2], wt, gu, rstd, xt)
+    torch.library.opcheck(torch.ops.sparkfp8.norm_swiglu_bwd.default, bargs, test_utils=utils)
+    x, w, offs, probe = _fused_case([100, 0, 200], rows=300, dim=256, inter=192)
+    fargs = (x.to(dev), w.to(dev), offs.to(dev))
+    torch.library.opcheck(torch.ops.sparkfp8.swiglu_fwd.default, fargs, test_utils=utils)
+    hh, gu2, plan = torch.ops.sparkfp8.swiglu_fwd(*fargs)
+    torch.library.opcheck(torch.ops.sparkfp8.swiglu_bwd.default, (probe.to(dev), fargs[0], fargs[1], gu2, plan),
+                          test_utils=utils)
