@@ -28,8 +28,11 @@ Also reported on the same JSON line:
                 the muP base block (T=8192, D=256, I=1024), and the FP8 MoE
                 experts (``_FP8Experts`` fwd+bwd + post-step hook) on 65536
                 tokens routed top-2 over 8 experts, D=1024, I=1536 (131072
-                expert rows: the dense headline's FLOP), with their in-step
-                kernels and roofline
+                expert rows: the dense headline's FLOP), and the reference's
+                default bf16 sub-block at the headline shape (h +
+                down_proj(_NormSwiGLU(h)) under bf16 autocast, the down
+                projection on torch), each with their in-step kernels and
+                roofline; `fp8_block_speedup` = bf16 step / FP8 step
   cpu_baseline  the same FP8 recipe emulated in torch on the host cores (the
                 CPU oracle) on a bounded token sample, in TFLOP/s; under
                 `other_workloads` the oracle on the muP base block, on a
@@ -39,7 +42,7 @@ Also reported on the same JSON line:
 ``--trace`` runs only the headline steps (prewarm, warm-up, timed and
 instrumented passes), so that a ``rocprofv3 --kernel-trace --stats`` summary
 of it averages in-step launches of the headline shape only; ``--trace moe``
-does the same for the MoE workload.
+and ``--trace bf16`` do the same for the MoE and the bf16 workloads.
 
 ``--probe`` runs, instead of the benchmark, one calibration copy (fp32 negate
 of 256 Mi elements: 1 GiB read + 1 GiB written) and then every kernel of the
@@ -79,9 +82,9 @@ def parse():
     p.add_argument("--quant-rows", type=int, default=65536)
     p.add_argument("--quant-cols", type=int, default=4096)
     p.add_argument("--probe", action="store_true", help="one launch of each kernel, for counter passes")
-    p.add_argument("--trace", nargs="?", const="dense", choices=("dense", "moe"), default=None,
+    p.add_argument("--trace", nargs="?", const="dense", choices=("dense", "moe", "bf16"), default=None,
                    help="steps of one workload only (no standalone kernels, quantizer, other shapes or CPU "
-                        "leg): the headline block (default) or the MoE experts")
+                        "leg): the headline block (default), the MoE experts or the bf16 sub-block")
     p.add_argument("--dist", choices=("normal", "student-t"), default="normal",
                    help="activations: N(0,1), or Student-t with 3 degrees of freedom (heavy tails)")
     return p.parse_args()
@@ -445,6 +448,74 @@ def make_moe(T: int, D: int, I: int, E: int, k: int, seed: int = 4):
     return step, counts.tolist()
 
 
+def bf16_launch_name(sym: str, a) -> str:
+    """Kernel name of a C-ABI launch of the bf16 SwiGLU path."""
+    return {"sfp8_bf16_weight_slabs": "bf16_weight_fold", "sfp8_bf16_rows_prep": "bf16_rows_prep",
+            "sfp8_bf16_gemm_swiglu_fwd": "bf16_gateup_swiglu_fwd", "sfp8_bf16_swiglu_bwd": "bf16_swiglu_bwd_rows",
+            "sfp8_bf16_gemm": "bf16_gateup_dgrad", "sfp8_bf16_norm_dh": "bf16_norm_bwd",
+            "sfp8_bf16_gemm_wgrad": "bf16_wgrad_gateup", "sfp8_bf16_fold_grads": "bf16_fold_grads"}.get(sym, sym)
+
+
+def time_bf16(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
+    """The reference's default (bf16) dense MLP sub-block at the same shape:
+    y = h + down_proj(_NormSwiGLU(h, norm_w, w_gu, eps)) under bf16 autocast
+    (train.py:2366-2369), forward + backward; _NormSwiGLU on this build's
+    kernels, the down projection on torch (hipBLASLt).  18*T*D*I FLOP per
+    step, 12*T*D*I of them in _NormSwiGLU."""
+    import torch
+
+    import spark_gpt_amd as sg
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(6)
+    h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(T, D, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    mlp = sg.MLP(D, I).to(dev).train()
+    with torch.no_grad():
+        mlp.gate_up_proj.weight.copy_(torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5)
+        mlp.down_proj.weight.copy_(torch.randn(D, I, device=dev, generator=g) * I ** -0.5)
+    norm_w = torch.ones(D, device=dev, requires_grad=True)
+    params = [norm_w, mlp.gate_up_proj.weight, mlp.down_proj.weight]
+
+    def step():
+        x = h.detach().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = x + mlp.down_proj(sg._NormSwiGLU.apply(x, norm_w, mlp.gate_up_proj.weight, 1e-6))
+        torch.autograd.backward(y, dy, inputs=[x] + params)
+        for p in params:
+            p.grad = None
+
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup + 1):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    work = {
+        "bf16_weight_fold": (None, 16.0 * I * D),
+        "bf16_rows_prep": (None, 4.0 * T * D + 4 * T),
+        "bf16_gateup_swiglu_fwd": (4.0 * T * D * I, None),
+        "bf16_swiglu_bwd_rows": (None, 14.0 * T * I),
+        "bf16_gateup_dgrad": (4.0 * T * D * I, None),
+        "bf16_norm_bwd": (None, 6.0 * T * D),
+        "bf16_wgrad_gateup": (4.0 * T * D * I, None),
+        "bf16_fold_grads": (None, 20.0 * I * D),
+    }
+    per = trace_steps(step, steps, stream, bf16_launch_name)
+    in_step, roofline = in_step_summary(per, steps, work)
+    roofline["peak"] = BF16_PEAK_TFLOPS if roofline["bound"] == "mfma" else HBM_PEAK_GBPS
+    roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
+    flop = 18.0 * T * D * I
+    return {"workload": "bf16_norm_swiglu_mlp_fwd_bwd", "tokens": T, "d_model": D, "ffn": I, "flop_per_step": flop,
+            "ms_per_step": round(ms, 4), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "norm_swiglu_ms_in_step": round(sum(v["ms"] * v["launches_per_step"] for v in in_step.values()), 4),
+            "roofline": roofline, "kernels_in_step": in_step}
+
+
 def time_moe(T: int, D: int, I: int, E: int, k: int, steps: int, warmup: int) -> dict:
     """GPU training-step time of the FP8 experts (prewarm step and scale roll
     first), its in-step kernels and the roofline of the dominant one.  The
@@ -502,6 +573,10 @@ def main() -> None:
     if args.trace == "moe":
         mw = MOE_WORKLOAD
         print(json.dumps({"moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], args.steps, args.warmup)}),
+              flush=True)
+        return
+    if args.trace == "bf16":
+        print(json.dumps({"bf16": time_bf16(args.tokens, args.d_model, args.ffn, args.steps, args.warmup)}),
               flush=True)
         return
     dev = torch.device("cuda:0")
@@ -643,7 +718,10 @@ def main() -> None:
         del h, dy, norm, mlp, step
         mw = MOE_WORKLOAD
         out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5),
-                                  "moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], 20, 5)}
+                                  "moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], 20, 5),
+                                  "bf16": time_bf16(T, D, I, 20, 5)}
+        out["other_workloads"]["bf16"]["fp8_block_speedup"] = round(
+            out["other_workloads"]["bf16"]["ms_per_step"] / ms, 3)
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline(args.cpu_tokens, D, I)
             out["cpu_baseline"]["other_workloads"] = cpu_extra(args.quant_rows, args.quant_cols)

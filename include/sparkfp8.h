@@ -1,9 +1,12 @@
 /*
- * libsparkfp8 -- C ABI of the MI355X (gfx950) FP8 SwiGLU MLP kernels.
+ * libsparkfp8 -- C ABI of the MI355X (gfx950) SwiGLU MLP kernels.
  *
- * Drop-in boundary for the FP8 MLP sub-block of N8python/spark-gpt
- * (``_FP8MLPBlock``, train.py:1193-1252).  Each entry point replaces one
- * kernel launch (or torch-op sequence) of the reference, cited per function.
+ * Drop-in boundary for the MLP paths of N8python/spark-gpt: the FP8 MLP
+ * sub-block (``_FP8MLPBlock``, train.py:1193-1252), the FP8 MoE experts
+ * (``_FP8Experts``, train.py:1255-1606) and the bf16 fused SwiGLU
+ * (``_NormSwiGLU`` / ``_FusedSwiGLU``, train.py:1608-2131).  Each entry point
+ * replaces one kernel launch (or torch-op sequence) of the reference, cited
+ * per function.
  *
  * Conventions
  *  - All pointers are device pointers (hipMalloc / torch CUDA tensors) except
@@ -76,7 +79,8 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
  * launched at train.py:1208-1210).  h [T, D] bf16, norm_w [D] fp32 ->
  * x8 (K-slab of [T, D]: [D/64][ldt][64]) e4m3, x8t (K-slab of [D, ldt])
  * e4m3, rstd [T] fp32; amax[0] max-accumulated.
- * D in {128, 256, 512, 1024, 2048, 4096}; ldt = T rounded up to 256. */
+ * D in {128, 256, 512, 1024, 2048, 4096}, or a multiple of 4096 from 8192
+ * on (a two-pass row-chunked form); ldt = T rounded up to 256. */
 int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
                     const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
                     void* stream);
@@ -358,8 +362,9 @@ int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t 
 
 /* _NormSwiGLU's fold of the weight gradient (train.py:2129-2131): dw =
  * f32(dwp) * nw (fp32 [M, N]) and dnw[n] = sum over m of f32(dwp[m, n]) *
- * w[m, n] (fp32, 64-row blocks in order, then their sum in order); part:
- * sfp8_bf16_fold_partials(M, N) floats. */
+ * w[m, n] (fp32: 16-row blocks in order, groups of 16 block sums in order,
+ * then the groups in order); part:
+ * sfp8_bf16_fold_partials(M, N) floats.  N % 4 == 0. */
 int64_t sfp8_bf16_fold_partials(int64_t M, int64_t N);
 int sfp8_bf16_fold_grads(const void* dwp, const float* w, const float* nw, int64_t M, int64_t N, float* dw,
                          float* dnw, float* part, int64_t part_floats, void* stream);

@@ -291,36 +291,46 @@ __global__ __launch_bounds__(256) void bf16_norm_dh_kernel(const uint16_t* __res
 // _NormSwiGLU's weight gradients from dwp, the bf16 gradient of the folded
 // weight W' (train.py:2129-2131):
 //   dw[m, n] = f32(dwp[m, n]) * nw[n]                         (fp32 [M, N])
-//   part[b, n] = sum over the 64 rows m of block b, ascending, of
+//   part[b, n] = sum over the kFoldRows rows m of block b, ascending, of
 //                f32(dwp[m, n]) * w[m, n]   (each product rounded first),
-// then bf16_colsum_kernel: dnw[n] = sum over b ascending of part[b, n].
+// then dnw[n] = the sum over b of part[b, n]: bf16_colsum_kernel sums
+// groups of kColGroup consecutive b in order, then the groups in order.
+// A thread takes 4 consecutive columns (N % 4 == 0).
+constexpr int kFoldRows = 16;
+constexpr int kColGroup = 16;
+
 __global__ __launch_bounds__(256) void bf16_fold_grads_kernel(const uint16_t* __restrict__ dwp,
                                                               const float* __restrict__ w,
                                                               const float* __restrict__ nw, int64_t M, int64_t N,
                                                               float* __restrict__ dw, float* __restrict__ part) {
 #pragma clang fp contract(off)
-  const int64_t n = (int64_t)blockIdx.y * 256 + threadIdx.x;
-  const int64_t m0 = (int64_t)blockIdx.x * 64;
+  const int64_t n = ((int64_t)blockIdx.y * 256 + threadIdx.x) * 4;
+  const int64_t m0 = (int64_t)blockIdx.x * kFoldRows;
   if (n >= N) return;
-  const float wn = nw[n];
-  const int64_t m1 = m0 + 64 < M ? m0 + 64 : M;
-  float acc = 0.0f;
+  const floatx4 wn = *reinterpret_cast<const floatx4*>(nw + n);
+  const int64_t m1 = m0 + kFoldRows < M ? m0 + kFoldRows : M;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int64_t m = m0; m < m1; ++m) {
-    const float g = bf16_bits_to_f32(dwp[m * N + n]);
-    dw[m * N + n] = g * wn;
-    const float prod = g * w[m * N + n];
+    const intx2 gb = *reinterpret_cast<const intx2*>(dwp + m * N + n);
+    const floatx4 g = {bf16_bits_to_f32((uint32_t)gb[0] & 0xffffu), bf16_bits_to_f32((uint32_t)gb[0] >> 16),
+                       bf16_bits_to_f32((uint32_t)gb[1] & 0xffffu), bf16_bits_to_f32((uint32_t)gb[1] >> 16)};
+    *reinterpret_cast<floatx4*>(dw + m * N + n) = g * wn;
+    const floatx4 prod = g * *reinterpret_cast<const floatx4*>(w + m * N + n);
     acc += prod;
   }
-  part[blockIdx.x * N + n] = acc;
+  *reinterpret_cast<floatx4*>(part + blockIdx.x * N + n) = acc;
 }
 
+// out[j, n] = sum over b in [j * group, min((j + 1) * group, nb)) ascending of part[b, n].
 __global__ __launch_bounds__(256) void bf16_colsum_kernel(const float* __restrict__ part, int64_t nb, int64_t N,
-                                                          float* __restrict__ out) {
+                                                          int group, float* __restrict__ out) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
+  const int64_t b0 = (int64_t)blockIdx.y * group;
+  const int64_t b1 = b0 + group < nb ? b0 + group : nb;
   float acc = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) acc += part[b * N + n];
-  out[n] = acc;
+  for (int64_t b = b0; b < b1; ++b) acc += part[b * N + n];
+  out[blockIdx.y * N + n] = acc;
 }
 
 }  // namespace sfp8
@@ -393,21 +403,30 @@ int sfp8_bf16_norm_dh(const void* p, const void* h, const float* rstd, int64_t T
 
 int64_t sfp8_bf16_fold_partials(int64_t M, int64_t N) {
   if (M <= 0 || N <= 0) return -1;
-  return (int64_t)bf_cdiv(M, 64) * N;
+  const int64_t nb = bf_cdiv(M, kFoldRows);
+  return (nb + bf_cdiv(nb, kColGroup)) * N;  // block partials, then group sums
 }
 
 int sfp8_bf16_fold_grads(const void* dwp, const float* w, const float* nw, int64_t M, int64_t N, float* dw,
                          float* dnw, float* part, int64_t part_floats, void* stream) {
   if (!dwp || !w || !nw || !dw || !dnw || !part) return kErrNullPointer;
-  if (M <= 0 || N <= 0) return kErrBadShape;
+  if (M <= 0 || N <= 0 || N % 4) return kErrBadShape;
+  if (!bf_al16(w) || !bf_al16(nw) || !bf_al16(dw) || !bf_al16(part) || (((uintptr_t)dwp) & 7u)) return kErrBadAlignment;
   if (part_floats < sfp8_bf16_fold_partials(M, N)) return kErrWorkspaceTooSmall;
   hipStream_t st = (hipStream_t)stream;
-  const unsigned nb = bf_cdiv(M, 64);
-  hipLaunchKernelGGL(bf16_fold_grads_kernel, dim3(nb, bf_cdiv(N, 256)), dim3(256), 0, st, (const uint16_t*)dwp, w, nw,
-                     M, N, dw, part);
+  const unsigned nb = bf_cdiv(M, kFoldRows);
+  hipLaunchKernelGGL(bf16_fold_grads_kernel, dim3(nb, bf_cdiv(N, 1024)), dim3(256), 0, st, (const uint16_t*)dwp, w,
+                     nw, M, N, dw, part);
   int rc = bf_status();
   if (rc) return rc;
-  hipLaunchKernelGGL(bf16_colsum_kernel, dim3(bf_cdiv(N, 256)), dim3(256), 0, st, part, (int64_t)nb, N, dnw);
+  const unsigned ng = bf_cdiv(nb, kColGroup);
+  float* grp = part + (int64_t)nb * N;
+  hipLaunchKernelGGL(bf16_colsum_kernel, dim3(bf_cdiv(N, 256), ng), dim3(256), 0, st, part, (int64_t)nb, N,
+                     kColGroup, grp);
+  rc = bf_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(bf16_colsum_kernel, dim3(bf_cdiv(N, 256), 1), dim3(256), 0, st, grp, (int64_t)ng, N, (int)ng,
+                     dnw);
   return bf_status();
 }
 

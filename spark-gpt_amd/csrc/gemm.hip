@@ -1204,6 +1204,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // expert-order rows urow(tm) .. + rows(tm); W of expert e at w + e * w_estride
 // (bytes).  Columns from I on (the last tile when I % 128 != 0) are not
 // written.
+constexpr int kGuStride = 272;  // staging row: 128 bf16 columns (256 bytes) + 16
+
 __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ rstd, uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int tiles_m, int tiles_n,
@@ -1227,42 +1229,62 @@ __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
       lds, reinterpret_cast<const uint8_t*>(x) + r0 * ldx, nrows * ldx, [=](int r) { return r * (int)ldx; },
       kStage, w, ldx * wr, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
       (int)(wr * kStage), (int)(ldx / kStage), acc);
+  // Epilogue in two passes of 128 tile rows: pass P takes the lanes' row
+  // blocks tb = 2P, 2P+1 (tile row 128 wm + 64 P + 32 (tb & 1) + fr, staging
+  // row 64 wm + 32 (tb & 1) + fr), stages g, u and h as bf16 rows in LDS,
+  // then writes them as whole 256-byte row runs.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1, fr = lane & 31, g = lane >> 5;
-  const int64_t c0 = n0 + 64 * wn + 32 * g;  // first of this lane's 32 columns
-  if (c0 >= I) return;  // no barrier follows
+  const int cb = 64 * wn + 32 * g;  // first of this lane's 32 columns in the tile
+  uint8_t* Gs = lds;
+  uint8_t* Us = lds + 128 * kGuStride;
+  uint8_t* Hs = lds + 2 * 128 * kGuStride;
   const float c_exp = -1.4426950408889634f;
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int lr = 128 * wm + 32 * tb + fr;  // row within the tile
-    if (lr >= nrows) continue;
-    const int64_t t = r0 + lr;
-    const float rs = rstd ? rstd[t] : 1.0f;
-    uint32_t gw[16], uw[16], hw[16];
+  for (int P = 0; P < 2; ++P) {
+    if (P) __syncthreads();  // the first pass's rows are out of the staging tiles
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int q = 0; q < 2; ++q) {
+      const int tb = 2 * P + q;
+      const int lr = 128 * wm + 32 * tb + fr;  // row within the tile
+      const float rs = (rstd && lr < nrows) ? rstd[r0 + lr] : 1.0f;
+      uint32_t gw[16], uw[16], hw[16];
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const uint32_t pg = pack2_bf16(acc[tb][nb][v] * rs, acc[tb][nb][v + 1] * rs);
-        const uint32_t pu = pack2_bf16(acc[tb][nb + 2][v] * rs, acc[tb][nb + 2][v + 1] * rs);
-        const float g0 = __uint_as_float(pg << 16), g1 = __uint_as_float(pg & 0xffff0000u);
-        const float u0 = __uint_as_float(pu << 16), u1 = __uint_as_float(pu & 0xffff0000u);
-        const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * c_exp));
-        const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * c_exp));
-        const int k = 8 * nb + v / 2;
-        gw[k] = pg;
-        uw[k] = pu;
-        hw[k] = pack2_bf16(g0 * s0 * u0, g1 * s1 * u1);
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const uint32_t pg = pack2_bf16(acc[tb][nb][v] * rs, acc[tb][nb][v + 1] * rs);
+          const uint32_t pu = pack2_bf16(acc[tb][nb + 2][v] * rs, acc[tb][nb + 2][v + 1] * rs);
+          const float g0 = __uint_as_float(pg << 16), g1 = __uint_as_float(pg & 0xffff0000u);
+          const float u0 = __uint_as_float(pu << 16), u1 = __uint_as_float(pu & 0xffff0000u);
+          const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * c_exp));
+          const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * c_exp));
+          const int k = 8 * nb + v / 2;
+          gw[k] = pg;
+          uw[k] = pu;
+          hw[k] = pack2_bf16(g0 * s0 * u0, g1 * s1 * u1);
+        }
+      }
+      const int sr = 64 * wm + 32 * q + fr;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        store16(Gs + sr * kGuStride + 2 * cb + 16 * j, {gw[4 * j], gw[4 * j + 1], gw[4 * j + 2], gw[4 * j + 3]});
+        store16(Us + sr * kGuStride + 2 * cb + 16 * j, {uw[4 * j], uw[4 * j + 1], uw[4 * j + 2], uw[4 * j + 3]});
+        store16(Hs + sr * kGuStride + 2 * cb + 16 * j, {hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]});
       }
     }
-    uint16_t* gp = gu + t * 2 * I + c0;
-    uint16_t* hp = h + t * I + c0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (c0 + 8 * j >= I) break;  // I % 8 == 0: whole 16-byte pieces
-      store16(gp + 8 * j, {gw[4 * j], gw[4 * j + 1], gw[4 * j + 2], gw[4 * j + 3]});
-      store16(gp + I + 8 * j, {uw[4 * j], uw[4 * j + 1], uw[4 * j + 2], uw[4 * j + 3]});
-      store16(hp + 8 * j, {hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]});
+    __syncthreads();
+    // 128 rows x 16 pieces of 16 bytes per output: sixteen lanes per row
+    for (int idx = threadIdx.x; idx < 128 * 16; idx += 256) {
+      const int sr = idx >> 4, c = idx & 15;
+      const int lr = half_tile_row(sr, P);
+      const int64_t col = n0 + 8 * c;
+      if (lr >= nrows || col >= I) continue;  // I % 8 == 0: whole pieces
+      const int64_t t = r0 + lr;
+      *reinterpret_cast<intx4*>(gu + t * 2 * I + col) = *reinterpret_cast<const intx4*>(Gs + sr * kGuStride + 16 * c);
+      *reinterpret_cast<intx4*>(gu + t * 2 * I + I + col) =
+          *reinterpret_cast<const intx4*>(Us + sr * kGuStride + 16 * c);
+      *reinterpret_cast<intx4*>(h + t * I + col) = *reinterpret_cast<const intx4*>(Hs + sr * kGuStride + 16 * c);
     }
   }
 }
@@ -1334,6 +1356,7 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
 static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
 static_assert(sfp8::kPipeLds <= 160 * 1024, "deferred-epilogue SwiGLU fits the 160 KiB LDS");
 static_assert(128 * sfp8::kBf16Stride <= sfp8::kMainLds, "bf16 epilogue staging fits the main loop's LDS");
+static_assert(3 * 128 * sfp8::kGuStride <= sfp8::kMainLds, "bf16 SwiGLU staging fits the main loop's LDS");
 
 // ============================================================================
 // C ABI

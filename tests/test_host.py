@@ -161,6 +161,9 @@ class _FakeCudaTensor:
     def __init__(self, shape, dtype=torch.bfloat16, is_cuda=True):
         self.shape, self.dtype, self.is_cuda = shape, dtype, is_cuda
 
+    def dim(self):
+        return len(self.shape)
+
 
 @pytest.mark.parametrize("d,inter,ok", [(1024, 3072, True), (256, 768, True), (384, 768, False),
                                         (1024, 3000, False), (8192, 1024, True), (16384, 3072, True),
@@ -237,11 +240,15 @@ def _integration_snippet():
 # Experts.forward's (train.py:2292-2296).
 _STUB_TRAINER_HEAD = """
 FP8_MLP = False
+FUSED_SWIGLU = True
+FUSED_NORM_MLP = True
 """
 _STUB_TRAINER_TAIL = """
-def main(fp8_mlp):
-    global FP8_MLP
+def main(fp8_mlp, fused_norm_mlp=True, fused_swiglu=True):
+    global FP8_MLP, FUSED_NORM_MLP, FUSED_SWIGLU
     FP8_MLP = fp8_mlp
+    FUSED_NORM_MLP = fused_norm_mlp
+    FUSED_SWIGLU = fused_swiglu
 
 class Block:
     def __init__(self, block):
@@ -252,6 +259,8 @@ class Block:
         if _use_fp8_mlp(b, h):
             return _FP8MLPBlock.apply(h, b.norm_w, b.mlp.gate_up_proj.weight, b.mlp.down_proj.weight,
                                       b.mlp.fp8_scale, b.mlp.fp8_amax, 1e-6)
+        if _use_fused_norm_mlp(b, h):
+            return _NormSwiGLU.apply(h, b.norm_w, b.mlp.gate_up_proj.weight, 1e-6)
         return "bf16"
 
 class Experts:
@@ -285,12 +294,13 @@ def test_documented_trainer_binding(monkeypatch):
             return "fp8"
 
     monkeypatch.setattr(train, "_FP8MLPBlock", _Recorder)
+    monkeypatch.setattr(train, "FUSED_NORM_MLP", False)  # the unfused bf16 path, as --no-fused-norm-mlp
     dense = _FakeBlock(1024, 3072).train()
     dense.norm_w = torch.ones(1024)
     blk = train.Block(dense)
     h = _FakeCudaTensor((10, 1024))
     assert blk.forward(h) == "bf16" and not calls  # --fp8-mlp not given
-    train.main(True)
+    train.main(True, fused_norm_mlp=False)
     assert sg.mlp.FP8_MLP is False  # the package's own switch is not involved
     assert blk.forward(h) == "fp8" and len(calls) == 1
     assert calls[0][2] is dense.mlp.gate_up_proj.weight
@@ -298,9 +308,49 @@ def test_documented_trainer_binding(monkeypatch):
     assert blk.forward(h) == "bf16"
     sparse = _FakeBlock(1024, 3072, sparse=True).train()
     assert train._use_fp8_mlp(sparse, h) is False
-    train.main(False)
+    train.main(False, fused_norm_mlp=False)
     dense.train()
     assert blk.forward(h) == "bf16"
+
+
+def test_documented_trainer_binding_bf16(monkeypatch):
+    """Without --fp8-mlp the same substitution routes a dense block to
+    _NormSwiGLU (the default, train.py:2366-2369); --no-fused-norm-mlp or
+    --no-fused-swiglu (main() rebinding the trainer's switches) routes it to
+    the unfused path, and a sparse block is never routed (checked first)."""
+    import types
+
+    train = types.ModuleType("train_stub")
+    exec(_STUB_TRAINER_HEAD + _integration_snippet() + _STUB_TRAINER_TAIL, train.__dict__)
+    assert train._NormSwiGLU is sg._NormSwiGLU and train._FusedSwiGLU is sg._FusedSwiGLU
+    calls = []
+
+    class _Recorder:
+        @staticmethod
+        def apply(*args):
+            calls.append(args)
+            return "bf16-fused"
+
+    monkeypatch.setattr(train, "_NormSwiGLU", _Recorder)
+    dense = _FakeBlock(1024, 3072).train()
+    dense.norm_w = torch.ones(1024)
+    blk = train.Block(dense)
+    h = _FakeCudaTensor((10, 1024))
+    train.main(False)
+    assert blk.forward(h) == "bf16-fused" and len(calls) == 1
+    assert calls[0][2] is dense.mlp.gate_up_proj.weight
+    dense.eval()
+    assert blk.forward(h) == "bf16-fused"  # the fused bf16 path is not training-only
+    train.main(False, fused_norm_mlp=False)
+    assert blk.forward(h) == "bf16"
+    train.main(False, fused_swiglu=False)
+    assert blk.forward(h) == "bf16"
+    train.main(False)
+    assert blk.forward(_FakeCudaTensor((10, 1000))) == "bf16"  # width not a multiple of 64
+    sparse = _FakeBlock(1024, 3072, sparse=True)
+    assert train._use_fused_norm_mlp(sparse, h) is False
+    assert train._use_fused_swiglu(h) is True
+    assert train._use_fused_swiglu(_FakeCudaTensor((10, 1024), dtype=torch.float32)) is False
 
 
 def test_documented_trainer_binding_experts(monkeypatch):
