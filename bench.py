@@ -658,6 +658,27 @@ def main() -> None:
                               "copy_bytes_written": 1 << 30}))
             return
         out_extra["kernels"] = {name: rates(work, name, timed_launches(fn, 10, stream)) for name, fn in kern.items()}
+        # the consumer of the gate/up weight gradient: the Muon momentum stage,
+        # after the gradient (two kernels, dW written and read back) or fused
+        # into its split reduction
+        v_mom = torch.zeros(2 * I, D, device=dev)
+        u_mom = torch.empty(2 * I, D, dtype=torch.bfloat16, device=dev)
+
+        def separate():
+            dw = ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1])
+            ops.momentum_stage(dw.view(-1), v_mom.view(-1), u_mom.view(-1), 0.95)
+
+        sep_ms = timed_launches(separate, 10, stream)
+        fused_ms = timed_launches(lambda: ops.wgrad_momentum(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1], v_mom,
+                                                             u_mom, 0.95), 10, stream)
+        g_mom = torch.randn(2 * I * D, device=dev)
+        stage_ms = timed_launches(lambda: ops.momentum_stage(g_mom, v_mom.view(-1), u_mom.view(-1), 0.95), 10,
+                                  stream)
+        out_extra["momentum_fusion"] = {
+            "wgrad_gateup_then_momentum_stage_ms": round(sep_ms, 4), "fused_ms": round(fused_ms, 4),
+            "saved_ms": round(sep_ms - fused_ms, 4),
+            "momentum_stage_alone": rates({"m": (None, 14.0 * 2 * I * D)}, "m", stage_ms)}
+        del v_mom, u_mom, g_mom
         del x8, x8t, rstd, w8, w8t, wd8, wdt, gu8, h8, h8t, dgu8, dgu8t, dxn, dh, dnw, dy8t
 
     # ---- timed steps (clean: nothing but the step's own launches) ----

@@ -369,6 +369,35 @@ int64_t sfp8_bf16_fold_partials(int64_t M, int64_t N);
 int sfp8_bf16_fold_grads(const void* dwp, const float* w, const float* nw, int64_t M, int64_t N, float* dw,
                          float* dnw, float* part, int64_t part_floats, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * The consumer of the fp32 weight gradients: the Muon optimizer's momentum
+ * stage (train.py:2805-2839), alone and fused into the weight gradient.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces _momentum_stage_kernel (train.py:2805-2820, launched by
+ * _momentum_stage 2829-2839): v <- lerp(v, g, w_v) in place (fp32), u =
+ * bf16(lerp(g, v_new, w_u)) (the Newton-Schulz staging matrix), each lerp in
+ * torch.lerp's form for its weight (w_v < 0.5 <= w_u): the reference's
+ * two-pass torch update bit for bit.  w_v = 1 - momentum, w_u = momentum,
+ * each rounded to fp32 from the caller's double.  n % 4 == 0; g, v 16-byte
+ * and u 8-byte aligned. */
+int sfp8_momentum_stage(const float* g, float* v, void* u, int64_t n, float w_v, float w_u, void* stream);
+
+/* sfp8_gemm_wgrad (e5m2 at, e4m3 bt) with the momentum stage applied as the
+ * split sum leaves the registers: d = dW, then v <- lerp(v, d, w_v), u =
+ * bf16(lerp(d, v_new, w_u)) ([M, N] bf16: the parameter's layout in the
+ * Newton-Schulz staging stack, train.py:2982-2999), grad = d when grad !=
+ * NULL.  No counterpart in the reference (its backward writes dW and the
+ * optimizer reads it back); valid when nothing reduces or accumulates the
+ * gradient between the backward and the optimizer step (one process, no
+ * gradient accumulation).  ws: fp32 workspace of
+ * sfp8_wgrad_momentum_workspace_floats(M, N, ldt) floats (NULL when ldt = 0:
+ * then d = 0). */
+int64_t sfp8_wgrad_momentum_workspace_floats(int64_t M, int64_t N, int64_t ldt);
+int sfp8_gemm_wgrad_momentum(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
+                             const float* sa, const float* sb, float* grad, float* v, void* u, float w_v, float w_u,
+                             float* ws, int64_t ws_floats, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,14 +9,15 @@ from .mlp import (FP8_HEADROOM_BINADES, FP8_SITE_MAX, MLP, _FP8MLPBlock, _use_fp
 from .moe import _FP8Experts, _use_fp8_moe, make_fp8_moe_guard
 from .swiglu import (_FusedSwiGLU, _NormSwiGLU, _use_fused_norm_mlp, _use_fused_swiglu, make_fused_norm_mlp_guard,
                      make_fused_swiglu_guard)
-from . import mlp, moe, ops, swiglu, torch_ops
+from .muon import _momentum_stage, _momentum_stage_supported
+from . import mlp, moe, muon, ops, swiglu, torch_ops
 
 __all__ = [
     "FP8_HEADROOM_BINADES", "FP8_SITE_MAX", "MLP", "_FP8MLPBlock", "_use_fp8_mlp",
     "fp8_mlp_block", "fp8_update_scales", "make_fp8_mlp_guard", "mlp", "ops", "set_fp8_mlp", "torch_ops",
     "_FP8Experts", "_use_fp8_moe", "make_fp8_moe_guard", "moe",
     "_FusedSwiGLU", "_NormSwiGLU", "_use_fused_norm_mlp", "_use_fused_swiglu", "make_fused_norm_mlp_guard",
-    "make_fused_swiglu_guard", "swiglu",
+    "make_fused_swiglu_guard", "swiglu", "_momentum_stage", "_momentum_stage_supported", "muon",
 ]
 
 

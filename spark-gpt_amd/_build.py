@@ -12,7 +12,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsparkfp8.so")
-SOURCES = ("quant.hip", "gemm.hip", "moe.hip", "bf16.hip")
+SOURCES = ("quant.hip", "gemm.hip", "moe.hip", "bf16.hip", "optim.hip")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

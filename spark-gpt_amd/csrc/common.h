@@ -192,6 +192,22 @@ SFP8_DEV float sigmoid_fast(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
+// The Muon momentum stage of four elements (train.py:2805-2820): v <- lerp(v,
+// g, w_v) (torch.lerp's weight < 0.5 form), u = bf16(lerp(g, v, 1 - w_u1))
+// (its weight >= 0.5 form), each lerp one fused multiply-add as torch's GPU
+// lerp evaluates it.  w_u1 = 1 - w_u.
+SFP8_DEV void momentum4(const floatx4& g, floatx4& v, float w_v, float w_u1, uint32_t (&u)[2]) {
+  floatx4 vn, un;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    vn[i] = __builtin_fmaf(w_v, g[i] - v[i], v[i]);
+    un[i] = __builtin_fmaf(-(vn[i] - g[i]), w_u1, vn[i]);
+  }
+  v = vn;
+  u[0] = pack2_bf16(un[0], un[1]);
+  u[1] = pack2_bf16(un[2], un[3]);
+}
+
 // fp8 byte -> fp32 (exact).  Hardware converter on gfx950.
 SFP8_DEV float e4m3_to_f32(uint32_t word, int byte) {
   switch (byte) {

@@ -1014,14 +1014,15 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
 // (frag_offset below: each wave store instruction is one contiguous 1 KiB
 // run) and splitk_reduce_kernel sums them in split order (deterministic) and
 // scatters them to [M, N].
-// BF16: bf16 operands (2 bytes per token: `ldt` and `kchunk` count K bytes),
-// and the partials always go to `out` as the workspace, for the bf16 reduce
-// (bf16_wgrad_reduce_kernel) to round.
+// With `partials` (and always with BF16) the raw partials go to `out` as the
+// workspace, also for one split (the reductions that round to bf16 or apply
+// the optimizer's momentum stage).  BF16: bf16 operands (2 bytes per token:
+// `ldt` and `kchunk` count K bytes).
 template <bool BF16, int FMT_A, int FMT_B>
 __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldt,
     int64_t kchunk, const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out,
-    int tiles_m, int tiles_n, int splits) {
+    int tiles_m, int tiles_n, int splits, int partials) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn, sp;
   split_tile_coords(blockIdx.x, tiles_m, tiles_n, splits, tm, tn, sp);
@@ -1039,7 +1040,7 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   MainLoop<BF16, FMT_A, FMT_B, false>::run(
       lds, a0, a_end - a0, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_end - b0,
       [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)(kchunk / kStage), acc);
-  if (BF16 || splits > 1) {
+  if (BF16 || partials) {
     // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
     float* frag = out + ((int64_t)sp * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
                   wave * (kTile * kTile / 4);
@@ -1351,6 +1352,39 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
     *reinterpret_cast<intx2*>(out + m * N + n) = intx2{(int)pack2_bf16(acc[0], acc[1]), (int)pack2_bf16(acc[2], acc[3])};
 }
 
+// The weight gradient with the optimizer's momentum stage fused into its
+// reduction (the consumer of dW, train.py:2805-2820, applied as the split
+// sum leaves the registers): d = (sum over s ascending of ws[s]) / (sa * sb),
+// then v <- lerp(v, d, w_v) in place and u = bf16(lerp(d, v, 1 - w_u1)) into
+// the Newton-Schulz staging matrix ([M, N] bf16, the parameter's layout);
+// grad[m, n] = d when grad is given.  splits == 0: d = 0 (no tokens).
+__global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __restrict__ ws, int splits, int64_t n4,
+                                                              int tiles_n, int64_t M, int64_t N,
+                                                              const float* __restrict__ sa,
+                                                              const float* __restrict__ sb, float* __restrict__ grad,
+                                                              float* __restrict__ v, uint16_t* __restrict__ u,
+                                                              float w_v, float w_u1) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= n4) return;
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  const int lane = (int)(q & 63), i = (int)(q >> 6) & 3, nb = (int)(q >> 8) & 3, tb = (int)(q >> 10) & 3;
+  const int wave = (int)(q >> 12) & 3;
+  const int64_t tile = q >> 14;
+  const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
+  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
+  const int64_t n = tn * kTile + 128 * (wave >> 1) + 64 * (lane >> 5) + 16 * nb + 4 * i;
+  if (m >= M || n >= N) return;
+  const floatx4 d = acc * (1.0f / (sa[0] * sb[0]));
+  if (grad) *reinterpret_cast<floatx4*>(grad + m * N + n) = d;
+  floatx4 vv = *reinterpret_cast<const floatx4*>(v + m * N + n);
+  uint32_t uu[2];
+  momentum4(d, vv, w_v, w_u1, uu);
+  *reinterpret_cast<floatx4*>(v + m * N + n) = vv;
+  *reinterpret_cast<intx2*>(u + m * N + n) = intx2{(int)uu[0], (int)uu[1]};
+}
+
 }  // namespace sfp8
 
 static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
@@ -1540,7 +1574,7 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   if (rc) return rc;
   hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
                      kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
-                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits);
+                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1));
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
@@ -1756,7 +1790,7 @@ int sfp8_bf16_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, i
   if (rc) return rc;
   hipLaunchKernelGGL((wgrad_kernel<true, 0, 0>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256), kMainLds,
                      st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws,
-                     tiles_m, tiles_n, (int)splits);
+                     tiles_m, tiles_n, (int)splits, 1);
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
@@ -1789,6 +1823,39 @@ int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t 
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
   hipLaunchKernelGGL(bf16_wgrad_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  return status();
+}
+
+// ---- the weight gradient fused with the optimizer's momentum stage ----
+int64_t sfp8_wgrad_momentum_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
+  return sfp8_wgrad_splits(M, N, ldt) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
+}
+
+int sfp8_gemm_wgrad_momentum(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
+                             const float* sa, const float* sb, float* grad, float* v, void* u, float w_v, float w_u,
+                             float* ws, int64_t ws_floats, void* stream) {
+  if (!sa || !sb || !v || !u || (ldt > 0 && (!at || !bt || !ws))) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || ldt < 0 || ldt % kTile || N % 4) return kErrBadShape;
+  if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3 || !(w_v > -0.5f && w_v < 0.5f) || !(w_u >= 0.5f)) return kErrBadShape;
+  if (!fits32(slab_rows(M), ldt) || !fits32(slab_rows(N), ldt)) return kErrBadShape;
+  if (!al16(at) || !al16(bt) || !al16(grad) || !al16(v) || !al16(ws) || (((uintptr_t)u) & 7u)) return kErrBadAlignment;
+  hipStream_t st = (hipStream_t)stream;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  int splits = 0;
+  if (ldt > 0) {
+    splits = (int)sfp8_wgrad_splits(M, N, ldt);
+    if (ws_floats < sfp8_wgrad_momentum_workspace_floats(M, N, ldt)) return kErrWorkspaceTooSmall;
+    int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
+    if (rc) return rc;
+    hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                       dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
+                       ws, tiles_m, tiles_n, splits, 1);
+    rc = status();
+    if (rc) return rc;
+  }
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  hipLaunchKernelGGL(splitk_momentum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws, splits, n4,
+                     tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
   return status();
 }
 

@@ -525,3 +525,29 @@ def bf16_fold_grads(dwp: torch.Tensor, w: torch.Tensor, norm_w: torch.Tensor):
     _lib.call("sfp8_bf16_fold_grads", dwp.data_ptr(), w.data_ptr(), norm_w.data_ptr(), M, N, dw.data_ptr(),
               dnw.data_ptr(), part.data_ptr(), part.numel(), _lib.stream_of(dwp))
     return dw, dnw
+
+
+# ----------------------------------------------------- the optimizer's momentum stage
+def momentum_stage(g: torch.Tensor, v: torch.Tensor, u: torch.Tensor, momentum: float) -> None:
+    """v <- lerp(v, g, 1 - momentum) in place; u <- bf16(lerp(g, v, momentum))."""
+    _need(g.is_cuda and g.dtype == torch.float32 and v.dtype == torch.float32 and u.dtype == BF16,
+          "g, v must be fp32 and u bf16 device tensors")
+    _need(g.is_contiguous() and v.is_contiguous() and u.is_contiguous(), "g, v, u must be contiguous")
+    _need(g.numel() == v.numel() == u.numel(), "g, v, u must have the same number of elements")
+    _lib.call("sfp8_momentum_stage", g.data_ptr(), v.data_ptr(), u.data_ptr(), g.numel(), 1.0 - momentum, momentum,
+              _lib.stream_of(g))
+
+
+def wgrad_momentum(at, bt, M: int, N: int, sa, sb, v: torch.Tensor, u: torch.Tensor, momentum: float, grad=None):
+    """wgrad(at, bt, M, N, sa, sb) handed straight to the momentum stage:
+    v <- lerp(v, dW, 1 - momentum), u <- bf16(lerp(dW, v, momentum)); dW is
+    also written to `grad` when given."""
+    _cuda_contig("at", at, E5M2, 3)
+    _cuda_contig("bt", bt, E4M3, 3)
+    _need(v.is_contiguous() and u.is_contiguous() and v.numel() == u.numel() == M * N, "v, u must be [M, N]")
+    ldt = at.shape[0] * SLAB
+    nws = _lib.query("sfp8_wgrad_momentum_workspace_floats", M, N, ldt)
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=at.device)
+    _lib.call("sfp8_gemm_wgrad_momentum", at.data_ptr(), FMT_E5M2, bt.data_ptr(), FMT_E4M3, M, N, ldt, sa.data_ptr(),
+              sb.data_ptr(), _lib.ptr(grad), v.data_ptr(), u.data_ptr(), 1.0 - momentum, momentum, ws.data_ptr(),
+              ws.numel(), _lib.stream_of(at))
