@@ -323,6 +323,8 @@ def launch_name(sym: str, a, D: int, I: int) -> str:
         return "weight_quant_gu" if a[1] == 2 * I else "weight_quant_down"
     if sym == "sfp8_gemm_wgrad":
         return "wgrad_down" if a[4] == D else "wgrad_gateup"
+    if sym == "sfp8_gemm_wgrad_rows":
+        return "wgrad_down" if a[6] == D else "wgrad_gateup"
     if sym == "sfp8_weight_quant_experts":
         return "weight_quant_gu" if a[2] == 2 * I else "weight_quant_down"
     if sym == "sfp8_moe_gemm_wgrad":
@@ -609,8 +611,8 @@ def main() -> None:
         wscale = torch.empty(2, device=dev)
         w8, w8t, _ = ops.weight_quant(mlp.gate_up_proj.weight.detach(), wscale[0:1], w8=True, w8t=True)
         wd8, _, wdt = ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True, bf16t=True)
-        gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I)
-        dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
+        gu8, h8, _ = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I, copy=False)
+        dgu8, _ = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax, copy=False)
         dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
         dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax)
 
@@ -629,13 +631,13 @@ def main() -> None:
                                                         w8t=True),
             "weight_quant_down": lambda: ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True,
                                                           bf16t=True),
-            "gateup_swiglu_fwd": lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I),
+            "gateup_swiglu_fwd": lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I, copy=False),
             "down_fwd": lambda: ops.down_fwd(h8, wd8, h, scale, wscale),
-            "down_dgrad_swiglu_bf16": lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax),
+            "down_dgrad_swiglu_bf16": lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax, copy=False),
             "gateup_dgrad": lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D),
             "norm_bwd": lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax),
-            "wgrad_down": lambda: ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3]),
-            "wgrad_gateup": lambda: ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1]),
+            "wgrad_down": lambda: ops.wgrad_rows(dy8t, h8, D, I, scale[4:5], scale[2:3], a_rows=False),
+            "wgrad_gateup": lambda: ops.wgrad_rows(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], b_rows=False),
         }
         if args.probe:
             # calibration copy of known size, then one launch of each kernel
@@ -665,12 +667,12 @@ def main() -> None:
         u_mom = torch.empty(2 * I, D, dtype=torch.bfloat16, device=dev)
 
         def separate():
-            dw = ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1])
+            dw = ops.wgrad_rows(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], b_rows=False)
             ops.momentum_stage(dw.view(-1), v_mom.view(-1), u_mom.view(-1), 0.95)
 
         sep_ms = timed_launches(separate, 10, stream)
-        fused_ms = timed_launches(lambda: ops.wgrad_momentum(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1], v_mom,
-                                                             u_mom, 0.95), 10, stream)
+        fused_ms = timed_launches(lambda: ops.wgrad_momentum(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], v_mom,
+                                                             u_mom, 0.95, a_rows=True), 10, stream)
         g_mom = torch.randn(2 * I * D, device=dev)
         stage_ms = timed_launches(lambda: ops.momentum_stage(g_mom, v_mom.view(-1), u_mom.view(-1), 0.95), 10,
                                   stream)
@@ -679,7 +681,7 @@ def main() -> None:
             "saved_ms": round(sep_ms - fused_ms, 4),
             "momentum_stage_alone": rates({"m": (None, 14.0 * 2 * I * D)}, "m", stage_ms)}
         del v_mom, u_mom, g_mom
-        del x8, x8t, rstd, w8, w8t, wd8, wdt, gu8, h8, h8t, dgu8, dgu8t, dxn, dh, dnw, dy8t
+        del x8, x8t, rstd, w8, w8t, wd8, wdt, gu8, h8, dgu8, dxn, dh, dnw, dy8t
 
     # ---- timed steps (clean: nothing but the step's own launches) ----
     for _ in range(args.warmup):

@@ -164,6 +164,19 @@ int64_t sfp8_slab_bytes(int64_t rows, int64_t k);
 int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt);
 
 
+/* The same weight gradient with either operand (or both) read from the row
+ * K-slab of the token-major activation the forward GEMMs use instead of the
+ * token-contiguous copy (a_rows / b_rows != 0: a = [M/64][ldt][64], b =
+ * [N/64][ldt][64] bytes: d_gu8 and h8 as their producers write them),
+ * through transposing LDS reads: bytes equal to sfp8_gemm_wgrad on the
+ * copies, which the producers then need not write.  M % 64 == 0 with
+ * a_rows, N % 64 == 0 with b_rows, at least one set; ws: fp32 workspace of
+ * sfp8_wgrad_rows_workspace_floats(M, N, ldt) floats. */
+int64_t sfp8_wgrad_rows_workspace_floats(int64_t M, int64_t N, int64_t ldt);
+int sfp8_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b, int fmt_b, int b_rows, int64_t M,
+                         int64_t N, int64_t ldt, const float* sa, const float* sb, float* out, float* ws,
+                         int64_t ws_floats, void* stream);
+
 /* ---- norm backward ------------------------------------------------------ */
 
 /* RMSNorm backward + residual, replaces _fp8_norm_bwd_kernel
@@ -383,8 +396,9 @@ int sfp8_bf16_fold_grads(const void* dwp, const float* w, const float* nw, int64
  * and u 8-byte aligned. */
 int sfp8_momentum_stage(const float* g, float* v, void* u, int64_t n, float w_v, float w_u, void* stream);
 
-/* sfp8_gemm_wgrad (e5m2 at, e4m3 bt) with the momentum stage applied as the
- * split sum leaves the registers: d = dW, then v <- lerp(v, d, w_v), u =
+/* sfp8_gemm_wgrad_rows (e5m2 a, e4m3 b; a_rows = b_rows = 0: the
+ * token-contiguous copies of sfp8_gemm_wgrad) with the momentum stage
+ * applied as the split sum leaves the registers: d = dW, then v <- lerp(v, d, w_v), u =
  * bf16(lerp(d, v_new, w_u)) ([M, N] bf16: the parameter's layout in the
  * Newton-Schulz staging stack, train.py:2982-2999), grad = d when grad !=
  * NULL.  No counterpart in the reference (its backward writes dW and the
@@ -394,9 +408,9 @@ int sfp8_momentum_stage(const float* g, float* v, void* u, int64_t n, float w_v,
  * sfp8_wgrad_momentum_workspace_floats(M, N, ldt) floats (NULL when ldt = 0:
  * then d = 0). */
 int64_t sfp8_wgrad_momentum_workspace_floats(int64_t M, int64_t N, int64_t ldt);
-int sfp8_gemm_wgrad_momentum(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
-                             const float* sa, const float* sb, float* grad, float* v, void* u, float w_v, float w_u,
-                             float* ws, int64_t ws_floats, void* stream);
+int sfp8_gemm_wgrad_momentum(const void* a, int fmt_a, int a_rows, const void* b, int fmt_b, int b_rows, int64_t M,
+                             int64_t N, int64_t ldt, const float* sa, const float* sb, float* grad, float* v, void* u,
+                             float w_v, float w_u, float* ws, int64_t ws_floats, void* stream);
 
 #ifdef __cplusplus
 }

@@ -67,11 +67,13 @@ SIGNATURES = {
     "sfp8_bf16_moe_gemm_wgrad": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
     "sfp8_bf16_fold_partials": (_I64, [_I64, _I64]),
     "sfp8_bf16_fold_grads": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
+    "sfp8_wgrad_rows_workspace_floats": (_I64, [_I64, _I64, _I64]),
+    "sfp8_gemm_wgrad_rows": (_INT, [_P, _INT, _INT, _P, _INT, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     # the optimizer's momentum stage, and the weight gradient fused with it
     "sfp8_momentum_stage": (_INT, [_P, _P, _P, _I64, _F32, _F32, _P]),
     "sfp8_wgrad_momentum_workspace_floats": (_I64, [_I64, _I64, _I64]),
-    "sfp8_gemm_wgrad_momentum": (_INT, [_P, _INT, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _F32, _F32, _P, _I64,
-                                        _P]),
+    "sfp8_gemm_wgrad_momentum": (_INT, [_P, _INT, _INT, _P, _INT, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _F32, _F32,
+                                        _P, _I64, _P]),
 }
 
 ERRORS = {

@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   lds_rows_to_kslab<2>(Gt, kTile, kEpiStride, gu8, ldt, m0, n0);
   lds_rows_to_kslab<2>(Ut, kTile, kEpiStride, gu8, ldt, m0, I + n0);
   lds_rows_to_kslab<2>(Ht, kTile, kEpiStride, h8, ldt, m0, n0);
-  lds_tile_store_slab_tr<8>(Ht, kEpiStride, h8t, slab_rows(I), m0, n0);
+  if (h8t) lds_tile_store_slab_tr<8>(Ht, kEpiStride, h8t, slab_rows(I), m0, n0);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
   if (lane == 0) { red[wave] = m_gu; red[4 + wave] = m_h; }
@@ -320,7 +320,7 @@ struct SwigluPipe {
     // there is none (has_next false: nra, nvoff_b = ra, voff_b)
     uint8_t* lds;
     __amdgpu_buffer_rsrc_t ra, rb, nra;
-    uint32_t voff_a[4], voff_b[2], nvoff_b[2], aoff[2], boff[2];
+    uint32_t voff_a[4], voff_b[2], nvoff_b[2], aoff[8], boff[8];
     bool has_next;
     int wave;
     typename ML::Frag f[2];
@@ -606,7 +606,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     // token rows of 64 bytes, one contiguous block; h8t transposed)
     if (c.prev) {
       pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
-      lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
+      if (h8t) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
     }
     // this tile's g, u (bf16, unscaled) become the next epilogue's input
 #pragma unroll
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     P::template tail_units<0>(c);
     __syncthreads();
     pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
-    lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
+    if (h8t) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
   }
   float* red = reinterpret_cast<float*>(lds + kPipeRing + 2 * kPipeHBytes);
   float mg = wave_max(c.m_gu * deq), mh = wave_max(c.m_h * (deq * deq));
@@ -936,8 +936,10 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
         }
         m3 = fmaxf(m3, mw);
       }
-      store16(G2 + lr * kEpiStride2 + c, pg);
-      store16(U2 + lr * kEpiStride2 + c, pu);
+      if (dgu8t) {  // staged for the token-contiguous copy
+        store16(G2 + lr * kEpiStride2 + c, pg);
+        store16(U2 + lr * kEpiStride2 + c, pu);
+      }
       // dgu8 is a K-slab [2I/64][ldt][64]; four lanes write one 64-byte row
       if (c < cols) {
         const int64_t j = n0 + c;
@@ -948,11 +950,13 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     __syncthreads();
     // the token-contiguous dgu8t: local rows 0-63 are tile rows 64P.., rows
     // 64-127 tile rows 128 + 64P.. (rows past T hold zero codes)
-    const int64_t rp2 = slab_rows(2 * I);
-    lds_rows_store_slab_tr<64>(G2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, n0);
-    lds_rows_store_slab_tr<64>(G2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, n0);
-    lds_rows_store_slab_tr<64>(U2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, I + n0);
-    lds_rows_store_slab_tr<64>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, I + n0);
+    if (dgu8t) {
+      const int64_t rp2 = slab_rows(2 * I);
+      lds_rows_store_slab_tr<64>(G2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, n0);
+      lds_rows_store_slab_tr<64>(G2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, n0);
+      lds_rows_store_slab_tr<64>(U2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, I + n0);
+      lds_rows_store_slab_tr<64>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, I + n0);
+    }
   }
   __syncthreads();  // the next tile's DMA overwrites the staging tiles
   }
@@ -1018,7 +1022,13 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
 // workspace, also for one split (the reductions that round to bf16 or apply
 // the optimizer's momentum stage).  BF16: bf16 operands (2 bytes per token:
 // `ldt` and `kchunk` count K bytes).
-template <bool BF16, int FMT_A, int FMT_B>
+// TRA / TRB: that operand is instead a row K-slab of the token-major
+// activation ([M/64][ldt][64] or [N/64][ldt][64]: h8 and dgu8 as their
+// producers write them for the forward GEMMs), read through transposing LDS
+// reads (MainLoop TR_A / TR_B); the partials then always go to `out` as the
+// workspace, in the same order (with TRB the columns unpermuted:
+// splitk_reduce_kernel<true>).
+template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false>
 __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldt,
     int64_t kchunk, const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out,
@@ -1030,17 +1040,26 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   floatx16 acc[4][4];
-  // K-slab operands: slab (kb / 64) of A starts at (kb / 64) * rpa * 64
   const int64_t kb = (int64_t)sp * kchunk;
-  const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
-  const uint8_t* a0 = at + (kb / kStage) * rpa * kStage + m0 * kStage;
-  const uint8_t* b0 = bt + (kb / kStage) * rpb * kStage + n0 * kStage;
-  const uint8_t* a_end = at + ldt * rpa;
-  const uint8_t* b_end = bt + ldt * rpb;
-  MainLoop<BF16, FMT_A, FMT_B, false>::run(
-      lds, a0, a_end - a0, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_end - b0,
-      [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)(kchunk / kStage), acc);
-  if (BF16 || partials) {
+  {
+    // K-slab operands: slab (kb / 64) of A starts at (kb / 64) * rpa * 64.
+    // Row K-slab (TR) operands: tile row r = token (r % 64) of the tile's
+    // 64-column slab r / 64; a 64-token stage is 4 KiB further on in every
+    // slab.
+    const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
+    const int ldti = (int)ldt;
+    const uint8_t* a0 = TRA ? at + (m0 / 64) * ldt * kStage + kb * kStage : at + (kb / kStage) * rpa * kStage + m0 * kStage;
+    const uint8_t* b0 = TRB ? bt + (n0 / 64) * ldt * kStage + kb * kStage : bt + (kb / kStage) * rpb * kStage + n0 * kStage;
+    const uint8_t* a_end = TRA ? at + (M / 64) * ldt * kStage : at + ldt * rpa;
+    const uint8_t* b_end = TRB ? bt + (N / 64) * ldt * kStage : bt + ldt * rpb;
+    MainLoop<BF16, FMT_A, FMT_B, false, 4, kStages, 0, TRA, TRB>::run(
+        lds, a0, a_end - a0,
+        [=](int r) { return TRA ? ((r >> 6) * ldti + (r & 63)) * kStage : r * kStage; },
+        TRA ? 64 * kStage : (int)(rpa * kStage), b0, b_end - b0,
+        [=](int r) { return TRB ? ((r >> 6) * ldti + (r & 63)) * kStage : plain_col(r) * kStage; },
+        TRB ? 64 * kStage : (int)(rpb * kStage), (int)(kchunk / kStage), acc);
+  }
+  if (BF16 || TRA || TRB || partials) {
     // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
     float* frag = out + ((int64_t)sp * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
                   wave * (kTile * kTile / 4);
@@ -1160,6 +1179,9 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ out,
 // q-th float4 of one split's partials; its (m, n) follows from the MFMA
 // accumulator layout (B-tile rows permuted by plain_col: accumulator v of
 // block nb, lane half g is column 128*wn + 64*g + 16*nb + v).
+// TR_B: partials of wgrad_kernel<.., true> (B tile unpermuted: accumulator
+// v of block nb, lane half g is column 128*wn + 32*nb + 8*(v/4) + 4*g + v%4).
+template <bool TR_B = false>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits,
                                                             int64_t n4, int tiles_n, int64_t M, int64_t N,
                                                             const float* __restrict__ sa,
@@ -1177,7 +1199,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const int64_t tile = q >> 14;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
   const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
-  const int64_t n = tn * kTile + 128 * (wave >> 1) + 64 * (lane >> 5) + 16 * nb + 4 * i;
+  const int64_t n = tn * kTile + 128 * (wave >> 1) +
+                    (TR_B ? 32 * nb + 8 * i + 4 * (lane >> 5) : 64 * (lane >> 5) + 16 * nb + 4 * i);
   if (m < M && n < N) {
     const float deq = 1.0f / (sa[0] * sb[0]);
     *reinterpret_cast<floatx4*>(out + m * N + n) = acc * deq;
@@ -1357,7 +1380,10 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
 // sum leaves the registers): d = (sum over s ascending of ws[s]) / (sa * sb),
 // then v <- lerp(v, d, w_v) in place and u = bf16(lerp(d, v, 1 - w_u1)) into
 // the Newton-Schulz staging matrix ([M, N] bf16, the parameter's layout);
-// grad[m, n] = d when grad is given.  splits == 0: d = 0 (no tokens).
+// grad[m, n] = d when grad is given.  splits == 0: d = 0 (no tokens).  TR_B:
+// the partials' columns are in the transposed-read B order, as for
+// splitk_reduce_kernel<true>.
+template <bool TR_B = false>
 __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __restrict__ ws, int splits, int64_t n4,
                                                               int tiles_n, int64_t M, int64_t N,
                                                               const float* __restrict__ sa,
@@ -1374,7 +1400,8 @@ __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __res
   const int64_t tile = q >> 14;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
   const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
-  const int64_t n = tn * kTile + 128 * (wave >> 1) + 64 * (lane >> 5) + 16 * nb + 4 * i;
+  const int64_t n = tn * kTile + 128 * (wave >> 1) +
+                    (TR_B ? 32 * nb + 8 * i + 4 * (lane >> 5) : 64 * (lane >> 5) + 16 * nb + 4 * i);
   if (m >= M || n >= N) return;
   const floatx4 d = acc * (1.0f / (sa[0] * sb[0]));
   if (grad) *reinterpret_cast<floatx4*>(grad + m * N + n) = d;
@@ -1433,13 +1460,38 @@ inline bool fits32(int64_t rows, int64_t ld) { return rows * ld < (int64_t)1 << 
 
 }  // namespace
 
+namespace {
+// The split partials ws[split][tile] (one 256 x 256 fp32 tile each, in MFMA
+// fragment order) of the FP8 weight gradient; TRA / TRB: that operand is the
+// row K-slab of the token-major activation instead of a token-contiguous copy.
+template <bool TRA, bool TRB>
+int wgrad_partials(const void* a, const void* b, int64_t M, int64_t N, int64_t ldt, const float* sa, const float* sb,
+                   float* ws, int splits, hipStream_t st) {
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  const int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                     dim3(256), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, ldt / splits, sa, sb, ws,
+                     tiles_m, tiles_n, splits, 1);
+  return status();
+}
+
+int wgrad_partials_any(bool a_rows, bool b_rows, const void* a, const void* b, int64_t M, int64_t N, int64_t ldt,
+                       const float* sa, const float* sb, float* ws, int splits, hipStream_t st) {
+  if (a_rows && b_rows) return wgrad_partials<true, true>(a, b, M, N, ldt, sa, sb, ws, splits, st);
+  if (a_rows) return wgrad_partials<true, false>(a, b, M, N, ldt, sa, sb, ws, splits, st);
+  if (b_rows) return wgrad_partials<false, true>(a, b, M, N, ldt, sa, sb, ws, splits, st);
+  return wgrad_partials<false, false>(a, b, M, N, ldt, sa, sb, ws, splits, st);
+}
+}  // namespace
+
 extern "C" {
 
 int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64_t D, int64_t I,
                                 const float* scale, const float* wscale, float* amax, void* gu8, void* h8,
                                 void* h8t, int64_t ldt, void* stream) {
   // token-sized buffers may be null when there are no tokens
-  if (!w8 || !scale || !wscale || !amax || (T > 0 && (!x8 || !gu8 || !h8 || !h8t))) return kErrNullPointer;
+  if (!w8 || !scale || !wscale || !amax || (T > 0 && (!x8 || !gu8 || !h8))) return kErrNullPointer;
   // the grid covers ceil(T / 256) token tiles, which write every padding
   // token of the outputs only when ldt is T rounded up to 256
   if (T < 0 || D <= 0 || I <= 0 || D % (2 * kStage) || I % 128 || ldt != (int64_t)cdiv(T, kTile) * kTile)
@@ -1490,7 +1542,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
                                 int64_t I, const float* scale, float* amax, void* dgu8, void* dgu8t,
                                 int64_t ldt, void* stream) {
-  if (!wdt || !scale || !amax || (T > 0 && (!dy || !gu8 || !dgu8 || !dgu8t))) return kErrNullPointer;
+  if (!wdt || !scale || !amax || (T > 0 && (!dy || !gu8 || !dgu8))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || (2 * D) % (2 * kStage) || I % 128 || ldt != (int64_t)cdiv(T, kTile) * kTile)
     return kErrBadShape;  // ldt = T rounded up to 256: the grid writes every padding token
   if (!fits32(kTile, 2 * D) || !fits32(slab_rows(I), 2 * D) || !fits32(ldt, 2 * I)) return kErrBadShape;
@@ -1578,7 +1630,7 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+  hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
@@ -1594,7 +1646,7 @@ inline bool moe_shape(int64_t E, int64_t D, int64_t I, int64_t ldp) {
 int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, int64_t D, int64_t I, const int* plan,
                                     int64_t ldp, const float* scale, const float* q_gu, float* amax, void* gu8,
                                     void* h8, void* h8t, void* stream) {
-  if (!x8 || !w8 || !plan || !scale || !q_gu || !amax || !gu8 || !h8 || !h8t) return kErrNullPointer;
+  if (!x8 || !w8 || !plan || !scale || !q_gu || !amax || !gu8 || !h8) return kErrNullPointer;
   if (!moe_shape(E, D, I, ldp) || !fits32(ldp, D) || !fits32(2 * I, D) || !fits32(ldp, 2 * I)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
   const int tiles_m = (int)(ldp / kTile), tiles_n = (int)(I / 128);
@@ -1623,7 +1675,7 @@ int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D
 int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const void* gu8, int64_t E, int64_t D,
                                     int64_t I, int64_t R, const int* plan, int64_t ldp, const float* scale,
                                     float* amax, void* dgu8, void* dgu8t, void* stream) {
-  if (!wdt || !gu8 || !plan || !scale || !amax || !dgu8 || !dgu8t || (R > 0 && !dout)) return kErrNullPointer;
+  if (!wdt || !gu8 || !plan || !scale || !amax || !dgu8 || (R > 0 && !dout)) return kErrNullPointer;
   if (!moe_shape(E, D, I, ldp) || R < 0) return kErrBadShape;
   if (!fits32(kTile, 2 * D) || !fits32(slab_rows(I), 2 * D) || !fits32(ldp, 2 * I)) return kErrBadShape;
   if (!al16(dout) || !al16(wdt) || !al16(gu8) || !al16(dgu8) || !al16(dgu8t)) return kErrBadAlignment;
@@ -1690,7 +1742,7 @@ int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, in
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
+  hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
@@ -1826,36 +1878,71 @@ int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t 
   return status();
 }
 
+// ---- the weight gradient with row K-slab operands ----
+int64_t sfp8_wgrad_rows_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
+  return sfp8_wgrad_splits(M, N, ldt) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
+}
+
+int sfp8_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b, int fmt_b, int b_rows, int64_t M,
+                         int64_t N, int64_t ldt, const float* sa, const float* sb, float* out, float* ws,
+                         int64_t ws_floats, void* stream) {
+  if (!sa || !sb || !out || (ldt > 0 && (!a || !b || !ws))) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || ldt < 0 || ldt % kTile || N % 4 || !(a_rows || b_rows)) return kErrBadShape;
+  if ((a_rows && M % 64) || (b_rows && N % 64)) return kErrBadShape;
+  if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3) return kErrBadShape;
+  if (!fits32(slab_rows(M), ldt) || !fits32(slab_rows(N), ldt)) return kErrBadShape;
+  if (!al16(a) || !al16(b) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  hipStream_t st = (hipStream_t)stream;
+  if (ldt == 0) {
+    const int64_t n = M * N;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, out, n);
+    return status();
+  }
+  const int splits = (int)sfp8_wgrad_splits(M, N, ldt);
+  if (ws_floats < sfp8_wgrad_rows_workspace_floats(M, N, ldt)) return kErrWorkspaceTooSmall;
+  const int rc = wgrad_partials_any(a_rows, b_rows, a, b, M, N, ldt, sa, sb, ws, splits, st);
+  if (rc) return rc;
+  const int tiles_n = cdiv(N, kTile);
+  const int64_t n4 = (int64_t)cdiv(M, kTile) * tiles_n * kTile * kTile / 4;
+  if (b_rows)
+    hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws, splits,
+                       n4, tiles_n, M, N, sa, sb, out);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+                       splits, n4, tiles_n, M, N, sa, sb, out);
+  return status();
+}
+
 // ---- the weight gradient fused with the optimizer's momentum stage ----
 int64_t sfp8_wgrad_momentum_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
   return sfp8_wgrad_splits(M, N, ldt) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
 }
 
-int sfp8_gemm_wgrad_momentum(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
-                             const float* sa, const float* sb, float* grad, float* v, void* u, float w_v, float w_u,
-                             float* ws, int64_t ws_floats, void* stream) {
-  if (!sa || !sb || !v || !u || (ldt > 0 && (!at || !bt || !ws))) return kErrNullPointer;
+int sfp8_gemm_wgrad_momentum(const void* a, int fmt_a, int a_rows, const void* b, int fmt_b, int b_rows, int64_t M,
+                             int64_t N, int64_t ldt, const float* sa, const float* sb, float* grad, float* v, void* u,
+                             float w_v, float w_u, float* ws, int64_t ws_floats, void* stream) {
+  if (!sa || !sb || !v || !u || (ldt > 0 && (!a || !b || !ws))) return kErrNullPointer;
   if (M <= 0 || N <= 0 || ldt < 0 || ldt % kTile || N % 4) return kErrBadShape;
+  if ((a_rows && M % 64) || (b_rows && N % 64)) return kErrBadShape;
   if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3 || !(w_v > -0.5f && w_v < 0.5f) || !(w_u >= 0.5f)) return kErrBadShape;
   if (!fits32(slab_rows(M), ldt) || !fits32(slab_rows(N), ldt)) return kErrBadShape;
-  if (!al16(at) || !al16(bt) || !al16(grad) || !al16(v) || !al16(ws) || (((uintptr_t)u) & 7u)) return kErrBadAlignment;
+  if (!al16(a) || !al16(b) || !al16(grad) || !al16(v) || !al16(ws) || (((uintptr_t)u) & 7u)) return kErrBadAlignment;
   hipStream_t st = (hipStream_t)stream;
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
   int splits = 0;
   if (ldt > 0) {
     splits = (int)sfp8_wgrad_splits(M, N, ldt);
     if (ws_floats < sfp8_wgrad_momentum_workspace_floats(M, N, ldt)) return kErrWorkspaceTooSmall;
-    int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
-    if (rc) return rc;
-    hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)),
-                       dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
-                       ws, tiles_m, tiles_n, splits, 1);
-    rc = status();
+    const int rc = wgrad_partials_any(a_rows, b_rows, a, b, M, N, ldt, sa, sb, ws, splits, st);
     if (rc) return rc;
   }
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(splitk_momentum_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws, splits, n4,
-                     tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
+  if (b_rows)
+    hipLaunchKernelGGL(splitk_momentum_kernel<true>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws, splits,
+                       n4, tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
+  else
+    hipLaunchKernelGGL(splitk_momentum_kernel<false>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws, splits,
+                       n4, tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
   return status();
 }
 

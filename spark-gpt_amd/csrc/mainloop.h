@@ -29,6 +29,8 @@
 //   reads and the DMA issues.  Stages past the end re-load the last stage into
 //   a buffer nobody reads, and read fragments nobody uses.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace sfp8 {
@@ -44,6 +46,14 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 SFP8_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
   const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (bytes < 0 ? 0 : (int)bytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+// The same descriptor as four dwords (base[47:0], stride 0, num_records,
+// flags), for DMA issued as inline asm.
+SFP8_DEV intx4 make_rsrc4(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffffLL ? 0x7fffffff : (bytes < 0 ? 0 : (int)bytes);
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return intx4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), n, 0x00020000};
 }
 
 // One work-group of 4 waves computes a 256 (A rows) x 64*NB (B rows) tile;
@@ -90,8 +100,39 @@ SFP8_DEV void sched_interleave_valu() {
   }
 }
 
-template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0>
+// TR_A / TR_B: the operand's tile arrives as four 64-row blocks [slab][64
+// K bytes][64 bytes of 64 M (or N) values] -- a row K-slab of the
+// transposed matrix, e.g. the token-major activations a weight gradient
+// reduces over -- and each fragment is assembled from four transposing
+// reads (ds_read_b64_tr_b8: 8 K bytes of one column per lane each) in the
+// same (lane half, byte) -> K order as the plain reads, so the MFMAs see the
+// same values.  Only for fp8 operands and a plain (unpaired) B.  With TR_B
+// the B tile is not permuted: accumulator v of block nb in lane half g is
+// column 32 nb + 8 (v / 4) + 4 g + v % 4 of the wave's 128.  These
+// instantiations issue their DMA as inline asm: the compiler treats a
+// transposing read as possibly aliasing any LDS DMA it knows to be in flight
+// and would wait for all of it first; the stage waits and barriers already
+// order every read after its stage's DMA.
+template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0,
+          bool TR_A = false, bool TR_B = false>
 struct MainLoop {
+  static_assert(!(TR_A || TR_B) || (!BF16 && !PAIRED && NB == 4), "transposing reads: fp8, plain, 256 x 256");
+  static constexpr bool kTr = TR_A || TR_B;
+  using Rsrc = typename std::conditional<kTr, intx4, __amdgpu_buffer_rsrc_t>::type;
+  static SFP8_DEV Rsrc rsrc(const void* base, int64_t bytes) {
+    if constexpr (kTr) return make_rsrc4(base, bytes);
+    else return make_rsrc(base, bytes);
+  }
+  // One 16-byte-per-lane DMA into LDS at dst (wave-uniform)
+  static SFP8_DEV void dma16(uint8_t* dst, Rsrc r, uint32_t voff, int soff) {
+    if constexpr (kTr) {
+      const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t)dst);
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :: "s"(m0v), "v"(voff), "s"(r), "s"(soff) : "memory");
+    } else {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff, soff, 0, 0);
+    }
+  }
   static_assert(NB == 2 || NB == 4, "2 or 4 B blocks per wave");
   static_assert(STAGES >= 3, "at least three LDS stages");
   static constexpr int kTileN = 64 * NB;                  // B rows per tile
@@ -103,20 +144,20 @@ struct MainLoop {
 
   // DMA instruction j of this wave's share of one stage: J < 4 are A blocks,
   // the rest B blocks (16 rows = 1 KiB each).
-  static SFP8_DEV void load_one(int j, uint8_t* lds, int buf, __amdgpu_buffer_rsrc_t ra,
-                                __amdgpu_buffer_rsrc_t rb, const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB],
+  static SFP8_DEV void load_one(int j, uint8_t* lds, int buf, Rsrc ra,
+                                Rsrc rb, const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB],
                                 int soff_a, int soff_b, int wave) {
     if (j < 4) {
       uint8_t* dst = lds + buf * kStageA + (64 * wave + 16 * j) * kStage;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, voff_a[j], soff_a, 0, 0);
+      dma16(dst, ra, voff_a[j], soff_a);
     } else {
       uint8_t* dst = lds + kLdsB + buf * kStageB + (16 * NB * wave + 16 * (j - 4)) * kStage;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, voff_b[j - 4], soff_b, 0, 0);
+      dma16(dst, rb, voff_b[j - 4], soff_b);
     }
   }
 
   // Issue this wave's DMA instructions of one stage.
-  static SFP8_DEV void load_stage(uint8_t* lds, int buf, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+  static SFP8_DEV void load_stage(uint8_t* lds, int buf, Rsrc ra, Rsrc rb,
                                   const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB], int soff_a, int soff_b,
                                   int wave) {
 #pragma unroll
@@ -132,23 +173,44 @@ struct MainLoop {
 
   // Fragment I of one stage (I < 4: A block I, else B block I - 4): two
   // 16-byte LDS reads.
+  // Four transposing reads of one block of a TR operand tile: block k (32
+  // columns) lives in 64-column slab k / 2; off[2 q + (k & 1)] addresses
+  // read q (K bytes 8 q .. 8 q + 7 of the lane half's 32).
+  template <int K>
+  static SFP8_DEV intx8 read_tr_block(const uint8_t* p, const uint32_t (&off)[8]) {
+    const uint8_t* q = p + (K >> 1) * (64 * kStage);
+    const intx2 r0 = lds_read_tr8(q + off[0 + (K & 1)]);
+    const intx2 r1 = lds_read_tr8(q + off[2 + (K & 1)]);
+    const intx2 r2 = lds_read_tr8(q + off[4 + (K & 1)]);
+    const intx2 r3 = lds_read_tr8(q + off[6 + (K & 1)]);
+    return intx8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+  }
+
   template <int I>
-  static SFP8_DEV void read_frag(const uint8_t* lds, int buf, const uint32_t (&aoff)[2], const uint32_t (&boff)[2],
+  static SFP8_DEV void read_frag(const uint8_t* lds, int buf, const uint32_t (&aoff)[8], const uint32_t (&boff)[8],
                                  Frag& f) {
     if constexpr (I < 4) {
-      const uint8_t* p = lds + buf * kStageA + I * 32 * kStage;
-      const intx4 lo = *reinterpret_cast<const intx4*>(p + aoff[0]);
-      const intx4 hi = *reinterpret_cast<const intx4*>(p + aoff[1]);
-      f.a[I] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      if constexpr (TR_A) {
+        f.a[I] = read_tr_block<I>(lds + buf * kStageA, aoff);
+      } else {
+        const uint8_t* p = lds + buf * kStageA + I * 32 * kStage;
+        const intx4 lo = *reinterpret_cast<const intx4*>(p + aoff[0]);
+        const intx4 hi = *reinterpret_cast<const intx4*>(p + aoff[1]);
+        f.a[I] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
     } else {
-      const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB>::off(I - 4) * kStage;
-      const intx4 lo = *reinterpret_cast<const intx4*>(p + boff[0]);
-      const intx4 hi = *reinterpret_cast<const intx4*>(p + boff[1]);
-      f.b[I - 4] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      if constexpr (TR_B) {
+        f.b[I - 4] = read_tr_block<I - 4>(lds + kLdsB + buf * kStageB, boff);
+      } else {
+        const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB>::off(I - 4) * kStage;
+        const intx4 lo = *reinterpret_cast<const intx4*>(p + boff[0]);
+        const intx4 hi = *reinterpret_cast<const intx4*>(p + boff[1]);
+        f.b[I - 4] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
     }
   }
 
-  static SFP8_DEV void read_frags(const uint8_t* lds, int buf, const uint32_t (&aoff)[2], const uint32_t (&boff)[2],
+  static SFP8_DEV void read_frags(const uint8_t* lds, int buf, const uint32_t (&aoff)[8], const uint32_t (&boff)[8],
                                   Frag& f) {
     read_frag<0>(lds, buf, aoff, boff, f);
     read_frag<1>(lds, buf, aoff, boff, f);
@@ -197,7 +259,7 @@ struct MainLoop {
   // one group the scheduler may not reorder with its neighbours.
   template <int M, int R0, int R1>
   static SFP8_DEV void mfma_then_reads(const uint8_t* lds, const Frag& cur, Frag& nxt, Acc& acc, int rd_buf,
-                                       const uint32_t (&aoff)[2], const uint32_t (&boff)[2]) {
+                                       const uint32_t (&aoff)[8], const uint32_t (&boff)[8]) {
     mfma_range<M, M + 1>(cur, acc);
     if constexpr (R0 < R1) read_frag<R0>(lds, rd_buf, aoff, boff, nxt);
     if constexpr (R0 + 1 < R1) read_frag<R0 + 1>(lds, rd_buf, aoff, boff, nxt);
@@ -207,7 +269,7 @@ struct MainLoop {
   // MFMA M of the stage, then DMA instructions [J0, J1) of stage `ld`.
   template <int M, int J0, int J1>
   static SFP8_DEV void mfma_then_dma(uint8_t* lds, const Frag& cur, Acc& acc, int dma_buf,
-                                     __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                     Rsrc ra, Rsrc rb,
                                      const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB], int soff_a,
                                      int soff_b, int wave) {
     mfma_range<M, M + 1>(cur, acc);
@@ -233,9 +295,9 @@ struct MainLoop {
   static constexpr int kSchedPre = 2;
   static_assert(kMfma >= kSchedPre + (4 + NB) / 2 + (4 + NB) / 2, "stage too short for the schedule");
   static SFP8_DEV void stage(uint8_t* lds, const Frag& cur, Frag& nxt, Acc& acc, int dma_buf, int ld, int rd_buf,
-                             __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, const uint32_t (&voff_a)[4],
-                             const uint32_t (&voff_b)[NB], int a_sstride, int b_sstride, const uint32_t (&aoff)[2],
-                             const uint32_t (&boff)[2], int wave) {
+                             Rsrc ra, Rsrc rb, const uint32_t (&voff_a)[4],
+                             const uint32_t (&voff_b)[NB], int a_sstride, int b_sstride, const uint32_t (&aoff)[8],
+                             const uint32_t (&boff)[8], int wave) {
     constexpr int P = kSchedPre;
     mfma_range<0, P>(cur, acc);
     __builtin_amdgcn_sched_barrier(0);
@@ -307,25 +369,50 @@ struct MainLoop {
                            const uint8_t* b_base, int64_t b_bytes, BRow b_rowoff, int b_sstride, int nk, Acc& acc) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a_base, a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(b_base, b_bytes);
+    const Rsrc ra = rsrc(a_base, a_bytes);
+    const Rsrc rb = rsrc(b_base, b_bytes);
     // DMA lane offsets: A instruction j covers tile rows 64*wave + 16*j + lane/4,
     // B instruction j rows 16*NB*wave + 16*j + lane/4; physical chunk lane%4
     // <- logical chunk (lane%4) ^ ((row >> 2) & 3)
     uint32_t voff_a[4], voff_b[NB];
     const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+    // TR operands: chunk c of row r at c ^ (2 * ((r >> 2) & 1)), so that the
+    // 8 rows x 2 chunks a half-wave's transposing read touches fill the 64
+    // banks (rows r and r + 4 share banks under the plain swizzle)
+    const uint32_t chunk_tr = (uint32_t)(((lane & 3) ^ (((lane >> 4) & 1) << 1)) << 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + chunk;
+    for (int j = 0; j < 4; ++j)
+      voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + (TR_A ? chunk_tr : chunk);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) voff_b[j] = (uint32_t)b_rowoff(16 * NB * wave + 16 * j + (lane >> 2)) + chunk;
+    for (int j = 0; j < NB; ++j)
+      voff_b[j] = (uint32_t)b_rowoff(16 * NB * wave + 16 * j + (lane >> 2)) + (TR_B ? chunk_tr : chunk);
     // fragment read offsets (lane half g reads logical chunks 2g, 2g+1)
     const int fr = lane & 31, g = lane >> 5;
     const int sw = (fr >> 2) & 3;
-    uint32_t aoff[2], boff[2];
+    uint32_t aoff[8], boff[8];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
       boff[h] = (uint32_t)(kLdsB + (BLayout<PAIRED, NB>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+    }
+    if constexpr (kTr) {
+      // Transposing reads: 16-lane group G = lane / 16 (lane half g = G / 2,
+      // column half G % 2 of the block's 32 columns); within it lane 2b + h
+      // addresses tile row (token) 32 g + 8 q + b of the block's slab and the
+      // 8 bytes 8 h.. of logical chunk 2 (k & 1) + G % 2 (at its TR swizzle
+      // position); the read returns to lane i rows 32 g + 8 q .. + 7 of column
+      // 16 (G % 2) + i.  Slab of the wave's rows: 2 wm (A) or 2 wn (B).
+      const int G = lane >> 4, li = lane & 15, bq = li >> 1, hb = li & 1, gh = G >> 1, gc = G & 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int k1 = 0; k1 < 2; ++k1) {
+          const int rr = 32 * gh + 8 * q + bq;  // row within the 64-row slab
+          const uint32_t cb = (uint32_t)((((2 * k1 + gc) ^ (((rr >> 2) & 1) << 1)) << 4) + 8 * hb);
+          if constexpr (TR_A) aoff[2 * q + k1] = (uint32_t)((128 * wm + rr) * kStage) + cb;
+          if constexpr (TR_B) boff[2 * q + k1] = (uint32_t)((128 * wn + rr) * kStage) + cb;
+        }
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -336,8 +423,8 @@ struct MainLoop {
     // Stages past the last keep their DMA instructions (the waits count
     // them) but read through descriptors of zero records: every lane is out
     // of range, so no memory is read and the unused ring slot gets zeros.
-    const __amdgpu_buffer_rsrc_t ra0 = make_rsrc(a_base, 0);
-    const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(b_base, 0);
+    const Rsrc ra0 = rsrc(a_base, 0);
+    const Rsrc rb0 = rsrc(b_base, 0);
     // prologue: stages 0 .. STAGES-2 in flight; stage 0 landed; its fragments read
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) {

@@ -160,10 +160,11 @@ def _kslab(name: str, t: torch.Tensor, dtype, R: int, L: int) -> None:
     _need(tuple(t.shape) == (L // n, slab_rows(R), n), f"{name} must be a K-slab of [{R}, {L}]")
 
 
-def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T: int, I: int):
+def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T: int, I: int, *, copy: bool = True):
     """(gu8 K-slab of [T, 2I], h8 K-slab of [T, I], h8t K-slab of [I, ldt]);
     x8 is the K-slab of [T, D], w8 that of [2I, D]; amax[1], amax[2]
-    max-accumulated."""
+    max-accumulated.  copy=False skips the token-contiguous h8t (None): the
+    weight gradient then reads h8 itself (wgrad_rows)."""
     _need(x8.dim() == 3, "x8 must be a K-slab")
     D = x8.shape[0] * SLAB
     ldt = ldt_of(T)
@@ -173,10 +174,10 @@ def gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T: int, I: int):
     dev = x8.device
     gu8 = kslab_empty(ldt, 2 * I, E4M3, dev)
     h8 = kslab_empty(ldt, I, E4M3, dev)
-    h8t = slab_empty(I, T, E4M3, dev)
+    h8t = slab_empty(I, T, E4M3, dev) if copy else None
     _lib.call("sfp8_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), T, D, I, scale.data_ptr(),
-              wscale.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr(), ldt,
-              _lib.stream_of(x8))
+              wscale.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr() if copy else 0,
+              ldt, _lib.stream_of(x8))
     return gu8, h8, h8t
 
 
@@ -197,10 +198,12 @@ def down_fwd(h8, wd8, res, scale, wscale):
     return y
 
 
-def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
+def down_dgrad_swiglu(dy, wdt, gu8, scale, amax, *, copy: bool = True):
     """(dgu8 K-slab of [T, 2I] e5m2, dgu8t K-slab of [2I, ldt] e5m2); wdt is
     the bf16 K-slab of W_down^T [I, D], gu8 the e4m3 K-slab of [T, 2I] the
-    forward wrote; amax[3] max-accumulated."""
+    forward wrote; amax[3] max-accumulated.  copy=False skips the
+    token-contiguous dgu8t (None): the weight gradient then reads dgu8 itself
+    (wgrad_rows)."""
     _cuda_contig("dy", dy, torch.bfloat16, 2)
     T, D = dy.shape
     _need(gu8.dim() == 3, "gu8 must be a K-slab")
@@ -210,9 +213,10 @@ def down_dgrad_swiglu(dy, wdt, gu8, scale, amax):
     _kslab("wdt", wdt, torch.bfloat16, I, D)
     _need(D % 64 == 0 and I % 128 == 0, "D must be a multiple of 64 and I of 128")
     dgu8 = kslab_empty(ldt, 2 * I, E5M2, dy.device)
-    dgu8t = slab_empty(2 * I, T, E5M2, dy.device)
+    dgu8t = slab_empty(2 * I, T, E5M2, dy.device) if copy else None
     _lib.call("sfp8_gemm_down_dgrad_swiglu", dy.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), T, D, I,
-              scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr(), ldt, _lib.stream_of(dy))
+              scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr() if copy else 0, ldt,
+              _lib.stream_of(dy))
     return dgu8, dgu8t
 
 
@@ -250,6 +254,27 @@ def wgrad(at, bt, M: int, N: int, sa, sb):
 
 
 # ------------------------------------------------------------------ norm backward
+def wgrad_rows(a8, b8, M: int, N: int, sa, sb, *, a_rows: bool = True, b_rows: bool = True):
+    """out [M, N] fp32 = sum over tokens of a8[t, m] b8[t, n] / (sa * sb): a8
+    (e5m2) and b8 (e4m3) each either the row K-slab of the token-major
+    activation ([rows/64, ldt, 64]: read through transposing LDS reads) or,
+    with a_rows / b_rows False, the token-contiguous copy ([ldt/64,
+    slab_rows, 64], as for wgrad)."""
+    _cuda_contig("a8", a8, E5M2, 3)
+    _cuda_contig("b8", b8, E4M3, 3)
+    _need(a_rows or b_rows, "at least one row K-slab operand (else use wgrad)")
+    ldt = a8.shape[1] if a_rows else a8.shape[0] * SLAB
+    _need((b8.shape[1] if b_rows else b8.shape[0] * SLAB) == ldt, "a8, b8 must cover the same tokens")
+    _need(not a_rows or a8.shape[0] * SLAB == M, "a8 must be the row K-slab of [ldt, M]")
+    _need(not b_rows or b8.shape[0] * SLAB == N, "b8 must be the row K-slab of [ldt, N]")
+    out = torch.empty(M, N, dtype=torch.float32, device=a8.device)
+    nws = _lib.query("sfp8_wgrad_rows_workspace_floats", M, N, ldt)
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=a8.device)
+    _lib.call("sfp8_gemm_wgrad_rows", a8.data_ptr(), FMT_E5M2, int(a_rows), b8.data_ptr(), FMT_E4M3, int(b_rows), M, N,
+              ldt, sa.data_ptr(), sb.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(a8))
+    return out
+
+
 def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
     """(dh [T, D] bf16, dnw [D] fp32, dy8t K-slab of D rows e5m2); amax[4] = max|dy|."""
     for n, t in (("h", h), ("dxn", dxn), ("dy", dy)):
@@ -538,16 +563,19 @@ def momentum_stage(g: torch.Tensor, v: torch.Tensor, u: torch.Tensor, momentum: 
               _lib.stream_of(g))
 
 
-def wgrad_momentum(at, bt, M: int, N: int, sa, sb, v: torch.Tensor, u: torch.Tensor, momentum: float, grad=None):
-    """wgrad(at, bt, M, N, sa, sb) handed straight to the momentum stage:
-    v <- lerp(v, dW, 1 - momentum), u <- bf16(lerp(dW, v, momentum)); dW is
-    also written to `grad` when given."""
-    _cuda_contig("at", at, E5M2, 3)
-    _cuda_contig("bt", bt, E4M3, 3)
+def wgrad_momentum(a8, b8, M: int, N: int, sa, sb, v: torch.Tensor, u: torch.Tensor, momentum: float, grad=None, *,
+                   a_rows: bool = False, b_rows: bool = False):
+    """wgrad (a_rows = b_rows = False) or wgrad_rows of the same operands
+    handed straight to the momentum stage: v <- lerp(v, dW, 1 - momentum),
+    u <- bf16(lerp(dW, v, momentum)); dW is also written to `grad` when
+    given."""
+    _cuda_contig("a8", a8, E5M2, 3)
+    _cuda_contig("b8", b8, E4M3, 3)
     _need(v.is_contiguous() and u.is_contiguous() and v.numel() == u.numel() == M * N, "v, u must be [M, N]")
-    ldt = at.shape[0] * SLAB
+    ldt = a8.shape[1] if a_rows else a8.shape[0] * SLAB
+    _need((b8.shape[1] if b_rows else b8.shape[0] * SLAB) == ldt, "a8, b8 must cover the same tokens")
     nws = _lib.query("sfp8_wgrad_momentum_workspace_floats", M, N, ldt)
-    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=at.device)
-    _lib.call("sfp8_gemm_wgrad_momentum", at.data_ptr(), FMT_E5M2, bt.data_ptr(), FMT_E4M3, M, N, ldt, sa.data_ptr(),
-              sb.data_ptr(), _lib.ptr(grad), v.data_ptr(), u.data_ptr(), 1.0 - momentum, momentum, ws.data_ptr(),
-              ws.numel(), _lib.stream_of(at))
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=a8.device)
+    _lib.call("sfp8_gemm_wgrad_momentum", a8.data_ptr(), FMT_E5M2, int(a_rows), b8.data_ptr(), FMT_E4M3, int(b_rows),
+              M, N, ldt, sa.data_ptr(), sb.data_ptr(), _lib.ptr(grad), v.data_ptr(), u.data_ptr(), 1.0 - momentum,
+              momentum, ws.data_ptr(), ws.numel(), _lib.stream_of(a8))

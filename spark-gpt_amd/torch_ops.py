@@ -10,7 +10,7 @@ atomic max (train.py:1015-1016, 1094).
 
 * ``sparkfp8::block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)`` returns
   y and the activations the backward needs (train.py:1200-1226).
-* ``sparkfp8::block_bwd(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t,
+* ``sparkfp8::block_bwd(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8,
   scale, amax)`` returns (dh, d_norm_w, dW_gate_up, dW_down)
   (train.py:1228-1252).
 * ``sparkfp8::update_scales(scale, amax)`` is the delayed-scale roll
@@ -128,17 +128,18 @@ def clear_weight_cache() -> None:
 @torch.library.custom_op("sparkfp8::block_fwd", mutates_args={"amax"})
 def block_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Tensor, amax: Tensor,
               eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """y, then for the backward: x8t, rstd, gu8 (K-slab of [T, 2I]), h8t.
-    The quantized weights stay in the weight cache: they are never an output
+    """y, then for the backward: x8t, rstd, gu8 (K-slab of [T, 2I]) and h8
+    (K-slab of [T, I]; the down weight gradient reads it through transposing
+    LDS reads, so no token-contiguous copy is written).  The quantized weights stay in the weight cache: they are never an output
     (a compiled graph may recycle the memory of the tensors it saves for
     backward), and the backward looks them up from the same masters."""
     I = w_down.shape[1]
     h = h.contiguous()
     x8, x8t, rstd = ops.norm_quant(h, _master(norm_w), scale, amax, eps)
     w8, _w8t, wd8, _wdt, wscale = cached_weights(w_gu, w_down)
-    gu8, h8, h8t = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, h.shape[0], I)
+    gu8, h8, _ = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, h.shape[0], I, copy=False)
     y = ops.down_fwd(h8, wd8, h, scale, wscale)
-    return y, x8t, rstd, gu8, h8t
+    return y, x8t, rstd, gu8, h8
 
 
 @block_fwd.register_fake
@@ -151,12 +152,12 @@ def _block_fwd_fake(h, norm_w, w_gu, w_down, scale, amax, eps):
             h.new_empty((ldt // 64, sr(D), 64), dtype=E4M3),
             h.new_empty((T,), dtype=torch.float32),
             h.new_empty((2 * I // 64, ldt, 64), dtype=E4M3),
-            h.new_empty((ldt // 64, sr(I), 64), dtype=E4M3))
+            h.new_empty((I // 64, ldt, 64), dtype=E4M3))
 
 
 @torch.library.custom_op("sparkfp8::block_bwd", mutates_args={"amax"})
 def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, x8t: Tensor, rstd: Tensor,
-              gu8: Tensor, h8t: Tensor, scale: Tensor, amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+              gu8: Tensor, h8: Tensor, scale: Tensor, amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """(dh bf16, d_norm_w fp32, dW_gate_up fp32, dW_down fp32).  W8^T, the
     bf16 W_down^T and the weight scales are the forward's (the cache entry of
     the same, unchanged masters; train.py:1224-1225 saves them instead)."""
@@ -167,18 +168,19 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tenso
     T, D = h.shape
     I = gu8.shape[0] * ops.SLAB // 2
     _w8, w8t, _wd8, wdt, wscale = cached_weights(w_gu, w_down)
-    dgu8, dgu8t = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax)
+    dgu8, _ = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax, copy=False)
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
-    del dgu8
     dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, _master(norm_w), scale, amax)
     del dxn
-    dwd = ops.wgrad(dy8t, h8t, D, I, scale[4:5], scale[2:3])
-    dwgu = ops.wgrad(dgu8t, x8t, 2 * I, D, scale[3:4], scale[0:1])
+    # the activations' weight-gradient operands are their row K-slabs (dgu8,
+    # h8); x8t and dy8t are the norm kernels' token-contiguous copies
+    dwd = ops.wgrad_rows(dy8t, h8, D, I, scale[4:5], scale[2:3], a_rows=False)
+    dwgu = ops.wgrad_rows(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], b_rows=False)
     return dh, dnw, dwgu, dwd
 
 
 @block_bwd.register_fake
-def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8t, scale, amax):
+def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8, scale, amax):
     T, D = h.shape
     I = gu8.shape[0] * ops.SLAB // 2
     return (h.new_empty((T, D), dtype=torch.bfloat16),

@@ -74,6 +74,13 @@ def test_swiglu_fwd_integer_operands(dev, T, D, I):
     assert torch.all(ht[:, T:] == 0)
     assert amax[1].item() == ra1.item()
     torch.testing.assert_close(amax[2].cpu(), ra2, rtol=1e-5, atol=0)
+    # without the token-contiguous copy: the same rows and amax
+    amax2 = torch.zeros(5, device=dev)
+    gu8b, h8b, none = sg.ops.gateup_swiglu_fwd(slab(x8, dev), slab(w8, dev), s.to(dev), ws.to(dev), amax2, T, I,
+                                               copy=False)
+    assert none is None
+    assert torch.equal(u8(gu8b), u8(gu8s)) and torch.equal(u8(h8b), u8(h8s))
+    assert torch.equal(amax2, amax)
 
 
 @pytest.mark.parametrize("T,D,I", [(300, 256, 256), (300, 1024, 256)])
@@ -165,6 +172,13 @@ def test_down_dgrad_swiglu_integer_operands(dev, T, D, I):
     assert torch.equal(dt[:, :T], u8(dgu8).t())
     assert torch.all(dt[:, T:] == 0)
     torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-5, atol=0)
+    # without the token-contiguous copy: the same rows and amax
+    amax2 = torch.zeros(5, device=dev)
+    dgu8b, none = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), slab(gu8, dev), s.to(dev), amax2,
+                                           copy=False)
+    assert none is None
+    assert torch.equal(u8(dgu8b), u8(dgu8s))
+    assert torch.equal(amax2, amax)
 
 
 @pytest.mark.parametrize("T,D,I", [(512, 256, 256), (8192, 1024, 3072)])
@@ -308,3 +322,25 @@ def test_wgrad_ragged_columns_stay_in_bounds(dev, M, N):
     ref = a.float().t() @ b.float()
     assert torch.equal(buf[: M * N].view(M, N).cpu(), ref)
     assert bool((buf[M * N:] == 12345.0).all())
+
+
+@pytest.mark.parametrize("M,N,T", [(6144, 1024, 4096), (1024, 3072, 16384), (320, 192, 1000), (256, 256, 65536)])
+def test_wgrad_rows_equals_token_contiguous(dev, M, N, T):
+    """The weight gradient read from the row K-slabs through transposing LDS
+    reads gives the bytes of the one read from the token-contiguous copies
+    (same values in the same MFMA K positions, same split sums): one split
+    and several, ragged tiles, and the same operands in both layouts."""
+    ops = sg.ops
+    g = torch.Generator(device=dev).manual_seed(M + N + T)
+    a = (torch.randn(T, M, device=dev, generator=g) * 8).to(ops.E5M2)
+    b = (torch.randn(T, N, device=dev, generator=g) * 8).to(ops.E4M3)
+    ldt = ops.ldt_of(T)
+    pad = lambda x: torch.cat([x, torch.zeros(ldt - T, x.shape[1], dtype=x.dtype, device=dev)])
+    a_rows, b_rows = ops.to_slab(pad(a)), ops.to_slab(pad(b))      # [M/64, ldt, 64]
+    a_t, b_t = ops.to_slab(pad(a).t().contiguous()), ops.to_slab(pad(b).t().contiguous())  # [ldt/64, M, 64]
+    sa = torch.tensor([2.0 ** 4], device=dev)
+    sb = torch.tensor([2.0 ** -2], device=dev)
+    ref = ops.wgrad(a_t, b_t, M, N, sa, sb)
+    assert torch.equal(ops.wgrad_rows(a_rows, b_rows, M, N, sa, sb), ref)
+    assert torch.equal(ops.wgrad_rows(a_rows, b_t, M, N, sa, sb, b_rows=False), ref)
+    assert torch.equal(ops.wgrad_rows(a_t, b_rows, M, N, sa, sb, a_rows=False), ref)

@@ -80,6 +80,16 @@ def test_wgrad_momentum_matches_wgrad_then_stage(dev, M, N, T):
     v2, u2 = v0.clone(), torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     ops.wgrad_momentum(at, bt, M, N, sa, sb, v2, u2, 0.95)
     assert torch.equal(v2, rv) and torch.equal(u2, ru)
+    # the same operands as row K-slabs ([rows/64, ldt, 64], read through
+    # transposing LDS reads), in each layout pair the backward can hand over
+    a_rows = ops.to_slab(ops.unslab(at, M).t().contiguous())
+    b_rows = ops.to_slab(ops.unslab(bt, N).t().contiguous())
+    for a8, b8, ar, br in ((a_rows, bt, True, False), (at, b_rows, False, True), (a_rows, b_rows, True, True)):
+        v3, u3 = v0.clone(), torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        grad3 = torch.empty(M, N, device=dev)
+        ops.wgrad_momentum(a8, b8, M, N, sa, sb, v3, u3, 0.95, grad=grad3, a_rows=ar, b_rows=br)
+        assert torch.equal(grad3, dw), (ar, br)
+        assert torch.equal(v3, rv) and torch.equal(u3, ru), (ar, br)
 
 
 def test_wgrad_momentum_zero_tokens(dev):

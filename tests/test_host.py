@@ -220,7 +220,7 @@ def test_custom_op_fake_shapes_match_allocations():
             ops.slab_empty(D, T, ops.E4M3, meta),
             torch.empty(T, device=meta),
             ops.kslab_empty(ops.ldt_of(T), 2 * I, ops.E4M3, meta),
-            ops.slab_empty(I, T, ops.E4M3, meta)]
+            ops.kslab_empty(ops.ldt_of(T), I, ops.E4M3, meta)]
     assert len(out) == len(want)
     for got, w in zip(out, want):
         assert got.shape == w.shape and got.dtype == w.dtype
