@@ -590,7 +590,7 @@ def main() -> None:
 
     # FLOP or algorithmic bytes per launch of each kernel
     work = {
-        "norm_quant": (None, T * (4.0 * D + 4)),
+        "norm_quant": (None, T * (3.0 * D + 4)),
         "weight_quant_gu": (None, 10.0 * 2 * I * D),
         "weight_quant_down": (None, 11.0 * D * I),
         "gateup_swiglu_fwd": (4.0 * T * D * I, None),
@@ -607,7 +607,7 @@ def main() -> None:
     if args.probe or not args.trace:
         # every kernel of the step alone (HIP events on the current stream)
         nwd = norm.weight.detach()
-        x8, x8t, rstd = ops.norm_quant(h, nwd, scale, amax, 1e-6)
+        x8, _, rstd = ops.norm_quant(h, nwd, scale, amax, 1e-6, copy=False)
         wscale = torch.empty(2, device=dev)
         w8, w8t, _ = ops.weight_quant(mlp.gate_up_proj.weight.detach(), wscale[0:1], w8=True, w8t=True)
         wd8, _, wdt = ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True, bf16t=True)
@@ -626,7 +626,7 @@ def main() -> None:
             "dy": at_max(dy8t, 0x7B),
             "elements": {"x": T * D, "gu": 2 * T * I, "h": T * I, "d_gu": 2 * T * I, "dy": T * D}}
         kern = {
-            "norm_quant": lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6),
+            "norm_quant": lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6, copy=False),
             "weight_quant_gu": lambda: ops.weight_quant(mlp.gate_up_proj.weight.detach(), wscale[0:1], w8=True,
                                                         w8t=True),
             "weight_quant_down": lambda: ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True,
@@ -637,7 +637,7 @@ def main() -> None:
             "gateup_dgrad": lambda: ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D),
             "norm_bwd": lambda: ops.norm_bwd(h, rstd, dxn, dy, nwd, scale, amax),
             "wgrad_down": lambda: ops.wgrad_rows(dy8t, h8, D, I, scale[4:5], scale[2:3], a_rows=False),
-            "wgrad_gateup": lambda: ops.wgrad_rows(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], b_rows=False),
+            "wgrad_gateup": lambda: ops.wgrad_rows(dgu8, x8, 2 * I, D, scale[3:4], scale[0:1]),
         }
         if args.probe:
             # calibration copy of known size, then one launch of each kernel
@@ -667,12 +667,12 @@ def main() -> None:
         u_mom = torch.empty(2 * I, D, dtype=torch.bfloat16, device=dev)
 
         def separate():
-            dw = ops.wgrad_rows(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], b_rows=False)
+            dw = ops.wgrad_rows(dgu8, x8, 2 * I, D, scale[3:4], scale[0:1])
             ops.momentum_stage(dw.view(-1), v_mom.view(-1), u_mom.view(-1), 0.95)
 
         sep_ms = timed_launches(separate, 10, stream)
-        fused_ms = timed_launches(lambda: ops.wgrad_momentum(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], v_mom,
-                                                             u_mom, 0.95, a_rows=True), 10, stream)
+        fused_ms = timed_launches(lambda: ops.wgrad_momentum(dgu8, x8, 2 * I, D, scale[3:4], scale[0:1], v_mom,
+                                                             u_mom, 0.95, a_rows=True, b_rows=True), 10, stream)
         g_mom = torch.randn(2 * I * D, device=dev)
         stage_ms = timed_launches(lambda: ops.momentum_stage(g_mom, v_mom.view(-1), u_mom.view(-1), 0.95), 10,
                                   stream)
@@ -681,7 +681,7 @@ def main() -> None:
             "saved_ms": round(sep_ms - fused_ms, 4),
             "momentum_stage_alone": rates({"m": (None, 14.0 * 2 * I * D)}, "m", stage_ms)}
         del v_mom, u_mom, g_mom
-        del x8, x8t, rstd, w8, w8t, wd8, wdt, gu8, h8, dgu8, dxn, dh, dnw, dy8t
+        del x8, rstd, w8, w8t, wd8, wdt, gu8, h8, dgu8, dxn, dh, dnw, dy8t
 
     # ---- timed steps (clean: nothing but the step's own launches) ----
     for _ in range(args.warmup):

@@ -28,9 +28,12 @@
  *    channels).  Padding rows r >= R hold zeros; producers write them.
  *    sfp8_slab_bytes(R, L) gives the buffer size.  Token-major activations
  *    (x8, h8, dgu8: R = T) have rpad = ldt = T rounded up to 256.
- *    The token-contiguous copies for the weight gradients (x8t, h8t, dgu8t,
- *    dy8t) are K-slabs of the transposed activation over ldt tokens
- *    (R = features, L = ldt); producers write zeros for tokens T..ldt-1.
+ *    The weight gradients read these token-major K-slabs (x8, h8, dgu8 and
+ *    the dy8 of sfp8_norm_bwd) directly (sfp8_gemm_wgrad_rows).  The
+ *    optional token-contiguous copies (x8t, h8t, dgu8t, dy8t: NULL skips
+ *    them) are K-slabs of the transposed activation over ldt tokens
+ *    (R = features, L = ldt), for sfp8_gemm_wgrad and the grouped MoE
+ *    gradient; producers write zeros for tokens T..ldt-1 in every layout.
  *    The standalone quantizer writes a plain row-major x8 and the same K-slab
  *    x8t.
  *  - `stream` is a hipStream_t; every call is asynchronous on it, never
@@ -77,8 +80,8 @@ int sfp8_quant_e4m3_rowcol(const void* x, int64_t rows, int64_t cols, const floa
 
 /* Norm-fused quantizer, replaces _fp8_norm_quant_kernel (train.py:955-972,
  * launched at train.py:1208-1210).  h [T, D] bf16, norm_w [D] fp32 ->
- * x8 (K-slab of [T, D]: [D/64][ldt][64]) e4m3, x8t (K-slab of [D, ldt])
- * e4m3, rstd [T] fp32; amax[0] max-accumulated.
+ * x8 (K-slab of [T, D]: [D/64][ldt][64]) e4m3, x8t (K-slab of [D, ldt];
+ * optional) e4m3, rstd [T] fp32; amax[0] max-accumulated.
  * D in {128, 256, 512, 1024, 2048, 4096}, or a multiple of 4096 from 8192
  * on (a two-pass row-chunked form); ldt = T rounded up to 256. */
 int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, float eps,
@@ -110,8 +113,8 @@ int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
  * (train.py:975-1016, launched at train.py:1216-1218).
  * x8 (K-slab of [T, D]) e4m3, w8 (K-slab of [2I, D], gate rows first) e4m3
  * -> gu8 (K-slab of [T, 2I], gate columns first, rpad = ldt) e4m3, h8
- * (K-slab of [T, I]) e4m3, h8t (K-slab of [I, ldt]: token-contiguous copy
- * of h8 for the down wgrad) e4m3; rows T..ldt of gu8 and h8 are zeros;
+ * (K-slab of [T, I]) e4m3, h8t (K-slab of [I, ldt]: optional
+ * token-contiguous copy of h8) e4m3; rows T..ldt of gu8 and h8 are zeros;
  * amax[1], amax[2] max-accumulated.  D % 128 == 0, I % 128 == 0, and
  * ldt == T rounded up to 256 (the outputs' padding tokens are written then;
  * any other ldt is SFP8_ERR_BAD_SHAPE). */
@@ -130,8 +133,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
  * (train.py:1049-1094, launched at train.py:1236-1238).  dy [T, D] bf16
  * row-major, wdt (K-slab of w_down^T [I, D], bf16), gu8 (K-slab of [T, 2I],
  * rpad = ldt, as the forward wrote it) e4m3 -> dgu8 (K-slab of [T, 2I]) e5m2,
- * dgu8t (K-slab of [2I, ldt])
- * e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is recorded by
+ * dgu8t (K-slab of [2I, ldt]; optional) e5m2; amax[3] max-accumulated.  (amax[4] = max|dy| is recorded by
  * sfp8_norm_bwd.)  D % 64 == 0, I % 128 == 0, ldt == T rounded up to 256
  * (as for sfp8_gemm_gateup_swiglu_fwd: every padding token is written). */
 int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8, int64_t T, int64_t D,
@@ -182,13 +184,14 @@ int sfp8_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b, in
 /* RMSNorm backward + residual, replaces _fp8_norm_bwd_kernel
  * (train.py:1130-1147, launched at train.py:1243-1246) and the dnw sum
  * (train.py:1252).  h, dxn, dy [T, D] bf16, rstd [T] -> dh [T, D] bf16,
- * dnw [D] fp32; also dy8t = e5m2(dy * scale[4]) as a K-slab copy (the down wgrad
- * operand quantized in registers at train.py:1171-1172) and amax[4] = max|dy|
- * (train.py:1074-1081).  partials: fp32 workspace of
+ * dnw [D] fp32; also e5m2(dy * scale[4]) (the down wgrad operand quantized
+ * in registers at train.py:1171-1172) as dy8 (K-slab of [T, D]:
+ * [D/64][ldt][64]) and/or dy8t (K-slab of [D, ldt]), each optional, and
+ * amax[4] = max|dy| (train.py:1074-1081).  partials: fp32 workspace of
  * sfp8_norm_bwd_partials(D, ldt) * D floats. */
 int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
                   int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
-                  float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream);
+                  float* partials, int64_t partials_cap, void* dy8, void* dy8t, int64_t ldt, void* stream);
 int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt);
 
 /* Allocation-free RMSNorm backward.  No counterpart in the reference: it is
@@ -206,8 +209,8 @@ int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt);
  * caller; nothing in it needs to start at zero. */
 #define SFP8_NOALLOC_SCRATCH_FLOATS (8LL << 20)
 int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
-                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
-                          int64_t ldt, void* stream);
+                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8,
+                          void* dy8t, int64_t ldt, void* stream);
 
 /* ---- FP8 MoE experts (grouped) ----------------------------------------- */
 /* The grouped twin of the block (_FP8Experts, train.py:1543-1605).  The R

@@ -34,9 +34,9 @@ SIGNATURES = {
     "sfp8_wgrad_splits": (_I64, [_I64, _I64, _I64]),
     "sfp8_wgrad_workspace_floats": (_I64, [_I64, _I64, _I64]),
     "sfp8_slab_bytes": (_I64, [_I64, _I64]),
-    "sfp8_norm_bwd": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _I64, _P]),
+    "sfp8_norm_bwd": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     "sfp8_norm_bwd_partials": (_I64, [_I64, _I64]),
-    "sfp8_norm_bwd_noalloc": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
+    "sfp8_norm_bwd_noalloc": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "sfp8_moe_plan_ints": (_I64, [_I64, _I64]),
     "sfp8_moe_padded_rows": (_I64, [_I64, _I64]),
     "sfp8_moe_plan": (_INT, [_P, _I64, _I64, _P, _I64, _P]),

@@ -332,6 +332,22 @@ SFP8_DEV void lds_rows_store_slab_tr(const uint8_t* lds, int ncols, int stride, 
   }
 }
 
+// The rows t0 .. t0 + NTOK - 1 of an LDS tile (NTOK rows of ncols bytes,
+// ncols % 64 == 0, `stride` bytes apart) into the K-slab [L/64][ldt][64] of a
+// token-major activation, columns c0 .. c0 + ncols - 1 (c0 % 64 == 0): each
+// 64-column block of the tile is one contiguous NTOK * 64-byte run of the
+// slab, written 16 bytes per lane.  NW = waves in the work-group.
+template <int NTOK, int NW = 4>
+SFP8_DEV void lds_rows_store_slab(const uint8_t* lds, int ncols, int stride, uint8_t* out, int64_t ldt, int64_t t0,
+                                  int64_t c0) {
+  const int pieces = (ncols >> 6) * NTOK * 4;
+  for (int i = threadIdx.x; i < pieces; i += 64 * NW) {
+    const int ch = i & 3, r = (i >> 2) % NTOK, k = (i >> 2) / NTOK;
+    const intx4 v = *reinterpret_cast<const intx4*>(lds + r * stride + 64 * k + 16 * ch);
+    *reinterpret_cast<intx4*>(out + ((c0 >> 6) + k) * ldt * 64 + (t0 + r) * 64 + 16 * ch) = v;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // MoE plan: the expert-order rows of a grouped (MoE) layer in "padded expert
 // order", every expert's rows starting on a 256-row boundary, so that each

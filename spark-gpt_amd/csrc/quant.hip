@@ -1,9 +1,10 @@
 // HBM-bound kernels of the FP8 MLP block (gfx950):
 //   quant_rowcol    standalone bf16 -> e4m3 row-major + transposed, amax
-//   norm_quant      RMSNorm -> e4m3 row-major + transposed, rstd, amax slot 0
+//   norm_quant      RMSNorm -> e4m3 K-slab (+ optional transposed copy), rstd, amax slot 0
 //   weight_quant    just-in-time per-tensor pow2 e4m3 copy of an fp32 master
 //   update_scales   delayed-scale roll of the 5 recipe slots
-//   norm_bwd        RMSNorm backward + residual, dnw partials, e5m2 dy^T, amax slot 4
+//   norm_bwd        RMSNorm backward + residual, dnw partials, e5m2 dy (K-slab and/or
+//                   transposed copy), amax slot 4
 //   reductions      dnw partial sum, split-K sum
 //
 // Byte transposes go through an LDS tile: the row-major pass writes the fp8
@@ -152,9 +153,11 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
 // Norm-fused quantizer (spark-gpt train.py:955-972).
 //   rstd[t] = fl32(1/sqrt(fl64(fl32(sum h^2)/D + eps)))   (sum exact in fp64)
 //   n = (h * rstd) * w;  x8 = e4m3(n * s0);  amax0 = max |n|
-// x8t is the K-slab token-contiguous copy (common.h) over ldt tokens (a
-// multiple of 256); tokens T..ldt-1 are written as zeros so a GEMM can
-// reduce over ldt tokens.
+// x8 is the K-slab [D/64][ldt][64] over ldt tokens (a multiple of 256);
+// tokens T..ldt-1 are written as zeros so a GEMM can reduce over ldt tokens.
+// x8t (optional: null skips it) is the token-contiguous
+// K-slab copy (common.h), for weight gradients that read token-contiguous
+// operands.
 // Each work-group owns RT rows; a row is split over LPR lanes holding CPL
 // 8-element chunks each.
 template <int D>
@@ -257,15 +260,18 @@ void norm_quant_kernel(
           hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
         }
         // x8 is a K-slab [D/64][ldt][64] (the gate/up GEMM's A operand),
-        // zeros for tokens T..ldt-1
+        // zeros for tokens T..ldt-1.  Written from the registers: without
+        // x8t the kernel needs no LDS tile, and the occupancy that buys
+        // outweighs whole-run stores staged through one (4 % at D = 1024)
         *reinterpret_cast<intx2*>(x8 + (int64_t)(d >> 6) * ldt * 64 + t * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
-        *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
+        if (x8t) *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
     }
   }
-  __syncthreads();
-  // rows past T hold zero codes
-  lds_rows_store_slab_tr<Cfg::RT, Cfg::QW>(tile, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0);
+  if (x8t) {  // the optional token-contiguous copy (rows past T hold zero codes)
+    __syncthreads();
+    lds_rows_store_slab_tr<Cfg::RT, Cfg::QW>(tile, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0);
+  }
   block_amax_atomic<Cfg::QW>(m, red, amax);
 }
 
@@ -275,8 +281,8 @@ void norm_quant_kernel(
 // a work-group of 64 tokens makes two passes.  Pass 1: each wave reduces
 // sum h^2 of 16 rows (fp64, exact) into rstd.  Pass 2, per 1024-column
 // chunk: each wave normalises and quantizes its 16 rows' chunk into the x8
-// K-slab and an LDS tile, and the 64 x 1024 tile leaves as whole 64-byte
-// rows of the token-contiguous x8t (transposing LDS reads).  The chunk's
+// K-slab and, when the token-contiguous x8t is asked for, an LDS tile that
+// leaves as whole 64-byte rows of x8t (transposing LDS reads).  The chunk's
 // second read of h mostly hits the caches.
 constexpr int kWideRows = 64;
 constexpr int kWideChunk = 1024;
@@ -373,13 +379,16 @@ __global__ __launch_bounds__(256) void norm_quant_wide_kernel(
           const int64_t d = cc + 512 * hf + 8 * lane;
           // x8 is a K-slab [D/64][ldt][64], zeros for tokens T..ldt-1
           *reinterpret_cast<intx2*>(x8 + (d >> 6) * ldt * 64 + t * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
-          *reinterpret_cast<intx2*>(tile + r * kWideStride + 512 * hf + 8 * lane) = intx2{(int)lo, (int)hi};
+          if (x8t)
+            *reinterpret_cast<intx2*>(tile + r * kWideStride + 512 * hf + 8 * lane) = intx2{(int)lo, (int)hi};
         }
       }
     }
-    __syncthreads();
-    lds_rows_store_slab_tr<kWideRows>(tile, kWideChunk, kWideStride, x8t, cp, t0, cc);
-    __syncthreads();  // the next chunk overwrites the tile
+    if (x8t) {
+      __syncthreads();
+      lds_rows_store_slab_tr<kWideRows>(tile, kWideChunk, kWideStride, x8t, cp, t0, cc);
+      __syncthreads();  // the next chunk overwrites the tile
+    }
   }
   block_amax_atomic<4>(m, red, amax);
 }
@@ -517,20 +526,22 @@ __global__ void update_scales_kernel(float* __restrict__ scale, float* __restric
 //   g = dxn, gw = g*w, S = sum_d gw*h
 //   dh = bf16(gw*r - h*(S*r*r*r*(1/D)) + dy)
 //   dnw_part[block][d] = sum over the block's rows of g*(h*r)
-// plus, for the down-proj weight gradient, dy8t = e5m2(dy * s4) as a K-slab
-// token-contiguous copy (zeros for tokens T..ldt-1), and amax slot 4 = max|dy|
+// plus, for the down-proj weight gradient, e5m2(dy * s4) as the K-slab dy8
+// [D/64][ldt][64] and/or the token-contiguous K-slab copy dy8t (each
+// optional; zeros for tokens T..ldt-1), and amax slot 4 = max|dy|
 // (recorded at train.py:1074-1081).
 template <int D>
 __global__ __launch_bounds__(256) void norm_bwd_kernel(
     const uint16_t* __restrict__ h, const float* __restrict__ rstd, const uint16_t* __restrict__ dxn,
     const uint16_t* __restrict__ dy, const float* __restrict__ nw, int64_t T,
     const float* __restrict__ scale, float* __restrict__ amax, uint16_t* __restrict__ dh,
-    float* __restrict__ dnw_part, uint8_t* __restrict__ dy8t, int64_t ldt) {
+    float* __restrict__ dnw_part, uint8_t* __restrict__ dy8, uint8_t* __restrict__ dy8t, int64_t ldt) {
   using Cfg = NormCfg<D>;
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[4];
   uint8_t* tile = smem;
-  // [4 waves][D] floats, in the tile's LDS after the dy8t copy has read it
+  // [4 waves][D] floats, in the tile's LDS after the dy8 / dy8t stores have
+  // read it (the only LDS when there is neither)
   float* dnw_red = reinterpret_cast<float*>(smem);
   static_assert(4 * D * sizeof(float) <= Cfg::RT * Cfg::STRIDE, "dnw reduction fits in the tile");
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -611,13 +622,17 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
           lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
           hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
         }
-        *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
+        // staged for whole 64-row slab runs of dy8 (7 % faster than 8-byte
+        // stores from the registers here, where the LDS is needed anyway)
+        if (dy8 || dy8t) *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
     }
   }
-  __syncthreads();
-  // rows past T hold zero codes
-  lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
+  if (dy8 || dy8t) {  // whole slab runs from the tile; rows past T hold zero codes
+    __syncthreads();
+    if (dy8) lds_rows_store_slab<Cfg::RT>(tile, D, Cfg::STRIDE, dy8, ldt, t0, 0);
+    if (dy8t) lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
+  }
   // fold this lane's dnw accumulators over the rows sharing its columns
 #pragma unroll
   for (int c = 0; c < Cfg::CPL; ++c)
@@ -645,13 +660,14 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
 // computation as norm_bwd_kernel in two passes over a work-group of 64
 // tokens: pass 1 reduces S = sum (g*w)*h per row; pass 2, per 1024-column
 // chunk, writes dh, accumulates the chunk's dnw partial (each wave over its
-// 16 rows in order, then the 4 waves in order) and stages e5m2(dy*s4) for
-// the token-contiguous dy8t, written as whole 64-byte rows.
+// 16 rows in order, then the 4 waves in order) and writes e5m2(dy*s4) into
+// the dy8 K-slab and/or stages it for the token-contiguous dy8t, written as
+// whole 64-byte rows.
 __global__ __launch_bounds__(256) void norm_bwd_wide_kernel(
     const uint16_t* __restrict__ h, const float* __restrict__ rstd, const uint16_t* __restrict__ dxn,
     const uint16_t* __restrict__ dy, const float* __restrict__ nw, int64_t T, int64_t D,
     const float* __restrict__ scale, float* __restrict__ amax, uint16_t* __restrict__ dh,
-    float* __restrict__ dnw_part, uint8_t* __restrict__ dy8t, int64_t ldt) {
+    float* __restrict__ dnw_part, uint8_t* __restrict__ dy8, uint8_t* __restrict__ dy8t, int64_t ldt) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float red[4];
   __shared__ float coef_sh[kWideRows], rs_sh[kWideRows];
@@ -757,7 +773,9 @@ __global__ __launch_bounds__(256) void norm_bwd_wide_kernel(
             lo = pack4_e5m2(dyf[0] * s4, dyf[1] * s4, dyf[2] * s4, dyf[3] * s4);
             hi = pack4_e5m2(dyf[4] * s4, dyf[5] * s4, dyf[6] * s4, dyf[7] * s4);
           }
-          *reinterpret_cast<intx2*>(tile + r * kWideStride + 512 * hf + 8 * lane) = intx2{(int)lo, (int)hi};
+          if (dy8) *reinterpret_cast<intx2*>(dy8 + (d >> 6) * ldt * 64 + t * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
+          if (dy8t)
+            *reinterpret_cast<intx2*>(tile + r * kWideStride + 512 * hf + 8 * lane) = intx2{(int)lo, (int)hi};
         }
       }
     }
@@ -767,7 +785,7 @@ __global__ __launch_bounds__(256) void norm_bwd_wide_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) dnw_red[wid * kWideChunk + 512 * hf + 8 * lane + j] = acc[hf][j];
     __syncthreads();
-    lds_rows_store_slab_tr<kWideRows>(tile, kWideChunk, kWideStride, dy8t, cp, t0, cc);
+    if (dy8t) lds_rows_store_slab_tr<kWideRows>(tile, kWideChunk, kWideStride, dy8t, cp, t0, cc);
     for (int d = threadIdx.x; d < kWideChunk; d += 256)
       dnw_part[(int64_t)blk * D + cc + d] =
           ((dnw_red[d] + dnw_red[kWideChunk + d]) + dnw_red[2 * kWideChunk + d]) + dnw_red[3 * kWideChunk + d];
@@ -869,7 +887,7 @@ template <int D>
 static int launch_norm_quant(const void* h, const float* nw, int64_t T, float eps, const float* scale,
                              float* amax, void* x8, void* x8t, int64_t ldt, float* rstd, hipStream_t st) {
   using Cfg = NormCfg<D>;
-  const size_t lds = (size_t)Cfg::RT * Cfg::STRIDE;
+  const size_t lds = x8t ? (size_t)Cfg::RT * Cfg::STRIDE : 0;  // the transposing tile
   const unsigned nblk = (unsigned)(ldt / Cfg::RT);
   const int rc = allow_lds(norm_quant_kernel<D>, lds);
   if (rc) return rc;
@@ -881,15 +899,16 @@ static int launch_norm_quant(const void* h, const float* nw, int64_t T, float ep
 template <int D>
 static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy,
                            const float* nw, int64_t T, const float* scale, float* amax, void* dh,
-                           float* dnw, float* part, void* dy8t, int64_t ldt, hipStream_t st) {
+                           float* dnw, float* part, void* dy8, void* dy8t, int64_t ldt, hipStream_t st) {
   using Cfg = NormCfg<D>;
-  const size_t lds = (size_t)Cfg::RT * Cfg::STRIDE;
+  // the transposing tile, or only the dnw reduction rows
+  const size_t lds = (dy8 || dy8t) ? (size_t)Cfg::RT * Cfg::STRIDE : (size_t)4 * D * sizeof(float);
   const unsigned nblk = (unsigned)(ldt / Cfg::RT);
   const int rc = allow_lds(norm_bwd_kernel<D>, lds);
   if (rc) return rc;
   hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, rstd,
                      (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, scale, amax, (uint16_t*)dh, part,
-                     (uint8_t*)dy8t, ldt);
+                     (uint8_t*)dy8, (uint8_t*)dy8t, ldt);
   // partial rows: nblk from the norm kernel, then the group sums after them
   const int64_t nb = (int64_t)nblk, G = colsum_groups(nb), rpg = (nb + G - 1) / G;
   float* group_sums = part + nb * D;
@@ -913,14 +932,14 @@ static int colsum_launch(float* part, int64_t nb, int64_t D, float* dnw, hipStre
 
 static int launch_norm_bwd_wide(const void* h, const float* rstd, const void* dxn, const void* dy, const float* nw,
                                 int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
-                                float* part, void* dy8t, int64_t ldt, hipStream_t st) {
+                                float* part, void* dy8, void* dy8t, int64_t ldt, hipStream_t st) {
   const size_t lds = (size_t)kWideLdsTile + 4 * kWideChunk * sizeof(float);
   const int rc = allow_lds(norm_bwd_wide_kernel, lds);
   if (rc) return rc;
   const int64_t nb = ldt / kWideRows;
   hipLaunchKernelGGL(norm_bwd_wide_kernel, dim3((unsigned)nb), dim3(256), lds, st, (const uint16_t*)h, rstd,
                      (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, D, scale, amax, (uint16_t*)dh, part,
-                     (uint8_t*)dy8t, ldt);
+                     (uint8_t*)dy8, (uint8_t*)dy8t, ldt);
   const int e = launch_status();
   return e ? e : colsum_launch(part, nb, D, dnw, st);
 }
@@ -966,7 +985,7 @@ int sfp8_norm_quant(const void* h, const float* norm_w, int64_t T, int64_t D, fl
                     const float* scale, float* amax, void* x8, void* x8t, int64_t ldt, float* rstd,
                     void* stream) {
   // token-sized buffers may be null when there are no tokens
-  if (!norm_w || !scale || !amax || (T > 0 && (!h || !x8 || !x8t || !rstd))) return kErrNullPointer;
+  if (!norm_w || !scale || !amax || (T > 0 && (!h || !x8 || !rstd))) return kErrNullPointer;
   if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
   if (!aligned16(h) || !aligned16(norm_w) || !aligned16(x8) || !aligned16(x8t)) return kErrBadAlignment;
   if (ldt == 0) return kOk;
@@ -1046,56 +1065,57 @@ int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt) {
 // (the fixed scratch); the arguments are checked by the callers.
 static int norm_bwd_launch(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
                            int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
-                           float* partials, void* dy8t, int64_t ldt, hipStream_t st) {
+                           float* partials, void* dy8, void* dy8t, int64_t ldt, hipStream_t st) {
   if (ldt == 0) {
     // no tokens: d_norm_w is an empty sum (zero); nothing else is written
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, dnw, D);
     return launch_status();
   }
   switch (D) {
-    case 128: return launch_norm_bwd<128>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
-    case 256: return launch_norm_bwd<256>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
-    case 512: return launch_norm_bwd<512>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
-    case 1024: return launch_norm_bwd<1024>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
-    case 2048: return launch_norm_bwd<2048>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
-    case 4096: return launch_norm_bwd<4096>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8t, ldt, st);
+    case 128: return launch_norm_bwd<128>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8, dy8t, ldt, st);
+    case 256: return launch_norm_bwd<256>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8, dy8t, ldt, st);
+    case 512: return launch_norm_bwd<512>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8, dy8t, ldt, st);
+    case 1024: return launch_norm_bwd<1024>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8, dy8t, ldt, st);
+    case 2048: return launch_norm_bwd<2048>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8, dy8t, ldt, st);
+    case 4096: return launch_norm_bwd<4096>(h, rstd, dxn, dy, norm_w, T, scale, amax, dh, dnw, partials, dy8, dy8t, ldt, st);
     default:
       if (wide_hidden(D)) return launch_norm_bwd_wide(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials,
-                                                     dy8t, ldt, st);
+                                                     dy8, dy8t, ldt, st);
       return kErrBadShape;
   }
 }
 
 // Argument checks common to both norm backward entry points.
 static int norm_bwd_check(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
-                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
-                          int64_t ldt) {
-  if (!norm_w || !scale || !amax || !dnw || (T > 0 && (!h || !rstd || !dxn || !dy || !dh || !dy8t)))
+                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8,
+                          void* dy8t, int64_t ldt) {
+  // dy8 and dy8t are each optional
+  if (!norm_w || !scale || !amax || !dnw || (T > 0 && (!h || !rstd || !dxn || !dy || !dh)))
     return kErrNullPointer;
   if (T < 0 || ldt < T || (ldt % 256) != 0) return kErrBadShape;
   if (sfp8_norm_bwd_partials(D, ldt) < 0) return kErrBadShape;
   if (!aligned16(h) || !aligned16(dxn) || !aligned16(dy) || !aligned16(dh) || !aligned16(norm_w) ||
-      !aligned16(dy8t))
+      !aligned16(dy8) || !aligned16(dy8t))
     return kErrBadAlignment;
   return kOk;
 }
 
 int sfp8_norm_bwd(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
                   int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
-                  float* partials, int64_t partials_cap, void* dy8t, int64_t ldt, void* stream) {
+                  float* partials, int64_t partials_cap, void* dy8, void* dy8t, int64_t ldt, void* stream) {
   // token-sized buffers (and the partials) may be null when there are no tokens
-  int rc = norm_bwd_check(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, dy8t, ldt);
+  int rc = norm_bwd_check(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, dy8, dy8t, ldt);
   if (rc) return rc;
   if (T > 0 && !partials) return kErrNullPointer;
   if (partials_cap < sfp8_norm_bwd_partials(D, ldt) * D) return kErrWorkspaceTooSmall;
-  return norm_bwd_launch(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials, dy8t, ldt,
+  return norm_bwd_launch(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials, dy8, dy8t, ldt,
                          (hipStream_t)stream);
 }
 
 int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,
-                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8t,
-                          int64_t ldt, void* stream) {
-  int rc = norm_bwd_check(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, dy8t, ldt);
+                          int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw, void* dy8,
+                          void* dy8t, int64_t ldt, void* stream) {
+  int rc = norm_bwd_check(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, dy8, dy8t, ldt);
   if (rc) return rc;
   // the dnw partials (every row of which the kernels write before reading:
   // nothing has to start at zero) must fit the fixed scratch
@@ -1103,7 +1123,7 @@ int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, con
   float* partials = nullptr;
   rc = scratch_address(&partials);
   if (rc) return rc;
-  return norm_bwd_launch(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials, dy8t, ldt,
+  return norm_bwd_launch(h, rstd, dxn, dy, norm_w, T, D, scale, amax, dh, dnw, partials, dy8, dy8t, ldt,
                          (hipStream_t)stream);
 }
 

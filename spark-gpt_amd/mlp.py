@@ -140,17 +140,17 @@ class _FP8MLPBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, norm_w, w_gu, w_down, scale, amax, eps):
-        y, x8t, rstd, gu8, h8 = torch.ops.sparkfp8.block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)
-        # backward needs x8t and h8 (weight grads), gu8 (SwiGLU backward)
+        y, x8, rstd, gu8, h8 = torch.ops.sparkfp8.block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)
+        # backward needs x8 and h8 (weight grads), gu8 (SwiGLU backward)
         # and the masters, whose quantized copies (W8^T for
         # the gate/up dgrad, bf16 Wd^T for the down dgrad) it finds cached
-        ctx.save_for_backward(h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8, scale, amax)
+        ctx.save_for_backward(h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8, scale, amax = ctx.saved_tensors
-        dh, dnw, dwgu, dwd = torch.ops.sparkfp8.block_bwd(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8,
+        h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax = ctx.saved_tensors
+        dh, dnw, dwgu, dwd = torch.ops.sparkfp8.block_bwd(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8,
                                                           scale, amax)
         return dh, dnw, dwgu, dwd, None, None, None
 

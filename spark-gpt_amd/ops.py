@@ -107,19 +107,21 @@ def quant_e4m3_rowcol(x: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor):
     return x8, x8t
 
 
-def norm_quant(h: torch.Tensor, norm_w: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor, eps: float):
+def norm_quant(h: torch.Tensor, norm_w: torch.Tensor, scale: torch.Tensor, amax: torch.Tensor, eps: float, *,
+               copy: bool = True):
     """(x8 K-slab of [T, D] ([D/64, ldt, 64]), x8t K-slab of [D, ldt], rstd
-    [T]); amax[0] max-accumulated."""
+    [T]); amax[0] max-accumulated.  copy=False skips the token-contiguous
+    x8t (None): the weight gradient then reads x8 itself (wgrad_rows)."""
     _cuda_contig("h", h, torch.bfloat16, 2)
     _cuda_contig("norm_w", norm_w, torch.float32, 1)
     _state(scale, amax)
     T, D = h.shape
     ldt = ldt_of(T)
     x8 = kslab_empty(ldt, D, E4M3, h.device)
-    x8t = slab_empty(D, T, E4M3, h.device)
+    x8t = slab_empty(D, T, E4M3, h.device) if copy else None
     rstd = torch.empty(T, dtype=torch.float32, device=h.device)
     _lib.call("sfp8_norm_quant", h.data_ptr(), norm_w.data_ptr(), T, D, float(eps), scale.data_ptr(),
-              amax.data_ptr(), x8.data_ptr(), x8t.data_ptr(), ldt, rstd.data_ptr(), _lib.stream_of(h))
+              amax.data_ptr(), x8.data_ptr(), _lib.ptr(x8t), ldt, rstd.data_ptr(), _lib.stream_of(h))
     return x8, x8t, rstd
 
 
@@ -275,8 +277,11 @@ def wgrad_rows(a8, b8, M: int, N: int, sa, sb, *, a_rows: bool = True, b_rows: b
     return out
 
 
-def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
-    """(dh [T, D] bf16, dnw [D] fp32, dy8t K-slab of D rows e5m2); amax[4] = max|dy|."""
+def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax, *, rows: bool = False):
+    """(dh [T, D] bf16, dnw [D] fp32, dy8 e5m2); amax[4] = max|dy|.  dy8 is
+    the token-contiguous K-slab copy of D rows ([ldt/64, slab_rows(D), 64]),
+    or with rows=True the K-slab of [T, D] ([D/64, ldt, 64], read by
+    wgrad_rows)."""
     for n, t in (("h", h), ("dxn", dxn), ("dy", dy)):
         _cuda_contig(n, t, torch.bfloat16, 2)
     _cuda_contig("rstd", rstd, torch.float32, 1)
@@ -286,14 +291,14 @@ def norm_bwd(h, rstd, dxn, dy, norm_w, scale, amax):
     dev = h.device
     dh = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
     dnw = torch.empty(D, dtype=torch.float32, device=dev)
-    dy8t = slab_empty(D, T, E5M2, dev)
+    dy8 = kslab_empty(ldt, D, E5M2, dev) if rows else slab_empty(D, T, E5M2, dev)
     nparts = _lib.query("sfp8_norm_bwd_partials", D, ldt)
     _need(nparts >= 0, f"unsupported hidden size {D}")
     parts = torch.empty(max(nparts * D, 1), dtype=torch.float32, device=dev)
     _lib.call("sfp8_norm_bwd", h.data_ptr(), rstd.data_ptr(), dxn.data_ptr(), dy.data_ptr(), norm_w.data_ptr(),
               T, D, scale.data_ptr(), amax.data_ptr(), dh.data_ptr(), dnw.data_ptr(), parts.data_ptr(),
-              parts.numel(), dy8t.data_ptr(), ldt, _lib.stream_of(h))
-    return dh, dnw, dy8t
+              parts.numel(), dy8.data_ptr() if rows else 0, 0 if rows else dy8.data_ptr(), ldt, _lib.stream_of(h))
+    return dh, dnw, dy8
 
 
 # ------------------------------------------------------------------ MoE experts (grouped)

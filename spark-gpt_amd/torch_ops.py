@@ -10,7 +10,7 @@ atomic max (train.py:1015-1016, 1094).
 
 * ``sparkfp8::block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)`` returns
   y and the activations the backward needs (train.py:1200-1226).
-* ``sparkfp8::block_bwd(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8,
+* ``sparkfp8::block_bwd(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8,
   scale, amax)`` returns (dh, d_norm_w, dW_gate_up, dW_down)
   (train.py:1228-1252).
 * ``sparkfp8::update_scales(scale, amax)`` is the delayed-scale roll
@@ -128,18 +128,19 @@ def clear_weight_cache() -> None:
 @torch.library.custom_op("sparkfp8::block_fwd", mutates_args={"amax"})
 def block_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Tensor, amax: Tensor,
               eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """y, then for the backward: x8t, rstd, gu8 (K-slab of [T, 2I]) and h8
-    (K-slab of [T, I]; the down weight gradient reads it through transposing
-    LDS reads, so no token-contiguous copy is written).  The quantized weights stay in the weight cache: they are never an output
+    """y, then for the backward: x8 (K-slab of [T, D]), rstd, gu8 (K-slab of
+    [T, 2I]) and h8 (K-slab of [T, I]).  The weight gradients read x8 and h8
+    through transposing LDS reads, so no token-contiguous copy is written.
+    The quantized weights stay in the weight cache: they are never an output
     (a compiled graph may recycle the memory of the tensors it saves for
     backward), and the backward looks them up from the same masters."""
     I = w_down.shape[1]
     h = h.contiguous()
-    x8, x8t, rstd = ops.norm_quant(h, _master(norm_w), scale, amax, eps)
+    x8, _, rstd = ops.norm_quant(h, _master(norm_w), scale, amax, eps, copy=False)
     w8, _w8t, wd8, _wdt, wscale = cached_weights(w_gu, w_down)
     gu8, h8, _ = ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, h.shape[0], I, copy=False)
     y = ops.down_fwd(h8, wd8, h, scale, wscale)
-    return y, x8t, rstd, gu8, h8
+    return y, x8, rstd, gu8, h8
 
 
 @block_fwd.register_fake
@@ -149,14 +150,14 @@ def _block_fwd_fake(h, norm_w, w_gu, w_down, scale, amax, eps):
     ldt = ops.ldt_of(T)
     sr = ops.slab_rows
     return (h.new_empty((T, D), dtype=torch.bfloat16),
-            h.new_empty((ldt // 64, sr(D), 64), dtype=E4M3),
+            h.new_empty((D // 64, ldt, 64), dtype=E4M3),
             h.new_empty((T,), dtype=torch.float32),
             h.new_empty((2 * I // 64, ldt, 64), dtype=E4M3),
             h.new_empty((I // 64, ldt, 64), dtype=E4M3))
 
 
 @torch.library.custom_op("sparkfp8::block_bwd", mutates_args={"amax"})
-def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, x8t: Tensor, rstd: Tensor,
+def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, x8: Tensor, rstd: Tensor,
               gu8: Tensor, h8: Tensor, scale: Tensor, amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """(dh bf16, d_norm_w fp32, dW_gate_up fp32, dW_down fp32).  W8^T, the
     bf16 W_down^T and the weight scales are the forward's (the cache entry of
@@ -172,15 +173,17 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tenso
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
     dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, _master(norm_w), scale, amax)
     del dxn
-    # the activations' weight-gradient operands are their row K-slabs (dgu8,
-    # h8); x8t and dy8t are the norm kernels' token-contiguous copies
+    # x8, h8 and dgu8 are read as the token-major K-slabs their producers
+    # wrote (transposing LDS reads); dy8t is the norm backward's
+    # token-contiguous copy (a gradient with both operands transposed on
+    # read is 2-3 % slower, the norm backward no faster for the row K-slab)
     dwd = ops.wgrad_rows(dy8t, h8, D, I, scale[4:5], scale[2:3], a_rows=False)
-    dwgu = ops.wgrad_rows(dgu8, x8t, 2 * I, D, scale[3:4], scale[0:1], b_rows=False)
+    dwgu = ops.wgrad_rows(dgu8, x8, 2 * I, D, scale[3:4], scale[0:1])
     return dh, dnw, dwgu, dwd
 
 
 @block_bwd.register_fake
-def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8t, rstd, gu8, h8, scale, amax):
+def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax):
     T, D = h.shape
     I = gu8.shape[0] * ops.SLAB // 2
     return (h.new_empty((T, D), dtype=torch.bfloat16),

@@ -36,6 +36,11 @@ def test_norm_quant_bit_exact(dev, T, D):
     assert torch.equal(xt[:, :T], u8(r8t))
     assert torch.all(xt[:, T:] == 0)
     assert amax[0].item() == ra.item()
+    # without the token-contiguous copy: the same x8 (padding included), rstd and amax
+    amax2 = torch.zeros(5, device=dev)
+    x8b, none, rstd2 = sg.ops.norm_quant(h.to(dev), nw.to(dev), scale, amax2, 1e-6, copy=False)
+    assert none is None
+    assert torch.equal(u8(x8b), u8(x8)) and torch.equal(rstd2, rstd) and torch.equal(amax2, amax)
 
 
 def test_norm_quant_heavy_tails(dev):
@@ -78,3 +83,13 @@ def test_norm_bwd(dev, T, D):
     assert torch.equal(yt[:, :T], u8(ref8).t())
     assert torch.all(yt[:, T:] == 0)
     assert amax[4].item() == dy.float().abs().max().item()
+    # dy8 as the K-slab of [T, D] instead: the same dh, dnw and amax
+    amax2 = torch.zeros(5, device=dev)
+    dh2, dnw2, dy8 = sg.ops.norm_bwd(h.to(dev), rstd.to(dev), dxn.to(dev), dy.to(dev), nw.to(dev), scale, amax2,
+                                     rows=True)
+    assert torch.equal(dh2, dh) and torch.equal(dnw2, dnw) and torch.equal(amax2, amax)
+    ldt = sg.ops.ldt_of(T)
+    assert dy8.shape == (D // 64, ldt, 64)
+    y8 = u8(sg.ops.unslab(dy8, ldt))
+    assert torch.equal(y8[:T], u8(ref8))
+    assert torch.all(y8[T:] == 0)

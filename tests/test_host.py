@@ -83,8 +83,8 @@ def test_invalid_arguments_rejected_before_launch():
     assert lib.sfp8_gemm_down_dgrad_swiglu(16, 16, 16, 300, 256, 384, 16, 16, 16, 16, 768, None) == -2
     assert lib.sfp8_gemm_wgrad(16, 1, 16, 0, 256, 102, 256, 16, 16, 16, 16, 0, None) == -2  # N % 4
     # the allocation-free norm backward refuses shapes beyond its fixed scratch on the host
-    assert lib.sfp8_norm_bwd_noalloc(16, 16, 16, 16, 16, 65536, 4096, 16, 16, 16, 16, 16, 65536, None) == -5
-    assert lib.sfp8_norm_bwd_noalloc(None, 16, 16, 16, 16, 256, 1024, 16, 16, 16, 16, 16, 256, None) == -1
+    assert lib.sfp8_norm_bwd_noalloc(16, 16, 16, 16, 16, 65536, 4096, 16, 16, 16, 16, 16, None, 65536, None) == -5
+    assert lib.sfp8_norm_bwd_noalloc(None, 16, 16, 16, 16, 256, 1024, 16, 16, 16, 16, None, 16, 256, None) == -1
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.check(-1, "x")
     with pytest.raises(RuntimeError, match="HIP error 1"):
@@ -217,7 +217,7 @@ def test_custom_op_fake_shapes_match_allocations():
                                              *out[1:], s, a)
     meta = "meta"
     want = [torch.empty(T, D, dtype=torch.bfloat16, device=meta),
-            ops.slab_empty(D, T, ops.E4M3, meta),
+            ops.kslab_empty(ops.ldt_of(T), D, ops.E4M3, meta),
             torch.empty(T, device=meta),
             ops.kslab_empty(ops.ldt_of(T), 2 * I, ops.E4M3, meta),
             ops.kslab_empty(ops.ldt_of(T), I, ops.E4M3, meta)]

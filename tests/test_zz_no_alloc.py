@@ -1,8 +1,9 @@
 """The allocation-free norm backward (sfp8_norm_bwd_noalloc) against the
 workspace form (sfp8_norm_bwd) through the C ABI: dh, d_norm_w, the e5m2
-dy8t copy and amax slot 4 bit-identical, on two calls in a row (the second
-smaller, so the fixed scratch holds the first call's partials when it
-starts), and a too-large shape refused before anything is launched."""
+dy8 (K-slab of [T, D]) or dy8t (token-contiguous copy) and amax slot 4
+bit-identical, on two calls in a row (the second smaller, so the fixed
+scratch holds the first call's partials when it starts), and a too-large
+shape refused before anything is launched."""
 import pytest
 import torch
 
@@ -27,32 +28,34 @@ def _inputs(dev, T, D, seed):
     return h, dxn, dy, rstd, nw, scale
 
 
-def _run_noalloc(fn, h, dxn, dy, rstd, nw, scale):
+def _run_noalloc(fn, h, dxn, dy, rstd, nw, scale, rows):
     T, D = h.shape
     ldt = ops.ldt_of(T)
     amax = torch.zeros(5, device=h.device)
     dh = torch.empty(T, D, dtype=torch.bfloat16, device=h.device)
     dnw = torch.empty(D, device=h.device)
-    dy8t = ops.slab_empty(D, T, ops.E5M2, h.device)
+    dy8 = ops.kslab_empty(ldt, D, ops.E5M2, h.device) if rows else ops.slab_empty(D, T, ops.E5M2, h.device)
     torch.cuda.synchronize()  # every buffer above exists before the call (no allocation after it)
     rc = fn(h.data_ptr(), rstd.data_ptr(), dxn.data_ptr(), dy.data_ptr(), nw.data_ptr(), T, D, scale.data_ptr(),
-            amax.data_ptr(), dh.data_ptr(), dnw.data_ptr(), dy8t.data_ptr(), ldt, _lib.stream_of(h))
+            amax.data_ptr(), dh.data_ptr(), dnw.data_ptr(), dy8.data_ptr() if rows else None,
+            None if rows else dy8.data_ptr(), ldt, _lib.stream_of(h))
     assert rc == 0, rc
-    return dh, dnw, dy8t, amax
+    return dh, dnw, dy8, amax
 
 
+@pytest.mark.parametrize("rows", [True, False])
 @pytest.mark.parametrize("shapes", [((1000, 1024), (300, 1024)), ((4096, 256), (257, 256)),
                                     ((65536, 1024), (1000, 1024))])
-def test_noalloc_matches_workspace_form(dev, shapes):
+def test_noalloc_matches_workspace_form(dev, shapes, rows):
     fn = _noalloc()
     for k, (T, D) in enumerate(shapes):
         args = _inputs(dev, T, D, 100 + k)
-        got = _run_noalloc(fn, *args)
+        got = _run_noalloc(fn, *args, rows)
         h, dxn, dy, rstd, nw, scale = args
         amax = torch.zeros(5, device=dev)
-        ref = ops.norm_bwd(h, rstd, dxn, dy, nw, scale, amax) + (amax,)
+        ref = ops.norm_bwd(h, rstd, dxn, dy, nw, scale, amax, rows=rows) + (amax,)
         torch.cuda.synchronize()
-        for name, a, b in zip(("dh", "dnw", "dy8t", "amax"), got, ref):
+        for name, a, b in zip(("dh", "dnw", "dy8", "amax"), got, ref):
             assert torch.equal(a.view(torch.uint8) if a.dtype == ops.E5M2 else a,
                                b.view(torch.uint8) if b.dtype == ops.E5M2 else b), (T, D, name)
 
@@ -63,4 +66,4 @@ def test_noalloc_refuses_beyond_scratch(dev):
     need = _lib.query("sfp8_norm_bwd_partials", D, ldt) * D
     assert need > 8 << 20  # SFP8_NOALLOC_SCRATCH_FLOATS
     # refused on the host (non-null stand-in pointers are never dereferenced)
-    assert fn(16, 16, 16, 16, 16, ldt, D, 16, 16, 16, 16, 16, ldt, None) == -5
+    assert fn(16, 16, 16, 16, 16, ldt, D, 16, 16, 16, 16, 16, None, ldt, None) == -5
