@@ -176,9 +176,13 @@ struct NormCfg {
   static constexpr int QW = D <= 1024 ? 8 : 4;
   static constexpr int QPASSES = RT / (QW * RPW);
   static constexpr int PB = (8 / CPL) < QPASSES ? ((8 / CPL) > 0 ? 8 / CPL : 1) : QPASSES;
-  // norm_bwd: 4 waves per work-group, PASSES row passes per wave, PB_BWD per batch
-  static constexpr int PASSES = RT / (4 * RPW);
-  static constexpr int PB_BWD = (4 / CPL) < PASSES ? ((4 / CPL) > 0 ? 4 / CPL : 1) : PASSES;
+  // norm_bwd: BW waves per work-group (8 up to D = 1024: 4 waves per SIMD
+  // beside the LDS tile, as for norm_quant), PASSES row passes per wave,
+  // PB_BWD per batch
+  static constexpr int BW = D <= 1024 ? 8 : 4;
+  static constexpr int PASSES = RT / (BW * RPW);
+  static constexpr int LB = (BW == 8 ? 2 : 4) / CPL;  // row chunks per lane in one load batch
+  static constexpr int PB_BWD = LB < PASSES ? (LB > 0 ? LB : 1) : PASSES;
   static_assert(QPASSES % PB == 0 && PASSES % PB_BWD == 0, "whole load batches");
 };
 
@@ -531,19 +535,20 @@ __global__ void update_scales_kernel(float* __restrict__ scale, float* __restric
 // optional; zeros for tokens T..ldt-1), and amax slot 4 = max|dy|
 // (recorded at train.py:1074-1081).
 template <int D>
-__global__ __launch_bounds__(256) void norm_bwd_kernel(
+__global__ __launch_bounds__(64 * NormCfg<D>::BW) __attribute__((amdgpu_waves_per_eu(NormCfg<D>::BW == 8 ? 4 : 1)))
+void norm_bwd_kernel(
     const uint16_t* __restrict__ h, const float* __restrict__ rstd, const uint16_t* __restrict__ dxn,
     const uint16_t* __restrict__ dy, const float* __restrict__ nw, int64_t T,
     const float* __restrict__ scale, float* __restrict__ amax, uint16_t* __restrict__ dh,
     float* __restrict__ dnw_part, uint8_t* __restrict__ dy8, uint8_t* __restrict__ dy8t, int64_t ldt) {
   using Cfg = NormCfg<D>;
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float red[4];
+  __shared__ float red[Cfg::BW];
   uint8_t* tile = smem;
-  // [4 waves][D] floats, in the tile's LDS after the dy8 / dy8t stores have
+  // [BW waves][D] floats, in the tile's LDS after the dy8 / dy8t stores have
   // read it (the only LDS when there is neither)
   float* dnw_red = reinterpret_cast<float*>(smem);
-  static_assert(4 * D * sizeof(float) <= Cfg::RT * Cfg::STRIDE, "dnw reduction fits in the tile");
+  static_assert(Cfg::BW * D * sizeof(float) <= Cfg::RT * Cfg::STRIDE, "dnw reduction fits in the tile");
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
   const int blk = xcd_row_block(blockIdx.x, gridDim.x);
@@ -559,14 +564,15 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; acc[c][j] = 0.f; acc[c][4 + j] = 0.f; }
   }
-  // wave wid takes row passes wid, wid + 4, ...; PB_BWD passes' loads are
+  // wave wid takes row passes wid, wid + BW, ...; PB_BWD passes' loads are
   // issued before any of them is used
+#pragma unroll 1
   for (int pb = 0; pb < Cfg::PASSES; pb += Cfg::PB_BWD) {
     intx4 vh[Cfg::PB_BWD][Cfg::CPL], vg[Cfg::PB_BWD][Cfg::CPL], vd[Cfg::PB_BWD][Cfg::CPL];
     float rsv[Cfg::PB_BWD];
 #pragma unroll
     for (int q = 0; q < Cfg::PB_BWD; ++q) {
-      const int64_t t = t0 + (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const int64_t t = t0 + (wid + Cfg::BW * (pb + q)) * Cfg::RPW + sr;
       const bool valid = t < T;
 #pragma unroll
       for (int c = 0; c < Cfg::CPL; ++c) {
@@ -580,7 +586,7 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
     }
 #pragma unroll
     for (int q = 0; q < Cfg::PB_BWD; ++q) {
-      const int r = (wid + 4 * (pb + q)) * Cfg::RPW + sr;
+      const int r = (wid + Cfg::BW * (pb + q)) * Cfg::RPW + sr;
       const int64_t t = t0 + r;
       const bool valid = t < T;
       const float rs = rsv[q];
@@ -630,8 +636,8 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
   }
   if (dy8 || dy8t) {  // whole slab runs from the tile; rows past T hold zero codes
     __syncthreads();
-    if (dy8) lds_rows_store_slab<Cfg::RT>(tile, D, Cfg::STRIDE, dy8, ldt, t0, 0);
-    if (dy8t) lds_rows_store_slab_tr<Cfg::RT>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
+    if (dy8) lds_rows_store_slab<Cfg::RT, Cfg::BW>(tile, D, Cfg::STRIDE, dy8, ldt, t0, 0);
+    if (dy8t) lds_rows_store_slab_tr<Cfg::RT, Cfg::BW>(tile, D, Cfg::STRIDE, dy8t, slab_rows(D), t0, 0);
   }
   // fold this lane's dnw accumulators over the rows sharing its columns
 #pragma unroll
@@ -650,10 +656,13 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(
       for (int j = 0; j < 8; ++j) dnw_red[wid * D + (c * Cfg::LPR + li) * 8 + j] = acc[c][j];
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += 256)
-    dnw_part[(int64_t)blk * D + d] =
-        ((dnw_red[d] + dnw_red[D + d]) + dnw_red[2 * D + d]) + dnw_red[3 * D + d];
-  block_amax_atomic<4>(m, red, amax + 4);
+  for (int d = threadIdx.x; d < D; d += 64 * Cfg::BW) {
+    float v = dnw_red[d];  // the waves' sums in wave order
+#pragma unroll
+    for (int w2 = 1; w2 < Cfg::BW; ++w2) v += dnw_red[w2 * D + d];
+    dnw_part[(int64_t)blk * D + d] = v;
+  }
+  block_amax_atomic<Cfg::BW>(m, red, amax + 4);
 }
 
 // RMSNorm backward for wide rows (D >= 8192, D % 4096 == 0), the same
@@ -902,11 +911,11 @@ static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, co
                            float* dnw, float* part, void* dy8, void* dy8t, int64_t ldt, hipStream_t st) {
   using Cfg = NormCfg<D>;
   // the transposing tile, or only the dnw reduction rows
-  const size_t lds = (dy8 || dy8t) ? (size_t)Cfg::RT * Cfg::STRIDE : (size_t)4 * D * sizeof(float);
+  const size_t lds = (dy8 || dy8t) ? (size_t)Cfg::RT * Cfg::STRIDE : (size_t)Cfg::BW * D * sizeof(float);
   const unsigned nblk = (unsigned)(ldt / Cfg::RT);
   const int rc = allow_lds(norm_bwd_kernel<D>, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(256), lds, st, (const uint16_t*)h, rstd,
+  hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(64 * Cfg::BW), lds, st, (const uint16_t*)h, rstd,
                      (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, scale, amax, (uint16_t*)dh, part,
                      (uint8_t*)dy8, (uint8_t*)dy8t, ldt);
   // partial rows: nblk from the norm kernel, then the group sums after them
