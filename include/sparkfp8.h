@@ -166,12 +166,14 @@ int64_t sfp8_slab_bytes(int64_t rows, int64_t k);
 int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt);
 
 
-/* The same weight gradient with either operand (or both) read from the row
- * K-slab of the token-major activation the forward GEMMs use instead of the
- * token-contiguous copy (a_rows / b_rows != 0: a = [M/64][ldt][64], b =
- * [N/64][ldt][64] bytes: d_gu8 and h8 as their producers write them),
- * through transposing LDS reads: bytes equal to sfp8_gemm_wgrad on the
- * copies, which the producers then need not write.  M % 64 == 0 with
+/* The same weight gradient (the block's replacement for _fp8_wgrad,
+ * train.py:1247, and for _fp8_mm_kernel on d_gu, train.py:1249-1251) with
+ * either operand (or both) read from the row K-slab of the token-major
+ * activation instead of the token-contiguous copy (a_rows / b_rows != 0:
+ * a = [M/64][ldt][64], b = [N/64][ldt][64] bytes: x8, h8, d_gu8 and the
+ * dy8 of sfp8_norm_bwd as their producers write them), through transposing
+ * LDS reads: bytes equal to sfp8_gemm_wgrad on the copies, which the
+ * producers then need not write.  M % 64 == 0 with
  * a_rows, N % 64 == 0 with b_rows, at least one set; ws: fp32 workspace of
  * sfp8_wgrad_rows_workspace_floats(M, N, ldt) floats. */
 int64_t sfp8_wgrad_rows_workspace_floats(int64_t M, int64_t N, int64_t ldt);
