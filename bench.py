@@ -329,6 +329,8 @@ def launch_name(sym: str, a, D: int, I: int) -> str:
         return "weight_quant_gu" if a[2] == 2 * I else "weight_quant_down"
     if sym == "sfp8_moe_gemm_wgrad":
         return "moe_wgrad_down" if a[4] == D else "moe_wgrad_gateup"
+    if sym == "sfp8_moe_gemm_wgrad_rows":
+        return "moe_wgrad_down" if a[6] == D else "moe_wgrad_gateup"
     if sym == "sfp8_moe_rows_quant":
         return "moe_gather_quant_x" if a[11] == 0 else "moe_quant_dout"
     return {"sfp8_norm_quant": "norm_quant", "sfp8_gemm_gateup_swiglu_fwd": "gateup_swiglu_fwd",
@@ -539,7 +541,7 @@ def time_moe(T: int, D: int, I: int, E: int, k: int, steps: int, warmup: int) ->
     flop = 18.0 * R * D * I
     work = {
         "moe_plan": (None, 4.0 * E),
-        "moe_gather_quant_x": (None, 4.0 * R * D),
+        "moe_gather_quant_x": (None, 3.0 * R * D),
         "moe_quant_dout": (None, 3.0 * R * D),
         "weight_quant_gu": (None, 10.0 * E * 2 * I * D),
         "weight_quant_down": (None, 11.0 * E * D * I),

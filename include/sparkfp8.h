@@ -239,7 +239,8 @@ int sfp8_moe_plan(const int* offsets, int64_t E, int64_t R, int* plan, int64_t p
  * valid rows; else zeros (and out-of-range indices read as zeros).
  *   fmt = e4m3 (0): replaces _fp8_moe_gather_quant_kernel (train.py:1300-1314):
  *     xs = K-slab of e4m3(clamp(x * scale[sslot])) over [ldp, D] (the gate/up
- *     GEMM's A), xt = its token-contiguous K-slab [D, ldp];
+ *     GEMM's A), xt = its token-contiguous K-slab [D, ldp]; either may be
+ *     NULL, not both;
  *   fmt = e5m2 (1), xs = NULL: the e5m2 dout copy the down weight gradient
  *     quantizes in registers (train.py:1525-1526), token-contiguous.
  * amax[aslot] = max |src| over the gathered rows.  D % 128 == 0. */
@@ -256,7 +257,8 @@ int sfp8_weight_quant_experts(const float* w, int64_t E, int64_t rows, int64_t c
 
 /* Grouped gate/up forward + SwiGLU, replaces _fp8_moe_swiglu_fwd_kernel
  * (train.py:1316-1353): as sfp8_gemm_gateup_swiglu_fwd over padded expert
- * order, expert e's W8 at w8 + e * D * slab_rows(2I) and q_gu[e]. */
+ * order, expert e's W8 at w8 + e * D * slab_rows(2I) and q_gu[e]; h8t
+ * optional. */
 int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, int64_t D, int64_t I, const int* plan,
                                     int64_t ldp, const float* scale, const float* q_gu, float* amax, void* gu8,
                                     void* h8, void* h8t, void* stream);
@@ -269,7 +271,7 @@ int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D
 /* Grouped bf16 down dgrad + SwiGLU backward, replaces
  * _fp8_moe_down_dgrad_swiglu_kernel (train.py:1381-1423): dout [R, D] bf16
  * expert-order rows, wdt per expert (bf16 K-slab of W_down[e]^T) ->
- * dgu8 / dgu8t over padded expert order; amax[3].  (amax[4] = max|dout| is
+ * dgu8 / dgu8t (optional) over padded expert order; amax[3].  (amax[4] = max|dout| is
  * recorded by the e5m2 dout copy, sfp8_moe_rows_quant.) */
 int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const void* gu8, int64_t E, int64_t D,
                                     int64_t I, int64_t R, const int* plan, int64_t ldp, const float* scale,
@@ -291,6 +293,19 @@ int64_t sfp8_moe_wgrad_workspace_floats(int64_t M, int64_t N, int64_t E);
 int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t E,
                         const int* plan, int64_t ldp, const float* sa, const float* sb, float* out, float* ws,
                         int64_t ws_floats, void* stream);
+
+/* The grouped weight gradient with either operand (or both) read from the
+ * row K-slab of the expert-order activation over padded rows (a_rows /
+ * b_rows != 0: a = [M/64][ldp][64], b = [N/64][ldp][64] bytes: xs, h8 and
+ * dgu8 as their producers write them) through transposing LDS reads, as
+ * sfp8_gemm_wgrad_rows is to sfp8_gemm_wgrad: bytes equal to
+ * sfp8_moe_gemm_wgrad on the token-contiguous copies.  M % 64 == 0 with
+ * a_rows, N % 64 == 0 with b_rows, at least one set; ws: fp32 workspace of
+ * sfp8_moe_wgrad_rows_workspace_floats(M, N, E) floats. */
+int64_t sfp8_moe_wgrad_rows_workspace_floats(int64_t M, int64_t N, int64_t E);
+int sfp8_moe_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b, int fmt_b, int b_rows, int64_t M,
+                             int64_t N, int64_t E, const int* plan, int64_t ldp, const float* sa, const float* sb,
+                             float* out, float* ws, int64_t ws_floats, void* stream);
 
 /* out[t] = bf16(sum over slots j < k of dx[inv[t*k + j]]), fp32 sum in slot
  * order: replaces _sum_topk_rows (train.py:2213-2217) in the experts'

@@ -49,6 +49,9 @@ SIGNATURES = {
     "sfp8_moe_wgrad_splits": (_I64, [_I64, _I64, _I64]),
     "sfp8_moe_wgrad_workspace_floats": (_I64, [_I64, _I64, _I64]),
     "sfp8_moe_gemm_wgrad": (_INT, [_P, _INT, _P, _INT, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _P]),
+    "sfp8_moe_wgrad_rows_workspace_floats": (_I64, [_I64, _I64, _I64]),
+    "sfp8_moe_gemm_wgrad_rows": (_INT, [_P, _INT, _INT, _P, _INT, _INT, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64,
+                                        _P]),
     "sfp8_moe_topk_sum": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _P]),
     # bf16 SwiGLU path
     "sfp8_bf16_slab_bytes": (_I64, [_I64, _I64]),

@@ -1105,7 +1105,7 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
 // ws[e][sp][tile], summed in split order by splitk_reduce_kernel.
 // BF16: bf16 operands, 2 bytes per padded row (`ldp` counts K bytes), and the
 // partials always go to ws, for bf16_wgrad_reduce_kernel to round.
-template <bool BF16, int FMT_A, int FMT_B>
+template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false>
 __global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldp,
     const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out, float* __restrict__ ws,
@@ -1126,14 +1126,22 @@ __global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
   const int64_t nk = nst - k0 < 0 ? 0 : (nst - k0 < q ? nst - k0 : q);
   const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
   const int64_t s0 = P.pstart(e) * kBpe / kStage + k0;  // first 64-byte stage
-  const uint8_t* a0 = at + s0 * rpa * kStage + m0 * kStage;
-  const uint8_t* b0 = bt + s0 * rpb * kStage + n0 * kStage;
-  const int64_t a_bytes = nk > 0 ? at + ldp * rpa - a0 : 0, b_bytes = nk > 0 ? bt + ldp * rpb - b0 : 0;
+  // Token-contiguous operands: stage s at s * rows * 64.  Row K-slab (TR)
+  // operands ([rows/64][ldp][64], as for wgrad_kernel): tile row r is token
+  // r % 64 of slab r / 64, and a 64-token stage is 4 KiB on in every slab.
+  const int ldpi = (int)ldp;
+  const uint8_t* a0 = TRA ? at + (m0 / 64) * ldp * kStage + s0 * 64 * kStage : at + s0 * rpa * kStage + m0 * kStage;
+  const uint8_t* b0 = TRB ? bt + (n0 / 64) * ldp * kStage + s0 * 64 * kStage : bt + s0 * rpb * kStage + n0 * kStage;
+  const uint8_t* a_end = TRA ? at + (M / 64) * ldp * kStage : at + ldp * rpa;
+  const uint8_t* b_end = TRB ? bt + (N / 64) * ldp * kStage : bt + ldp * rpb;
+  const int64_t a_bytes = nk > 0 ? a_end - a0 : 0, b_bytes = nk > 0 ? b_end - b0 : 0;
   floatx16 acc[4][4];
-  MainLoop<BF16, FMT_A, FMT_B, false>::run(
-      lds, a0, a_bytes, [=](int r) { return r * kStage; }, (int)(rpa * kStage), b0, b_bytes,
-      [=](int r) { return plain_col(r) * kStage; }, (int)(rpb * kStage), (int)nk, acc);
-  if (BF16 || splits > 1) {
+  MainLoop<BF16, FMT_A, FMT_B, false, 4, kStages, 0, TRA, TRB>::run(
+      lds, a0, a_bytes, [=](int r) { return TRA ? ((r >> 6) * ldpi + (r & 63)) * kStage : r * kStage; },
+      TRA ? 64 * kStage : (int)(rpa * kStage), b0, b_bytes,
+      [=](int r) { return TRB ? ((r >> 6) * ldpi + (r & 63)) * kStage : plain_col(r) * kStage; },
+      TRB ? 64 * kStage : (int)(rpb * kStage), (int)nk, acc);
+  if (BF16 || TRA || TRB || splits > 1) {
     // accumulator order: [expert][split][tile][wave][tb][nb][i][lane][4]
     float* frag = ws + (((int64_t)e * splits + sp) * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
                   wave * (kTile * kTile / 4);
@@ -1744,6 +1752,58 @@ int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, in
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
   hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  return status();
+}
+
+// ---- the grouped weight gradient with row K-slab operands ----
+int64_t sfp8_moe_wgrad_rows_workspace_floats(int64_t M, int64_t N, int64_t E) {
+  return E * sfp8_moe_wgrad_splits(M, N, E) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
+}
+
+int sfp8_moe_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b, int fmt_b, int b_rows, int64_t M,
+                             int64_t N, int64_t E, const int* plan, int64_t ldp, const float* sa, const float* sb,
+                             float* out, float* ws, int64_t ws_floats, void* stream) {
+  if (!a || !b || !plan || !sa || !sb || !out || !ws) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || E <= 0 || N % 4 || ldp <= 0 || ldp % kTile || !(a_rows || b_rows)) return kErrBadShape;
+  if ((a_rows && M % 64) || (b_rows && N % 64)) return kErrBadShape;
+  if (fmt_a != kFmtE5M2 || fmt_b != kFmtE4M3) return kErrBadShape;
+  if (!fits32(slab_rows(M), ldp) || !fits32(slab_rows(N), ldp)) return kErrBadShape;
+  if (!al16(a) || !al16(b) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  const int64_t splits = sfp8_moe_wgrad_splits(M, N, E);
+  if (ws_floats < sfp8_moe_wgrad_rows_workspace_floats(M, N, E)) return kErrWorkspaceTooSmall;
+  hipStream_t st = (hipStream_t)stream;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)E);
+  int rc;
+  if (a_rows && b_rows) {
+    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, true>, kMainLds);
+    if (!rc)
+      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, true>), grid, dim3(256), kMainLds, st,
+                         (const uint8_t*)a, (const uint8_t*)b, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
+                         (int)splits);
+  } else if (a_rows) {
+    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, false>, kMainLds);
+    if (!rc)
+      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, false>), grid, dim3(256), kMainLds, st,
+                         (const uint8_t*)a, (const uint8_t*)b, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
+                         (int)splits);
+  } else {
+    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, true>, kMainLds);
+    if (!rc)
+      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, true>), grid, dim3(256), kMainLds, st,
+                         (const uint8_t*)a, (const uint8_t*)b, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
+                         (int)splits);
+  }
+  if (rc) return rc;
+  rc = status();
+  if (rc) return rc;
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  if (b_rows)
+    hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st,
+                       ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st,
+                       ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
 

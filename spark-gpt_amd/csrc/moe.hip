@@ -64,9 +64,10 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ o
 // Gathered rows -> fp8 in padded expert order.  Padded row p of tile
 // t = p / 256 takes source row map[urow(t) + j] (token gather; map == null:
 // urow(t) + j) for j = p % 256 < rows(t), else zeros.  Writes
-//   q = fmt(clamp(src * scale[sslot]))  as the K-slab of [ldp, D] (xs,
-//   optional: the gate/up GEMM's A operand) and as the token-contiguous
-//   K-slab of [D, ldp] (xt: the weight gradients' operand),
+//   q = fmt(clamp(src * scale[sslot]))  as the K-slab of [ldp, D] (xs: the
+//   gate/up GEMM's A operand, and a weight gradient's through transposing
+//   reads) and/or as the token-contiguous K-slab of [D, ldp] (xt: a weight
+//   gradient's plain operand),
 //   amax[aslot] = max |src| over the gathered rows.
 // A work-group takes 64 padded rows; columns go in chunks of up to 512 (the
 // last one ragged), staged in a 17 KiB LDS tile (eight work-groups per CU)
@@ -143,13 +144,15 @@ __global__ __launch_bounds__(256) void moe_rows_quant_kernel(
           if (xs)
             *reinterpret_cast<intx2*>(xs + ((cc >> 6) + c) * ldp * 64 + (p0 + r) * 64 + 8 * k) =
                 intx2{(int)lo, (int)hi};
-          *reinterpret_cast<intx2*>(tile + r * stride + 64 * c + 8 * k) = intx2{(int)lo, (int)hi};
+          if (xt) *reinterpret_cast<intx2*>(tile + r * stride + 64 * c + 8 * k) = intx2{(int)lo, (int)hi};
         }
       }
     }
-    __syncthreads();
-    lds_rows_store_slab_tr<kRqRows>(tile, C, stride, xt, cp, p0, cc);
-    __syncthreads();  // the next chunk overwrites the tile
+    if (xt) {  // work-group uniform
+      __syncthreads();
+      lds_rows_store_slab_tr<kRqRows>(tile, C, stride, xt, cp, p0, cc);
+      __syncthreads();  // the next chunk overwrites the tile
+    }
   }
   block_amax_atomic<4>(m, red, amax + aslot);
 }
@@ -229,7 +232,7 @@ int sfp8_moe_plan(const int* offsets, int64_t E, int64_t R, int* plan, int64_t p
 int sfp8_moe_rows_quant(const void* src, int64_t nsrc, int64_t D, const int64_t* map, int64_t nmap,
                         const int* plan, int64_t ldp, const float* scale, int sslot, float* amax, int aslot,
                         int fmt, void* xs, void* xt, void* stream) {
-  if (!scale || !amax || !plan || (ldp > 0 && !xt) || (nsrc > 0 && !src)) return kErrNullPointer;
+  if (!scale || !amax || !plan || (ldp > 0 && !xs && !xt) || (nsrc > 0 && !src)) return kErrNullPointer;
   if (D <= 0 || D % 128 || ldp < 0 || ldp % 256 || nsrc < 0 || nmap < 0) return kErrBadShape;
   if (sslot < 0 || sslot > 4 || aslot < 0 || aslot > 4 || (fmt != kFmtE4M3 && fmt != kFmtE5M2) ||
       (xs && fmt != kFmtE4M3))
@@ -237,7 +240,7 @@ int sfp8_moe_rows_quant(const void* src, int64_t nsrc, int64_t D, const int64_t*
   if (!moe_al16(src) || !moe_al16(xs) || !moe_al16(xt)) return kErrBadAlignment;
   if (ldp == 0) return kOk;
   const int64_t C = D < kRqChunk ? D : kRqChunk;
-  const size_t lds = (size_t)kRqRows * (C + 16);
+  const size_t lds = xt ? (size_t)kRqRows * (C + 16) : 0;  // the transposing tile
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)(ldp / kRqRows));
   const int rc = fmt == kFmtE4M3 ? moe_allow_lds(moe_rows_quant_kernel<kFmtE4M3>, lds)

@@ -54,15 +54,15 @@ class _FP8Experts(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_gu, w_d, token_index, inverse_permutation, offsets, top_k, scale, amax):
-        out, plan, x8t, gu8, h8t = torch.ops.sparkfp8.moe_fwd(x, w_gu, w_d, token_index, offsets, scale, amax)
-        ctx.save_for_backward(w_gu, w_d, plan, x8t, gu8, h8t, inverse_permutation, scale, amax)
+        out, plan, x8, gu8, h8 = torch.ops.sparkfp8.moe_fwd(x, w_gu, w_d, token_index, offsets, scale, amax)
+        ctx.save_for_backward(w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, scale, amax)
         ctx.shape = (x.shape[0], int(top_k))
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        w_gu, w_d, plan, x8t, gu8, h8t, inverse_permutation, scale, amax = ctx.saved_tensors
+        w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, scale, amax = ctx.saved_tensors
         T, top_k = ctx.shape
-        dxn, dw_gu, dw_d = torch.ops.sparkfp8.moe_bwd(dout, w_gu, w_d, plan, x8t, gu8, h8t, inverse_permutation, T,
+        dxn, dw_gu, dw_d = torch.ops.sparkfp8.moe_bwd(dout, w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, T,
                                                       top_k, scale, amax)
         return dxn, dw_gu, dw_d, None, None, None, None, None, None

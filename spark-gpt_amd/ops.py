@@ -322,21 +322,22 @@ def moe_plan(offsets: torch.Tensor, R: int) -> torch.Tensor:
 
 
 def moe_rows_quant(src: torch.Tensor, index, plan: torch.Tensor, ldp: int, scale, sslot: int, amax, aslot: int,
-                   fmt: int, with_rows: bool):
+                   fmt: int, with_rows: bool, with_copy: bool = True):
     """fp8 copies of gathered rows in padded expert order: (xs, xt) = (K-slab of
-    [ldp, D] or None, token-contiguous K-slab of [D, ldp]); row u of the expert
-    order is src[index[u]] (or src[u] without index)."""
+    [ldp, D] or None, token-contiguous K-slab of [D, ldp] or None); row u of
+    the expert order is src[index[u]] (or src[u] without index)."""
     _cuda_contig("src", src, torch.bfloat16, 2)
     n, D = src.shape
     dt = E4M3 if fmt == FMT_E4M3 else E5M2
+    _need(with_rows or with_copy, "at least one output layout")
     xs = kslab_empty(ldp, D, E4M3, src.device) if with_rows else None
-    xt = kslab_empty(D, ldp, dt, src.device)
+    xt = kslab_empty(D, ldp, dt, src.device) if with_copy else None
     idx = None
     if index is not None:
         _need(index.is_cuda and index.dtype == torch.int64, "row index must be an int64 device tensor")
         idx = index.contiguous()
     _lib.call("sfp8_moe_rows_quant", src.data_ptr(), n, D, _lib.ptr(idx), 0 if idx is None else idx.numel(),
-              plan.data_ptr(), ldp, scale.data_ptr(), sslot, amax.data_ptr(), aslot, fmt, _lib.ptr(xs), xt.data_ptr(),
+              plan.data_ptr(), ldp, scale.data_ptr(), sslot, amax.data_ptr(), aslot, fmt, _lib.ptr(xs), _lib.ptr(xt),
               _lib.stream_of(src))
     return xs, xt
 
@@ -358,17 +359,17 @@ def weight_quant_experts(w: torch.Tensor, q_out: torch.Tensor, *, w8: bool = Tru
     return o8, o8t, obt
 
 
-def moe_gateup_swiglu_fwd(x8, w8, plan, scale, q_gu, amax, I: int):
+def moe_gateup_swiglu_fwd(x8, w8, plan, scale, q_gu, amax, I: int, *, copy: bool = True):
     """(gu8, h8, h8t) over padded expert order; x8 the K-slab of [ldp, D], w8
-    the stacked per-expert K-slabs of [2I, D]."""
+    the stacked per-expert K-slabs of [2I, D].  copy=False skips h8t (None)."""
     D, ldp = x8.shape[0] * SLAB, x8.shape[1]
     E = w8.shape[0]
     dev = x8.device
     gu8 = kslab_empty(ldp, 2 * I, E4M3, dev)
     h8 = kslab_empty(ldp, I, E4M3, dev)
-    h8t = kslab_empty(I, ldp, E4M3, dev)
+    h8t = kslab_empty(I, ldp, E4M3, dev) if copy else None
     _lib.call("sfp8_moe_gemm_gateup_swiglu_fwd", x8.data_ptr(), w8.data_ptr(), E, D, I, plan.data_ptr(), ldp,
-              scale.data_ptr(), q_gu.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), h8t.data_ptr(),
+              scale.data_ptr(), q_gu.data_ptr(), amax.data_ptr(), gu8.data_ptr(), h8.data_ptr(), _lib.ptr(h8t),
               _lib.stream_of(x8))
     return gu8, h8, h8t
 
@@ -383,18 +384,19 @@ def moe_down_fwd(h8, wd8, plan, scale, q_d, R: int, D: int):
     return out
 
 
-def moe_down_dgrad_swiglu(dout, wdt, gu8, plan, scale, amax):
+def moe_down_dgrad_swiglu(dout, wdt, gu8, plan, scale, amax, *, copy: bool = True):
     """(dgu8, dgu8t) e5m2 over padded expert order; dout [R, D] bf16 expert-order
-    rows, wdt the stacked bf16 K-slabs of W_down[e]^T."""
+    rows, wdt the stacked bf16 K-slabs of W_down[e]^T.  copy=False skips dgu8t
+    (None)."""
     _cuda_contig("dout", dout, torch.bfloat16, 2)
     R, D = dout.shape
     I2, ldp = gu8.shape[0] * SLAB, gu8.shape[1]
     E = wdt.shape[0]
     dev = dout.device
     dgu8 = kslab_empty(ldp, I2, E5M2, dev)
-    dgu8t = kslab_empty(I2, ldp, E5M2, dev)
+    dgu8t = kslab_empty(I2, ldp, E5M2, dev) if copy else None
     _lib.call("sfp8_moe_gemm_down_dgrad_swiglu", dout.data_ptr(), wdt.data_ptr(), gu8.data_ptr(), E, D, I2 // 2, R,
-              plan.data_ptr(), ldp, scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), dgu8t.data_ptr(),
+              plan.data_ptr(), ldp, scale.data_ptr(), amax.data_ptr(), dgu8.data_ptr(), _lib.ptr(dgu8t),
               _lib.stream_of(dout))
     return dgu8, dgu8t
 
@@ -420,6 +422,26 @@ def moe_wgrad(at, bt, M: int, N: int, E: int, plan, sa, sb):
     ws = torch.empty(max(nws, 1), dtype=torch.float32, device=at.device)
     _lib.call("sfp8_moe_gemm_wgrad", at.data_ptr(), FMT_E5M2, bt.data_ptr(), FMT_E4M3, M, N, E, plan.data_ptr(), ldp,
               sa.data_ptr(), sb.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(at))
+    return out
+
+
+def moe_wgrad_rows(a8, b8, M: int, N: int, E: int, plan, sa, sb, *, a_rows: bool = True, b_rows: bool = True):
+    """moe_wgrad with a8 (e5m2) and/or b8 (e4m3) the row K-slab of the
+    expert-order activation over padded rows ([rows/64, ldp, 64]: read
+    through transposing LDS reads) instead of the token-contiguous copy."""
+    _cuda_contig("a8", a8, E5M2, 3)
+    _cuda_contig("b8", b8, E4M3, 3)
+    _need(a_rows or b_rows, "at least one row K-slab operand (else use moe_wgrad)")
+    ldp = a8.shape[1] if a_rows else a8.shape[0] * SLAB
+    _need((b8.shape[1] if b_rows else b8.shape[0] * SLAB) == ldp, "a8, b8 must cover the same padded rows")
+    _need(not a_rows or a8.shape[0] * SLAB == M, "a8 must be the row K-slab of [ldp, M]")
+    _need(not b_rows or b8.shape[0] * SLAB == N, "b8 must be the row K-slab of [ldp, N]")
+    out = torch.empty(E, M, N, dtype=torch.float32, device=a8.device)
+    nws = _lib.query("sfp8_moe_wgrad_rows_workspace_floats", M, N, E)
+    ws = torch.empty(max(nws, 1), dtype=torch.float32, device=a8.device)
+    _lib.call("sfp8_moe_gemm_wgrad_rows", a8.data_ptr(), FMT_E5M2, int(a_rows), b8.data_ptr(), FMT_E4M3, int(b_rows),
+              M, N, E, plan.data_ptr(), ldp, sa.data_ptr(), sb.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+              _lib.stream_of(a8))
     return out
 
 

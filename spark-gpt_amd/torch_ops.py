@@ -197,18 +197,20 @@ def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax)
 def moe_fwd(x: Tensor, w_gu: Tensor, w_d: Tensor, token_index: Tensor, offsets: Tensor, scale: Tensor,
             amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """_FP8Experts.forward (train.py:1552-1587): out [R, D] bf16 expert-order
-    rows (unweighted), then for the backward the plan, x8t, gu8 and h8t (over
-    padded expert order).  Quantized expert weights stay in the weight cache."""
+    rows (unweighted), then for the backward the plan, x8, gu8 and h8 (K-slabs
+    over padded expert order; the weight gradients read x8 and h8 through
+    transposing LDS reads).  Quantized expert weights stay in the weight
+    cache."""
     x = x.contiguous()
     R = token_index.numel()
     E, I2, D = w_gu.shape
     plan = ops.moe_plan(offsets, R)
     ldp = ops.moe_padded_rows(R, E)
-    x8, x8t = ops.moe_rows_quant(x, token_index, plan, ldp, scale, 0, amax, 0, ops.FMT_E4M3, True)
+    x8, _ = ops.moe_rows_quant(x, token_index, plan, ldp, scale, 0, amax, 0, ops.FMT_E4M3, True, False)
     w8, _w8t, wd8, _wdt, wscale = cached_weights(w_gu, w_d)
-    gu8, h8, h8t = ops.moe_gateup_swiglu_fwd(x8, w8, plan, scale, wscale[0], amax, I2 // 2)
+    gu8, h8, _ = ops.moe_gateup_swiglu_fwd(x8, w8, plan, scale, wscale[0], amax, I2 // 2, copy=False)
     out = ops.moe_down_fwd(h8, wd8, plan, scale, wscale[1], R, D)
-    return out, plan, x8t, gu8, h8t
+    return out, plan, x8, gu8, h8
 
 
 @moe_fwd.register_fake
@@ -218,13 +220,13 @@ def _moe_fwd_fake(x, w_gu, w_d, token_index, offsets, scale, amax):
     ldp = 256 * ((R + 255) // 256 + E)
     return (x.new_empty((R, D), dtype=torch.bfloat16),
             x.new_empty((8 + 2 * E + 3 * (ldp // 256),), dtype=torch.int32),
-            x.new_empty(ops.kslab_shape(D, ldp, E4M3), dtype=E4M3),
+            x.new_empty(ops.kslab_shape(ldp, D, E4M3), dtype=E4M3),
             x.new_empty(ops.kslab_shape(ldp, I2, E4M3), dtype=E4M3),
-            x.new_empty(ops.kslab_shape(I2 // 2, ldp, E4M3), dtype=E4M3))
+            x.new_empty(ops.kslab_shape(ldp, I2 // 2, E4M3), dtype=E4M3))
 
 
 @torch.library.custom_op("sparkfp8::moe_bwd", mutates_args={"amax"})
-def moe_bwd(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8t: Tensor, gu8: Tensor, h8t: Tensor,
+def moe_bwd(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8: Tensor, gu8: Tensor, h8: Tensor,
             inverse_permutation: Tensor, T: int, top_k: int, scale: Tensor,
             amax: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """_FP8Experts.backward (train.py:1589-1605): (dx [T, D] bf16 summed over
@@ -238,17 +240,18 @@ def moe_bwd(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8t: Tensor, 
     _w8, w8t, _wd8, wdt, wscale = cached_weights(w_gu, w_d)
     # e5m2 dout over padded expert order (the down wgrad's operand) and amax[4]
     _, dout8t = ops.moe_rows_quant(dout, None, plan, ldp, scale, 4, amax, 4, ops.FMT_E5M2, False)
-    dgu8, dgu8t = ops.moe_down_dgrad_swiglu(dout, wdt, gu8, plan, scale, amax)
+    dgu8, _ = ops.moe_down_dgrad_swiglu(dout, wdt, gu8, plan, scale, amax, copy=False)
     dx = ops.moe_gateup_dgrad(dgu8, w8t, plan, scale, wscale[0], R, D)
-    del dgu8
-    dw_gu = ops.moe_wgrad(dgu8t, x8t, I2, D, E, plan, scale[3:4], scale[0:1])
-    dw_d = ops.moe_wgrad(dout8t, h8t, D, I2 // 2, E, plan, scale[4:5], scale[2:3])
+    # d_gu8, x8 and h8 read as their K-slabs (transposing LDS reads), dout8t
+    # token-contiguous, as in the dense block
+    dw_gu = ops.moe_wgrad_rows(dgu8, x8, I2, D, E, plan, scale[3:4], scale[0:1])
+    dw_d = ops.moe_wgrad_rows(dout8t, h8, D, I2 // 2, E, plan, scale[4:5], scale[2:3], a_rows=False)
     dxn = ops.moe_topk_sum(dx, inverse_permutation, T, top_k)
     return dxn, dw_gu, dw_d
 
 
 @moe_bwd.register_fake
-def _moe_bwd_fake(dout, w_gu, w_d, plan, x8t, gu8, h8t, inverse_permutation, T, top_k, scale, amax):
+def _moe_bwd_fake(dout, w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, T, top_k, scale, amax):
     E, I2, D = w_gu.shape
     return (dout.new_empty((T, D), dtype=torch.bfloat16),
             dout.new_empty((E, I2, D), dtype=torch.float32),

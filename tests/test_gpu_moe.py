@@ -96,6 +96,11 @@ def test_gather_quant_bit_exact(dev, D):
     assert torch.equal(gt.t(), got)
     finite = x[tok].float().abs()
     assert amax[0].item() == finite[~torch.isnan(finite)].max().item()
+    # the row K-slab alone (no token-contiguous copy): the same bytes and amax
+    amax2 = torch.zeros(5, device=dev)
+    x8b, none = sg.ops.moe_rows_quant(x.to(dev), tok.to(dev), plan, ldp, scale, 0, amax2, 0, sg.ops.FMT_E4M3, True,
+                                      False)
+    assert none is None and torch.equal(_u8(x8b), _u8(x8)) and torch.equal(amax2, amax)
 
 
 def test_dout_quant_e5m2_bit_exact(dev):
@@ -122,6 +127,38 @@ def test_dout_quant_e5m2_bit_exact(dev):
     assert torch.equal(gt.t()[valid], ref[rows[valid]])
     assert torch.all(gt[:, ~valid] == 0)
     assert amax[4].item() == dout.float().abs().max().item() and amax[:4].sum().item() == 0
+
+
+@pytest.mark.parametrize("M_,N_,counts", [(1536, 1024, [300, 0, 513, 1, 0, 186]), (1024, 768, [4000, 2600, 0, 900]),
+                                           (256, 320, [70])])
+def test_moe_wgrad_rows_equals_token_contiguous(dev, M_, N_, counts):
+    """The grouped weight gradient with row K-slab operands (transposing LDS
+    reads) gives the bytes of the one on token-contiguous copies, in every
+    layout pair; experts without rows get zeros."""
+    ops = sg.ops
+    counts = torch.tensor(counts)
+    E = counts.numel()
+    offsets = torch.cumsum(counts, 0).to(torch.int32)
+    R = int(counts.sum())
+    plan = ops.moe_plan(offsets.to(dev), R)
+    ldp = ops.moe_padded_rows(R, E)
+    rows = _padded_rows(offsets, ldp).to(dev)
+    g = torch.Generator(device=dev).manual_seed(M_ + N_ + R)
+    a = (torch.randn(ldp, M_, device=dev, generator=g) * 8).to(ops.E5M2)
+    b = (torch.randn(ldp, N_, device=dev, generator=g) * 8).to(ops.E4M3)
+    a.view(torch.uint8)[rows < 0] = 0  # padding rows are zeros, as the producers write them
+    b.view(torch.uint8)[rows < 0] = 0
+    a_rows, b_rows = ops.to_slab(a), ops.to_slab(b)                                # [cols/64, ldp, 64]
+    a_t, b_t = ops.to_slab(a.t().contiguous()), ops.to_slab(b.t().contiguous())    # [ldp/64, cols, 64]
+    sa = torch.tensor([2.0 ** 4], device=dev)
+    sb = torch.tensor([2.0 ** -2], device=dev)
+    ref = ops.moe_wgrad(a_t, b_t, M_, N_, E, plan, sa, sb)
+    assert torch.equal(ops.moe_wgrad_rows(a_rows, b_rows, M_, N_, E, plan, sa, sb), ref)
+    assert torch.equal(ops.moe_wgrad_rows(a_rows, b_t, M_, N_, E, plan, sa, sb, b_rows=False), ref)
+    assert torch.equal(ops.moe_wgrad_rows(a_t, b_rows, M_, N_, E, plan, sa, sb, a_rows=False), ref)
+    for e in range(E):
+        if int(counts[e]) == 0:
+            assert torch.all(ref[e] == 0)
 
 
 def _make(dev, E, D, I, seed, std=None):
