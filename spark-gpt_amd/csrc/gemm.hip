@@ -1398,20 +1398,31 @@ __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __res
                                                               const float* __restrict__ sb, float* __restrict__ grad,
                                                               float* __restrict__ v, uint16_t* __restrict__ u,
                                                               float w_v, float w_u1) {
+  // Work-group b sums the b-th 256 float4s of every split: a 32 x 32 block of
+  // dW (fixed tile, wave, row block tb, column block nb), passed through LDS
+  // so that eight lanes then cover 32 contiguous columns of one row of v, u
+  // and grad (n4 is a multiple of 256: no partial work-group).
+  __shared__ floatx4 blk[32][9];
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (q >= n4) return;
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
-  const int lane = (int)(q & 63), i = (int)(q >> 6) & 3, nb = (int)(q >> 8) & 3, tb = (int)(q >> 10) & 3;
-  const int wave = (int)(q >> 12) & 3;
-  const int64_t tile = q >> 14;
+  const int lane = threadIdx.x & 63, i = threadIdx.x >> 6;
+  const int64_t b = blockIdx.x;
+  const int nb = (int)(b & 3), tb = (int)(b >> 2) & 3, wave = (int)(b >> 4) & 3;
+  const int64_t tile = b >> 6;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
-  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
-  const int64_t n = tn * kTile + 128 * (wave >> 1) +
-                    (TR_B ? 32 * nb + 8 * i + 4 * (lane >> 5) : 64 * (lane >> 5) + 16 * nb + 4 * i);
+  // local column (0..31) of this thread's float4 in the block
+  const int c = TR_B ? 8 * i + 4 * (lane >> 5) : 16 * (lane >> 5) + 4 * i;
+  blk[lane & 31][c >> 2] = acc * (1.0f / (sa[0] * sb[0]));
+  __syncthreads();
+  const int r = threadIdx.x >> 3, c2 = 4 * (threadIdx.x & 7);
+  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + r;
+  // local column -> output column: TR_B blocks are 32 contiguous columns,
+  // the plain layout's two 16-column halves lie 64 columns apart
+  const int64_t n = tn * kTile + 128 * (wave >> 1) + (TR_B ? 32 * nb + c2 : 16 * nb + (c2 < 16 ? c2 : 48 + c2));
   if (m >= M || n >= N) return;
-  const floatx4 d = acc * (1.0f / (sa[0] * sb[0]));
+  const floatx4 d = blk[r][c2 >> 2];
   if (grad) *reinterpret_cast<floatx4*>(grad + m * N + n) = d;
   floatx4 vv = *reinterpret_cast<const floatx4*>(v + m * N + n);
   uint32_t uu[2];
