@@ -457,7 +457,8 @@ def bf16_launch_name(sym: str, a) -> str:
     return {"sfp8_bf16_weight_slabs": "bf16_weight_fold", "sfp8_bf16_rows_prep": "bf16_rows_prep",
             "sfp8_bf16_gemm_swiglu_fwd": "bf16_gateup_swiglu_fwd", "sfp8_bf16_swiglu_bwd": "bf16_swiglu_bwd_rows",
             "sfp8_bf16_gemm": "bf16_gateup_dgrad", "sfp8_bf16_norm_dh": "bf16_norm_bwd",
-            "sfp8_bf16_gemm_wgrad": "bf16_wgrad_gateup", "sfp8_bf16_fold_grads": "bf16_fold_grads"}.get(sym, sym)
+            "sfp8_bf16_gemm_wgrad": "bf16_wgrad_gateup", "sfp8_bf16_gemm_wgrad_rows": "bf16_wgrad_gateup",
+            "sfp8_bf16_fold_grads": "bf16_fold_grads"}.get(sym, sym)
 
 
 def time_bf16(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
@@ -500,9 +501,9 @@ def time_bf16(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
     ms = (time.perf_counter() - t0) * 1e3 / steps
     work = {
         "bf16_weight_fold": (None, 16.0 * I * D),
-        "bf16_rows_prep": (None, 4.0 * T * D + 4 * T),
+        "bf16_rows_prep": (None, 2.0 * T * D + 4 * T),
         "bf16_gateup_swiglu_fwd": (4.0 * T * D * I, None),
-        "bf16_swiglu_bwd_rows": (None, 14.0 * T * I),
+        "bf16_swiglu_bwd_rows": (None, 10.0 * T * I),
         "bf16_gateup_dgrad": (4.0 * T * D * I, None),
         "bf16_norm_bwd": (None, 6.0 * T * D),
         "bf16_wgrad_gateup": (4.0 * T * D * I, None),

@@ -335,10 +335,11 @@ int sfp8_bf16_weight_slabs(const void* w, int src_bf16, const float* nw, int64_t
                            void* wt, void* stream);
 
 /* x [nsrc, D] bf16 rows in padded order (plan, or rows 0..nsrc-1 when plan
- * is NULL) -> xt, the token-contiguous bf16 K-slab of x^T over ldp rows (the
- * weight gradient's operand; zeros past the rows), and with rstd (plan NULL
- * only) rstd[t] = 1 / sqrt(sum x^2 / D + eps): the row statistic
- * _swiglu_gemm_kernel accumulates in its NORM mode (train.py:1689-1700). */
+ * is NULL) -> xt (optional), the token-contiguous bf16 K-slab of x^T over ldp
+ * rows (a weight gradient's plain operand; zeros past the rows), and with
+ * rstd (plan NULL only) rstd[t] = 1 / sqrt(sum x^2 / D + eps): the row
+ * statistic _swiglu_gemm_kernel accumulates in its NORM mode
+ * (train.py:1689-1700).  At least one of xt, rstd. */
 int sfp8_bf16_rows_prep(const void* x, int64_t nsrc, int64_t D, const int* plan, int64_t ldp, float eps, float* rstd,
                         void* xt, void* stream);
 
@@ -359,7 +360,8 @@ int sfp8_bf16_moe_gemm_swiglu_fwd(const void* x, const void* w, int64_t E, int64
  * _swiglu_dgrad_kernel and _swiglu_wgrad_kernel (train.py:1899-2026), once
  * for both: G' = [bf16(dh u sig (1 + g (1 - sig))) | bf16(dh g sig)] with
  * dh = dout * rstd (rstd NULL: 1), written as gs = its bf16 K-slab over ldp
- * padded rows and gt = the token-contiguous K-slab of G'^T; padding zero. */
+ * padded rows and (optionally) gt = the token-contiguous K-slab of G'^T;
+ * padding zero. */
 int sfp8_bf16_swiglu_bwd(const void* gu, const void* dout, int64_t nsrc, int64_t I, const float* rstd,
                          const int* plan, int64_t ldp, void* gs, void* gt, void* stream);
 
@@ -392,6 +394,22 @@ int sfp8_bf16_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, i
 int64_t sfp8_bf16_moe_wgrad_workspace_floats(int64_t M, int64_t N, int64_t E);
 int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, int64_t E, const int* plan,
                              int64_t ldp, void* out, float* ws, int64_t ws_floats, void* stream);
+
+/* The bf16 weight gradients with A read from gs, the bf16 K-slab of G'
+ * over the padded rows (the dgrad's A operand, [M/32][ldt][64] bytes),
+ * through transposing LDS reads (ds_read_b64_tr_b16), so that no
+ * token-contiguous copy of G' is written; bytes equal to
+ * sfp8_bf16_gemm_wgrad / sfp8_bf16_moe_gemm_wgrad on the copies.
+ * Dense: B is x itself with x_rows != 0, row-major [T, N] bf16 (rows
+ * T..ldt-1 read as zero), also transposed on read (N % 32 == 0), or with
+ * x_rows == 0 the token-contiguous K-slab of x^T over ldt tokens
+ * (sfp8_bf16_rows_prep); M % 32 == 0, T * N * 2 < 2^31; ws as for
+ * sfp8_bf16_gemm_wgrad.  Grouped: B is the token-contiguous K-slab of x^T
+ * over the padded rows; ws as for sfp8_bf16_moe_gemm_wgrad. */
+int sfp8_bf16_gemm_wgrad_rows(const void* gs, const void* x, int x_rows, int64_t M, int64_t N, int64_t T, int64_t ldt,
+                              void* out, float* ws, int64_t ws_floats, void* stream);
+int sfp8_bf16_moe_gemm_wgrad_rows(const void* gs, const void* bt, int64_t M, int64_t N, int64_t E, const int* plan,
+                                  int64_t ldp, void* out, float* ws, int64_t ws_floats, void* stream);
 
 /* _NormSwiGLU's fold of the weight gradient (train.py:2129-2131): dw =
  * f32(dwp) * nw (fp32 [M, N]) and dnw[n] = sum over m of f32(dwp[m, n]) *

@@ -68,6 +68,8 @@ SIGNATURES = {
     "sfp8_bf16_gemm_wgrad": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "sfp8_bf16_moe_wgrad_workspace_floats": (_I64, [_I64, _I64, _I64]),
     "sfp8_bf16_moe_gemm_wgrad": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
+    "sfp8_bf16_gemm_wgrad_rows": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+    "sfp8_bf16_moe_gemm_wgrad_rows": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P]),
     "sfp8_bf16_fold_partials": (_I64, [_I64, _I64]),
     "sfp8_bf16_fold_grads": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
     "sfp8_wgrad_rows_workspace_floats": (_I64, [_I64, _I64, _I64]),

@@ -123,9 +123,10 @@ __global__ __launch_bounds__(256) void bf16_weight_slabs_kernel(const void* __re
   }
 }
 
-// x rows ([nsrc, D] bf16) in padded order -> xt, the token-contiguous bf16
-// K-slab of x^T over the grid's 64 * gridDim.x padded rows
-// ([2 ldp / 64][slab_rows(D)][64]: the weight gradient's B operand), and,
+// x rows ([nsrc, D] bf16) in padded order -> xt (optional), the
+// token-contiguous bf16 K-slab of x^T over the grid's 64 * gridDim.x padded
+// rows ([2 ldp / 64][slab_rows(D)][64]: a weight gradient's plain B operand),
+// and,
 // when rstd is given (no plan), rstd[p] = 1 / sqrt(sum_d x[p, d]^2 / D + eps)
 // for p < nsrc (the row scale of _swiglu_gemm_kernel's NORM mode,
 // train.py:1689-1700; the sum of squares is exact, in fp64).  A work-group
@@ -154,8 +155,9 @@ __global__ __launch_bounds__(256) void bf16_rows_prep_kernel(const uint16_t* __r
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss[k] = __builtin_fma((double)f[j], (double)f[j], ss[k]);  // exact
       const uint32_t o[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
-      tr_put8(tile, c8, r, o);
+      if (xt) tr_put8(tile, c8, r, o);
     }
+    if (!xt) continue;  // work-group uniform
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -188,8 +190,9 @@ __global__ __launch_bounds__(256) void bf16_rows_prep_kernel(const uint16_t* __r
 //   sig = sigmoid(g),
 //   d_gate = bf16(dh * u * (sig * (1 + g * (1 - sig)))),  d_up = bf16(dh * g * sig).
 // G' = [d_gate | d_up] goes to gs, its bf16 K-slab over the grid's ldp padded
-// rows ([4I/64][ldp][64]: the dgrad's A), and to gt, the token-contiguous
-// K-slab of G'^T ([2 ldp / 64][slab_rows(2I)][64]: the weight gradient's A).
+// rows ([4I/64][ldp][64]: the dgrad's A, and the weight gradient's through
+// transposing reads), and optionally to gt, the token-contiguous K-slab of
+// G'^T ([2 ldp / 64][slab_rows(2I)][64]: a weight gradient's plain A).
 // Padding rows are zero.  Work-group (pb, ib): padded rows 64 pb..,
 // columns 64 ib.. of each half.  I % 64 == 0.
 __global__ __launch_bounds__(256) void bf16_swiglu_bwd_kernel(const uint16_t* __restrict__ gu,
@@ -238,9 +241,12 @@ __global__ __launch_bounds__(256) void bf16_swiglu_bwd_kernel(const uint16_t* __
     }
     *reinterpret_cast<intx4*>(gs + bslab(p0 + r, i, ldp)) = intx4{(int)og[0], (int)og[1], (int)og[2], (int)og[3]};
     *reinterpret_cast<intx4*>(gs + bslab(p0 + r, I + i, ldp)) = intx4{(int)ou[0], (int)ou[1], (int)ou[2], (int)ou[3]};
-    tr_put8(tile[0], c8, r, og);
-    tr_put8(tile[1], c8, r, ou);
+    if (gt) {
+      tr_put8(tile[0], c8, r, og);
+      tr_put8(tile[1], c8, r, ou);
+    }
   }
+  if (!gt) return;  // work-group uniform
   __syncthreads();
   const int64_t ip = slab_rows(2 * I);
 #pragma unroll
@@ -369,7 +375,7 @@ int sfp8_bf16_weight_slabs(const void* w, int src_bf16, const float* nw, int64_t
 
 int sfp8_bf16_rows_prep(const void* x, int64_t nsrc, int64_t D, const int* plan, int64_t ldp, float eps, float* rstd,
                         void* xt, void* stream) {
-  if ((ldp > 0 && !xt) || (nsrc > 0 && !x)) return kErrNullPointer;
+  if ((ldp > 0 && !xt && !rstd) || (nsrc > 0 && !x)) return kErrNullPointer;
   if (rstd && plan) return kErrBadShape;
   if (nsrc < 0 || D <= 0 || D % 64 || ldp < 0 || ldp % 256 || (!plan && ldp < nsrc)) return kErrBadShape;
   if (!bf_al16(x) || !bf_al16(xt)) return kErrBadAlignment;
@@ -381,7 +387,7 @@ int sfp8_bf16_rows_prep(const void* x, int64_t nsrc, int64_t D, const int* plan,
 
 int sfp8_bf16_swiglu_bwd(const void* gu, const void* dout, int64_t nsrc, int64_t I, const float* rstd,
                          const int* plan, int64_t ldp, void* gs, void* gt, void* stream) {
-  if ((ldp > 0 && (!gs || !gt)) || (nsrc > 0 && (!gu || !dout))) return kErrNullPointer;
+  if ((ldp > 0 && !gs) || (nsrc > 0 && (!gu || !dout))) return kErrNullPointer;
   if (nsrc < 0 || I <= 0 || I % 64 || ldp < 0 || ldp % 256 || (!plan && ldp < nsrc)) return kErrBadShape;
   if (!bf_al16(gu) || !bf_al16(dout) || !bf_al16(gs) || !bf_al16(gt)) return kErrBadAlignment;
   if (ldp == 0) return kOk;

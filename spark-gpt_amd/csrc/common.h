@@ -112,6 +112,14 @@ SFP8_DEV intx2 lds_read_tr8(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) intx2*)p);
 }
 
+// ds_read_b64_tr_b16: in each 16-lane group, lane 4a + b receives element b
+// of the 4 16-bit elements addressed by lanes a, a + 4, a + 8, a + 12.
+SFP8_DEV intx2 lds_read_tr16(const uint8_t* p) {
+  typedef short shortx4 __attribute__((ext_vector_type(4)));
+  const shortx4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)p);
+  return __builtin_bit_cast(intx2, t);
+}
+
 SFP8_DEV uint32_t pack4_e5m2(float a, float b, float c, float d) {
   int v = 0;
   v = __builtin_amdgcn_cvt_pk_bf8_f32(__builtin_amdgcn_fmed3f(a, -kE5M2Max, kE5M2Max),

@@ -1028,11 +1028,20 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
 // reads (MainLoop TR_A / TR_B); the partials then always go to `out` as the
 // workspace, in the same order (with TRB the columns unpermuted:
 // splitk_reduce_kernel<true>).
+// Addressing of a transposed-read operand: row r of block r / 64 (fp8) or
+// r / 32 (bf16) at token t lies at base + block * bs + t * ts, and ext bytes
+// are readable from base (the rest reads as zero).  A row K-slab of [T, L]
+// over ldt tokens: ts = 64, bs = ldt * 64; row-major [T, L] rows: ts = the row
+// bytes, bs = 64, ext = T * ts.
+struct TrOp {
+  int64_t ts, bs, ext;
+};
+
 template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false>
 __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldt,
     int64_t kchunk, const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out,
-    int tiles_m, int tiles_n, int splits, int partials) {
+    int tiles_m, int tiles_n, int splits, int partials, TrOp tra, TrOp trb) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn, sp;
   split_tile_coords(blockIdx.x, tiles_m, tiles_n, splits, tm, tn, sp);
@@ -1043,21 +1052,21 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   const int64_t kb = (int64_t)sp * kchunk;
   {
     // K-slab operands: slab (kb / 64) of A starts at (kb / 64) * rpa * 64.
-    // Row K-slab (TR) operands: tile row r = token (r % 64) of the tile's
-    // 64-column slab r / 64; a 64-token stage is 4 KiB further on in every
-    // slab.
+    // TR operands (TrOp): tile row r is row r % kRows of block r / kRows at
+    // the stage's tokens; a stage (64 K bytes: kRows tokens) is kRows * ts on.
+    constexpr int kRows = BF16 ? 32 : 64;
     const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
-    const int ldti = (int)ldt;
-    const uint8_t* a0 = TRA ? at + (m0 / 64) * ldt * kStage + kb * kStage : at + (kb / kStage) * rpa * kStage + m0 * kStage;
-    const uint8_t* b0 = TRB ? bt + (n0 / 64) * ldt * kStage + kb * kStage : bt + (kb / kStage) * rpb * kStage + n0 * kStage;
-    const uint8_t* a_end = TRA ? at + (M / 64) * ldt * kStage : at + ldt * rpa;
-    const uint8_t* b_end = TRB ? bt + (N / 64) * ldt * kStage : bt + ldt * rpb;
+    const int64_t t0 = kb / (BF16 ? 2 : 1);  // first token of the split
+    const int ats = (int)tra.ts, abs_ = (int)tra.bs, bts = (int)trb.ts, bbs = (int)trb.bs;
+    const uint8_t* a0 = TRA ? at + (m0 / kRows) * tra.bs + t0 * tra.ts : at + (kb / kStage) * rpa * kStage + m0 * kStage;
+    const uint8_t* b0 = TRB ? bt + (n0 / kRows) * trb.bs + t0 * trb.ts : bt + (kb / kStage) * rpb * kStage + n0 * kStage;
+    const uint8_t* a_end = TRA ? at + tra.ext : at + ldt * rpa;
+    const uint8_t* b_end = TRB ? bt + trb.ext : bt + ldt * rpb;
     MainLoop<BF16, FMT_A, FMT_B, false, 4, kStages, 0, TRA, TRB>::run(
-        lds, a0, a_end - a0,
-        [=](int r) { return TRA ? ((r >> 6) * ldti + (r & 63)) * kStage : r * kStage; },
-        TRA ? 64 * kStage : (int)(rpa * kStage), b0, b_end - b0,
-        [=](int r) { return TRB ? ((r >> 6) * ldti + (r & 63)) * kStage : plain_col(r) * kStage; },
-        TRB ? 64 * kStage : (int)(rpb * kStage), (int)(kchunk / kStage), acc);
+        lds, a0, a_end - a0, [=](int r) { return TRA ? (r / kRows) * abs_ + (r % kRows) * ats : r * kStage; },
+        TRA ? kRows * ats : (int)(rpa * kStage), b0, b_end - b0,
+        [=](int r) { return TRB ? (r / kRows) * bbs + (r % kRows) * bts : plain_col(r) * kStage; },
+        TRB ? kRows * bts : (int)(rpb * kStage), (int)(kchunk / kStage), acc);
   }
   if (BF16 || TRA || TRB || partials) {
     // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
@@ -1127,20 +1136,23 @@ __global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
   const int64_t rpa = slab_rows(M), rpb = slab_rows(N);
   const int64_t s0 = P.pstart(e) * kBpe / kStage + k0;  // first 64-byte stage
   // Token-contiguous operands: stage s at s * rows * 64.  Row K-slab (TR)
-  // operands ([rows/64][ldp][64], as for wgrad_kernel): tile row r is token
-  // r % 64 of slab r / 64, and a 64-token stage is 4 KiB on in every slab.
-  const int ldpi = (int)ldp;
-  const uint8_t* a0 = TRA ? at + (m0 / 64) * ldp * kStage + s0 * 64 * kStage : at + s0 * rpa * kStage + m0 * kStage;
-  const uint8_t* b0 = TRB ? bt + (n0 / 64) * ldp * kStage + s0 * 64 * kStage : bt + s0 * rpb * kStage + n0 * kStage;
-  const uint8_t* a_end = TRA ? at + (M / 64) * ldp * kStage : at + ldp * rpa;
-  const uint8_t* b_end = TRB ? bt + (N / 64) * ldp * kStage : bt + ldp * rpb;
+  // operands ([rows/kRows][padded rows][64], as for wgrad_kernel): tile row r
+  // is token r % kRows of slab r / kRows, and a stage (kRows tokens) is
+  // kRows * 64 bytes on in every slab.
+  constexpr int kRows = BF16 ? 32 : 64;
+  const int64_t ldt_tok = ldp / kBpe;  // padded rows (ldp counts K bytes)
+  const int ltok = (int)ldt_tok;
+  const uint8_t* a0 = TRA ? at + (m0 / kRows) * ldt_tok * kStage + s0 * kRows * kStage : at + s0 * rpa * kStage + m0 * kStage;
+  const uint8_t* b0 = TRB ? bt + (n0 / kRows) * ldt_tok * kStage + s0 * kRows * kStage : bt + s0 * rpb * kStage + n0 * kStage;
+  const uint8_t* a_end = TRA ? at + (M / kRows) * ldt_tok * kStage : at + ldp * rpa;
+  const uint8_t* b_end = TRB ? bt + (N / kRows) * ldt_tok * kStage : bt + ldp * rpb;
   const int64_t a_bytes = nk > 0 ? a_end - a0 : 0, b_bytes = nk > 0 ? b_end - b0 : 0;
   floatx16 acc[4][4];
   MainLoop<BF16, FMT_A, FMT_B, false, 4, kStages, 0, TRA, TRB>::run(
-      lds, a0, a_bytes, [=](int r) { return TRA ? ((r >> 6) * ldpi + (r & 63)) * kStage : r * kStage; },
-      TRA ? 64 * kStage : (int)(rpa * kStage), b0, b_bytes,
-      [=](int r) { return TRB ? ((r >> 6) * ldpi + (r & 63)) * kStage : plain_col(r) * kStage; },
-      TRB ? 64 * kStage : (int)(rpb * kStage), (int)nk, acc);
+      lds, a0, a_bytes, [=](int r) { return TRA ? ((r / kRows) * ltok + (r % kRows)) * kStage : r * kStage; },
+      TRA ? kRows * kStage : (int)(rpa * kStage), b0, b_bytes,
+      [=](int r) { return TRB ? ((r / kRows) * ltok + (r % kRows)) * kStage : plain_col(r) * kStage; },
+      TRB ? kRows * kStage : (int)(rpb * kStage), (int)nk, acc);
   if (BF16 || TRA || TRB || splits > 1) {
     // accumulator order: [expert][split][tile][wave][tb][nb][i][lane][4]
     float* frag = ws + (((int64_t)e * splits + sp) * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
@@ -1363,6 +1375,7 @@ __global__ __launch_bounds__(256, 1) void bf16_gemm_kernel(
 // ascending of ws[s]) (the bf16 result of _swiglu_wgrad_kernel,
 // train.py:1983-2026), partials in wgrad_kernel's accumulator order;
 // blockIdx.y = expert of a grouped gradient (out [E, M, N]).
+template <bool TR_B = false>
 __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __restrict__ ws, int splits, int64_t n4,
                                                                 int tiles_n, int64_t M, int64_t N,
                                                                 uint16_t* __restrict__ out) {
@@ -1378,7 +1391,8 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
   const int64_t tile = q >> 14;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
   const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
-  const int64_t n = tn * kTile + 128 * (wave >> 1) + 64 * (lane >> 5) + 16 * nb + 4 * i;
+  const int64_t n = tn * kTile + 128 * (wave >> 1) +
+                    (TR_B ? 32 * nb + 8 * i + 4 * (lane >> 5) : 64 * (lane >> 5) + 16 * nb + 4 * i);
   if (m < M && n < N)  // N % 4 == 0: the 4 values are wholly inside or past the row
     *reinterpret_cast<intx2*>(out + m * N + n) = intx2{(int)pack2_bf16(acc[0], acc[1]), (int)pack2_bf16(acc[2], acc[3])};
 }
@@ -1489,9 +1503,11 @@ int wgrad_partials(const void* a, const void* b, int64_t M, int64_t N, int64_t l
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
   const int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>, kMainLds);
   if (rc) return rc;
+  // row K-slabs over ldt tokens
+  const TrOp tra{kStage, ldt * kStage, (M / 64) * ldt * kStage}, trb{kStage, ldt * kStage, (N / 64) * ldt * kStage};
   hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>), dim3((unsigned)(tiles_m * tiles_n * splits)),
                      dim3(256), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, ldt / splits, sa, sb, ws,
-                     tiles_m, tiles_n, splits, 1);
+                     tiles_m, tiles_n, splits, 1, tra, trb);
   return status();
 }
 
@@ -1645,7 +1661,7 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   if (rc) return rc;
   hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
                      kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
-                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1));
+                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1), TrOp{}, TrOp{});
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
@@ -1913,11 +1929,11 @@ int sfp8_bf16_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, i
   if (rc) return rc;
   hipLaunchKernelGGL((wgrad_kernel<true, 0, 0>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256), kMainLds,
                      st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws,
-                     tiles_m, tiles_n, (int)splits, 1);
+                     tiles_m, tiles_n, (int)splits, 1, TrOp{}, TrOp{});
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
@@ -1944,8 +1960,82 @@ int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t 
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
+  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
                      (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  return status();
+}
+
+// ---- the bf16 weight gradients read through transposing LDS reads ----
+int sfp8_bf16_gemm_wgrad_rows(const void* a, const void* x, int x_rows, int64_t M, int64_t N, int64_t T, int64_t ldt,
+                              void* out, float* ws, int64_t ws_floats, void* stream) {
+  if (!out || (T > 0 && (!a || !x))) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || M % 32 || N % (x_rows ? 32 : 4) || T < 0 || ldt < T || ldt % kTile || (M * N) % 8)
+    return kErrBadShape;
+  if (!fits32(slab_rows(M), 2 * ldt) || !fits32(slab_rows(N), 2 * ldt) || T * N * 2 >= ((int64_t)1 << 31))
+    return kErrBadShape;
+  if (!al16(a) || !al16(x) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  hipStream_t st = (hipStream_t)stream;
+  if (ldt == 0) {
+    const int64_t n = M * N / 2;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, (float*)out, n);
+    return status();
+  }
+  const int64_t splits = sfp8_bf16_wgrad_splits(M, N, ldt);
+  if (!ws || ws_floats < sfp8_bf16_wgrad_workspace_floats(M, N, ldt)) return kErrWorkspaceTooSmall;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  // a: the bf16 K-slab of [ldt, M] (32 columns per 64-byte row); x (x_rows):
+  // row-major [T, N] bf16, tokens T..ldt-1 read as zero through the range
+  // check, or else the token-contiguous bf16 K-slab of x^T over ldt tokens
+  const TrOp tra{kStage, ldt * kStage, (M / 32) * ldt * kStage}, trb{2 * N, kStage, T * 2 * N};
+  const dim3 grid((unsigned)(tiles_m * tiles_n * splits));
+  int rc;
+  if (x_rows) {
+    rc = prep(wgrad_kernel<true, 0, 0, true, true>, kMainLds);
+    if (!rc)
+      hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, true, true>), grid, dim3(256), kMainLds, st, (const uint8_t*)a,
+                         (const uint8_t*)x, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws, tiles_m, tiles_n,
+                         (int)splits, 1, tra, trb);
+  } else {
+    rc = prep(wgrad_kernel<true, 0, 0, true, false>, kMainLds);
+    if (!rc)
+      hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, true, false>), grid, dim3(256), kMainLds, st, (const uint8_t*)a,
+                         (const uint8_t*)x, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws, tiles_m, tiles_n,
+                         (int)splits, 1, tra, TrOp{});
+  }
+  if (rc) return rc;
+  rc = status();
+  if (rc) return rc;
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  if (x_rows)
+    hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<true>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+                       (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
+                       (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  return status();
+}
+
+int sfp8_bf16_moe_gemm_wgrad_rows(const void* a, const void* bt, int64_t M, int64_t N, int64_t E, const int* plan,
+                                  int64_t ldp, void* out, float* ws, int64_t ws_floats, void* stream) {
+  if (!a || !bt || !plan || !out) return kErrNullPointer;
+  if (M <= 0 || N <= 0 || E <= 0 || M % 32 || N % 4 || ldp <= 0 || ldp % kTile) return kErrBadShape;
+  if (!fits32(slab_rows(M), 2 * ldp) || !fits32(slab_rows(N), 2 * ldp)) return kErrBadShape;
+  if (!al16(a) || !al16(bt) || !al16(out) || !al16(ws)) return kErrBadAlignment;
+  const int64_t splits = sfp8_moe_wgrad_splits(M, N, E);
+  if (!ws || ws_floats < sfp8_bf16_moe_wgrad_workspace_floats(M, N, E)) return kErrWorkspaceTooSmall;
+  hipStream_t st = (hipStream_t)stream;
+  const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
+  int rc = prep(moe_wgrad_kernel<true, 0, 0, true, false>, kMainLds);
+  if (rc) return rc;
+  hipLaunchKernelGGL((moe_wgrad_kernel<true, 0, 0, true, false>),
+                     dim3((unsigned)(tiles_m * tiles_n), (unsigned)splits, (unsigned)E), dim3(256), kMainLds, st,
+                     (const uint8_t*)a, (const uint8_t*)bt, M, N, 2 * ldp, nullptr, nullptr, nullptr, ws, plan,
+                     tiles_m, tiles_n, (int)splits);
+  rc = status();
+  if (rc) return rc;
+  const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
+  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0,
+                     st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
 

@@ -100,15 +100,15 @@ SFP8_DEV void sched_interleave_valu() {
   }
 }
 
-// TR_A / TR_B: the operand's tile arrives as four 64-row blocks [slab][64
-// K bytes][64 bytes of 64 M (or N) values] -- a row K-slab of the
-// transposed matrix, e.g. the token-major activations a weight gradient
-// reduces over -- and each fragment is assembled from four transposing
-// reads (ds_read_b64_tr_b8: 8 K bytes of one column per lane each) in the
-// same (lane half, byte) -> K order as the plain reads, so the MFMAs see the
-// same values.  Only for fp8 operands and a plain (unpaired) B.  With TR_B
-// the B tile is not permuted: accumulator v of block nb in lane half g is
-// column 32 nb + 8 (v / 4) + 4 g + v % 4 of the wave's 128.  These
+// TR_A / TR_B: the operand's tile arrives as blocks of 64 (fp8) or 32 (bf16)
+// rows, each [tokens of the K stage][64 bytes of 64 (32) M or N values] -- a
+// row K-slab (or the row-major rows) of the token-major activation a weight
+// gradient reduces over -- and each fragment is assembled from four
+// transposing reads (ds_read_b64_tr_b8: 8 tokens of one column per lane;
+// ds_read_b64_tr_b16: 4 tokens) in the same (lane half, K) order as the plain
+// reads, so the MFMAs see the same values.  Only for a plain (unpaired) B.
+// With TR_B the B tile is not permuted: accumulator v of block nb in lane
+// half g is column 32 nb + 8 (v / 4) + 4 g + v % 4 of the wave's 128.  These
 // instantiations issue their DMA as inline asm: the compiler treats a
 // transposing read as possibly aliasing any LDS DMA it knows to be in flight
 // and would wait for all of it first; the stage waits and barriers already
@@ -116,7 +116,7 @@ SFP8_DEV void sched_interleave_valu() {
 template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0,
           bool TR_A = false, bool TR_B = false>
 struct MainLoop {
-  static_assert(!(TR_A || TR_B) || (!BF16 && !PAIRED && NB == 4), "transposing reads: fp8, plain, 256 x 256");
+  static_assert(!(TR_A || TR_B) || (!PAIRED && NB == 4), "transposing reads: plain, 256 x 256");
   static constexpr bool kTr = TR_A || TR_B;
   using Rsrc = typename std::conditional<kTr, intx4, __amdgpu_buffer_rsrc_t>::type;
   static SFP8_DEV Rsrc rsrc(const void* base, int64_t bytes) {
@@ -178,12 +178,23 @@ struct MainLoop {
   // read q (K bytes 8 q .. 8 q + 7 of the lane half's 32).
   template <int K>
   static SFP8_DEV intx8 read_tr_block(const uint8_t* p, const uint32_t (&off)[8]) {
-    const uint8_t* q = p + (K >> 1) * (64 * kStage);
-    const intx2 r0 = lds_read_tr8(q + off[0 + (K & 1)]);
-    const intx2 r1 = lds_read_tr8(q + off[2 + (K & 1)]);
-    const intx2 r2 = lds_read_tr8(q + off[4 + (K & 1)]);
-    const intx2 r3 = lds_read_tr8(q + off[6 + (K & 1)]);
-    return intx8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    if constexpr (BF16) {
+      // bf16: block k is 32-row slab k; read q returns tokens 4 q .. 4 q + 3
+      // of the lane half's 16 (the two MFMA steps' 8 each)
+      const uint8_t* q = p + K * (32 * kStage);
+      const intx2 r0 = lds_read_tr16(q + off[0]);
+      const intx2 r1 = lds_read_tr16(q + off[1]);
+      const intx2 r2 = lds_read_tr16(q + off[2]);
+      const intx2 r3 = lds_read_tr16(q + off[3]);
+      return intx8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    } else {
+      const uint8_t* q = p + (K >> 1) * (64 * kStage);
+      const intx2 r0 = lds_read_tr8(q + off[0 + (K & 1)]);
+      const intx2 r1 = lds_read_tr8(q + off[2 + (K & 1)]);
+      const intx2 r2 = lds_read_tr8(q + off[4 + (K & 1)]);
+      const intx2 r3 = lds_read_tr8(q + off[6 + (K & 1)]);
+      return intx8{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+    }
   }
 
   template <int I>
@@ -376,10 +387,12 @@ struct MainLoop {
     // <- logical chunk (lane%4) ^ ((row >> 2) & 3)
     uint32_t voff_a[4], voff_b[NB];
     const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
-    // TR operands: chunk c of row r at c ^ (2 * ((r >> 2) & 1)), so that the
-    // 8 rows x 2 chunks a half-wave's transposing read touches fill the 64
-    // banks (rows r and r + 4 share banks under the plain swizzle)
-    const uint32_t chunk_tr = (uint32_t)(((lane & 3) ^ (((lane >> 4) & 1) << 1)) << 4);
+    // fp8 TR operands: chunk c of row r at c ^ (2 * ((r >> 2) & 1)), so that
+    // the 8 rows x 2 chunks a half-wave's transposing read touches fill the
+    // 64 banks (rows r and r + 4 share banks under the plain swizzle).  bf16
+    // TR operands: unswizzled (a half-wave reads 4 whole 64-byte rows).
+    const uint32_t chunk_tr =
+        BF16 ? (uint32_t)((lane & 3) << 4) : (uint32_t)(((lane & 3) ^ (((lane >> 4) & 1) << 1)) << 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + (TR_A ? chunk_tr : chunk);
@@ -395,7 +408,22 @@ struct MainLoop {
       aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
       boff[h] = (uint32_t)(kLdsB + (BLayout<PAIRED, NB>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
     }
-    if constexpr (kTr) {
+    if constexpr (kTr && BF16) {
+      // bf16 transposing reads: 16-lane group G = lane / 16 (lane half G / 2,
+      // column half G % 2 of the slab's 32 columns); for read q lane 16 G + j
+      // addresses token 16 (G / 2) + 4 q + j / 4 and columns 16 (G % 2) +
+      // 4 (j % 4) .. + 3; the read returns to lane 16 G + 4 a + b tokens
+      // 16 (G / 2) + 4 q .. + 3 of column 16 (G % 2) + 4 a + b.  Slabs of the
+      // wave's rows: 4 wm (A) or 4 wn (B).
+      const int G = lane >> 4, j = lane & 15;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int tok = 16 * (G >> 1) + 4 * q + (j >> 2);
+        const uint32_t cb = (uint32_t)(32 * (G & 1) + 8 * (j & 3));
+        if constexpr (TR_A) aoff[q] = (uint32_t)((128 * wm + tok) * kStage) + cb;
+        if constexpr (TR_B) boff[q] = (uint32_t)((128 * wn + tok) * kStage) + cb;
+      }
+    } else if constexpr (kTr) {
       // Transposing reads: 16-lane group G = lane / 16 (lane half g = G / 2,
       // column half G % 2 of the block's 32 columns); within it lane 2b + h
       // addresses tile row (token) 32 g + 8 q + b of the block's slab and the

@@ -478,16 +478,18 @@ def bf16_weight_slabs(w: torch.Tensor, norm_w=None, *, rows: bool = True, transp
     return ws, wt
 
 
-def bf16_rows_prep(x: torch.Tensor, plan, ldp: int, eps=None):
-    """(rstd [rows] fp32 or None, xt): xt the token-contiguous bf16 K-slab of
-    x^T over ldp padded rows; rstd = 1/sqrt(mean(x^2) + eps) when eps is given
-    (dense rows only)."""
+def bf16_rows_prep(x: torch.Tensor, plan, ldp: int, eps=None, *, copy: bool = True):
+    """(rstd [rows] fp32 or None, xt or None): xt the token-contiguous bf16
+    K-slab of x^T over ldp padded rows (copy=False skips it: bf16_wgrad_rows
+    reads x itself); rstd = 1/sqrt(mean(x^2) + eps) when eps is given (dense
+    rows only)."""
     _cuda_contig("x", x, BF16, 2)
     n, D = x.shape
-    xt = kslab_empty(D, ldp, BF16, x.device)
+    _need(copy or eps is not None, "nothing to compute")
+    xt = kslab_empty(D, ldp, BF16, x.device) if copy else None
     rstd = torch.empty(n, dtype=torch.float32, device=x.device) if eps is not None else None
     _lib.call("sfp8_bf16_rows_prep", x.data_ptr(), n, D, _lib.ptr(plan), ldp, float(eps or 0.0), _lib.ptr(rstd),
-              xt.data_ptr(), _lib.stream_of(x))
+              _lib.ptr(xt), _lib.stream_of(x))
     return rstd, xt
 
 
@@ -507,17 +509,18 @@ def bf16_swiglu_fwd(x: torch.Tensor, ws: torch.Tensor, I: int, rstd=None, plan=N
     return gu, h
 
 
-def bf16_swiglu_bwd(gu: torch.Tensor, dout: torch.Tensor, rstd, plan, ldp: int):
+def bf16_swiglu_bwd(gu: torch.Tensor, dout: torch.Tensor, rstd, plan, ldp: int, *, copy: bool = True):
     """(gs, gt): G' = bf16 SwiGLU gradient of the rows (times rstd when given)
-    as the K-slab over ldp padded rows and its token-contiguous transpose."""
+    as the K-slab over ldp padded rows and its token-contiguous transpose
+    (copy=False skips gt, None: the weight gradient then reads gs itself)."""
     _cuda_contig("gu", gu, BF16, 2)
     _cuda_contig("dout", dout, BF16, 2)
     n, I2 = gu.shape
     _need(dout.shape == (n, I2 // 2), "dout must be [rows, I]")
     gs = kslab_empty(ldp, I2, BF16, gu.device)
-    gt = kslab_empty(I2, ldp, BF16, gu.device)
+    gt = kslab_empty(I2, ldp, BF16, gu.device) if copy else None
     _lib.call("sfp8_bf16_swiglu_bwd", gu.data_ptr(), dout.data_ptr(), n, I2 // 2, _lib.ptr(rstd), _lib.ptr(plan), ldp,
-              gs.data_ptr(), gt.data_ptr(), _lib.stream_of(gu))
+              gs.data_ptr(), _lib.ptr(gt), _lib.stream_of(gu))
     return gs, gt
 
 
@@ -563,6 +566,40 @@ def bf16_wgrad(at: torch.Tensor, bt: torch.Tensor, M: int, N: int, plan=None, E:
         ws = torch.empty(max(nws, 1), dtype=torch.float32, device=dev)
         _lib.call("sfp8_bf16_moe_gemm_wgrad", at.data_ptr(), bt.data_ptr(), M, N, E, plan.data_ptr(), ldp,
                   out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(at))
+    return out
+
+
+def bf16_wgrad_rows(gs: torch.Tensor, b: torch.Tensor, M: int, N: int, plan=None, E: int = 1, T=None):
+    """bf16_wgrad with A read from gs, the bf16 K-slab of G' over the padded
+    rows, through transposing LDS reads.  Dense (no plan): b is x itself,
+    row-major [T, N] bf16, also transposed on read, or (3-d) the
+    token-contiguous K-slab of x^T (bf16_rows_prep; T then gives the tokens);
+    with a plan b is the token-contiguous K-slab of x^T over the padded rows."""
+    _cuda_contig("gs", gs, BF16, 3)
+    ldp = gs.shape[1]
+    _need(gs.shape[0] * (SLAB // 2) == M, "gs must be the bf16 K-slab of [ldp, M]")
+    dev = gs.device
+    if plan is None:
+        x_rows = b.dim() == 2
+        _cuda_contig("x", b, BF16, 2 if x_rows else 3)
+        if x_rows:
+            _need(b.shape[1] == N and b.shape[0] <= ldp, "x must be [T, N] with T <= the padded rows")
+            T = b.shape[0]
+        else:
+            _need(b.shape[0] * (SLAB // 2) == ldp and T is not None, "xt must cover the padded rows; give T")
+        out = torch.empty(M, N, dtype=BF16, device=dev)
+        nws = _lib.query("sfp8_bf16_wgrad_workspace_floats", M, N, ldp)
+        ws = torch.empty(max(nws, 1), dtype=torch.float32, device=dev)
+        _lib.call("sfp8_bf16_gemm_wgrad_rows", gs.data_ptr(), b.data_ptr(), int(x_rows), M, N, T, ldp, out.data_ptr(),
+                  ws.data_ptr(), ws.numel(), _lib.stream_of(gs))
+    else:
+        _cuda_contig("bt", b, BF16, 3)
+        _need(b.shape[0] * (SLAB // 2) == ldp, "bt must cover the same padded rows")
+        out = torch.empty(E, M, N, dtype=BF16, device=dev)
+        nws = _lib.query("sfp8_bf16_moe_wgrad_workspace_floats", M, N, E)
+        ws = torch.empty(max(nws, 1), dtype=torch.float32, device=dev)
+        _lib.call("sfp8_bf16_moe_gemm_wgrad_rows", gs.data_ptr(), b.data_ptr(), M, N, E, plan.data_ptr(), ldp,
+                  out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(gs))
     return out
 
 

@@ -88,8 +88,8 @@ class _FusedSwiGLU(torch.autograd.Function):
 class _NormSwiGLU(torch.autograd.Function):
     """SwiGLU(gate_up(rmsnorm(h))) of a dense MLP (train.py:2101-2131), the
     norm weight folded into the gate/up weight (W' = bf16(w_gu * norm_w)) and
-    the rows normalised in the GEMM epilogue (rstd from a row pass that also
-    writes the token-contiguous h^T the weight gradient reads).
+    the rows normalised in the GEMM epilogue (rstd from a row pass; the weight
+    gradient reads h and G' through transposing LDS reads).
 
     Returns out [T, I] bf16 (the down projection and the residual stay the
     caller's, train.py:2366-2369).  Backward: (dh bf16, dnorm_w fp32 [D],
@@ -98,12 +98,12 @@ class _NormSwiGLU(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, norm_w, w_gu, eps):
-        out, wt, gu, rstd, xt = torch.ops.sparkfp8.norm_swiglu_fwd(h, norm_w, w_gu, float(eps))
-        ctx.save_for_backward(h, norm_w, w_gu, wt, gu, rstd, xt)
+        out, wt, gu, rstd = torch.ops.sparkfp8.norm_swiglu_fwd(h, norm_w, w_gu, float(eps))
+        ctx.save_for_backward(h, norm_w, w_gu, wt, gu, rstd)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        h, norm_w, w_gu, wt, gu, rstd, xt = ctx.saved_tensors
-        dh, dnw, dw = torch.ops.sparkfp8.norm_swiglu_bwd(dout, h, norm_w, w_gu, wt, gu, rstd, xt)
+        h, norm_w, w_gu, wt, gu, rstd = ctx.saved_tensors
+        dh, dnw, dw = torch.ops.sparkfp8.norm_swiglu_bwd(dout, h, norm_w, w_gu, wt, gu, rstd)
         return dh, dnw, dw, None

@@ -273,19 +273,19 @@ BF16 = torch.bfloat16
 
 
 @torch.library.custom_op("sparkfp8::norm_swiglu_fwd", mutates_args=())
-def norm_swiglu_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor,
-                                                                                   Tensor]:
+def norm_swiglu_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """_NormSwiGLU.forward (train.py:2111-2121): out = SwiGLU(gate_up(rmsnorm(h)))
     [T, I] bf16, the norm weight folded into the gate/up weight (W' =
     bf16(w_gu * norm_w)); then, for the backward, the bf16 K-slab of W'^T, gu
-    [T, 2I], rstd [T] and the token-contiguous bf16 K-slab of h^T."""
+    [T, 2I] and rstd [T] (the weight gradient reads h itself, through
+    transposing LDS reads)."""
     h = h.contiguous()
     T, D = h.shape
     I = w_gu.shape[0] // 2
     ws, wt = ops.bf16_weight_slabs(w_gu.detach().contiguous().unsqueeze(0), norm_w.detach().contiguous())
-    rstd, xt = ops.bf16_rows_prep(h, None, ops.ldt_of(T), float(eps))
+    rstd, _ = ops.bf16_rows_prep(h, None, ops.ldt_of(T), float(eps), copy=False)
     gu, out = ops.bf16_swiglu_fwd(h, ws, I, rstd=rstd)
-    return out, wt, gu, rstd, xt
+    return out, wt, gu, rstd
 
 
 @norm_swiglu_fwd.register_fake
@@ -293,13 +293,12 @@ def _norm_swiglu_fwd_fake(h, norm_w, w_gu, eps):
     T, D = h.shape
     I2 = w_gu.shape[0]
     return (h.new_empty((T, I2 // 2), dtype=BF16), h.new_empty((1,) + ops.kslab_shape(D, I2, BF16), dtype=BF16),
-            h.new_empty((T, I2), dtype=BF16), h.new_empty((T,), dtype=torch.float32),
-            h.new_empty(ops.kslab_shape(D, ops.ldt_of(T), BF16), dtype=BF16))
+            h.new_empty((T, I2), dtype=BF16), h.new_empty((T,), dtype=torch.float32))
 
 
 @torch.library.custom_op("sparkfp8::norm_swiglu_bwd", mutates_args=())
-def norm_swiglu_bwd(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: Tensor, gu: Tensor, rstd: Tensor,
-                    xt: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+def norm_swiglu_bwd(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: Tensor, gu: Tensor,
+                    rstd: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """_NormSwiGLU.backward (train.py:2123-2131): (dh bf16 [T, D], dnorm_w fp32
     [D], dw_gu fp32 [2I, D]).  G' = rstd * d_gu (bf16) once for both GEMMs:
     p = bf16(G' W'), dh = bf16(p - rstd^2 sum(h p) / D h), dW' = bf16(G'^T h),
@@ -310,18 +309,18 @@ def norm_swiglu_bwd(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: T
     h = h.contiguous()
     T, D = h.shape
     I2 = gu.shape[1]
-    ldt = xt.shape[0] * (ops.SLAB // 2)
-    gs, gt = ops.bf16_swiglu_bwd(gu, dout, rstd, None, ldt)
+    gs, _ = ops.bf16_swiglu_bwd(gu, dout, rstd, None, ops.ldt_of(T), copy=False)
     p = ops.bf16_gemm(gs, wt, T, D, I2)
-    del gs
     dh = ops.bf16_norm_dh(p, h, rstd)
-    dwp = ops.bf16_wgrad(gt, xt, I2, D)
+    del p
+    # G' and h both read through transposing LDS reads (no copies)
+    dwp = ops.bf16_wgrad_rows(gs, h, I2, D)
     dw, dnw = ops.bf16_fold_grads(dwp, w_gu.detach().contiguous(), norm_w.detach().contiguous())
     return dh, dnw, dw
 
 
 @norm_swiglu_bwd.register_fake
-def _norm_swiglu_bwd_fake(dout, h, norm_w, w_gu, wt, gu, rstd, xt):
+def _norm_swiglu_bwd_fake(dout, h, norm_w, w_gu, wt, gu, rstd):
     T, D = h.shape
     return (h.new_empty((T, D), dtype=BF16), h.new_empty((D,), dtype=torch.float32),
             h.new_empty(tuple(w_gu.shape), dtype=torch.float32))
@@ -369,10 +368,10 @@ def swiglu_bwd(dh: Tensor, x: Tensor, weight: Tensor, gu: Tensor, plan: Tensor) 
     ldp = ops.moe_padded_rows(R, E)
     _, wt = ops.bf16_weight_slabs(weight, rows=False, transposed=True)
     _, xt = ops.bf16_rows_prep(x, plan, ldp)
-    gs, gt = ops.bf16_swiglu_bwd(gu, dh, None, plan, ldp)
+    gs, _ = ops.bf16_swiglu_bwd(gu, dh, None, plan, ldp, copy=False)
     dx = ops.bf16_gemm(gs, wt, R, D, I2, plan=plan)
-    del gs
-    dw = ops.bf16_wgrad(gt, xt, I2, D, plan=plan, E=E)
+    # G' read through transposing LDS reads, x as its token-contiguous copy
+    dw = ops.bf16_wgrad_rows(gs, xt, I2, D, plan=plan, E=E)
     return dx, dw
 
 

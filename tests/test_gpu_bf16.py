@@ -70,13 +70,16 @@ def test_norm_swiglu_rstd_and_gu(dev):
     rstd bit-exact to the oracle's spec, gu within one bf16 ulp."""
     T, D, I = 700, 512, 256
     h, norm_w, w_gu, _ = _norm_case(dev, T, D, I, 4)
-    out, wt, gu, rstd, xt = torch.ops.sparkfp8.norm_swiglu_fwd(h.to(dev), norm_w.to(dev), w_gu.to(dev), 1e-6)
+    out, wt, gu, rstd = torch.ops.sparkfp8.norm_swiglu_fwd(h.to(dev), norm_w.to(dev), w_gu.to(dev), 1e-6)
     _, saved = B.norm_swiglu_forward(h, norm_w, w_gu, 1e-6)
     assert torch.equal(rstd.cpu(), saved["rstd"])
     _assert_bf16_close(gu, saved["gu"], "gu")
-    # W'^T slab and the token-contiguous h^T: exact copies
+    # W'^T slab: an exact copy
     wp = B.fold_weight(w_gu, norm_w).to(torch.bfloat16)
     assert torch.equal(sg.ops.unslab(wt[0], D).cpu(), wp.t().contiguous())
+    # the row pass with the token-contiguous h^T: the same rstd, an exact copy
+    rstd2, xt = sg.ops.bf16_rows_prep(h.to(dev), None, sg.ops.ldt_of(T), 1e-6)
+    assert torch.equal(rstd2, rstd)
     ht = sg.ops.unslab(xt, D).cpu()
     assert torch.equal(ht[:, :T], h.t()) and torch.all(ht[:, T:] == 0)
 
@@ -279,9 +282,9 @@ def test_bf16_ops_opcheck(dev):
     h, norm_w, w_gu, _ = _norm_case(dev, T, D, I, 7)
     args = (h.to(dev), norm_w.to(dev), w_gu.to(dev), 1e-6)
     torch.library.opcheck(torch.ops.sparkfp8.norm_swiglu_fwd.default, args, test_utils=utils)
-    out, wt, gu, rstd, xt = torch.ops.sparkfp8.norm_swiglu_fwd(*args)
+    out, wt, gu, rstd = torch.ops.sparkfp8.norm_swiglu_fwd(*args)
     dout = torch.randn(T, I, device=dev).to(torch.bfloat16)
-    bargs = (dout, args[0], args[1], args[2], wt, gu, rstd, xt)
+    bargs = (dout, args[0], args[1], args[2], wt, gu, rstd)
     torch.library.opcheck(torch.ops.sparkfp8.norm_swiglu_bwd.default, bargs, test_utils=utils)
     x, w, offs, probe = _fused_case([100, 0, 200], rows=300, dim=256, inter=192)
     fargs = (x.to(dev), w.to(dev), offs.to(dev))
@@ -289,3 +292,52 @@ def test_bf16_ops_opcheck(dev):
     hh, gu2, plan = torch.ops.sparkfp8.swiglu_fwd(*fargs)
     torch.library.opcheck(torch.ops.sparkfp8.swiglu_bwd.default, (probe.to(dev), fargs[0], fargs[1], gu2, plan),
                           test_utils=utils)
+
+
+@pytest.mark.parametrize("T,M,N", [(4096, 1536, 1024), (1000, 768, 512), (65536, 6144, 1024), (1, 256, 256)])
+def test_bf16_wgrad_rows_equals_token_contiguous(dev, T, M, N):
+    """The bf16 weight gradient read through transposing LDS reads (G' from
+    its K-slab, x row-major) gives the bytes of the one on the
+    token-contiguous copies: one split and several, ragged T."""
+    ops = sg.ops
+    ldt = ops.ldt_of(T)
+    g = torch.Generator(device=dev).manual_seed(T + M)
+    gp = torch.randn(T, M, device=dev, generator=g).to(torch.bfloat16)
+    x = torch.randn(T, N, device=dev, generator=g).to(torch.bfloat16)
+    pad = lambda t: torch.cat([t, torch.zeros(ldt - T, t.shape[1], dtype=t.dtype, device=dev)])
+    gs = ops.to_slab(pad(gp))                       # [M/32, ldt, 64 bytes]
+    gt = ops.to_slab(pad(gp).t().contiguous())      # [ldt/32, slab_rows(M), 64 bytes]
+    xt = ops.to_slab(pad(x).t().contiguous())
+    ref = ops.bf16_wgrad(gt, xt, M, N)
+    assert torch.equal(ops.bf16_wgrad_rows(gs, x, M, N), ref)
+    assert torch.equal(ops.bf16_wgrad_rows(gs, xt, M, N, T=T), ref)  # G' transposed on read only
+
+
+@pytest.mark.parametrize("counts", [[300, 0, 513, 1, 0, 186], [4000, 2600, 0, 900]])
+def test_bf16_moe_wgrad_rows_equals_token_contiguous(dev, counts):
+    """The grouped form: G' read through transposing LDS reads over padded
+    expert order, x as its token-contiguous copy; experts without rows get
+    zeros."""
+    ops = sg.ops
+    counts = torch.tensor(counts)
+    E, M, N = counts.numel(), 768, 512
+    offsets = torch.cumsum(counts, 0).to(torch.int32)
+    R = int(counts.sum())
+    plan = ops.moe_plan(offsets.to(dev), R)
+    ldp = ops.moe_padded_rows(R, E)
+    g = torch.Generator(device=dev).manual_seed(R)
+    x = torch.randn(R, N, device=dev, generator=g).to(torch.bfloat16)
+    gp = torch.randn(R, M // 2, device=dev, generator=g).to(torch.bfloat16)
+    dout = torch.randn(R, M // 2, device=dev, generator=g).to(torch.bfloat16)
+    gu = torch.cat([gp, gp * 0.5], 1).contiguous()
+    _, xt = ops.bf16_rows_prep(x, plan, ldp)
+    gs, gt = ops.bf16_swiglu_bwd(gu, dout, None, plan, ldp)
+    ref = ops.bf16_wgrad(gt, xt, M, N, plan=plan, E=E)
+    got = ops.bf16_wgrad_rows(gs, xt, M, N, plan=plan, E=E)
+    assert torch.equal(got, ref)
+    for e in range(E):
+        if int(counts[e]) == 0:
+            assert torch.all(ref[e] == 0)
+    # the SwiGLU gradient without its token-contiguous copy: the same K-slab
+    gs2, none = ops.bf16_swiglu_bwd(gu, dout, None, plan, ldp, copy=False)
+    assert none is None and torch.equal(gs2, gs)
