@@ -1,7 +1,9 @@
 // FP8 / bf16 MFMA GEMMs of the FP8 MLP block (gfx950, CDNA4).
 //
 // Every GEMM here is C[m, n] = sum_k A[m, k] * B[n, k]: both operands are
-// K-contiguous rows in HBM.  One work-group (256 threads = 4 waves, one wave
+// K-contiguous rows in HBM, except that a weight gradient (K = tokens) may
+// read either operand as the token-major activation its producer wrote,
+// through transposing LDS reads (MainLoop TR_A / TR_B).  One work-group (256 threads = 4 waves, one wave
 // per SIMD) computes a 256 x 256 output tile with the pipelined main loop of
 // mainloop.h; each wave owns 128 x 128 as 4 x 4 blocks of 32 x 32 MFMA
 // accumulators.
@@ -250,7 +252,8 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   m_h *= deq * deq;
   __syncthreads();
   // gu8 (gate and up halves) and h8 as 64-column K-slab blocks (every tile
-  // row: rows past T are zero padding), then the token-contiguous h8t
+  // row: rows past T are zero padding), then, when asked for, the
+  // token-contiguous h8t
   lds_rows_to_kslab<2>(Gt, kTile, kEpiStride, gu8, ldt, m0, n0);
   lds_rows_to_kslab<2>(Ut, kTile, kEpiStride, gu8, ldt, m0, I + n0);
   lds_rows_to_kslab<2>(Ht, kTile, kEpiStride, h8, ldt, m0, n0);
@@ -603,7 +606,8 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     // in flight)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // the previous tile's h tile is complete: its K-slab copies (h8: 256
-    // token rows of 64 bytes, one contiguous block; h8t transposed)
+    // token rows of 64 bytes, one contiguous block; the optional h8t
+    // transposed)
     if (c.prev) {
       pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
       if (h8t) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
@@ -795,7 +799,8 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
 // (a9) bf16 down dgrad + SwiGLU backward (spark-gpt train.py:1049-1094):
 //   dh = bf16(dy @ Wd); g, u = gu8 / s1; sig = sigmoid(g)
 //   d_gate = dh*u*(sig*(1+g*(1-sig))), d_up = dh*g*sig
-//   dgu8 = e5m2(d * s3) as K-slabs of [T, 2I] and of [2I, ldt], amax slot 3.
+//   dgu8 = e5m2(d * s3) as the K-slab of [T, 2I] (and optionally of [2I,
+//   ldt]: the token-contiguous dgu8t), amax slot 3.
 // B = Wd^T (bf16, [I, D]).  Tile 256 tokens x 256 intermediate columns.
 constexpr int kEpiStride2 = 272;
 constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 16;  // after Gt, Ut and the reduction slots
@@ -868,7 +873,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   // Row-order epilogue, in two passes of 128 tile rows (the rows of
   // stage_bf16_half<P>): dh staged in LDS as bf16, then each thread takes
   // 16-column chunks of one row, reading gu8 and writing dgu8 as whole K-slab
-  // rows; the codes also go to LDS for the token-contiguous dgu8t.
+  // rows; with dgu8t the codes also go to LDS for the token-contiguous copy.
   const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 64, 2 * I * ldt - m0 * 64);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
   uint8_t* DH = lds;
