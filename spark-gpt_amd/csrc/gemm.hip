@@ -322,7 +322,7 @@ struct SwigluPipe {
     // the next tile (nra, nvoff_b), or repeat this tile's last stage when
     // there is none (has_next false: nra, nvoff_b = ra, voff_b)
     uint8_t* lds;
-    __amdgpu_buffer_rsrc_t ra, rb, nra;
+    __amdgpu_buffer_rsrc_t ra, rb, nra, nrb;
     uint32_t voff_a[4], voff_b[2], nvoff_b[2], aoff[8], boff[8];
     bool has_next;
     int wave;
@@ -336,8 +336,10 @@ struct SwigluPipe {
     bool prev;            // a previous tile exists
     int64_t pm0, pn0;     // its origin
     uint8_t* hbuf;        // its LDS h tile
-    // scales and outputs
-    float c_exp, inv1, bnd1, inv2, bnd2;
+    // scales (of the previous tile's weight: the epilogue's) and outputs
+    float deq, c_exp, inv1, bnd1, inv2, bnd2;
+    float s0, s1, s2;  // scale[0], scale[1], scale[2]
+    float mx_gu, mx_h;  // amax so far, dequantized
     int64_t T, I, ldt;
     uint8_t* gu8;
     uint8_t* h8;
@@ -437,7 +439,7 @@ struct SwigluPipe {
       ML::load_stage(c.lds, slot, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
     } else {
       const int ld = c.has_next ? KT + kSt - 1 - NK : NK - 1;
-      ML::load_stage(c.lds, slot, c.nra, c.rb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
+      ML::load_stage(c.lds, slot, c.nra, c.nrb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
     }
     ML::read_frags(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
     ML::template mfma_range<0, ML::kMfma>(c.f[cur], c.acc);
@@ -503,6 +505,23 @@ struct SwigluPipe {
       tail_units<U0 + 1>(c);
     }
   }
+
+  // The finished epilogue's maxima, dequantized with its tile's scale, join
+  // the running amax (exact: the scales are powers of two); then the next
+  // epilogue's constants for weight scale q (all powers of two).
+  static SFP8_DEV void next_scales(Ctx& c, float q) {
+    c.mx_gu = fmaxf(c.mx_gu, c.m_gu * c.deq);
+    c.mx_h = fmaxf(c.mx_h, c.m_h * (c.deq * c.deq));
+    c.m_gu = 0.f;
+    c.m_h = 0.f;
+    c.deq = 1.0f / (c.s0 * q);
+    c.c_exp = c.deq * -1.4426950408889634f;
+    const float m1 = c.deq * c.s1, m2 = c.deq * c.deq * c.s2;
+    c.inv1 = 1.0f / m1;
+    c.inv2 = 1.0f / m2;
+    c.bnd1 = kE4M3Max * c.inv1;
+    c.bnd2 = kE4M3Max * c.inv2;
+  }
 };
 
 template <int NK>
@@ -510,28 +529,30 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, float* __restrict__ amax,
     uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int64_t ldt, int tiles_m,
-    int tiles_n) {
+    int tiles_n, const int* __restrict__ plan, int64_t w_estride) {
   using P = SwigluPipe<NK>;
   using ML = typename P::ML;
   extern __shared__ __align__(16) uint8_t lds[];
   typename P::Ctx c;
   c.lds = lds;
   c.wave = threadIdx.x >> 6;
-  // scales folded as in swiglu_fwd_kernel (all powers of two)
-  const float deq = 1.0f / (scale[0] * wscale[0]);
-  c.c_exp = deq * -1.4426950408889634f;
-  const float m1 = deq * scale[1], m2 = deq * deq * scale[2];
-  c.inv1 = 1.0f / m1;
-  c.inv2 = 1.0f / m2;
-  c.bnd1 = kE4M3Max * c.inv1;
-  c.bnd2 = kE4M3Max * c.inv2;
+  // scales folded as in swiglu_fwd_kernel (all powers of two); with a plan
+  // each tile's expert has its own weight scale wscale[e]
+  c.s0 = scale[0];
+  c.s1 = scale[1];
+  c.s2 = scale[2];
+  c.m_gu = 0.f;
+  c.m_h = 0.f;
+  c.mx_gu = 0.f;
+  c.mx_h = 0.f;
+  c.deq = 1.f;
+  P::next_scales(c, wscale[0]);
+  if (plan) tiles_m = MoePlan{plan}.ntiles();
   c.T = T;
   c.I = I;
   c.ldt = ldt;
   c.gu8 = gu8;
   c.h8 = h8;
-  c.m_gu = 0.f;
-  c.m_h = 0.f;
   c.bad = false;
 #pragma unroll
   for (int q = 0; q < 4; ++q) c.gw[q] = c.uw[q] = c.hw[q] = 0u;
@@ -559,15 +580,19 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   const int a_ss = (int)(ldt * kStage), b_ss = (int)(2 * I * kStage);
 #pragma unroll
   for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * kStage) + chunk;
-  c.rb = make_rsrc(w8, D * 2 * I);
-  // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64]; tile origin
-  // (m0, n0) -> A descriptor and B lane offsets
-  auto tile_operands = [&](int tile, int64_t& m0, int64_t& n0, __amdgpu_buffer_rsrc_t& ra, uint32_t (&voff_b)[2]) {
+  // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64] (with a plan:
+  // tile row tm's expert e at w8 + e * w_estride, its scale wscale[e]); tile
+  // origin (m0, n0) -> A and B descriptors, B lane offsets, weight scale
+  auto tile_operands = [&](int tile, int64_t& m0, int64_t& n0, __amdgpu_buffer_rsrc_t& ra,
+                           __amdgpu_buffer_rsrc_t& rb, uint32_t (&voff_b)[2], float& q) {
     int tm, tn;
     tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
     m0 = (int64_t)tm * kTile;
     n0 = (int64_t)tn * 64;
     ra = make_rsrc(x8 + m0 * kStage, D * ldt - m0 * kStage);
+    const int e = plan ? MoePlan{plan}.expert(tm) : 0;
+    rb = make_rsrc(w8 + e * w_estride, D * 2 * I);
+    q = wscale[e];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int r = 32 * c.wave + 16 * j + (lane >> 2);
@@ -576,11 +601,12 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   };
   int it = 0;
   int64_t m0 = 0, n0 = 0;
+  float q = 1.f, nq = 1.f;  // weight scale of the current tile and of the next
   if (blockIdx.x < ntiles) {
     // prologue, once per work-group: the first tile's stages 0..2 in flight,
     // stage 0 landed, its fragments read.  Later tiles' first stages are
     // loaded by the last stages of the tile before.
-    tile_operands(blockIdx.x, m0, n0, c.ra, c.voff_b);
+    tile_operands(blockIdx.x, m0, n0, c.ra, c.rb, c.voff_b, q);
 #pragma unroll
     for (int s = 0; s < 3; ++s) ML::load_stage(lds, s, c.ra, c.rb, c.voff_a, c.voff_b, s * a_ss, s * b_ss, c.wave);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * ML::kDma) : "memory");
@@ -590,9 +616,10 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     int64_t nm0 = m0, nn0 = n0;
     c.has_next = tile + (int)gridDim.x < ntiles;
     if (c.has_next) {
-      tile_operands(tile + (int)gridDim.x, nm0, nn0, c.nra, c.nvoff_b);
+      tile_operands(tile + (int)gridDim.x, nm0, nn0, c.nra, c.nrb, c.nvoff_b, nq);
     } else {
       c.nra = c.ra;
+      c.nrb = c.rb;
       c.nvoff_b[0] = c.voff_b[0];
       c.nvoff_b[1] = c.voff_b[1];
     }
@@ -621,9 +648,14 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     c.pm0 = m0;
     c.pn0 = n0;
     c.hbuf = lds + kPipeRing + (it & 1) * kPipeHBytes;
+    // the previous epilogue is complete: its amax joins, and this tile's
+    // weight scale sets the next epilogue's constants
+    P::next_scales(c, q);
     m0 = nm0;
     n0 = nn0;
+    q = nq;
     c.ra = c.nra;
+    c.rb = c.nrb;
     c.voff_b[0] = c.nvoff_b[0];
     c.voff_b[1] = c.nvoff_b[1];
   }
@@ -635,8 +667,9 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
     if (h8t) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
   }
+  P::next_scales(c, 1.f);  // folds the last epilogue's maxima
   float* red = reinterpret_cast<float*>(lds + kPipeRing + 2 * kPipeHBytes);
-  float mg = wave_max(c.m_gu * deq), mh = wave_max(c.m_h * (deq * deq));
+  float mg = wave_max(c.mx_gu), mh = wave_max(c.mx_h);
   if (lane == 0) {
     red[c.wave] = mg;
     red[4 + c.wave] = mh;
@@ -1551,7 +1584,8 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
     if (rc) return rc;
     hipLaunchKernelGGL(swiglu_pipe_kernel<16>, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kPipeLds,
                        (hipStream_t)stream, (const uint8_t*)x8, (const uint8_t*)w8, T, D, I, scale, wscale, amax,
-                       (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n);
+                       (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n, (const int*)nullptr,
+                       (int64_t)0);
     return status();
   }
   const int tiles_m = cdiv(T, kTile), tiles_n = (int)(I / 128);
@@ -1689,6 +1723,22 @@ int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, i
   if (!x8 || !w8 || !plan || !scale || !q_gu || !amax || !gu8 || !h8) return kErrNullPointer;
   if (!moe_shape(E, D, I, ldp) || !fits32(ldp, D) || !fits32(2 * I, D) || !fits32(ldp, 2 * I)) return kErrBadShape;
   if (!al16(x8) || !al16(w8) || !al16(gu8) || !al16(h8) || !al16(h8t)) return kErrBadAlignment;
+  if (D == 1024) {
+    // the persistent kernel walks the plan's tiles (its count read on the
+    // device); the grid is sized for the worst case
+    const int tiles_m = (int)(ldp / kTile), tiles_n = (int)(I / 64);
+    const int ntiles = tiles_m * tiles_n;
+    int n_cu = 0;
+    int rc = cu_count(&n_cu);
+    if (rc) return rc;
+    rc = prep(swiglu_pipe_kernel<16>, kPipeLds);
+    if (rc) return rc;
+    hipLaunchKernelGGL(swiglu_pipe_kernel<16>, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kPipeLds,
+                       (hipStream_t)stream, (const uint8_t*)x8, (const uint8_t*)w8, ldp, D, I, scale, q_gu, amax,
+                       (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, ldp, tiles_m, tiles_n, plan,
+                       D * slab_rows(2 * I));
+    return status();
+  }
   const int tiles_m = (int)(ldp / kTile), tiles_n = (int)(I / 128);
   int rc = prep(swiglu_fwd_kernel, kMainLds);
   if (rc) return rc;
