@@ -19,6 +19,10 @@
  *    max-accumulate into `amax`; nothing is read back to the host.
  *  - `wscale` points at the 2 just-in-time weight scales [q_gu, q_d]
  *    (train.py:1213).
+ *  - Every scale is a power of two, as fp8_update_scales and the weight
+ *    quantizer produce them (train.py:942-943, 951); the kernels rely on it
+ *    to fold scales into exact multiplies and into the converters' scale
+ *    operand.
  *  - K-slab layout.  Every FP8 GEMM operand, and the bf16 W_down^T, is stored
  *    as a K-slab of a row-major matrix X [R, L] (L = the GEMM's reduction
  *    dimension K, in bytes): [L / 64][rpad][64] bytes, rpad = R rounded up to

@@ -280,6 +280,23 @@ SFP8_DEV void block_amax_atomic(float v, float* red, float* dst) {
   }
 }
 
+// The same for a caller that holds its wave index in a scalar register: the
+// lane index is recomputed (mbcnt), so the work-item id need not stay live
+// to the kernel's end.
+template <int NWAVES>
+SFP8_DEV void block_amax_atomic_w(float v, float* red, float* dst, int wid_s) {
+  v = wave_max(v);
+  const bool lane0 = __lane_id() == 0;
+  if (lane0) red[wid_s] = v;
+  __syncthreads();
+  if (lane0 && wid_s == 0) {
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < NWAVES; ++i) m = fmaxf(m, red[i]);
+    atomic_max_nonneg(dst, m);
+  }
+}
+
 // K-slab layout of a token-contiguous FP8 copy of an R-row operand (the weight
 // gradients' operands x8t, h8t, d_gu8t, dy8t): [ldt / 64][slab_rows(R)][64]
 // bytes, element (r, t) at

@@ -172,10 +172,13 @@ struct NormCfg {
   // norm_quant: 8 waves per work-group up to D = 1024 (two work-groups per
   // CU fit the LDS, so 4 waves per SIMD), 4 beyond (whose registers need 2
   // waves per SIMD); QPASSES row passes per wave, PB of them with their loads
-  // issued together (about 8 chunks of 16 bytes per lane)
+  // issued together and their square roots taken together: about 8 chunks
+  // of 16 bytes per lane, 4 from D = 1024 on (at D = 1024 eight need more
+  // than the 128 registers of 4 waves per SIMD, and spill)
   static constexpr int QW = D <= 1024 ? 8 : 4;
   static constexpr int QPASSES = RT / (QW * RPW);
-  static constexpr int PB = (8 / CPL) < QPASSES ? ((8 / CPL) > 0 ? 8 / CPL : 1) : QPASSES;
+  static constexpr int QCH = CPL >= 2 ? 4 : 8;
+  static constexpr int PB = (QCH / CPL) < QPASSES ? ((QCH / CPL) > 0 ? QCH / CPL : 1) : QPASSES;
   // norm_bwd: BW waves per work-group (8 up to D = 1024: 4 waves per SIMD
   // beside the LDS tile, as for norm_quant), PASSES row passes per wave,
   // PB_BWD per batch
@@ -197,10 +200,12 @@ void norm_quant_kernel(
   __shared__ float red[Cfg::QW];
   uint8_t* tile = smem;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wid_s = __builtin_amdgcn_readfirstlane(wid);
   const int sr = lane / Cfg::LPR, li = lane % Cfg::LPR;
   const int blk = xcd_row_block(blockIdx.x, gridDim.x);
   const int64_t t0 = (int64_t)blk * Cfg::RT;
   const float s0 = scale[0];
+  const float inv0 = 1.0f / s0, bnd0 = kE4M3Max * inv0;
   float m = 0.0f;
   // norm weight for this lane's chunks
   float w[Cfg::CPL][8];
@@ -226,12 +231,37 @@ void norm_quant_kernel(
         v[q][c] = t < T ? *reinterpret_cast<const intx4*>(h + t * D + d) : intx4{0, 0, 0, 0};
       }
     }
+    // the batch's row sums first; then lane li of each row group evaluates
+    // the rstd of the batch's row li (one square root and division per lane
+    // for PB rows), and every lane takes its rows' values back
+    double ss[Cfg::PB];
+#pragma unroll
+    for (int q = 0; q < Cfg::PB; ++q) {
+      ss[q] = 0.0;
+#pragma unroll
+      for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t u = (uint32_t)v[q][c][j];
+          const float a = bf16_bits_to_f32(u & 0xffffu), b = bf16_bits_to_f32(u >> 16);
+          // squares of bf16 values are exact in fp64
+          ss[q] = __builtin_fma((double)a, (double)a, ss[q]);
+          ss[q] = __builtin_fma((double)b, (double)b, ss[q]);
+        }
+#pragma unroll
+      for (int o = Cfg::LPR / 2; o > 0; o >>= 1) ss[q] += __shfl_xor(ss[q], o, 64);
+    }
+    static_assert(Cfg::PB <= Cfg::LPR, "one lane per row of the batch");
+    double sel = ss[0];
+#pragma unroll
+    for (int q = 1; q < Cfg::PB; ++q) sel = li == q ? ss[q] : sel;
+    const float rl = (float)(1.0 / __builtin_sqrt((double)((float)sel / (float)D + eps)));
 #pragma unroll
     for (int q = 0; q < Cfg::PB; ++q) {
       const int r = (wid + Cfg::QW * (pb + q)) * Cfg::RPW + sr;
       const int64_t t = t0 + r;
       const bool valid = t < T;
-      double ss = 0.0;
+      const float r_ = __shfl(rl, sr * Cfg::LPR + q, 64);
       float f[Cfg::CPL][8];
 #pragma unroll
       for (int c = 0; c < Cfg::CPL; ++c)
@@ -240,28 +270,40 @@ void norm_quant_kernel(
           const uint32_t u = (uint32_t)v[q][c][j];
           f[c][2 * j] = bf16_bits_to_f32(u & 0xffffu);
           f[c][2 * j + 1] = bf16_bits_to_f32(u >> 16);
-          // squares of bf16 values are exact in fp64
-          ss = __builtin_fma((double)f[c][2 * j], (double)f[c][2 * j], ss);
-          ss = __builtin_fma((double)f[c][2 * j + 1], (double)f[c][2 * j + 1], ss);
         }
-#pragma unroll
-      for (int o = Cfg::LPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float var = (float)ss / (float)D + eps;
-      const float r_ = (float)(1.0 / __builtin_sqrt((double)var));
       if (valid && li == 0) rstd[t] = r_;
+      float n[Cfg::CPL][8];
+      float mw = 0.0f;  // max |n| over this lane's values, NaN if one is NaN
+#pragma unroll
+      for (int c = 0; c < Cfg::CPL; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          n[c][j] = (f[c][j] * r_) * w[c][j];
+          n[c][j + 1] = (f[c][j + 1] * r_) * w[c][j + 1];
+          mw = max3_nan(mw, fabsf(n[c][j]), fabsf(n[c][j + 1]));
+        }
+      // Common case, decided once per row set of the wave: every value finite
+      // and |n * s0| <= 448, so the clamp is the identity and the scaled
+      // converter (which divides by 1/s0, exact for a power of two) gives the
+      // codes directly.  Otherwise the clamp and the NaN codes per value.
+      const bool fast = !__builtin_amdgcn_ballot_w64(!(mw <= bnd0));
+      if (fast && valid) m = fmaxf(m, mw);
 #pragma unroll
       for (int c = 0; c < Cfg::CPL; ++c) {
         const int d = (c * Cfg::LPR + li) * 8;
-        float n[8];
+        uint32_t lo, hi;
+        if (fast) {
+          lo = pack4_e4m3_scaled_noclamp(n[c][0], n[c][1], n[c][2], n[c][3], inv0, 0u);
+          hi = pack4_e4m3_scaled_noclamp(n[c][4], n[c][5], n[c][6], n[c][7], inv0, 0u);
+          if (!valid) lo = hi = 0u;
+        } else {
+          lo = hi = 0u;
+          if (valid) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          n[j] = (f[c][j] * r_) * w[c][j];
-          if (valid) m = fmaxf(m, fabsf(n[j]));
-        }
-        uint32_t lo = 0u, hi = 0u;
-        if (valid) {
-          lo = pack4_e4m3(n[0] * s0, n[1] * s0, n[2] * s0, n[3] * s0);
-          hi = pack4_e4m3(n[4] * s0, n[5] * s0, n[6] * s0, n[7] * s0);
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(n[c][j]));
+            lo = pack4_e4m3(n[c][0] * s0, n[c][1] * s0, n[c][2] * s0, n[c][3] * s0);
+            hi = pack4_e4m3(n[c][4] * s0, n[c][5] * s0, n[c][6] * s0, n[c][7] * s0);
+          }
         }
         // x8 is a K-slab [D/64][ldt][64] (the gate/up GEMM's A operand),
         // zeros for tokens T..ldt-1.  Written from the registers: without
@@ -270,13 +312,14 @@ void norm_quant_kernel(
         *reinterpret_cast<intx2*>(x8 + (int64_t)(d >> 6) * ldt * 64 + t * 64 + (d & 63)) = intx2{(int)lo, (int)hi};
         if (x8t) *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
+      __builtin_amdgcn_sched_barrier(0);  // rows one after another (register pressure)
     }
   }
   if (x8t) {  // the optional token-contiguous copy (rows past T hold zero codes)
     __syncthreads();
     lds_rows_store_slab_tr<Cfg::RT, Cfg::QW>(tile, D, Cfg::STRIDE, x8t, slab_rows(D), t0, 0);
   }
-  block_amax_atomic<Cfg::QW>(m, red, amax);
+  block_amax_atomic_w<Cfg::QW>(m, red, amax, wid_s);
 }
 
 // --------------------------------------------------------------------------
