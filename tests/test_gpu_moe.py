@@ -161,6 +161,52 @@ def test_moe_wgrad_rows_equals_token_contiguous(dev, M_, N_, counts):
             assert torch.all(ref[e] == 0)
 
 
+@pytest.mark.parametrize("I,counts", [(256, [700, 0, 1500, 1, 2049]), (1536, [3000, 257, 0, 5000])])
+def test_moe_swiglu_pipe_equals_dense_per_expert(dev, I, counts):
+    """At D = 1024 the grouped gate/up forward runs the persistent SwiGLU
+    pipe over the plan's tiles, changing expert (weights and scale) from
+    tile to tile: each expert's gu8 and h8 rows are the bytes the dense
+    forward gives for that expert's rows alone, padding rows stay zero, and
+    amax slots 1, 2 are the maxima of the per-expert amax."""
+    ops = sg.ops
+    D = 1024
+    counts = torch.tensor(counts)
+    E = counts.numel()
+    offsets = torch.cumsum(counts, 0).to(torch.int32)
+    R = int(counts.sum())
+    plan = ops.moe_plan(offsets.to(dev), R)
+    ldp = ops.moe_padded_rows(R, E)
+    g = torch.Generator(device=dev).manual_seed(I + R)
+    x = (torch.randn(R, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+    w = torch.randn(E, 2 * I, D, device=dev, generator=g) * 0.03
+    w[1] *= 4.0  # experts with different weight scales
+    scale = torch.tensor([4.0, 2.0 ** -3, 2.0 ** -2, 1.0, 1.0], device=dev)
+    amax = torch.zeros(5, device=dev)
+    xs, _ = ops.moe_rows_quant(x, None, plan, ldp, scale, 0, amax, 0, ops.FMT_E4M3, True, with_copy=False)
+    q = torch.empty(E, device=dev)
+    w8, _, _ = ops.weight_quant_experts(w, q)
+    gu8, h8, _ = ops.moe_gateup_swiglu_fwd(xs, w8, plan, scale, q, amax, I, copy=False)
+    torch.cuda.synchronize()
+    gu_rows, h_rows = ops.unslab(gu8, ldp), ops.unslab(h8, ldp)  # [ldp, 2I], [ldp, I] (padded order)
+    a1 = a2 = 0.0
+    p = 0
+    for e in range(E):
+        n = int(counts[e])
+        if n == 0:
+            continue
+        npad = -(-n // 256) * 256
+        x8e = xs[:, p:p + npad, :].contiguous()  # the expert's K-slab over its padded rows
+        ae = torch.zeros(5, device=dev)
+        gue, he, _ = ops.gateup_swiglu_fwd(x8e, w8[e], scale, q[e:e + 1], ae, n, I, copy=False)
+        torch.cuda.synchronize()
+        assert torch.equal(gu_rows[p:p + n].view(torch.uint8), ops.unslab(gue, n).view(torch.uint8)), e
+        assert torch.equal(h_rows[p:p + n].view(torch.uint8), ops.unslab(he, n).view(torch.uint8)), e
+        assert torch.all(gu_rows[p + n:p + npad].view(torch.uint8) == 0), e
+        a1, a2 = max(a1, float(ae[1])), max(a2, float(ae[2]))
+        p += npad
+    assert float(amax[1]) == a1 and float(amax[2]) == a2
+
+
 def _make(dev, E, D, I, seed, std=None):
     ex = _Experts(E, D, I)
     g = torch.Generator().manual_seed(seed)
