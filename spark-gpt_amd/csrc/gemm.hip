@@ -846,7 +846,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ wdt, const uint8_t* __restrict__ gu8,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, float* __restrict__ amax,
     uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n,
-    int stagger_iters, const int* __restrict__ plan, int64_t w_estride) {
+    const int* __restrict__ plan, int64_t w_estride) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -876,11 +876,9 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   uint8_t* Ut = lds + kTile * kEpiStride2;
   float* red = reinterpret_cast<float*>(lds + 2 * kTile * kEpiStride2);  // 4 floats after both tiles
   float m3 = 0.f;
-  // Persistent: work-group pid runs tiles pid, pid + gridDim.x, ...  Every
-  // tile ends in a burst of 256 KiB of stores; work-groups that share an XCD
-  // start a quarter of a tile apart (a bounded sleep) so that their bursts
-  // do not coincide.
-  for (int i = 0; i < ((int)(blockIdx.x >> 3) & 3) * stagger_iters; ++i) __builtin_amdgcn_s_sleep(127);
+  // Persistent: work-group pid runs tiles pid, pid + gridDim.x, ...  (Work-
+  // groups started a quarter of a tile apart per XCD, so that the tiles'
+  // 256 KiB store bursts would not coincide, measured 2 % slower.)
   if (plan) tiles_m = MoePlan{plan}.ntiles();
   const int ntiles = tiles_m * tiles_n;
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
@@ -1628,14 +1626,11 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
   int rc = cu_count(&n_cu);
   if (rc) return rc;
   const int grid = ntiles < n_cu ? ntiles : n_cu;
-  // a quarter of a tile: (2D / 64) K stages of ~4k cycles with the epilogue,
-  // s_sleep 127 ~ 8k cycles; only worth it when every work-group runs several tiles
-  const int stagger = ntiles >= 4 * n_cu ? (int)((2 * D / kStage) * 4000 / 4 / 8128) : 0;
   rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
   if (rc) return rc;
   hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(grid), dim3(256), kDgradLds, (hipStream_t)stream,
                      (const uint16_t*)dy, (const uint16_t*)wdt, (const uint8_t*)gu8, T, D, I, scale, amax,
-                     (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, stagger, (const int*)nullptr, (int64_t)0);
+                     (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
 }
 
@@ -1778,7 +1773,7 @@ int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const voi
   if (rc) return rc;
   hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kDgradLds,
                      (hipStream_t)stream, (const uint16_t*)dout, (const uint16_t*)wdt, (const uint8_t*)gu8, R, D, I,
-                     scale, amax, (uint8_t*)dgu8, (uint8_t*)dgu8t, ldp, tiles_m, tiles_n, 0, plan,
+                     scale, amax, (uint8_t*)dgu8, (uint8_t*)dgu8t, ldp, tiles_m, tiles_n, plan,
                      2 * D * slab_rows(I));
   return status();
 }
