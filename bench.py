@@ -501,7 +501,7 @@ def time_bf16(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
     ms = (time.perf_counter() - t0) * 1e3 / steps
     work = {
         "bf16_weight_fold": (None, 16.0 * I * D),
-        "bf16_rows_prep": (None, 2.0 * T * D + 4 * T),
+        "bf16_rows_prep": (None, 4.0 * T * D + 4 * T),
         "bf16_gateup_swiglu_fwd": (4.0 * T * D * I, None),
         "bf16_swiglu_bwd_rows": (None, 10.0 * T * I),
         "bf16_gateup_dgrad": (4.0 * T * D * I, None),

@@ -340,20 +340,24 @@ int sfp8_bf16_weight_slabs(const void* w, int src_bf16, const float* nw, int64_t
 
 /* x [nsrc, D] bf16 rows in padded order (plan, or rows 0..nsrc-1 when plan
  * is NULL) -> xt (optional), the token-contiguous bf16 K-slab of x^T over ldp
- * rows (a weight gradient's plain operand; zeros past the rows), and with
- * rstd (plan NULL only) rstd[t] = 1 / sqrt(sum x^2 / D + eps): the row
+ * rows (a weight gradient's plain operand; zeros past the rows); xs
+ * (optional), the row K-slab of x over ldp rows ([2D/64][ldp][64] bytes,
+ * zeros past the rows: the gate/up forward's A operand with x_slab); and
+ * with rstd (plan NULL only) rstd[t] = 1 / sqrt(sum x^2 / D + eps): the row
  * statistic _swiglu_gemm_kernel accumulates in its NORM mode
- * (train.py:1689-1700).  At least one of xt, rstd. */
+ * (train.py:1689-1700).  At least one of xt, xs, rstd. */
 int sfp8_bf16_rows_prep(const void* x, int64_t nsrc, int64_t D, const int* plan, int64_t ldp, float eps, float* rstd,
-                        void* xt, void* stream);
+                        void* xt, void* xs, void* stream);
 
 /* Gate/up GEMM with the SwiGLU epilogue, replaces _swiglu_gemm_kernel
- * (train.py:1625-1716, launch 1719-1743): x [T, D] bf16, w = bf16 K-slab of
- * W [2I, D] (gate rows first), rstd [T] or NULL (the folded-norm row scale):
+ * (train.py:1625-1716, launch 1719-1743): x [T, D] bf16 (x_slab 0), or its
+ * row K-slab over T rounded up to 256 rows (x_slab 1: the xs of
+ * sfp8_bf16_rows_prep, the faster read), w = bf16 K-slab of W [2I, D] (gate
+ * rows first), rstd [T] or NULL (the folded-norm row scale):
  * gu = [bf16(acc_g * rs) | bf16(acc_u * rs)] [T, 2I], h = bf16(g sigmoid(g) u)
- * [T, I]. */
-int sfp8_bf16_gemm_swiglu_fwd(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd,
-                              void* gu, void* h, void* stream);
+ * [T, I].  Both layouts give the same bytes. */
+int sfp8_bf16_gemm_swiglu_fwd(const void* x, int x_slab, const void* w, int64_t T, int64_t D, int64_t I,
+                              const float* rstd, void* gu, void* h, void* stream);
 
 /* The same grouped (E experts, _FusedSwiGLU with several groups): x, gu, h
  * in expert order, w the stacked per-expert K-slabs. */

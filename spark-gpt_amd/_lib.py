@@ -56,8 +56,8 @@ SIGNATURES = {
     # bf16 SwiGLU path
     "sfp8_bf16_slab_bytes": (_I64, [_I64, _I64]),
     "sfp8_bf16_weight_slabs": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P, _P]),
-    "sfp8_bf16_rows_prep": (_INT, [_P, _I64, _I64, _P, _I64, _F32, _P, _P, _P]),
-    "sfp8_bf16_gemm_swiglu_fwd": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "sfp8_bf16_rows_prep": (_INT, [_P, _I64, _I64, _P, _I64, _F32, _P, _P, _P, _P]),
+    "sfp8_bf16_gemm_swiglu_fwd": (_INT, [_P, _INT, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "sfp8_bf16_moe_gemm_swiglu_fwd": (_INT, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
     "sfp8_bf16_swiglu_bwd": (_INT, [_P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P]),
     "sfp8_bf16_gemm": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),

@@ -134,7 +134,8 @@ __global__ __launch_bounds__(256) void bf16_weight_slabs_kernel(const void* __re
 // transpose.  D % 64 == 0.
 __global__ __launch_bounds__(256) void bf16_rows_prep_kernel(const uint16_t* __restrict__ x, int64_t nsrc, int64_t D,
                                                              const int* __restrict__ plan, float eps,
-                                                             float* __restrict__ rstd, uint8_t* __restrict__ xt) {
+                                                             float* __restrict__ rstd, uint8_t* __restrict__ xt,
+                                                             uint8_t* __restrict__ xs) {
   __shared__ __align__(16) uint8_t tile[64 * kTrStride];
   __shared__ int64_t rsrc[64];
   const int64_t p0 = (int64_t)blockIdx.x * 64;
@@ -150,6 +151,11 @@ __global__ __launch_bounds__(256) void bf16_rows_prep_kernel(const uint16_t* __r
       const int64_t s = rsrc[r];
       intx4 v = {0, 0, 0, 0};
       if (s >= 0) v = *reinterpret_cast<const intx4*>(x + s * D + c0 + 8 * c8);
+      // the row K-slab [2D/64][ldp][64]: columns c0 + 8 c8 .. are 16 bytes of
+      // slab (c0 + 8 c8) / 32; eight lanes write two rows' 64-byte runs
+      if (xs)
+        *reinterpret_cast<intx4*>(xs + ((c0 >> 5) + (c8 >> 2)) * (int64_t)gridDim.x * 64 * 64 + (p0 + r) * 64 +
+                                  16 * (c8 & 3)) = v;
       float f[8];
       unpack8_bf16(v, f);
 #pragma unroll
@@ -374,14 +380,14 @@ int sfp8_bf16_weight_slabs(const void* w, int src_bf16, const float* nw, int64_t
 }
 
 int sfp8_bf16_rows_prep(const void* x, int64_t nsrc, int64_t D, const int* plan, int64_t ldp, float eps, float* rstd,
-                        void* xt, void* stream) {
-  if ((ldp > 0 && !xt && !rstd) || (nsrc > 0 && !x)) return kErrNullPointer;
+                        void* xt, void* xs, void* stream) {
+  if ((ldp > 0 && !xt && !rstd && !xs) || (nsrc > 0 && !x)) return kErrNullPointer;
   if (rstd && plan) return kErrBadShape;
   if (nsrc < 0 || D <= 0 || D % 64 || ldp < 0 || ldp % 256 || (!plan && ldp < nsrc)) return kErrBadShape;
-  if (!bf_al16(x) || !bf_al16(xt)) return kErrBadAlignment;
+  if (!bf_al16(x) || !bf_al16(xt) || !bf_al16(xs)) return kErrBadAlignment;
   if (ldp == 0) return kOk;
   hipLaunchKernelGGL(bf16_rows_prep_kernel, dim3((unsigned)(ldp / 64)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, nsrc, D, plan, eps, rstd, (uint8_t*)xt);
+                     (const uint16_t*)x, nsrc, D, plan, eps, rstd, (uint8_t*)xt, (uint8_t*)xs);
   return bf_status();
 }
 

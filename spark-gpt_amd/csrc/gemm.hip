@@ -1289,7 +1289,7 @@ constexpr int kGuStride = 272;  // staging row: 128 bf16 columns (256 bytes) + 1
 __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ rstd, uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int tiles_m, int tiles_n,
-    const int* __restrict__ plan, int64_t w_estride) {
+    const int* __restrict__ plan, int64_t w_estride, int64_t ldxs) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn;
   tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
@@ -1305,9 +1305,15 @@ __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
   const int64_t ldx = D * 2;  // bytes per x row = K bytes
   const int64_t wr = slab_rows(2 * I);
   floatx16 acc[4][4];
+  // A: x row-major [T, D] (rows past the tile's last read as zero through
+  // the range check), or with ldxs > 0 its row K-slab [2D/64][ldxs][64]
+  // (zero padding rows): a K stage of the tile is then one 16 KiB block of
+  // whole 128-byte lines instead of 256 half lines 2D bytes apart
+  const bool xslab = ldxs > 0;
   MainLoop<true, 0, 0, true>::run(
-      lds, reinterpret_cast<const uint8_t*>(x) + r0 * ldx, nrows * ldx, [=](int r) { return r * (int)ldx; },
-      kStage, w, ldx * wr, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
+      lds, reinterpret_cast<const uint8_t*>(x) + r0 * (xslab ? kStage : ldx),
+      xslab ? ldx * ldxs - r0 * kStage : nrows * ldx, [=](int r) { return r * (xslab ? kStage : (int)ldx); },
+      xslab ? (int)(ldxs * kStage) : kStage, w, ldx * wr, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
       (int)(wr * kStage), (int)(ldx / kStage), acc);
   // Epilogue in two passes of 128 tile rows: pass P takes the lanes' row
   // blocks tb = 2P, 2P+1 (tile row 128 wm + 64 P + 32 (tb & 1) + fr, staging
@@ -1890,13 +1896,13 @@ namespace {
 inline bool bf16_shape(int64_t D, int64_t I) { return D > 0 && I > 0 && D % 64 == 0 && I % 64 == 0; }
 
 int bf16_swiglu_launch(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd, void* gu,
-                       void* h, const int* plan, int64_t E, int tiles_m, hipStream_t st) {
+                       void* h, const int* plan, int64_t E, int tiles_m, int64_t ldxs, hipStream_t st) {
   const int tiles_n = cdiv(I, 128);
   int rc = prep(bf16_swiglu_fwd_kernel, kMainLds);
   if (rc) return rc;
   hipLaunchKernelGGL(bf16_swiglu_fwd_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), kMainLds, st,
                      (const uint16_t*)x, (const uint8_t*)w, T, D, I, rstd, (uint16_t*)gu, (uint16_t*)h, tiles_m,
-                     tiles_n, plan, plan ? 2 * D * slab_rows(2 * I) : 0);
+                     tiles_n, plan, plan ? 2 * D * slab_rows(2 * I) : 0, ldxs);
   (void)E;
   return status();
 }
@@ -1913,13 +1919,15 @@ int bf16_gemm_launch(const void* a, const void* b, int64_t T, int64_t N, int64_t
 }
 }  // namespace
 
-int sfp8_bf16_gemm_swiglu_fwd(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd,
-                              void* gu, void* h, void* stream) {
+int sfp8_bf16_gemm_swiglu_fwd(const void* x, int x_slab, const void* w, int64_t T, int64_t D, int64_t I,
+                              const float* rstd, void* gu, void* h, void* stream) {
   if (!w || (T > 0 && (!x || !gu || !h))) return kErrNullPointer;
   if (T < 0 || !bf16_shape(D, I) || !fits32(kTile, 2 * D) || !fits32(slab_rows(2 * I), 2 * D)) return kErrBadShape;
+  if (x_slab && !fits32(slab_rows(T), 2 * D)) return kErrBadShape;
   if (!al16(x) || !al16(w) || !al16(gu) || !al16(h)) return kErrBadAlignment;
   if (T == 0) return kOk;
-  return bf16_swiglu_launch(x, w, T, D, I, rstd, gu, h, nullptr, 1, cdiv(T, kTile), (hipStream_t)stream);
+  return bf16_swiglu_launch(x, w, T, D, I, rstd, gu, h, nullptr, 1, cdiv(T, kTile), x_slab ? slab_rows(T) : 0,
+                            (hipStream_t)stream);
 }
 
 int sfp8_bf16_moe_gemm_swiglu_fwd(const void* x, const void* w, int64_t E, int64_t D, int64_t I, const int* plan,
@@ -1930,7 +1938,7 @@ int sfp8_bf16_moe_gemm_swiglu_fwd(const void* x, const void* w, int64_t E, int64
     return kErrBadShape;
   if (!al16(x) || !al16(w) || !al16(gu) || !al16(h)) return kErrBadAlignment;
   if (ldp == 0) return kOk;
-  return bf16_swiglu_launch(x, w, 0, D, I, nullptr, gu, h, plan, E, (int)(ldp / kTile), (hipStream_t)stream);
+  return bf16_swiglu_launch(x, w, 0, D, I, nullptr, gu, h, plan, E, (int)(ldp / kTile), 0, (hipStream_t)stream);
 }
 
 int sfp8_bf16_gemm(const void* a, const void* b, int64_t T, int64_t N, int64_t K, int64_t lda, void* out,

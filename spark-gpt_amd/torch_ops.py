@@ -283,8 +283,10 @@ def norm_swiglu_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tupl
     T, D = h.shape
     I = w_gu.shape[0] // 2
     ws, wt = ops.bf16_weight_slabs(w_gu.detach().contiguous().unsqueeze(0), norm_w.detach().contiguous())
-    rstd, _ = ops.bf16_rows_prep(h, None, ops.ldt_of(T), float(eps), copy=False)
-    gu, out = ops.bf16_swiglu_fwd(h, ws, I, rstd=rstd)
+    # rstd, and the row K-slab of h that the GEMM reads (whole 128-byte
+    # lines per K stage; the weight gradient reads h itself)
+    rstd, _, hs = ops.bf16_rows_prep(h, None, ops.ldt_of(T), float(eps), copy=False, rows=True)
+    gu, out = ops.bf16_swiglu_fwd(h, ws, I, rstd=rstd, xs=hs)
     return out, wt, gu, rstd
 
 
@@ -367,7 +369,7 @@ def swiglu_bwd(dh: Tensor, x: Tensor, weight: Tensor, gu: Tensor, plan: Tensor) 
     E, I2, _ = weight.shape
     ldp = ops.moe_padded_rows(R, E)
     _, wt = ops.bf16_weight_slabs(weight, rows=False, transposed=True)
-    _, xt = ops.bf16_rows_prep(x, plan, ldp)
+    _, xt, _ = ops.bf16_rows_prep(x, plan, ldp)
     gs, _ = ops.bf16_swiglu_bwd(gu, dh, None, plan, ldp, copy=False)
     dx = ops.bf16_gemm(gs, wt, R, D, I2, plan=plan)
     # G' read through transposing LDS reads, x as its token-contiguous copy

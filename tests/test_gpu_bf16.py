@@ -78,10 +78,42 @@ def test_norm_swiglu_rstd_and_gu(dev):
     wp = B.fold_weight(w_gu, norm_w).to(torch.bfloat16)
     assert torch.equal(sg.ops.unslab(wt[0], D).cpu(), wp.t().contiguous())
     # the row pass with the token-contiguous h^T: the same rstd, an exact copy
-    rstd2, xt = sg.ops.bf16_rows_prep(h.to(dev), None, sg.ops.ldt_of(T), 1e-6)
+    rstd2, xt, xs = sg.ops.bf16_rows_prep(h.to(dev), None, sg.ops.ldt_of(T), 1e-6, rows=True)
     assert torch.equal(rstd2, rstd)
     ht = sg.ops.unslab(xt, D).cpu()
     assert torch.equal(ht[:, :T], h.t()) and torch.all(ht[:, T:] == 0)
+    # and the row K-slab of h (zero padding rows)
+    assert torch.equal(sg.ops.unslab(xs, sg.ops.ldt_of(T)).cpu()[:T], h)
+    assert torch.all(sg.ops.unslab(xs, sg.ops.ldt_of(T))[T:] == 0)
+
+
+@pytest.mark.parametrize("T,D,I", [(1000, 512, 384), (257, 1024, 256), (4099, 256, 192)])
+def test_bf16_forward_reads_row_slab(dev, T, D, I):
+    """The gate/up forward reading h's row K-slab (rows pass, rows=True)
+    gives the bytes of the one reading h row-major; the rows pass's slab is
+    an exact copy over the grouped padded order too."""
+    ops = sg.ops
+    h, norm_w, w_gu, _ = _norm_case(dev, T, D, I, 7)
+    h, norm_w, w_gu = h.to(dev), norm_w.to(dev), w_gu.to(dev)
+    ws, _ = ops.bf16_weight_slabs(w_gu.unsqueeze(0).contiguous(), norm_w, transposed=False)
+    rstd, _, hs = ops.bf16_rows_prep(h, None, ops.ldt_of(T), 1e-6, copy=False, rows=True)
+    gu_a, out_a = ops.bf16_swiglu_fwd(h, ws[0], I, rstd=rstd)
+    gu_b, out_b = ops.bf16_swiglu_fwd(h, ws[0], I, rstd=rstd, xs=hs)
+    assert torch.equal(gu_a, gu_b) and torch.equal(out_a, out_b)
+    counts = torch.tensor([T // 3, 0, T - T // 3])
+    offsets = torch.cumsum(counts, 0).to(torch.int32)
+    plan = ops.moe_plan(offsets.to(dev), T)
+    ldp = ops.moe_padded_rows(T, 3)
+    _, xt, xs = ops.bf16_rows_prep(h, plan, ldp, rows=True)
+    rows = sg.ops.unslab(xs, ldp).cpu()
+    p = 0
+    for e, n in enumerate(counts.tolist()):
+        r0 = int(offsets[e]) - n
+        assert torch.equal(rows[p:p + n], h[r0:r0 + n].cpu()), e
+        npad = -(-n // 256) * 256
+        assert torch.all(rows[p + n:p + npad] == 0), e
+        p += npad
+    assert torch.equal(sg.ops.unslab(xt, D).cpu().t(), rows)
 
 
 @pytest.mark.parametrize("hidden", [512, 1024])
@@ -330,7 +362,7 @@ def test_bf16_moe_wgrad_rows_equals_token_contiguous(dev, counts):
     gp = torch.randn(R, M // 2, device=dev, generator=g).to(torch.bfloat16)
     dout = torch.randn(R, M // 2, device=dev, generator=g).to(torch.bfloat16)
     gu = torch.cat([gp, gp * 0.5], 1).contiguous()
-    _, xt = ops.bf16_rows_prep(x, plan, ldp)
+    _, xt, _ = ops.bf16_rows_prep(x, plan, ldp)
     gs, gt = ops.bf16_swiglu_bwd(gu, dout, None, plan, ldp)
     ref = ops.bf16_wgrad(gt, xt, M, N, plan=plan, E=E)
     got = ops.bf16_wgrad_rows(gs, xt, M, N, plan=plan, E=E)
