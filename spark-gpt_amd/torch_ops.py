@@ -171,14 +171,19 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tenso
     _w8, w8t, _wd8, wdt, wscale = cached_weights(w_gu, w_down)
     dgu8, _ = ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax, copy=False)
     dxn = ops.gateup_dgrad(dgu8, w8t, scale, wscale, T, D)
-    dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, _master(norm_w), scale, amax)
-    del dxn
     # x8, h8 and dgu8 are read as the token-major K-slabs their producers
     # wrote (transposing LDS reads); dy8t is the norm backward's
     # token-contiguous copy (a gradient with both operands transposed on
-    # read is 2-3 % slower, the norm backward no faster for the row K-slab)
-    dwd = ops.wgrad_rows(dy8t, h8, D, I, scale[4:5], scale[2:3], a_rows=False)
+    # read is 2-3 % slower, the norm backward no faster for the row K-slab).
+    # The gate/up weight gradient runs right after the other reader of
+    # d_gu8, while part of it is still in the last-level cache (the launch
+    # order of train.py:1249-1251 is a9, a10, a11, a12, a13; the results
+    # do not depend on it): about 1 % off the backward.
     dwgu = ops.wgrad_rows(dgu8, x8, 2 * I, D, scale[3:4], scale[0:1])
+    del dgu8
+    dh, dnw, dy8t = ops.norm_bwd(h, rstd, dxn, dy, _master(norm_w), scale, amax)
+    del dxn
+    dwd = ops.wgrad_rows(dy8t, h8, D, I, scale[4:5], scale[2:3], a_rows=False)
     return dh, dnw, dwgu, dwd
 
 
