@@ -161,13 +161,16 @@ def test_moe_wgrad_rows_equals_token_contiguous(dev, M_, N_, counts):
             assert torch.all(ref[e] == 0)
 
 
-@pytest.mark.parametrize("I,counts", [(256, [700, 0, 1500, 1, 2049]), (1536, [3000, 257, 0, 5000])])
+@pytest.mark.parametrize("I,counts", [(256, [700, 0, 1500, 1, 2049]), (1536, [3000, 257, 0, 5000]),
+                                      (1536, [16476, 16579, 16396, 16215, 16245, 16370, 16368, 16423])])
 def test_moe_swiglu_pipe_equals_dense_per_expert(dev, I, counts):
     """At D = 1024 the grouped gate/up forward runs the persistent SwiGLU
     pipe over the plan's tiles, changing expert (weights and scale) from
     tile to tile: each expert's gu8 and h8 rows are the bytes the dense
     forward gives for that expert's rows alone, padding rows stay zero, and
-    amax slots 1, 2 are the maxima of the per-expert amax."""
+    amax slots 1, 2 are the maxima of the per-expert amax.  The last case is
+    the MoE workload's full size (131 072 routed rows over 8 experts: about
+    49 tiles per work-group of the persistent kernel)."""
     ops = sg.ops
     D = 1024
     counts = torch.tensor(counts)
