@@ -1659,9 +1659,15 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
 // Number of K splits the library uses for an (M, N, ldt) weight gradient and
 // the workspace (floats) it needs: splits * M * N when splits > 1, else 0.
 int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
+  // Splits double while the grid has fewer than 512 work-groups, but stop
+  // at 8 once it has 384: with 8 splits each XCD takes one K range of every
+  // tile (split_tile_coords), and the halved partials outweigh the grid's
+  // last half-filled round (the down gradient at T=65536, D=1024, I=3072:
+  // 48 tiles, 0.195 ms with 8 splits against 0.206 with 16)
   const int64_t tiles = (int64_t)cdiv(M, kTile) * cdiv(N, kTile);
   int64_t s = 1;
-  while (tiles * s < 512 && ldt % (s * 2) == 0 && (ldt / (s * 2)) % (2 * kStage) == 0 && ldt / (s * 2) >= 2048)
+  while (tiles * s < 512 && !(s >= 8 && tiles * s >= 384) && ldt % (s * 2) == 0 &&
+         (ldt / (s * 2)) % (2 * kStage) == 0 && ldt / (s * 2) >= 2048)
     s *= 2;
   return s;
 }
