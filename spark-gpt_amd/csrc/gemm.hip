@@ -1807,9 +1807,13 @@ int sfp8_moe_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t E, int
 // K splits of a grouped weight gradient: enough work-groups to fill the GPU
 // (about 512) when there are few experts and tiles.
 int64_t sfp8_moe_wgrad_splits(int64_t M, int64_t N, int64_t E) {
+  // at least 2 splits, then doubling until the grid has 384 work-groups (8 at
+  // most): at the MoE headline shape (8 experts, D=1024, I=1536) the down
+  // gradient takes 0.234 ms with 2 splits against 0.245 with 4, the gate/up
+  // one 0.397 with 2 against 0.413 with 1
   const int64_t wgs = (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * E;
   int64_t s = 1;
-  while (s < 8 && wgs * s < 512) s *= 2;
+  while (s < 8 && (s < 2 || wgs * s < 384)) s *= 2;
   return s;
 }
 
