@@ -464,8 +464,8 @@ def bf16_launch_name(sym: str, a) -> str:
 def time_bf16(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
     """The reference's default (bf16) dense MLP sub-block at the same shape:
     y = h + down_proj(_NormSwiGLU(h, norm_w, w_gu, eps)) under bf16 autocast
-    (train.py:2366-2369), forward + backward; _NormSwiGLU on this build's
-    kernels, the down projection on torch (hipBLASLt).  18*T*D*I FLOP per
+    (train.py:2366-2369), forward + backward; _NormSwiGLU on the HIP
+    kernels of libsparkfp8, the down projection on torch (hipBLASLt).  18*T*D*I FLOP per
     step, 12*T*D*I of them in _NormSwiGLU."""
     import torch
 

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package imports this
 directory; only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline leg
-of ``bench.py`` use it, and only as the checker (or as the timed CPU baseline),
+of ``bench.py`` use it, and only to check results (or as the timed CPU baseline),
 never as the thing being measured on the GPU.
 
 ``fp8_mlp`` restates the reference recipe (spark-gpt ``train.py:911-1253``) in

@@ -1,5 +1,6 @@
 """Torch-CPU restatement of spark-gpt's bf16 SwiGLU MLP path (its default,
-non-FP8 path).  TEST INFRASTRUCTURE ONLY (the checker; never shipped).
+non-FP8 path).  TEST INFRASTRUCTURE ONLY (results are checked against it;
+never shipped).
 
 Follows ``train.py`` of N8python/spark-gpt: ``_swiglu_gemm_kernel``
 (train.py:1625-1716), ``_swiglu_tiles`` / ``_swiglu_dgrad_kernel`` /

@@ -1,5 +1,6 @@
 """Torch-CPU restatement of spark-gpt's FP8 SwiGLU MLP block.  TEST
-INFRASTRUCTURE ONLY (the checker and the timed CPU baseline; never shipped).
+INFRASTRUCTURE ONLY (results are checked against it, and it is the timed CPU
+baseline; never shipped).
 
 Every function follows one piece of the reference (``train.py`` in
 N8python/spark-gpt) and cites it.  Arithmetic is fp32 with the reference's

@@ -1,5 +1,5 @@
 """Torch-CPU restatement of spark-gpt's FP8 MoE experts (``_FP8Experts``).
-TEST INFRASTRUCTURE ONLY (the checker; never shipped).
+TEST INFRASTRUCTURE ONLY (results are checked against it; never shipped).
 
 Follows ``train.py`` of N8python/spark-gpt, lines 1255-1606, per expert with
 the dense block's pieces (``oracle/fp8_mlp.py``): the expert-order gather and

@@ -125,7 +125,7 @@ def test_quant_rowcol_amax_ignores_nan(dev, C):
     assert amax[0].item() == 37.5
 
 
-def test_quant_rowcol_north_star_size(dev):
+def test_quant_rowcol_full_size(dev):
     """65536 x 4096 bf16 with 0.1% outlier columns x50, delayed scale from a
     prewarm pass; bytes, transpose, amax and next scale bit-exact."""
     g = torch.Generator().manual_seed(3)

@@ -1,5 +1,5 @@
-"""CPU tests that pin the oracle (oracle/fp8_mlp.py) before it is trusted as
-the GPU path's checker.
+"""CPU tests that pin the oracle (oracle/fp8_mlp.py) before the GPU path is
+tested against it.
 
 The reference holds no golden vectors for this path (its only test is a
 tolerance test against an fp32 autograd MLP, spark-gpt tests/test_fp8_mlp.py),
