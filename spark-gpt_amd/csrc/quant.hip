@@ -459,8 +459,20 @@ __global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restric
   partials += (int64_t)blockIdx.y * gridDim.x;
   float m = 0.0f;
   const int64_t n4 = n >> 2;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
-    const floatx4 v = reinterpret_cast<const floatx4*>(w)[i];
+  const int64_t step = (int64_t)gridDim.x * 256;
+  const floatx4* w4 = reinterpret_cast<const floatx4*>(w);
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // four independent loads in flight per trip
+  for (; i + 3 * step < n4; i += 4 * step) {
+    floatx4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = w4[i + u * step];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u][0]), fabsf(v[u][1])), fmaxf(fabsf(v[u][2]), fabsf(v[u][3]))));
+  }
+  for (; i < n4; i += step) {
+    const floatx4 v = w4[i];
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
   }
   if (blockIdx.x == 0)
@@ -494,6 +506,21 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
     if (w8t) w8t += e * R * cp_;
     if (wbt) wbt += e * R * cp_;
   }
+  // The grid covers rows and columns up to multiples of 256, so that the
+  // padding rows of every K-slab output are written (as zeros).
+  const int64_t r0 = (int64_t)blockIdx.x * WQ_TILE, c0 = (int64_t)blockIdx.y * WQ_TILE;
+  const int64_t rp = (R + 255) / 256 * 256, cp = (C + 255) / 256 * 256;
+  // each thread: 4 consecutive columns of 4 rows (64x64 tile = 1024 quads);
+  // the tile's loads are issued first, so their latency overlaps the fold
+  // of the amax partials below
+  floatx4 vq[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = threadIdx.x + 256 * k;
+    const int64_t gr = r0 + idx / (WQ_TILE / 4), gc = c0 + (idx % (WQ_TILE / 4)) * 4;
+    vq[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (gr < R && gc < C) vq[k] = *reinterpret_cast<const floatx4*>(w + gr * C + gc);
+  }
   float m = 0.0f;
   for (int i = threadIdx.x; i < nparts; i += 256) m = fmaxf(m, partials[i]);
   m = wave_max(m);
@@ -508,16 +535,12 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
   }
   __syncthreads();
   const float q = qs;
-  // The grid covers rows and columns up to multiples of 256, so that the
-  // padding rows of every K-slab output are written (as zeros).
-  const int64_t r0 = (int64_t)blockIdx.x * WQ_TILE, c0 = (int64_t)blockIdx.y * WQ_TILE;
-  const int64_t rp = (R + 255) / 256 * 256, cp = (C + 255) / 256 * 256;
-  // each thread: 4 consecutive columns of 4 rows (64x64 tile = 1024 quads)
-  for (int idx = threadIdx.x; idx < WQ_TILE * WQ_TILE / 4; idx += 256) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = threadIdx.x + 256 * k;
     const int r = idx / (WQ_TILE / 4), c4 = idx % (WQ_TILE / 4);
     const int64_t gr = r0 + r, gc = c0 + c4 * 4;
-    floatx4 v = {0.f, 0.f, 0.f, 0.f};
-    if (gr < R && gc < C) v = *reinterpret_cast<const floatx4*>(w + gr * C + gc);
+    const floatx4 v = vq[k];
     const uint32_t p = pack4_e4m3(v[0] * q, v[1] * q, v[2] * q, v[3] * q);
     // w8: K-slab of W over its columns, [C/64][rp][64]
     if (w8 && c0 < C) *reinterpret_cast<uint32_t*>(w8 + (gc >> 6) * rp * 64 + gr * 64 + (gc & 63)) = p;
