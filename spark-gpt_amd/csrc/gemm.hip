@@ -59,6 +59,14 @@ SFP8_DEV void split_tile_coords(int pid, int tiles_m, int tiles_n, int splits, i
     const int xcd = pid & 7, local = pid >> 3;
     split = xcd * (splits >> 3) + local / tiles;
     raster(local % tiles, tiles_m, tiles_n, tm, tn);
+  } else if ((8 % splits) == 0 && ((tiles * splits) & 7) == 0) {
+    // 2 or 4 splits: each takes 8 / splits XCDs, and each of those XCDs a
+    // contiguous run of its tiles, so the work-groups of one XCD share the
+    // split's K range out of their L2 (1.5-2 % faster than split-major
+    // order at 4 and 2 splits)
+    const int xcd = pid & 7, local = pid >> 3, per = 8 / splits;
+    split = xcd / per;
+    raster((xcd % per) * (tiles / per) + local, tiles_m, tiles_n, tm, tn);
   } else {
     split = pid / tiles;
     tile_coords(pid % tiles, tiles, tiles_m, tiles_n, tm, tn);
@@ -1658,18 +1666,45 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
 
 // Number of K splits the library uses for an (M, N, ldt) weight gradient and
 // the workspace (floats) it needs: splits * M * N when splits > 1, else 0.
-int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
-  // Splits double while the grid has fewer than 512 work-groups, but stop
-  // at 8 once it has 384: with 8 splits each XCD takes one K range of every
-  // tile (split_tile_coords), and the halved partials outweigh the grid's
-  // last half-filled round (the down gradient at T=65536, D=1024, I=3072:
-  // 48 tiles, 0.195 ms with 8 splits against 0.206 with 16)
+// A split count s is usable when it leaves every split a whole number of
+// 128-token stage pairs and at least 2048 tokens.
+static bool wgrad_split_ok(int64_t s, int64_t ldt) {
+  return s == 1 || (ldt % s == 0 && (ldt / s) % (2 * kStage) == 0 && ldt / s >= 2048);
+}
+
+// bf16 operands (ldt counts K bytes): splits double while the grid has fewer
+// than 512 work-groups, stopping at 8 once it has 384.
+static int64_t wgrad_splits_doubling(int64_t M, int64_t N, int64_t ldt) {
   const int64_t tiles = (int64_t)cdiv(M, kTile) * cdiv(N, kTile);
   int64_t s = 1;
-  while (tiles * s < 512 && !(s >= 8 && tiles * s >= 384) && ldt % (s * 2) == 0 &&
-         (ldt / (s * 2)) % (2 * kStage) == 0 && ldt / (s * 2) >= 2048)
-    s *= 2;
+  while (tiles * s < 512 && !(s >= 8 && tiles * s >= 384) && wgrad_split_ok(2 * s, ldt)) s *= 2;
   return s;
+}
+
+int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
+  // The power of two that minimises the modelled time: the rounds of
+  // work-groups the 256 CUs run, times each one's 64-token K stages, plus
+  // the split partials' traffic (4 bytes written and read per output and
+  // split, at about 5 TB/s: M * N * 8 / 3.5e6 stage times of 0.7 us).
+  // Measured at T = 65536 (ms): the down gradient (48 tiles) 0.313 / 0.191 /
+  // 0.211 / 0.222 with 2 / 4 / 8 / 16 splits, the gate/up one (96 tiles)
+  // 0.397 / 0.369 / 0.449 with 4 / 8 / 16; the model orders both alike.
+  // Ties go to fewer splits.
+  constexpr int64_t kCUs = 256;
+  const int64_t tiles = (int64_t)cdiv(M, kTile) * cdiv(N, kTile);
+  const double stages = (double)ldt / kStage;
+  const double part = (double)M * (double)N * 8.0 / 3.5e6;
+  int64_t best = 1;
+  double best_cost = 0.0;
+  for (int64_t s = 1; s <= 64 && tiles * s <= 2048; s *= 2) {
+    if (!wgrad_split_ok(s, ldt)) continue;
+    const double cost = (double)((tiles * s + kCUs - 1) / kCUs) * (stages / (double)s) + (s > 1 ? s * part : 0.0);
+    if (s == 1 || cost < best_cost - 1e-9) {
+      best = s;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 int64_t sfp8_slab_bytes(int64_t rows, int64_t k) {
@@ -1682,6 +1717,7 @@ int64_t sfp8_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
   const int64_t s = sfp8_wgrad_splits(M, N, ldt);
   return s > 1 ? s * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile : 0;
 }
+
 
 
 int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
@@ -1971,7 +2007,7 @@ int sfp8_bf16_moe_gemm(const void* a, const void* b, int64_t E, int64_t N, int64
   return bf16_gemm_launch(a, b, 0, N, K, ldp, out, plan, (int)(ldp / kTile), (hipStream_t)stream);
 }
 
-int64_t sfp8_bf16_wgrad_splits(int64_t M, int64_t N, int64_t ldt) { return sfp8_wgrad_splits(M, N, 2 * ldt); }
+int64_t sfp8_bf16_wgrad_splits(int64_t M, int64_t N, int64_t ldt) { return wgrad_splits_doubling(M, N, 2 * ldt); }
 
 int64_t sfp8_bf16_wgrad_workspace_floats(int64_t M, int64_t N, int64_t ldt) {
   return sfp8_bf16_wgrad_splits(M, N, ldt) * (int64_t)cdiv(M, kTile) * cdiv(N, kTile) * kTile * kTile;
