@@ -209,13 +209,18 @@ int64_t sfp8_norm_bwd_partials(int64_t D, int64_t ldt);
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments and results as sfp8_norm_bwd without the partials workspace:
  * the dnw partials live in a fixed file-scope device array of
- * SFP8_NOALLOC_SCRATCH_FLOATS floats (32 MiB), one per GPU, held until the
- * process ends.  Shapes whose sfp8_norm_bwd_partials(D, ldt) * D exceeds it
- * return SFP8_ERR_SCRATCH_LIMIT before anything is launched (ldt up to
- * 522240 tokens at D=1024, 130048 at D=2048, 32256 at D=4096).  The call allocates
+ * SFP8_NOALLOC_SCRATCH_FLOATS floats (32 MiB), one per GPU.  The array is
+ * part of the library's code object: every process that loads the library
+ * holds 32 MiB of device memory on each GPU it uses, until it exits,
+ * whether or not it ever calls this entry point.  Shapes whose
+ * sfp8_norm_bwd_partials(D, ldt) * D exceeds it return
+ * SFP8_ERR_SCRATCH_LIMIT before anything is launched (ldt up to 522240
+ * tokens at D=1024, 130048 at D=2048, 32256 at D=4096).  The call allocates
  * nothing; the first call on a device looks up that device's address of the
- * array.  Every call on one GPU shares its array: calls that overlap on one
- * GPU (concurrent streams, threads) race and must be serialised by the
+ * array (hipGetSymbolAddress), so make that first call outside graph
+ * capture; later calls may be captured (they launch kernels only, no
+ * memset).  Every call on one GPU shares its array: calls that overlap on
+ * one GPU (concurrent streams, threads) race and must be serialised by the
  * caller; nothing in it needs to start at zero. */
 #define SFP8_NOALLOC_SCRATCH_FLOATS (8LL << 20)
 int sfp8_norm_bwd_noalloc(const void* h, const float* rstd, const void* dxn, const void* dy, const float* norm_w,

@@ -49,28 +49,22 @@ SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, i
   raster(lid, tiles_m, tiles_n, tm, tn);
 }
 
-// Split-K mapping of a 1-D grid of tiles * splits work-groups.  With splits a
-// multiple of 8, XCD x runs splits [x*splits/8, (x+1)*splits/8) over every
-// tile, so the work-groups resident on one XCD read the same K range of A
-// and B and share it in that XCD's L2.  Otherwise split = pid / tiles.
+// Split-K mapping of a 1-D grid of tiles * splits work-groups.  Work-groups
+// are dispatched round-robin over the 8 XCDs (pid % 8); each XCD takes a
+// contiguous run of the split-major order (split, tile), so the work-groups
+// resident on one XCD read the same K range of A and B (one split, or two
+// where a run crosses a split boundary) and share it in that XCD's L2.  With
+// splits a multiple of 8 each XCD runs whole splits over every tile; with 2
+// or 4 each split takes 8 / splits XCDs (1.5-2 % faster than split-major
+// order over all XCDs at 4 and 2 splits).  Tiles of a split are rastered as
+// in tile_coords.
 SFP8_DEV void split_tile_coords(int pid, int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
-  const int tiles = tiles_m * tiles_n;
-  if ((splits & 7) == 0) {
-    const int xcd = pid & 7, local = pid >> 3;
-    split = xcd * (splits >> 3) + local / tiles;
-    raster(local % tiles, tiles_m, tiles_n, tm, tn);
-  } else if ((8 % splits) == 0 && ((tiles * splits) & 7) == 0) {
-    // 2 or 4 splits: each takes 8 / splits XCDs, and each of those XCDs a
-    // contiguous run of its tiles, so the work-groups of one XCD share the
-    // split's K range out of their L2 (1.5-2 % faster than split-major
-    // order at 4 and 2 splits)
-    const int xcd = pid & 7, local = pid >> 3, per = 8 / splits;
-    split = xcd / per;
-    raster((xcd % per) * (tiles / per) + local, tiles_m, tiles_n, tm, tn);
-  } else {
-    split = pid / tiles;
-    tile_coords(pid % tiles, tiles, tiles_m, tiles_n, tm, tn);
-  }
+  const int tiles = tiles_m * tiles_n, nwg = tiles * splits;
+  const int per = nwg >> 3, rem = nwg & 7;
+  const int xcd = pid & 7, local = pid >> 3;
+  const int lid = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  split = lid / tiles;
+  raster(lid % tiles, tiles_m, tiles_n, tm, tn);
 }
 
 // Output column (within the 256-column tile) held in B-tile row r, plain
@@ -1057,7 +1051,9 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
 //   out[m, n] = sum_t A[m, t] * B[n, t] / (sa * sb)
 // A, B are K-slab token-contiguous fp8 copies (common.h) over ldt tokens
 // (zeros past T): a tile's K stage is one contiguous 16 KiB block of each.
-// The grid is tiles * splits work-groups (split_tile_coords); with splits > 1
+// The grid is tiles * splits work-groups (split_tile_coords); split sp takes
+// K bytes [sp * kchunk, min((sp + 1) * kchunk, ldt)) (the last split may be
+// shorter; every split is a whole number of 128-byte stage pairs); with splits > 1
 // each split writes its raw fp32 accumulators to ws in accumulator order
 // (frag_offset below: each wave store instruction is one contiguous 1 KiB
 // run) and splitk_reduce_kernel sums them in split order (deterministic) and
@@ -1110,7 +1106,7 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
         lds, a0, a_end - a0, [=](int r) { return TRA ? (r / kRows) * abs_ + (r % kRows) * ats : r * kStage; },
         TRA ? kRows * ats : (int)(rpa * kStage), b0, b_end - b0,
         [=](int r) { return TRB ? (r / kRows) * bbs + (r % kRows) * bts : plain_col(r) * kStage; },
-        TRB ? kRows * bts : (int)(rpb * kStage), (int)(kchunk / kStage), acc);
+        TRB ? kRows * bts : (int)(rpb * kStage), (int)((kchunk < ldt - kb ? kchunk : ldt - kb) / kStage), acc);
   }
   if (BF16 || TRA || TRB || partials) {
     // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
@@ -1541,6 +1537,13 @@ inline int cu_count(int* n) {
 // offsets inside one operand tile are 32-bit
 inline bool fits32(int64_t rows, int64_t ld) { return rows * ld < (int64_t)1 << 31; }
 
+// K bytes per weight-gradient split: ldt / s rounded up to whole 128-byte
+// stage pairs (the last split takes what remains).
+inline int64_t wgrad_chunk(int64_t ldt, int64_t s) {
+  const int64_t per = (ldt + s - 1) / s;
+  return (per + 2 * kStage - 1) / (2 * kStage) * (2 * kStage);
+}
+
 }  // namespace
 
 namespace {
@@ -1556,8 +1559,8 @@ int wgrad_partials(const void* a, const void* b, int64_t M, int64_t N, int64_t l
   // row K-slabs over ldt tokens
   const TrOp tra{kStage, ldt * kStage, (M / 64) * ldt * kStage}, trb{kStage, ldt * kStage, (N / 64) * ldt * kStage};
   hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>), dim3((unsigned)(tiles_m * tiles_n * splits)),
-                     dim3(256), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, ldt / splits, sa, sb, ws,
-                     tiles_m, tiles_n, splits, 1, tra, trb);
+                     dim3(256), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, wgrad_chunk(ldt, splits), sa,
+                     sb, ws, tiles_m, tiles_n, splits, 1, tra, trb);
   return status();
 }
 
@@ -1666,39 +1669,46 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
 
 // Number of K splits the library uses for an (M, N, ldt) weight gradient and
 // the workspace (floats) it needs: splits * M * N when splits > 1, else 0.
-// A split count s is usable when it leaves every split a whole number of
-// 128-token stage pairs and at least 2048 tokens.
+// Split sp covers K [sp * c, min((sp + 1) * c, ldt)) with c = wgrad_chunk:
+// ldt / s rounded up to whole 128-token (128-byte) stage pairs, so the last
+// split may be shorter.  s is usable when every split has at least 2048
+// tokens' worth of chunk and the last split is not empty.
 static bool wgrad_split_ok(int64_t s, int64_t ldt) {
-  return s == 1 || (ldt % s == 0 && (ldt / s) % (2 * kStage) == 0 && ldt / s >= 2048);
+  if (s == 1) return true;
+  const int64_t c = wgrad_chunk(ldt, s);
+  return c >= 2048 && ldt - (s - 1) * c > 0;
 }
 
 // bf16 operands (ldt counts K bytes): splits double while the grid has fewer
-// than 512 work-groups, stopping at 8 once it has 384.
+// than 512 work-groups, stopping at 8 once it has 384; every split equal.
 static int64_t wgrad_splits_doubling(int64_t M, int64_t N, int64_t ldt) {
   const int64_t tiles = (int64_t)cdiv(M, kTile) * cdiv(N, kTile);
   int64_t s = 1;
-  while (tiles * s < 512 && !(s >= 8 && tiles * s >= 384) && wgrad_split_ok(2 * s, ldt)) s *= 2;
+  while (tiles * s < 512 && !(s >= 8 && tiles * s >= 384) && ldt % (2 * s) == 0 &&
+         (ldt / (2 * s)) % (2 * kStage) == 0 && ldt / (2 * s) >= 2048)
+    s *= 2;
   return s;
 }
 
 int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt) {
-  // The power of two that minimises the modelled time: the rounds of
-  // work-groups the 256 CUs run, times each one's 64-token K stages, plus
-  // the split partials' traffic (4 bytes written and read per output and
-  // split, at about 5 TB/s: M * N * 8 / 3.5e6 stage times of 0.7 us).
-  // Measured at T = 65536 (ms): the down gradient (48 tiles) 0.313 / 0.191 /
-  // 0.211 / 0.222 with 2 / 4 / 8 / 16 splits, the gate/up one (96 tiles)
-  // 0.397 / 0.369 / 0.449 with 4 / 8 / 16; the model orders both alike.
-  // Ties go to fewer splits.
+  // The count (any, not only a power of two) that minimises the modelled
+  // time: the rounds of work-groups the 256 CUs run, times the longest
+  // split's 64-token K stages, plus the split partials' traffic (4 bytes
+  // written and read per output and split, at about 5 TB/s: M * N * 8 /
+  // 3.5e6 stage times of 0.7 us).  At T = 65536 this gives 5 splits for both
+  // the down gradient (48 tiles: 240 work-groups in one round, where 4
+  // splits leave 64 CUs idle) and the gate/up one (96 tiles: 480 work-groups
+  // in two rounds, against three rounds of 256 with 8).  Ties go to fewer
+  // splits.
   constexpr int64_t kCUs = 256;
   const int64_t tiles = (int64_t)cdiv(M, kTile) * cdiv(N, kTile);
-  const double stages = (double)ldt / kStage;
   const double part = (double)M * (double)N * 8.0 / 3.5e6;
   int64_t best = 1;
   double best_cost = 0.0;
-  for (int64_t s = 1; s <= 64 && tiles * s <= 2048; s *= 2) {
+  for (int64_t s = 1; s <= 64 && tiles * s <= 2048; ++s) {
     if (!wgrad_split_ok(s, ldt)) continue;
-    const double cost = (double)((tiles * s + kCUs - 1) / kCUs) * (stages / (double)s) + (s > 1 ? s * part : 0.0);
+    const double stages = (double)wgrad_chunk(ldt, s) / kStage;
+    const double cost = (double)((tiles * s + kCUs - 1) / kCUs) * stages + (s > 1 ? s * part : 0.0);
     if (s == 1 || cost < best_cost - 1e-9) {
       best = s;
       best_cost = cost;
@@ -1742,8 +1752,8 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
   if (rc) return rc;
   hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
-                     kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, ldt / splits, sa, sb,
-                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1), TrOp{}, TrOp{});
+                     kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, wgrad_chunk(ldt, splits), sa,
+                     sb, splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1), TrOp{}, TrOp{});
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;

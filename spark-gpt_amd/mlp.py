@@ -117,7 +117,7 @@ class MLP(nn.Module):
         self.register_buffer("fp8_amax", torch.zeros(5), persistent=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if _swiglu._use_fused_swiglu(x) and self.gate_up_proj.weight.shape[0] % 128 == 0:
+        if _swiglu._use_fused_swiglu(x):
             weight = self.gate_up_proj.weight.to(dtype=x.dtype).unsqueeze(0)
             offs = torch.full((1,), x.shape[0], device=x.device, dtype=torch.int32)
             return self.down_proj(_swiglu._FusedSwiGLU.apply(x, weight, offs))

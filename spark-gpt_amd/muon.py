@@ -28,10 +28,18 @@ from . import ops
 
 
 def _momentum_stage_supported(g, v, u, momentum: float) -> bool:
-    return (g.is_cuda and g.is_contiguous() and v.is_contiguous() and u.is_contiguous()
+    """The reference's predicate plus what the kernel needs: a bf16 u, a
+    length divisible by 4, one device, g and v 16-byte and u 8-byte aligned,
+    and -0.5 < 1 - momentum (the kernel's fp32 weights).  Anything else takes
+    the caller's torch path."""
+    import numpy as np
+
+    return (g.is_cuda and v.is_cuda and u.is_cuda and v.device == g.device and u.device == g.device
+            and g.is_contiguous() and v.is_contiguous() and u.is_contiguous()
             and g.dtype == torch.float32 and v.dtype == torch.float32 and u.dtype == torch.bfloat16
             and g.numel() == v.numel() == u.numel() and g.numel() % 4 == 0
-            and 1.0 - momentum < 0.5 <= momentum)
+            and g.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0 and u.data_ptr() % 8 == 0
+            and bool(-0.5 < np.float32(1.0 - momentum) < 0.5 <= np.float32(momentum)))
 
 
 def _momentum_stage(g, v, u, momentum: float) -> None:

@@ -624,13 +624,38 @@ def bf16_fold_grads(dwp: torch.Tensor, w: torch.Tensor, norm_w: torch.Tensor):
 
 
 # ----------------------------------------------------- the optimizer's momentum stage
+def _flat_state(name: str, t, dtype: torch.dtype, numel: int, device, align: int) -> None:
+    """t is a contiguous `dtype` tensor of `numel` elements on `device` whose
+    data pointer is `align`-byte aligned (what the kernels' vector accesses
+    need); raises ValueError before anything is launched."""
+    _need(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _need(t.is_cuda and t.device == device, f"{name} must be a ROCm device tensor on {device}")
+    _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+    _need(t.numel() == numel, f"{name} must have {numel} elements, got {t.numel()}")
+    _need(t.data_ptr() % align == 0, f"{name} must be {align}-byte aligned")
+
+
+def _momentum_weights(momentum: float) -> None:
+    """The kernels take w_v = 1 - momentum and w_u = momentum as fp32 values
+    (ctypes rounds them as the reference's launch does) with
+    -0.5 < w_v < 0.5 <= w_u."""
+    import numpy as np
+
+    w_v, w_u = np.float32(1.0 - momentum), np.float32(momentum)
+    _need(bool(-0.5 < w_v < 0.5 <= w_u), f"momentum {momentum} outside the kernel's range (0.5 <= momentum < 1.5)")
+
+
 def momentum_stage(g: torch.Tensor, v: torch.Tensor, u: torch.Tensor, momentum: float) -> None:
     """v <- lerp(v, g, 1 - momentum) in place; u <- bf16(lerp(g, v, momentum))."""
-    _need(g.is_cuda and g.dtype == torch.float32 and v.dtype == torch.float32 and u.dtype == BF16,
-          "g, v must be fp32 and u bf16 device tensors")
-    _need(g.is_contiguous() and v.is_contiguous() and u.is_contiguous(), "g, v, u must be contiguous")
-    _need(g.numel() == v.numel() == u.numel(), "g, v, u must have the same number of elements")
-    _lib.call("sfp8_momentum_stage", g.data_ptr(), v.data_ptr(), u.data_ptr(), g.numel(), 1.0 - momentum, momentum,
+    _need(isinstance(g, torch.Tensor) and g.is_cuda, "g must be a ROCm device tensor")
+    n = g.numel()
+    _need(n % 4 == 0, "g, v, u need a multiple of 4 elements")
+    _flat_state("g", g, torch.float32, n, g.device, 16)
+    _flat_state("v", v, torch.float32, n, g.device, 16)
+    _flat_state("u", u, BF16, n, g.device, 8)
+    _momentum_weights(momentum)
+    _lib.call("sfp8_momentum_stage", g.data_ptr(), v.data_ptr(), u.data_ptr(), n, 1.0 - momentum, momentum,
               _lib.stream_of(g))
 
 
@@ -639,10 +664,19 @@ def wgrad_momentum(a8, b8, M: int, N: int, sa, sb, v: torch.Tensor, u: torch.Ten
     """wgrad (a_rows = b_rows = False) or wgrad_rows of the same operands
     handed straight to the momentum stage: v <- lerp(v, dW, 1 - momentum),
     u <- bf16(lerp(dW, v, momentum)); dW is also written to `grad` when
-    given."""
+    given.  v and grad are fp32, u bf16, each [M, N] on the operands' device;
+    sa and sb are fp32 scales there."""
     _cuda_contig("a8", a8, E5M2, 3)
     _cuda_contig("b8", b8, E4M3, 3)
-    _need(v.is_contiguous() and u.is_contiguous() and v.numel() == u.numel() == M * N, "v, u must be [M, N]")
+    _need(b8.device == a8.device, "a8, b8 must be on the same device")
+    _flat_state("v", v, torch.float32, M * N, a8.device, 16)
+    _flat_state("u", u, BF16, M * N, a8.device, 8)
+    if grad is not None:
+        _flat_state("grad", grad, torch.float32, M * N, a8.device, 16)
+    for name, t in (("sa", sa), ("sb", sb)):
+        _need(isinstance(t, torch.Tensor) and t.is_cuda and t.device == a8.device and t.dtype == torch.float32
+              and t.numel() >= 1, f"{name} must be an fp32 scale on {a8.device}")
+    _momentum_weights(momentum)
     ldt = a8.shape[1] if a_rows else a8.shape[0] * SLAB
     _need((b8.shape[1] if b_rows else b8.shape[0] * SLAB) == ldt, "a8, b8 must cover the same tokens")
     nws = _lib.query("sfp8_wgrad_momentum_workspace_floats", M, N, ldt)

@@ -258,6 +258,53 @@ def test_mlp_forward_takes_the_fused_path(dev, monkeypatch):
     assert O.rel_l2(y.float().cpu(), y_ref.float().cpu()) < 1e-2
 
 
+def test_bf16_path_shapes_the_kernels_refuse(dev):
+    """D = 192, I = 96 (I % 64 != 0; the reference's Triton kernels mask any
+    shape): MLP.forward, _FusedSwiGLU and _NormSwiGLU run the reference's
+    unfused torch path instead of raising, match the bf16 oracle within
+    rel-L2 1e-2 (one more bf16 rounding: F.silu(gate) is rounded before the
+    product), and a few optimizer steps train through the drop-in."""
+    T, D, I = 500, 192, 96
+    x, w, offs, probe = _fused_case([T], rows=T, dim=D, inter=I, seed=11)
+    h, dx, dw = _gpu_fused(dev, x, w, offs, probe)
+    r_h, r_gu = B.fused_swiglu_forward(x, w, offs)
+    r_dx, r_dw = B.fused_swiglu_backward(probe, x, w, r_gu, offs)
+    for name, a, r in (("h", h, r_h), ("dx", dx, r_dx), ("dw", dw, r_dw)):
+        assert a.dtype == torch.bfloat16, name
+        assert O.rel_l2(a.float().cpu(), r.float()) < 1e-2, name
+    # grouped, with a group without rows
+    x3, w3, offs3, probe3 = _fused_case([200, 0, 300], rows=T, dim=D, inter=I, seed=12)
+    h3, dx3, dw3 = _gpu_fused(dev, x3, w3, offs3, probe3)
+    r_h3, r_gu3 = B.fused_swiglu_forward(x3, w3, offs3)
+    r_dx3, r_dw3 = B.fused_swiglu_backward(probe3, x3, w3, r_gu3, offs3)
+    assert O.rel_l2(h3.float().cpu(), r_h3.float()) < 1e-2
+    assert O.rel_l2(dx3.float().cpu(), r_dx3.float()) < 1e-2
+    assert torch.all(dw3[1] == 0)
+    # the norm-folded sub-block
+    hn, norm_w, w_gu, probe_n = _norm_case(dev, T, D, I, 13)
+    out, dh, dnw, dwg = _gpu_norm_step(dev, hn, norm_w, w_gu, probe_n)
+    r_out, saved = B.norm_swiglu_forward(hn, norm_w, w_gu, 1e-6)
+    r_dh, r_dnw, r_dw = B.norm_swiglu_backward(probe_n.to(torch.bfloat16), saved)
+    for name, a, r in (("out", out, r_out), ("dh", dh, r_dh), ("dnorm_w", dnw, r_dnw), ("dw_gu", dwg, r_dw)):
+        assert torch.isfinite(a.float()).all(), name
+        assert O.rel_l2(a.float().cpu(), r.float()) < 1e-2, name
+    # the drop-in MLP trains: its loss falls over a few SGD steps
+    torch.manual_seed(2)
+    mlp = sg.MLP(D, I).to(dev)
+    xin = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    target = torch.randn(T, D, device=dev) * 0.1
+    opt = torch.optim.SGD(mlp.parameters(), lr=0.5)
+    losses = []
+    for _ in range(5):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = (mlp(xin).float() - target).pow(2).mean()
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        losses.append(float(loss.detach()))
+    assert all(torch.isfinite(torch.tensor(losses))) and losses[-1] < losses[0], losses
+
+
 def test_norm_swiglu_deterministic_and_zero_rows(dev):
     h, norm_w, w_gu, probe = _norm_case(dev, 600, 256, 256, 6)
     a = _gpu_norm_step(dev, h, norm_w, w_gu, probe)

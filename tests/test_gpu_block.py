@@ -274,12 +274,16 @@ def _rmsnorm_ref(x, weight, eps):
 
 @pytest.mark.parametrize("T,D,I", [(4096, 1024, 3072)])
 def test_block_vs_bf16_mlp(dev, T, D, I, capsys):
-    """The FP8 block against the reference's bf16 path for the same sub-block
+    """The FP8 block against an independent bf16 MLP for the same sub-block
     (train.py:2370-2374: RMSNorm, then the MLP under bf16 autocast, plus the
-    residual), same weights and upstream gradient.  The FP8 recipe differs
-    from bf16 by its e4m3/e5m2 roundings: the reference measured 5-8 % per
-    element (CHANGES.md:372-373); rel-L2 here stays under the reference
-    test's 0.12 bound, and each number is printed for the record."""
+    residual), same weights and upstream gradient.  The comparator is the
+    reference's unfused torch branch of MLP.forward (train.py:260-261:
+    gate_up_proj, chunk, F.silu(gate) * up, down_proj) on torch's own
+    matmuls and autograd, so no kernel of this library is on its path.  The
+    FP8 recipe differs from bf16 by its e4m3/e5m2 roundings: the reference
+    measured 5-8 % per element (CHANGES.md:372-373); rel-L2 here stays under
+    the reference test's 0.12 bound, and each number is printed for the
+    record."""
     norm, mlp = _setup(dev, T, D, I, 41)
     g = torch.Generator(device=dev).manual_seed(42)
     h = torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16)
@@ -296,7 +300,8 @@ def test_block_vs_bf16_mlp(dev, T, D, I, capsys):
     got = fp8()
     x = h.clone().requires_grad_(True)
     with torch.autocast("cuda", dtype=torch.bfloat16):
-        y = x + mlp(_rmsnorm_ref(x, norm.weight, norm.eps))
+        gate, up = mlp.gate_up_proj(_rmsnorm_ref(x, norm.weight, norm.eps)).chunk(2, dim=-1)
+        y = x + mlp.down_proj(torch.nn.functional.silu(gate) * up)
     ref = [y] + list(torch.autograd.grad(y, [x] + params, dy))
     errs = {}
     for name, a, r in zip(("y - h", "dh", "dnorm_w", "dW_gate_up", "dW_down"), got, ref):

@@ -147,6 +147,48 @@ def test_headline_full_size_row_local(dev):
     assert torch.equal(tail[1], full[1][T - R:])
 
 
+def test_headline_block_weight_gradients_vs_matmul(dev, monkeypatch):
+    """tokens=65536, d_model=1024, ffn=3072: the block's own dW_gate_up and
+    dW_down (split-K over 65536 tokens, both gate/up operands and h8 read
+    through transposing LDS reads) against a float64 matmul of the operands
+    the block itself produced in that backward (d_gu8 and x8, dy8t and h8,
+    dequantized with the scales it used): rel-L2 < 1e-4 (the fp32
+    accumulation's own error is about 1e-5 at this length)."""
+    T, D, I = 65536, 1024, 3072
+    ops = sg.ops
+    norm, mlp = make_layer(dev, D, I, 8)
+    gen = torch.Generator(device=dev).manual_seed(58)
+    h = torch.randn(T, D, generator=gen, device=dev).to(torch.bfloat16)
+    dy = (torch.randn(T, D, generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
+    block_step(h, dy, norm, mlp)
+    sg.fp8_update_scales(mlp)
+    seen = []
+    real = ops.wgrad_rows
+
+    def spy(a8, b8, M, N, sa, sb, **kw):
+        out = real(a8, b8, M, N, sa, sb, **kw)
+        seen.append((a8, b8, M, N, sa.clone(), sb.clone(), kw, out))
+        return out
+
+    monkeypatch.setattr(ops, "wgrad_rows", spy)
+    _, _, _, dwgu, dwd = block_step(h, dy, norm, mlp)
+    monkeypatch.setattr(ops, "wgrad_rows", real)
+    assert len(seen) == 2
+    (g8, x8, M1, N1, s3, s0, kw1, o1), (d8t, h8, M2, N2, s4, s2, kw2, o2) = seen
+    assert (M1, N1, kw1) == (2 * I, D, {}) and (M2, N2, kw2) == (D, I, {"a_rows": False})
+    assert o1 is dwgu and o2 is dwd
+    # the row K-slabs [cols/64, ldt, 64] and the token-contiguous dy8t [ldt/64, D, 64]
+    G = ops.unslab(g8, T).double()          # [T, 2I] e5m2 codes of d_gu
+    X = ops.unslab(x8, T).double()          # [T, D]
+    Y = ops.unslab(d8t, D)[:, :T].double()  # [D, T]
+    H = ops.unslab(h8, T).double()          # [T, I]
+    ref_gu = (G.t() @ X) / (s3.double() * s0.double())
+    ref_d = (Y @ H) / (s4.double() * s2.double())
+    for name, got, ref in (("dW_gate_up", dwgu, ref_gu), ("dW_down", dwd, ref_d)):
+        assert torch.isfinite(got).all(), name
+        assert float((got.double() - ref).norm() / ref.norm()) < 1e-4, name
+
+
 def test_wide_full_size_wgrad_gemm(dev):
     """The down-proj weight gradient at tokens=65536 (split-K over the whole
     token range) against a float32 matmul of the same e5m2 / e4m3 operands."""

@@ -324,13 +324,21 @@ def test_wgrad_ragged_columns_stay_in_bounds(dev, M, N):
     assert bool((buf[M * N:] == 12345.0).all())
 
 
-@pytest.mark.parametrize("M,N,T", [(6144, 1024, 4096), (1024, 3072, 16384), (320, 192, 1000), (256, 256, 65536)])
-def test_wgrad_rows_equals_token_contiguous(dev, M, N, T):
+@pytest.mark.parametrize("M,N,T,splits", [(6144, 1024, 4096, 2), (1024, 3072, 16384, 5), (1024, 1024, 8192, 4),
+                                          (1024, 1024, 16384, 8), (320, 192, 1000, 1), (256, 256, 65536, 32)])
+def test_wgrad_rows_equals_token_contiguous(dev, M, N, T, splits):
     """The weight gradient read from the row K-slabs through transposing LDS
     reads gives the bytes of the one read from the token-contiguous copies
     (same values in the same MFMA K positions, same split sums): one split
-    and several, ragged tiles, and the same operands in both layouts."""
+    and several (2 and 4 splits: each split on 8 / splits XCDs; 5: uneven
+    splits, the last shorter, runs of the split-major order crossing split
+    boundaries; 8 and 32: whole splits per XCD), ragged tiles, and the same
+    operands in both layouts.  The result is also checked against a float64
+    matmul of the same operands, which no split mapping shares."""
+    from spark_gpt_amd import _lib
+
     ops = sg.ops
+    assert _lib.query("sfp8_wgrad_splits", M, N, ops.ldt_of(T)) == splits
     g = torch.Generator(device=dev).manual_seed(M + N + T)
     a = (torch.randn(T, M, device=dev, generator=g) * 8).to(ops.E5M2)
     b = (torch.randn(T, N, device=dev, generator=g) * 8).to(ops.E4M3)
@@ -341,6 +349,9 @@ def test_wgrad_rows_equals_token_contiguous(dev, M, N, T):
     sa = torch.tensor([2.0 ** 4], device=dev)
     sb = torch.tensor([2.0 ** -2], device=dev)
     ref = ops.wgrad(a_t, b_t, M, N, sa, sb)
+    exact = (a.double().t() @ b.double()) / (sa.double() * sb.double())
+    # fp32 accumulation over T products: rel-L2 about 1e-5 at T = 65536
+    assert float((ref.double() - exact).norm() / exact.norm()) < 1e-4
     assert torch.equal(ops.wgrad_rows(a_rows, b_rows, M, N, sa, sb), ref)
     assert torch.equal(ops.wgrad_rows(a_rows, b_t, M, N, sa, sb, b_rows=False), ref)
     assert torch.equal(ops.wgrad_rows(a_t, b_rows, M, N, sa, sb, a_rows=False), ref)

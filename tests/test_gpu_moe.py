@@ -253,12 +253,14 @@ def test_fp8_experts_track_fp32_reference(dev):
 
 
 @pytest.mark.parametrize("T,D,I,E,k,skew", [(500, 256, 128, 4, 2, False), (4096, 1024, 256, 8, 2, True),
-                                            (300, 128, 384, 3, 1, False)])
+                                            (300, 128, 384, 3, 1, False), (65536, 1024, 1536, 8, 2, False)])
 def test_moe_matches_oracle(dev, T, D, I, E, k, skew):
     """Same inputs and scales: every output and gradient within rel-L2 1e-2 of
     the oracle; amax slots 0 and 4 bit-exact.  `skew` routes half of the
     tokens' first slot to expert 0 (the imbalance spark-gpt sees in
-    practice)."""
+    practice).  The last case is the MoE workload's full size (65536 tokens
+    top-2 of 8 experts, D=1024, I=1536: about 16.4k rows per expert), forward
+    and backward."""
     ex = _make(dev, E, D, I, T + E)
     g = torch.Generator().manual_seed(T)
     x = torch.randn(T, D, generator=g).to(torch.bfloat16)

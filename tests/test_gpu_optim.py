@@ -43,6 +43,52 @@ def test_momentum_stage_predicate(dev):
     assert not sg._momentum_stage_supported(g, g.clone(), u.float(), 0.95)  # u not bf16
     assert not sg._momentum_stage_supported(g[:6], g[:6].clone(), u[:6], 0.95)  # length % 4
     assert not sg._momentum_stage_supported(g.cpu(), g.cpu(), u.cpu(), 0.95)
+    # what the kernel refuses takes the torch path instead of raising:
+    # 1 - momentum <= -0.5, and storage offsets that break the alignment
+    assert not sg._momentum_stage_supported(g, g.clone(), u, 1.6)
+    g12 = torch.zeros(12, device=dev)
+    u12 = torch.zeros(12, dtype=torch.bfloat16, device=dev)
+    assert not sg._momentum_stage_supported(g12[2:10], g12[:8].clone(), u12[:8], 0.95)  # g at 8 bytes
+    assert not sg._momentum_stage_supported(g12[:8], g12[2:10], u12[:8], 0.95)  # v at 8 bytes
+    assert not sg._momentum_stage_supported(g12[:8], g12[:8].clone(), u12[2:10], 0.95)  # u at 4 bytes
+    assert not sg._momentum_stage_supported(g, g.clone(), u.to("cpu"), 0.95)
+
+
+def test_momentum_wrappers_reject_bad_state(dev):
+    """ops.momentum_stage and ops.wgrad_momentum refuse, with ValueError and
+    before any launch, every state tensor of the wrong dtype, size, device or
+    alignment (the kernels write fp32 v / grad and packed bf16 u through raw
+    pointers)."""
+    ops = sg.ops
+    M, N, T = 256, 128, 512
+    at, bt, sa, sb = _wgrad_operands(dev, M, N, T, 5)
+    v0 = torch.zeros(M, N, device=dev)
+    u0 = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+    bad_v = (v0.to(torch.bfloat16), v0[:-1], v0.cpu(), torch.zeros(M * N + 4, device=dev)[1:M * N + 1])
+    bad_u = (u0.float(), u0[:-1], u0.cpu(), torch.zeros(M * N + 4, dtype=torch.bfloat16, device=dev)[1:M * N + 1])
+    sentinel = torch.full((M, N), 7.0, device=dev)
+    for v in bad_v:
+        with pytest.raises(ValueError):
+            ops.wgrad_momentum(at, bt, M, N, sa, sb, v, u0, 0.95)
+    for u in bad_u:
+        with pytest.raises(ValueError):
+            ops.wgrad_momentum(at, bt, M, N, sa, sb, v0, u, 0.95)
+    for grad in (torch.zeros(M, N, dtype=torch.bfloat16, device=dev), torch.zeros(M * N // 2, device=dev),
+                 torch.zeros(M, N)):
+        with pytest.raises(ValueError):
+            ops.wgrad_momentum(at, bt, M, N, sa, sb, v0, u0, 0.95, grad=grad)
+    for scale in (sa.cpu(), sa.double(), torch.empty(0, device=dev)):
+        with pytest.raises(ValueError):
+            ops.wgrad_momentum(at, bt, M, N, scale, sb, v0, u0, 0.95)
+    with pytest.raises(ValueError):
+        ops.wgrad_momentum(at, bt, M, N, sa, sb, v0, u0, 1.6)
+    g = sentinel.view(-1)
+    for v, u in ((bad_v[0].view(-1), u0.view(-1)), (v0.view(-1)[:-4], u0.view(-1)), (v0.view(-1), bad_u[0].view(-1)),
+                 (v0.view(-1).cpu(), u0.view(-1)), (v0.view(-1), bad_u[3])):
+        with pytest.raises(ValueError):
+            ops.momentum_stage(g, v, u, 0.95)
+    torch.cuda.synchronize()
+    assert bool((v0 == 0).all()) and bool((u0 == 0).all()) and bool((sentinel == 7.0).all())
 
 
 def _wgrad_operands(dev, M, N, T, seed):

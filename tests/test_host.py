@@ -59,7 +59,11 @@ def test_size_queries_need_no_gpu():
     assert _lib.query("sfp8_norm_bwd_partials", 12288, 256) == 4 + 4  # any multiple of 4096 from 8192
     assert _lib.query("sfp8_norm_bwd_partials", 10240, 256) == -1
     s = _lib.query("sfp8_wgrad_splits", 6144, 1024, 65536)
-    assert s >= 1 and 65536 % s == 0 and (65536 // s) % 128 == 0
+    # any count, each split a whole number of 128-token stage pairs (the last
+    # takes the rest); at the headline shape both gradients take 5
+    chunk = -(-(-(-65536 // s)) // 128) * 128
+    assert s == 5 and chunk % 128 == 0 and 0 < 65536 - (s - 1) * chunk <= chunk
+    assert _lib.query("sfp8_wgrad_splits", 1024, 3072, 65536) == 5
     assert _lib.query("sfp8_wgrad_workspace_floats", 6144, 1024, 65536) == (s * 6144 * 1024 if s > 1 else 0)
     # partials are whole 256 x 256 tiles per split
     s2 = _lib.query("sfp8_wgrad_splits", 384, 128, 65536)

@@ -67,3 +67,46 @@ def test_noalloc_refuses_beyond_scratch(dev):
     assert need > 8 << 20  # SFP8_NOALLOC_SCRATCH_FLOATS
     # refused on the host (non-null stand-in pointers are never dereferenced)
     assert fn(16, 16, 16, 16, 16, ldt, D, 16, 16, 16, 16, 16, None, ldt, None) == -5
+
+
+def test_noalloc_under_graph_capture(dev):
+    """The entry point as a captured HIP graph: after one eager call on the
+    device (which looks up the scratch address), a capture of one call
+    replays with the bytes of sfp8_norm_bwd on whatever the static inputs
+    hold at each replay.  Each replay is checked against its own eager
+    result, with eager work and synchronisations between the replays; the
+    graph holds only kernel launches (no memset nodes)."""
+    fn = _noalloc()
+    T, D = 4096, 1024
+    h, dxn, dy, rstd, nw, scale = _inputs(dev, T, D, 7)
+    ldt = ops.ldt_of(T)
+    amax = torch.zeros(5, device=dev)
+    dh = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    dnw = torch.empty(D, device=dev)
+    dy8t = ops.slab_empty(D, T, ops.E5M2, dev)
+    args = lambda: (h.data_ptr(), rstd.data_ptr(), dxn.data_ptr(), dy.data_ptr(), nw.data_ptr(), T, D,  # noqa: E731
+                    scale.data_ptr(), amax.data_ptr(), dh.data_ptr(), dnw.data_ptr(), None, dy8t.data_ptr(), ldt,
+                    _lib.stream_of(h))
+    assert fn(*args()) == 0  # eager: resolves this device's scratch address
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = fn(*args())
+    torch.cuda.current_stream().wait_stream(side)
+    assert rc == 0, rc
+    for rep in range(4):
+        nh, ndxn, ndy, nrstd, nnw, _ = _inputs(dev, T, D, 200 + rep)
+        for dst, src in ((h, nh), (dxn, ndxn), (dy, ndy), (rstd, nrstd), (nw, nnw)):
+            dst.copy_(src)
+        amax.zero_()
+        ref_amax = torch.zeros(5, device=dev)
+        ref = ops.norm_bwd(h, rstd, dxn, dy, nw, scale, ref_amax, rows=False)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("dh", "dnw", "dy8t", "amax"), (dh, dnw, dy8t, amax), ref + (ref_amax,)):
+            assert torch.equal(a.view(torch.uint8) if a.dtype == ops.E5M2 else a,
+                               b.view(torch.uint8) if b.dtype == ops.E5M2 else b), (rep, name)
