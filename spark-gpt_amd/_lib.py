@@ -120,16 +120,25 @@ def check(rc: int, name: str) -> None:
 
 
 def call(name: str, *args) -> None:
-    check(getattr(load(), name)(*args), name)
+    rc = getattr(_lib or load(), name)(*args)
+    if rc != 0:
+        check(rc, name)
 
 
 def query(name: str, *args) -> int:
     return int(getattr(load(), name)(*args))
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """Handle of torch's current stream on t's device (the stream every call
+    is launched on)."""
     if not t.is_cuda:
         raise RuntimeError("libsparkfp8 kernels need ROCm device tensors")
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -134,13 +134,14 @@ class _FP8MLPBlock(torch.autograd.Function):
     gate/up FP8 dgrad -> RMSNorm backward (+ e5m2 dy^T) -> the two FP8 weight
     gradients reduced over tokens.
 
-    The two halves run as the custom operators ``sparkfp8::block_fwd`` and
+    The two halves are the custom operators ``sparkfp8::block_fwd`` and
     ``sparkfp8::block_bwd`` (torch_ops.py), so a ``torch.compile``d model
-    (train.py:3787) traces them as two opaque nodes."""
+    (train.py:3787) traces them as two opaque nodes; eager calls run their
+    implementations directly (``torch_ops.op``)."""
 
     @staticmethod
     def forward(ctx, h, norm_w, w_gu, w_down, scale, amax, eps):
-        y, x8, rstd, gu8, h8 = torch.ops.sparkfp8.block_fwd(h, norm_w, w_gu, w_down, scale, amax, eps)
+        y, x8, rstd, gu8, h8 = torch_ops.op("block_fwd")(h, norm_w, w_gu, w_down, scale, amax, eps)
         # backward needs x8 and h8 (weight grads), gu8 (SwiGLU backward)
         # and the masters, whose quantized copies (W8^T for
         # the gate/up dgrad, bf16 Wd^T for the down dgrad) it finds cached
@@ -150,7 +151,7 @@ class _FP8MLPBlock(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax = ctx.saved_tensors
-        dh, dnw, dwgu, dwd = torch.ops.sparkfp8.block_bwd(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8,
+        dh, dnw, dwgu, dwd = torch_ops.op("block_bwd")(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8,
                                                           scale, amax)
         return dh, dnw, dwgu, dwd, None, None, None
 

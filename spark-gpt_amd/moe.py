@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 
 from . import mlp as _mlp
-from . import torch_ops  # noqa: F401  (registers sparkfp8::moe_fwd / moe_bwd)
+from . import torch_ops  # the sparkfp8::moe_fwd / moe_bwd operators and their implementations
 
 
 def make_fp8_moe_guard(flag):
@@ -54,7 +54,7 @@ class _FP8Experts(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_gu, w_d, token_index, inverse_permutation, offsets, top_k, scale, amax):
-        out, plan, x8, gu8, h8 = torch.ops.sparkfp8.moe_fwd(x, w_gu, w_d, token_index, offsets, scale, amax)
+        out, plan, x8, gu8, h8 = torch_ops.op("moe_fwd")(x, w_gu, w_d, token_index, offsets, scale, amax)
         ctx.save_for_backward(w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, scale, amax)
         ctx.shape = (x.shape[0], int(top_k))
         return out
@@ -63,6 +63,6 @@ class _FP8Experts(torch.autograd.Function):
     def backward(ctx, dout):
         w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, scale, amax = ctx.saved_tensors
         T, top_k = ctx.shape
-        dxn, dw_gu, dw_d = torch.ops.sparkfp8.moe_bwd(dout, w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, T,
+        dxn, dw_gu, dw_d = torch_ops.op("moe_bwd")(dout, w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, T,
                                                       top_k, scale, amax)
         return dxn, dw_gu, dw_d, None, None, None, None, None, None

@@ -25,6 +25,14 @@ def ldt_of(T: int) -> int:
 
 
 SLAB = 64  # bytes of K per slab row
+# bytes per element of the dtypes the K-slabs hold
+_ESIZE = {torch.float8_e4m3fn: 1, torch.float8_e5m2: 1, torch.uint8: 1, torch.bfloat16: 2, torch.float16: 2,
+          torch.float32: 4}
+
+
+def _esize(dtype) -> int:
+    n = _ESIZE.get(dtype)
+    return n if n is not None else torch.empty((), dtype=dtype).element_size()
 
 
 def slab_rows(R: int) -> int:
@@ -38,14 +46,14 @@ def kslab_empty(R: int, L: int, dtype, device) -> torch.Tensor:
     (r, l) at [l // n, r, l % n] with n = 64 / size.  Every FP8 GEMM operand
     (and the bf16 W_down^T) uses this layout; one 64-byte K stage of a
     256-row tile is one contiguous 16 KiB block."""
-    n = SLAB // torch.empty((), dtype=dtype).element_size()
+    n = SLAB // _esize(dtype)
     _need(L % n == 0, f"K extent {L} must be a multiple of {n}")
     return torch.empty(L // n, slab_rows(R), n, dtype=dtype, device=device)
 
 
 def kslab_shape(R: int, L: int, dtype) -> tuple:
     """Shape of kslab_empty(R, L, dtype)."""
-    n = SLAB // torch.empty((), dtype=dtype).element_size()
+    n = SLAB // _esize(dtype)
     _need(L % n == 0, f"K extent {L} must be a multiple of {n}")
     return (L // n, slab_rows(R), n)
 
@@ -157,7 +165,7 @@ def update_scales(scale: torch.Tensor, amax: torch.Tensor) -> None:
 
 # ------------------------------------------------------------------ GEMMs
 def _kslab(name: str, t: torch.Tensor, dtype, R: int, L: int) -> None:
-    n = SLAB // torch.empty((), dtype=dtype).element_size()
+    n = SLAB // _esize(dtype)
     _cuda_contig(name, t, dtype, 3)
     _need(tuple(t.shape) == (L // n, slab_rows(R), n), f"{name} must be a K-slab of [{R}, {L}]")
 

@@ -33,7 +33,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from . import torch_ops  # noqa: F401  (registers the sparkfp8:: bf16 operators)
+from . import torch_ops  # the sparkfp8:: bf16 operators and their implementations
 
 FUSED_SWIGLU = True  # --no-fused-swiglu (train.py:1618)
 FUSED_NORM_MLP = True  # --no-fused-norm-mlp (train.py:2093)
@@ -137,7 +137,7 @@ class _FusedSwiGLU(torch.autograd.Function):
         ctx.torch_graph = None
         if not _kernel_shape(x.shape[-1], weight.shape[1] // 2) or weight.shape[1] % 2:
             return _torch_forward(ctx, _unfused_swiglu, x, weight, offs)
-        h, gu, plan = torch.ops.sparkfp8.swiglu_fwd(x, weight, offs)
+        h, gu, plan = torch_ops.op("swiglu_fwd")(x, weight, offs)
         ctx.save_for_backward(x, weight, gu, plan)
         return h
 
@@ -146,7 +146,7 @@ class _FusedSwiGLU(torch.autograd.Function):
         if ctx.torch_graph is not None:
             return _torch_backward(ctx, dh, 2) + (None,)
         x, weight, gu, plan = ctx.saved_tensors
-        dx, dw = torch.ops.sparkfp8.swiglu_bwd(dh, x, weight, gu, plan)
+        dx, dw = torch_ops.op("swiglu_bwd")(dh, x, weight, gu, plan)
         return dx, dw, None
 
 
@@ -166,7 +166,7 @@ class _NormSwiGLU(torch.autograd.Function):
         ctx.torch_graph = None
         if not _kernel_shape(h.shape[-1], w_gu.shape[0] // 2) or w_gu.shape[0] % 2:
             return _torch_forward(ctx, _unfused_norm_swiglu, h, norm_w, w_gu, eps)
-        out, wt, gu, rstd = torch.ops.sparkfp8.norm_swiglu_fwd(h, norm_w, w_gu, float(eps))
+        out, wt, gu, rstd = torch_ops.op("norm_swiglu_fwd")(h, norm_w, w_gu, float(eps))
         ctx.save_for_backward(h, norm_w, w_gu, wt, gu, rstd)
         return out
 
@@ -175,5 +175,5 @@ class _NormSwiGLU(torch.autograd.Function):
         if ctx.torch_graph is not None:
             return _torch_backward(ctx, dout, 3) + (None,)
         h, norm_w, w_gu, wt, gu, rstd = ctx.saved_tensors
-        dh, dnw, dw = torch.ops.sparkfp8.norm_swiglu_bwd(dout, h, norm_w, w_gu, wt, gu, rstd)
+        dh, dnw, dw = torch_ops.op("norm_swiglu_bwd")(dout, h, norm_w, w_gu, wt, gu, rstd)
         return dh, dnw, dw, None

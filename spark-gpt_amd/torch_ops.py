@@ -16,6 +16,10 @@ atomic max (train.py:1015-1016, 1094).
 * ``sparkfp8::update_scales(scale, amax)`` is the delayed-scale roll
   (train.py:937-946).
 
+Each operator's Python implementation is ``<name>_impl``; ``op(name)`` hands
+the autograd Functions the operator while torch.compile traces and the
+implementation itself in eager mode.
+
 The forward's e4m3 weight copies come from a cache keyed on the fp32
 masters (``cached_weights``), so the two just-in-time quantizations of
 train.py:1211-1212 run once per optimizer step rather than once per forward.
@@ -105,6 +109,17 @@ def cached_weights(w_gu: Tensor, w_down: Tensor):
     return q
 
 
+def op(name: str):
+    """The callable the autograd Functions run for operator ``name``: under
+    torch.compile the registered ``sparkfp8::`` operator (one opaque node of
+    the compiled graph); in eager mode its Python implementation itself,
+    which does the same launches without the dispatcher's custom-operator
+    layer (tens of microseconds per call, felt by small steps)."""
+    if torch.compiler.is_compiling():
+        return getattr(torch.ops.sparkfp8, name)
+    return globals()[name + "_impl"]
+
+
 @torch.no_grad()
 def refresh_weight_cache(w_gu: Tensor, w_down: Tensor) -> None:
     """Re-quantize the cached copies of (w_gu, w_down), if there are any:
@@ -125,8 +140,7 @@ def clear_weight_cache() -> None:
         _WCACHE.clear()
 
 
-@torch.library.custom_op("sparkfp8::block_fwd", mutates_args={"amax"})
-def block_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Tensor, amax: Tensor,
+def block_fwd_impl(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Tensor, amax: Tensor,
               eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """y, then for the backward: x8 (K-slab of [T, D]), rstd, gu8 (K-slab of
     [T, 2I]) and h8 (K-slab of [T, I]).  The weight gradients read x8 and h8
@@ -143,6 +157,9 @@ def block_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, scale: Te
     return y, x8, rstd, gu8, h8
 
 
+block_fwd = torch.library.custom_op("sparkfp8::block_fwd", block_fwd_impl, mutates_args={"amax"})
+
+
 @block_fwd.register_fake
 def _block_fwd_fake(h, norm_w, w_gu, w_down, scale, amax, eps):
     T, D = h.shape
@@ -156,8 +173,7 @@ def _block_fwd_fake(h, norm_w, w_gu, w_down, scale, amax, eps):
             h.new_empty((I // 64, ldt, 64), dtype=E4M3))
 
 
-@torch.library.custom_op("sparkfp8::block_bwd", mutates_args={"amax"})
-def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, x8: Tensor, rstd: Tensor,
+def block_bwd_impl(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tensor, x8: Tensor, rstd: Tensor,
               gu8: Tensor, h8: Tensor, scale: Tensor, amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """(dh bf16, d_norm_w fp32, dW_gate_up fp32, dW_down fp32).  W8^T, the
     bf16 W_down^T and the weight scales are the forward's (the cache entry of
@@ -187,6 +203,9 @@ def block_bwd(dy: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, w_down: Tenso
     return dh, dnw, dwgu, dwd
 
 
+block_bwd = torch.library.custom_op("sparkfp8::block_bwd", block_bwd_impl, mutates_args={"amax"})
+
+
 @block_bwd.register_fake
 def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax):
     T, D = h.shape
@@ -198,8 +217,7 @@ def _block_bwd_fake(dy, h, norm_w, w_gu, w_down, x8, rstd, gu8, h8, scale, amax)
 
 
 # ------------------------------------------------------------ MoE experts
-@torch.library.custom_op("sparkfp8::moe_fwd", mutates_args={"amax"})
-def moe_fwd(x: Tensor, w_gu: Tensor, w_d: Tensor, token_index: Tensor, offsets: Tensor, scale: Tensor,
+def moe_fwd_impl(x: Tensor, w_gu: Tensor, w_d: Tensor, token_index: Tensor, offsets: Tensor, scale: Tensor,
             amax: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """_FP8Experts.forward (train.py:1552-1587): out [R, D] bf16 expert-order
     rows (unweighted), then for the backward the plan, x8, gu8 and h8 (K-slabs
@@ -218,6 +236,9 @@ def moe_fwd(x: Tensor, w_gu: Tensor, w_d: Tensor, token_index: Tensor, offsets: 
     return out, plan, x8, gu8, h8
 
 
+moe_fwd = torch.library.custom_op("sparkfp8::moe_fwd", moe_fwd_impl, mutates_args={"amax"})
+
+
 @moe_fwd.register_fake
 def _moe_fwd_fake(x, w_gu, w_d, token_index, offsets, scale, amax):
     R = token_index.numel()
@@ -230,8 +251,7 @@ def _moe_fwd_fake(x, w_gu, w_d, token_index, offsets, scale, amax):
             x.new_empty(ops.kslab_shape(ldp, I2 // 2, E4M3), dtype=E4M3))
 
 
-@torch.library.custom_op("sparkfp8::moe_bwd", mutates_args={"amax"})
-def moe_bwd(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8: Tensor, gu8: Tensor, h8: Tensor,
+def moe_bwd_impl(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8: Tensor, gu8: Tensor, h8: Tensor,
             inverse_permutation: Tensor, T: int, top_k: int, scale: Tensor,
             amax: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """_FP8Experts.backward (train.py:1589-1605): (dx [T, D] bf16 summed over
@@ -255,6 +275,9 @@ def moe_bwd(dout: Tensor, w_gu: Tensor, w_d: Tensor, plan: Tensor, x8: Tensor, g
     return dxn, dw_gu, dw_d
 
 
+moe_bwd = torch.library.custom_op("sparkfp8::moe_bwd", moe_bwd_impl, mutates_args={"amax"})
+
+
 @moe_bwd.register_fake
 def _moe_bwd_fake(dout, w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, T, top_k, scale, amax):
     E, I2, D = w_gu.shape
@@ -263,9 +286,11 @@ def _moe_bwd_fake(dout, w_gu, w_d, plan, x8, gu8, h8, inverse_permutation, T, to
             dout.new_empty((E, D, I2 // 2), dtype=torch.float32))
 
 
-@torch.library.custom_op("sparkfp8::update_scales", mutates_args={"scale", "amax"})
-def update_scales(scale: Tensor, amax: Tensor) -> None:
+def update_scales_impl(scale: Tensor, amax: Tensor) -> None:
     ops.update_scales(scale, amax)
+
+
+update_scales = torch.library.custom_op("sparkfp8::update_scales", update_scales_impl, mutates_args={"scale", "amax"})
 
 
 @update_scales.register_fake
@@ -277,8 +302,7 @@ def _update_scales_fake(scale, amax):
 BF16 = torch.bfloat16
 
 
-@torch.library.custom_op("sparkfp8::norm_swiglu_fwd", mutates_args=())
-def norm_swiglu_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+def norm_swiglu_fwd_impl(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     """_NormSwiGLU.forward (train.py:2111-2121): out = SwiGLU(gate_up(rmsnorm(h)))
     [T, I] bf16, the norm weight folded into the gate/up weight (W' =
     bf16(w_gu * norm_w)); then, for the backward, the bf16 K-slab of W'^T, gu
@@ -295,6 +319,9 @@ def norm_swiglu_fwd(h: Tensor, norm_w: Tensor, w_gu: Tensor, eps: float) -> Tupl
     return out, wt, gu, rstd
 
 
+norm_swiglu_fwd = torch.library.custom_op("sparkfp8::norm_swiglu_fwd", norm_swiglu_fwd_impl, mutates_args=())
+
+
 @norm_swiglu_fwd.register_fake
 def _norm_swiglu_fwd_fake(h, norm_w, w_gu, eps):
     T, D = h.shape
@@ -303,8 +330,7 @@ def _norm_swiglu_fwd_fake(h, norm_w, w_gu, eps):
             h.new_empty((T, I2), dtype=BF16), h.new_empty((T,), dtype=torch.float32))
 
 
-@torch.library.custom_op("sparkfp8::norm_swiglu_bwd", mutates_args=())
-def norm_swiglu_bwd(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: Tensor, gu: Tensor,
+def norm_swiglu_bwd_impl(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: Tensor, gu: Tensor,
                     rstd: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """_NormSwiGLU.backward (train.py:2123-2131): (dh bf16 [T, D], dnorm_w fp32
     [D], dw_gu fp32 [2I, D]).  G' = rstd * d_gu (bf16) once for both GEMMs:
@@ -326,6 +352,9 @@ def norm_swiglu_bwd(dout: Tensor, h: Tensor, norm_w: Tensor, w_gu: Tensor, wt: T
     return dh, dnw, dw
 
 
+norm_swiglu_bwd = torch.library.custom_op("sparkfp8::norm_swiglu_bwd", norm_swiglu_bwd_impl, mutates_args=())
+
+
 @norm_swiglu_bwd.register_fake
 def _norm_swiglu_bwd_fake(dout, h, norm_w, w_gu, wt, gu, rstd):
     T, D = h.shape
@@ -337,8 +366,7 @@ def _plan_ints(R: int, E: int) -> int:
     return 8 + 2 * E + 3 * ((R + 255) // 256 + E)
 
 
-@torch.library.custom_op("sparkfp8::swiglu_fwd", mutates_args=())
-def swiglu_fwd(x: Tensor, weight: Tensor, offs: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+def swiglu_fwd_impl(x: Tensor, weight: Tensor, offs: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """_FusedSwiGLU.forward (train.py:2077-2081): h = SwiGLU(x W_e^T) [R, I]
     bf16 for the rows of each group e (offs: inclusive int32 row-count prefix
     sums), then gu [R, 2I] and the device-built row plan for the backward."""
@@ -353,6 +381,9 @@ def swiglu_fwd(x: Tensor, weight: Tensor, offs: Tensor) -> Tuple[Tensor, Tensor,
     return h, gu, plan
 
 
+swiglu_fwd = torch.library.custom_op("sparkfp8::swiglu_fwd", swiglu_fwd_impl, mutates_args=())
+
+
 @swiglu_fwd.register_fake
 def _swiglu_fwd_fake(x, weight, offs):
     R, D = x.shape
@@ -361,8 +392,7 @@ def _swiglu_fwd_fake(x, weight, offs):
             x.new_empty((_plan_ints(R, E),), dtype=torch.int32))
 
 
-@torch.library.custom_op("sparkfp8::swiglu_bwd", mutates_args=())
-def swiglu_bwd(dh: Tensor, x: Tensor, weight: Tensor, gu: Tensor, plan: Tensor) -> Tuple[Tensor, Tensor]:
+def swiglu_bwd_impl(dh: Tensor, x: Tensor, weight: Tensor, gu: Tensor, plan: Tensor) -> Tuple[Tensor, Tensor]:
     """_FusedSwiGLU.backward (train.py:2083-2090): (dx [R, D] bf16, dW [E, 2I, D]
     bf16), the SwiGLU gradient G' (bf16) computed once for both GEMMs."""
     dh = dh.contiguous()
@@ -380,6 +410,9 @@ def swiglu_bwd(dh: Tensor, x: Tensor, weight: Tensor, gu: Tensor, plan: Tensor) 
     # G' read through transposing LDS reads, x as its token-contiguous copy
     dw = ops.bf16_wgrad_rows(gs, xt, I2, D, plan=plan, E=E)
     return dx, dw
+
+
+swiglu_bwd = torch.library.custom_op("sparkfp8::swiglu_bwd", swiglu_bwd_impl, mutates_args=())
 
 
 @swiglu_bwd.register_fake
