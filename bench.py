@@ -24,20 +24,26 @@ Also reported on the same JSON line:
                 algorithmic traffic / mean duration vs 8 TB/s HBM
   kernels       per-kernel mean durations (each kernel alone, 10 launches),
                 with TFLOP/s or algorithmic GB/s
-  other_workloads  on the GPU, wall clock over 20 steps after 5 warm-up steps:
-                the muP base block (T=8192, D=256, I=1024), and the FP8 MoE
-                experts (``_FP8Experts`` fwd+bwd + post-step hook) on 65536
-                tokens routed top-2 over 8 experts, D=1024, I=1536 (131072
-                expert rows: the dense headline's FLOP), and the reference's
-                default bf16 sub-block at the headline shape (h +
+  other_workloads  on the GPU, wall clock after warm-up steps: the muP base
+                block (T=8192, D=256, I=1024); the wide block with
+                heavy-tailed activations (T=65536, D=2048, I=6144, Student-t
+                with 3 degrees of freedom); the stack of 28 blocks (T=16384,
+                D=4096, I=12288, each block's RMSNorm between layers, full
+                forward + backward in one step); the FP8 MoE experts
+                (``_FP8Experts`` fwd+bwd + post-step hook) on 65536 tokens
+                routed top-2 over 8 experts, D=1024, I=1536 (131072 expert
+                rows: the dense headline's FLOP); and the reference's default
+                bf16 sub-block at the headline shape (h +
                 down_proj(_NormSwiGLU(h)) under bf16 autocast, the down
-                projection on torch), each with their in-step kernels and
-                roofline; `fp8_block_speedup` = bf16 step / FP8 step
+                projection on torch).  All but the muP base block carry their
+                in-step kernels and the roofline of the dominant one (the
+                MoE and bf16 `traffic` from their committed counter
+                summaries); `fp8_block_speedup` = bf16 step / FP8 step
   cpu_baseline  the same FP8 recipe emulated in torch on the host cores (the
-                CPU oracle) on a bounded token sample, in TFLOP/s; under
-                `other_workloads` the oracle on the muP base block, on a
-                token sample of the MoE workload and on an 8192-row sample of
-                the quantizer input
+                CPU oracle) at the headline's full 65536 tokens, in TFLOP/s;
+                under `other_workloads` the oracle on the muP base block and
+                on the full 65536 x 4096 quantizer input, and on a token
+                sample of the MoE workload
 
 ``--trace`` runs only the headline steps (prewarm, warm-up, timed and
 instrumented passes), so that a ``rocprofv3 --kernel-trace --stats`` summary
@@ -64,6 +70,9 @@ BF16_PEAK_TFLOPS = 2516.5  # MI355X dense bf16 MFMA
 HBM_PEAK_GBPS = 8000.0     # MI355X HBM3E
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_fwd_bwd_T65536_D1024_I3072.md")
 TRAFFIC_WORKLOAD = (65536, 1024, 3072)
+# counter summaries of the MoE and bf16 workloads (the same table layout)
+TRAFFIC_PROFILE_MOE = os.path.join(ROOT, "profiles", "traffic_moe_fwd_bwd_T65536_E8_top2_D1024_I1536.md")
+TRAFFIC_PROFILE_BF16 = os.path.join(ROOT, "profiles", "traffic_bf16_norm_swiglu_fwd_bwd_T65536_D1024_I3072.md")
 # the compute-matched MoE of the headline width: top-2 of 8 experts at half the
 # dense ffn (the same 18*T*k*D*I FLOP per step as the dense block)
 MOE_WORKLOAD = {"T": 65536, "D": 1024, "I": 1536, "E": 8, "k": 2}
@@ -78,7 +87,7 @@ def parse():
     p.add_argument("--d-model", type=int, default=1024)
     p.add_argument("--ffn", type=int, default=3072)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-tokens", type=int, default=16384)
+    p.add_argument("--cpu-tokens", type=int, default=65536)
     p.add_argument("--quant-rows", type=int, default=65536)
     p.add_argument("--quant-cols", type=int, default=4096)
     p.add_argument("--probe", action="store_true", help="one launch of each kernel, for counter passes")
@@ -90,11 +99,11 @@ def parse():
     return p.parse_args()
 
 
-def read_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed counter summary: the
+def read_traffic(kernel: str, profile: str = TRAFFIC_PROFILE):
+    """HBM bytes per launch of `kernel` from a committed counter summary: the
     table row `| kernel | ... | traffic_bytes |` (last column)."""
     try:
-        with open(TRAFFIC_PROFILE) as fh:
+        with open(profile) as fh:
             for line in fh:
                 cells = [c.strip() for c in line.strip().strip("|").split("|")]
                 if len(cells) >= 2 and cells[0] == kernel:
@@ -168,9 +177,9 @@ def cpu_baseline(T: int, D: int, I: int) -> dict:
 
 
 def cpu_extra(quant_rows: int, quant_cols: int) -> dict:
-    """The CPU oracle on the other two measured workloads: the muP base block
-    (T=8192, D=256, I=1024, full size) and the standalone quantizer on a
-    bounded row sample of its 65536 x 4096 input."""
+    """The CPU oracle on the other measured workloads: the muP base block
+    (T=8192, D=256, I=1024) and the standalone quantizer (65536 x 4096), both
+    at full size, and the MoE experts on a token sample."""
     import torch
 
     from oracle import fp8_mlp as O
@@ -199,7 +208,7 @@ def cpu_extra(quant_rows: int, quant_cols: int) -> dict:
     med = sorted(times)[1]
     out["muP_base_T8192_D256_I1024"] = {"TFLOP/s": round(18.0 * T * D * I / med / 1e12, 4),
                                         "s_per_step": round(med, 4)}
-    R = min(quant_rows, 8192)
+    R = quant_rows
     x = torch.randn(R, quant_cols, generator=g)
     x[:, : max(1, quant_cols // 1000)] *= 50.0
     x = x.to(torch.bfloat16)
@@ -298,13 +307,28 @@ def make_block(T: int, D: int, I: int, dist: str = "normal", seed: int = 1):
     return h, dy, norm, mlp, step
 
 
-def time_block(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
-    """GPU training-step time of the block at another shape (prewarm step and
-    scale roll first, as for the headline workload)."""
+def block_work(T: int, D: int, I: int) -> dict:
+    """FLOP (or algorithmic bytes) per launch of each kernel of one block."""
+    return {
+        "norm_quant": (None, T * (3.0 * D + 4)),
+        "weight_quant_gu": (None, 10.0 * 2 * I * D),
+        "weight_quant_down": (None, 11.0 * D * I),
+        "gateup_swiglu_fwd": (4.0 * T * D * I, None),
+        "down_fwd": (2.0 * T * D * I, None),
+        "down_dgrad_swiglu_bf16": (2.0 * T * D * I, None),
+        "gateup_dgrad": (4.0 * T * D * I, None),
+        "norm_bwd": (None, T * (9.0 * D + 4)),
+        "wgrad_down": (2.0 * T * D * I, None),
+        "wgrad_gateup": (4.0 * T * D * I, None),
+        "update_scales": (None, 40.0),
+    }
+
+
+def timed_steps(step, steps: int, warmup: int) -> float:
+    """Wall-clock ms per step over `steps` steps after `warmup` untimed ones,
+    bracketed by device synchronisations."""
     import torch
 
-    _h, _dy, _norm, _mlp, step = make_block(T, D, I)
-    step()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -312,9 +336,71 @@ def time_block(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    return {"tokens": T, "d_model": D, "ffn": I, "ms_per_step": round(ms, 4),
-            "TFLOP/s": round(18.0 * T * D * I / (ms * 1e-3) / 1e12, 2)}
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def time_block(T: int, D: int, I: int, steps: int, warmup: int, dist: str = "normal", trace: bool = False,
+               workload: str = "fp8_swiglu_mlp_block_fwd_bwd") -> dict:
+    """GPU training-step time of the block at another shape (prewarm step and
+    scale roll first, as for the headline workload); with `trace`, also its
+    in-step kernels and the roofline of the dominant one."""
+    import torch
+
+    _h, _dy, _norm, _mlp, step = make_block(T, D, I, dist)
+    step()
+    ms = timed_steps(step, steps, warmup)
+    flop = 18.0 * T * D * I
+    out = {"workload": workload, "tokens": T, "d_model": D, "ffn": I, "activations": dist,
+           "flop_per_step": flop, "ms_per_step": round(ms, 4),
+           "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+           "frac_fp8_peak": round(flop / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+    if trace:
+        per = trace_steps(step, steps, torch.cuda.current_stream(), lambda sym, a: launch_name(sym, a, D, I))
+        out["kernels_in_step"], out["roofline"] = in_step_summary(per, steps, block_work(T, D, I))
+    return out
+
+
+def time_stack(T: int, D: int, I: int, L: int, steps: int, warmup: int) -> dict:
+    """A stack of L blocks, each with its own RMSNorm (y = h + MLP(norm(h)),
+    chained), full forward + backward in one step, then the post-step hook on
+    every block; in-step kernels averaged over the layers."""
+    import torch
+
+    import spark_gpt_amd as sg
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    layers = []
+    for _ in range(L):
+        mlp = sg.MLP(D, I).to(dev).train()
+        with torch.no_grad():
+            mlp.gate_up_proj.weight.copy_(torch.randn(2 * I, D, device=dev, generator=g) * D ** -0.5)
+            mlp.down_proj.weight.copy_(torch.randn(D, I, device=dev, generator=g) * I ** -0.5)
+        layers.append((_Norm(torch.ones(D, device=dev, requires_grad=True)), mlp))
+    h = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(T, D, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    params = [p for norm, mlp in layers for p in (norm.weight, mlp.gate_up_proj.weight, mlp.down_proj.weight)]
+
+    def step():
+        x = h.detach().requires_grad_(True)
+        y = x
+        for norm, mlp in layers:
+            y = sg.fp8_mlp_block(y, norm, mlp)
+        torch.autograd.backward(y, dy, inputs=[x] + params)
+        for p in params:
+            p.grad = None
+        for _, mlp in layers:
+            sg.fp8_update_scales(mlp)
+
+    step()
+    ms = timed_steps(step, steps, warmup)
+    flop = 18.0 * T * D * I * L
+    per = trace_steps(step, steps, torch.cuda.current_stream(), lambda sym, a: launch_name(sym, a, D, I))
+    in_step, roofline = in_step_summary(per, steps, block_work(T, D, I))
+    return {"workload": f"fp8_swiglu_mlp_stack{L}_fwd_bwd", "layers": L, "tokens": T, "d_model": D, "ffn": I,
+            "flop_per_step": flop, "ms_per_step": round(ms, 3), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
+            "frac_fp8_peak": round(flop / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "roofline": roofline, "kernels_in_step": in_step}
 
 
 def launch_name(sym: str, a, D: int, I: int) -> str:
@@ -510,7 +596,8 @@ def time_bf16(T: int, D: int, I: int, steps: int, warmup: int) -> dict:
         "bf16_fold_grads": (None, 20.0 * I * D),
     }
     per = trace_steps(step, steps, stream, bf16_launch_name)
-    in_step, roofline = in_step_summary(per, steps, work)
+    in_step, roofline = in_step_summary(
+        per, steps, work, lambda k: read_traffic(k, TRAFFIC_PROFILE_BF16) if (T, D, I) == TRAFFIC_WORKLOAD else None)
     roofline["peak"] = BF16_PEAK_TFLOPS if roofline["bound"] == "mfma" else HBM_PEAK_GBPS
     roofline["frac"] = round(roofline["achieved"] / roofline["peak"], 4)
     flop = 18.0 * T * D * I
@@ -556,7 +643,11 @@ def time_moe(T: int, D: int, I: int, E: int, k: int, steps: int, warmup: int) ->
         "update_scales": (None, 40.0),
     }
     per = trace_steps(step, steps, stream, lambda sym, a: launch_name(sym, a, D, I))
-    in_step, roofline = in_step_summary(per, steps, work)
+    mw = MOE_WORKLOAD
+    in_step, roofline = in_step_summary(
+        per, steps, work,
+        lambda kern: read_traffic(kern, TRAFFIC_PROFILE_MOE)
+        if (T, D, I, E, k) == (mw["T"], mw["D"], mw["I"], mw["E"], mw["k"]) else None)
     return {"workload": "fp8_moe_experts_fwd_bwd", "tokens": T, "top_k": k, "experts": E, "d_model": D, "ffn": I,
             "routed_rows": R, "rows_per_expert": counts, "flop_per_step": flop, "ms_per_step": round(ms, 4),
             "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 2),
@@ -592,19 +683,7 @@ def main() -> None:
     stream = torch.cuda.current_stream(dev)
 
     # FLOP or algorithmic bytes per launch of each kernel
-    work = {
-        "norm_quant": (None, T * (3.0 * D + 4)),
-        "weight_quant_gu": (None, 10.0 * 2 * I * D),
-        "weight_quant_down": (None, 11.0 * D * I),
-        "gateup_swiglu_fwd": (4.0 * T * D * I, None),
-        "down_fwd": (2.0 * T * D * I, None),
-        "down_dgrad_swiglu_bf16": (2.0 * T * D * I, None),
-        "gateup_dgrad": (4.0 * T * D * I, None),
-        "norm_bwd": (None, T * (9.0 * D + 4)),
-        "wgrad_down": (2.0 * T * D * I, None),
-        "wgrad_gateup": (4.0 * T * D * I, None),
-        "update_scales": (None, 40.0),
-    }
+    work = block_work(T, D, I)
 
     out_extra = {}
     if args.probe or not args.trace:
@@ -743,9 +822,12 @@ def main() -> None:
         # the muP base block (T=8192, D=256, I=1024): timed, not targeted
         del h, dy, norm, mlp, step
         mw = MOE_WORKLOAD
-        out["other_workloads"] = {"muP_base": time_block(8192, 256, 1024, 20, 5),
-                                  "moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], 20, 5),
-                                  "bf16": time_bf16(T, D, I, 20, 5)}
+        out["other_workloads"] = {
+            "muP_base": time_block(8192, 256, 1024, 20, 5),
+            "wide_student_t": time_block(65536, 2048, 6144, 10, 3, dist="student-t", trace=True),
+            "stack28": time_stack(16384, 4096, 12288, 28, 5, 2),
+            "moe": time_moe(mw["T"], mw["D"], mw["I"], mw["E"], mw["k"], 20, 5),
+            "bf16": time_bf16(T, D, I, 20, 5)}
         out["other_workloads"]["bf16"]["fp8_block_speedup"] = round(
             out["other_workloads"]["bf16"]["ms_per_step"] / ms, 3)
         if not args.no_cpu_baseline:
