@@ -871,8 +871,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   // are powers of two, d_gate = dg*s_gu and d_up = du*s_gu with
   //   dg = (dh*u8)*(sig*(1 + g*(1-sig))),  du = (dh*g8)*sig  (factors from lut),
   //   dgu8 = e5m2(d*q3) = e5m2(d'*(s_gu*q3)),  amax3 = s_gu*max(|dg|,|du|).
-  const float s_gu = 1.0f / scale[1];
-  const float m3s = s_gu * scale[3];
+  const float m3s = (1.0f / scale[1]) * scale[3];
   const float inv3 = 1.0f / m3s, bnd3 = kE5M2Max * inv3;
   uint8_t* Gt = lds;
   uint8_t* Ut = lds + kTile * kEpiStride2;
@@ -998,7 +997,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   }
   __syncthreads();  // the next tile's DMA overwrites the staging tiles
   }
-  m3 *= s_gu;
+  m3 *= 1.0f / scale[1];  // s_gu, read again rather than held across the tile loop
   block_amax_atomic<4>(m3, red, amax + 3);
 }
 
@@ -1029,7 +1028,6 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
     u0 = P.urow(tm);
     uend = u0 + P.rows(tm);
   }
-  const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   floatx16 acc[4][4];
   // K-slab operands: dgu8 [2I/64][ldt][64], w8t [2I/64][slab_rows(D)][64]
@@ -1037,6 +1035,8 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
       lds, dgu8 + m0 * kStage, K * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage),
       w8t + n0 * kStage, K * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
       (int)(K / kStage), acc);
+  // the scales are read after the K loop, so that nothing is held across it
+  const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
   stage_bf16_half<0>(lds, acc, sab);
   __syncthreads();
   write_bf16_half(lds, 0, u0, n0, uend, D, D, nullptr, dxn);
