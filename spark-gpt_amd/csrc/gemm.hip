@@ -63,9 +63,12 @@ SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, i
 // or 4 each split takes 8 / splits XCDs (1.5-2 % faster than split-major
 // order over all XCDs at 4 and 2 splits).  Tiles of a split are rastered as
 // in tile_coords.
-SFP8_DEV void split_tile_coords(int pid, int tiles_m, int tiles_n, int splits, int& tm, int& tn, int& split) {
+// The grid may be padded past tiles * splits (wgrad_grid); padding work-groups
+// get split = splits and do nothing.
+SFP8_DEV void split_tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int splits, int& tm, int& tn,
+                                int& split) {
   const int tiles = tiles_m * tiles_n;
-  const int lid = xcd_run(pid, tiles * splits);
+  const int lid = xcd_run(pid, nwg);
   split = lid / tiles;
   raster(lid % tiles, tiles_m, tiles_n, tm, tn);
 }
@@ -1087,7 +1090,8 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     int tiles_m, int tiles_n, int splits, int partials, TrOp tra, TrOp trb) {
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn, sp;
-  split_tile_coords(blockIdx.x, tiles_m, tiles_n, splits, tm, tn, sp);
+  split_tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, splits, tm, tn, sp);
+  if (sp >= splits) return;  // grid padding (work-group uniform)
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -1546,6 +1550,16 @@ inline int cu_count(int* n) {
 // offsets inside one operand tile are 32-bit
 inline bool fits32(int64_t rows, int64_t ld) { return rows * ld < (int64_t)1 << 31; }
 
+// Work-groups launched for a split-K weight gradient of `tiles` tiles: when
+// padding the grid to whole 32-tile runs per XCD (256 work-groups a round)
+// adds no round of work-groups, it is padded, so that every round of an XCD
+// runs 32 consecutive tiles of one split (one raster group of 8 tile rows x
+// 4 tile columns at 4 tile columns); the padding work-groups exit at once.
+inline int wgrad_grid(int tiles, int splits) {
+  const int n = tiles * splits, padded = (n + 255) / 256 * 256;
+  return splits > 1 && (tiles % 32) == 0 ? padded : n;
+}
+
 // K bytes per weight-gradient split: ldt / s rounded up to whole 128-byte
 // stage pairs (the last split takes what remains).
 inline int64_t wgrad_chunk(int64_t ldt, int64_t s) {
@@ -1567,7 +1581,7 @@ int wgrad_partials(const void* a, const void* b, int64_t M, int64_t N, int64_t l
   if (rc) return rc;
   // row K-slabs over ldt tokens
   const TrOp tra{kStage, ldt * kStage, (M / 64) * ldt * kStage}, trb{kStage, ldt * kStage, (N / 64) * ldt * kStage};
-  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>), dim3((unsigned)wgrad_grid(tiles_m * tiles_n, splits)),
                      dim3(256), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, wgrad_chunk(ldt, splits), sa,
                      sb, ws, tiles_m, tiles_n, splits, 1, tra, trb);
   return status();
@@ -1760,7 +1774,7 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
   int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256),
+  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)wgrad_grid(tiles_m * tiles_n, (int)splits)), dim3(256),
                      kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, wgrad_chunk(ldt, splits), sa,
                      sb, splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1), TrOp{}, TrOp{});
   rc = status();
