@@ -716,14 +716,41 @@ SFP8_DEV void stage_bf16_half(uint8_t* lds, const floatx16 (&acc)[4][4], float s
   }
 }
 
+// The same for the 8-wave tile layout (wave (wm, wn), wn = 0..3, owns A rows
+// 128 wm.. and output columns 64 wn.. as 4 x 2 blocks; lane half g of block
+// nb holds columns 64 wn + 32 g + 16 nb + v).
+template <int P>
+SFP8_DEV void stage_bf16_half8(uint8_t* lds, const floatx16 (&acc)[4][2], float s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
+  const int fr = lane & 31, g = lane >> 5, cb = 64 * wn + 32 * g;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int lr = 64 * wm + 32 * tt + fr;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      uint32_t w0[4], w1[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w0[i] = pack2_bf16(acc[2 * P + tt][nb][2 * i] * s, acc[2 * P + tt][nb][2 * i + 1] * s);
+        w1[i] = pack2_bf16(acc[2 * P + tt][nb][8 + 2 * i] * s, acc[2 * P + tt][nb][8 + 2 * i + 1] * s);
+      }
+      uint8_t* q = lds + lr * kBf16Stride + (cb + 16 * nb) * 2;
+      store16(q, w0);
+      store16(q + 16, w1);
+    }
+  }
+}
+
 // Tile row held in staging row lr of pass p.
 SFP8_DEV int half_tile_row(int lr, int p) { return 128 * (lr >> 6) + 64 * p + (lr & 63); }
 
 // Writes one staged pass to out[t, n] (bf16, leading dimension ld), adding the
 // bf16 residual res[t, n] first when res is given: out = bf16(res + staged).
+// NT = threads of the work-group.
+template <int NT = 256>
 SFP8_DEV void write_bf16_half(const uint8_t* lds, int p, int64_t m0, int64_t n0, int64_t T, int64_t N,
                               int64_t ld, const uint16_t* __restrict__ res, uint16_t* __restrict__ out) {
-  for (int idx = threadIdx.x; idx < 128 * 32; idx += 256) {
+  for (int idx = threadIdx.x; idx < 128 * 32; idx += NT) {
     const int lr = idx >> 5, c = idx & 31;
     const int64_t t = m0 + half_tile_row(lr, p), n = n0 + 8 * c;
     if (t >= T || n >= N) continue;
@@ -741,12 +768,13 @@ SFP8_DEV void write_bf16_half(const uint8_t* lds, int p, int64_t m0, int64_t n0,
   }
 }
 
-// Residual words of staged half p, in write_bf16_half's order (16 per
+// Residual words of staged half p, in write_bf16_half's order (4096 / NT per
 // thread); rows past T read as zero through the descriptor.
-SFP8_DEV void load_res_half(__amdgpu_buffer_rsrc_t rres, int p, int64_t n0, int64_t D, intx4 (&rv)[16]) {
+template <int NT>
+SFP8_DEV void load_res_half(__amdgpu_buffer_rsrc_t rres, int p, int64_t n0, int64_t D, intx4 (&rv)[4096 / NT]) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int idx = (int)threadIdx.x + 256 * k;
+  for (int k = 0; k < 4096 / NT; ++k) {
+    const int idx = (int)threadIdx.x + NT * k;
     const int lr = idx >> 5, c = idx & 31;
     const uint32_t off = (uint32_t)((half_tile_row(lr, p) * D + n0 + 8 * c) * 2);
     rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0);
@@ -754,11 +782,12 @@ SFP8_DEV void load_res_half(__amdgpu_buffer_rsrc_t rres, int p, int64_t n0, int6
 }
 
 // write_bf16_half with the residual already in registers.
+template <int NT>
 SFP8_DEV void write_bf16_half_res(const uint8_t* lds, int p, int64_t m0, int64_t n0, int64_t T, int64_t D,
-                                  const intx4 (&rv)[16], uint16_t* __restrict__ out) {
+                                  const intx4 (&rv)[4096 / NT], uint16_t* __restrict__ out) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int idx = (int)threadIdx.x + 256 * k;
+  for (int k = 0; k < 4096 / NT; ++k) {
+    const int idx = (int)threadIdx.x + NT * k;
     const int lr = idx >> 5, c = idx & 31;
     const int64_t t = m0 + half_tile_row(lr, p), n = n0 + 8 * c;
     if (t >= T || n >= D) continue;
@@ -780,7 +809,7 @@ SFP8_DEV void write_bf16_half_res(const uint8_t* lds, int p, int64_t m0, int64_t
 // its rows(tm) valid rows to y rows urow(tm).. (expert order, unpadded);
 // W_down8 of expert e at wd8 + e * w_estride, its scale wscale[e] (the dense
 // call passes wscale + 1: [q_gu, q_d]).
-__global__ __launch_bounds__(256, 1) void down_fwd_kernel(
+__global__ __launch_bounds__(512, 1) void down_fwd_kernel(
     const uint8_t* __restrict__ h8, const uint8_t* __restrict__ wd8, const uint16_t* __restrict__ res,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, const float* __restrict__ wscale,
     uint16_t* __restrict__ y, int64_t ldt, int tiles_m, int tiles_n, const int* __restrict__ plan,
@@ -799,23 +828,23 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
     urows = P.rows(tm);
   }
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-  floatx16 acc[4][4];
+  floatx16 acc[4][2];
   // K-slab operands: h8 [I/64][ldt][64], wd8 [I/64][slab_rows(D)][64]
   const int64_t dp = slab_rows(D);
-  MainLoop<false, kFmtE4M3, kFmtE4M3, false>::run(
+  MainLoop<false, kFmtE4M3, kFmtE4M3, false, 2, kStages, 0, false, false, 4>::run(
       lds, h8 + m0 * kStage, I * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage),
-      wd8 + n0 * kStage, I * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
-      (int)(I / kStage), acc);
+      wd8 + n0 * kStage, I * dp - n0 * kStage, [=](int r) { return plain_col_nb<2>(r) * kStage; },
+      (int)(dp * kStage), (int)(I / kStage), acc);
   const float deq = 1.0f / (scale[2] * wscale[0]);
   if (plan) {
     // expert rows, no residual: out rounded to bf16 (train.py:1377-1378 stores acc / (s2 q_d) as bf16)
-    stage_bf16_half<0>(lds, acc, deq);
+    stage_bf16_half8<0>(lds, acc, deq);
     __syncthreads();
-    write_bf16_half(lds, 0, u0, n0, u0 + urows, D, D, nullptr, y);
+    write_bf16_half<512>(lds, 0, u0, n0, u0 + urows, D, D, nullptr, y);
     __syncthreads();
-    stage_bf16_half<1>(lds, acc, deq);
+    stage_bf16_half8<1>(lds, acc, deq);
     __syncthreads();
-    write_bf16_half(lds, 1, u0, n0, u0 + urows, D, D, nullptr, y);
+    write_bf16_half<512>(lds, 1, u0, n0, u0 + urows, D, D, nullptr, y);
     return;
   }
   const __amdgpu_buffer_rsrc_t rres = make_rsrc(res + m0 * D, (T - m0) * D * 2);
@@ -823,17 +852,17 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
   // memory latency), in the order the staged rows are written, so both the
   // residual reads and the y writes are whole rows; rows past T read as zero
   // through the descriptor's range check and are not stored.
-  intx4 rv0[16], rv1[16];
-  load_res_half(rres, 0, n0, D, rv0);
-  load_res_half(rres, 1, n0, D, rv1);
+  intx4 rv0[8], rv1[8];
+  load_res_half<512>(rres, 0, n0, D, rv0);
+  load_res_half<512>(rres, 1, n0, D, rv1);
   // out rounded to bf16 before the residual add (train.py:1043)
-  stage_bf16_half<0>(lds, acc, deq);
+  stage_bf16_half8<0>(lds, acc, deq);
   __syncthreads();
-  write_bf16_half_res(lds, 0, m0, n0, T, D, rv0, y);
+  write_bf16_half_res<512>(lds, 0, m0, n0, T, D, rv0, y);
   __syncthreads();
-  stage_bf16_half<1>(lds, acc, deq);
+  stage_bf16_half8<1>(lds, acc, deq);
   __syncthreads();
-  write_bf16_half_res(lds, 1, m0, n0, T, D, rv1, y);
+  write_bf16_half_res<512>(lds, 1, m0, n0, T, D, rv1, y);
 }
 
 // ---------------------------------------------------------------------------
@@ -842,15 +871,19 @@ __global__ __launch_bounds__(256, 1) void down_fwd_kernel(
 //   d_gate = dh*u*(sig*(1+g*(1-sig))), d_up = dh*g*sig
 //   dgu8 = e5m2(d * s3) as the K-slab of [T, 2I] (and optionally of [2I,
 //   ldt]: the token-contiguous dgu8t), amax slot 3.
-// B = Wd^T (bf16, [I, D]).  Tile 256 tokens x 256 intermediate columns.
+// B = Wd^T (bf16, [I, D]).  Tile 256 tokens x 256 intermediate columns,
+// one work-group of 8 waves (two per SIMD, each 128 x 64 of the tile): the
+// second wave on a SIMD runs while the first waits, in the K loop and above
+// all in the epilogue, whose loads, LDS round trips and barriers a single
+// wave per SIMD left exposed.
 constexpr int kEpiStride2 = 272;
-constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 16;  // after Gt, Ut and the reduction slots
+constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 32;  // after Gt, Ut and the 8 reduction slots
 
 // With a MoE plan: tile rows are padded expert order (gu8, dgu8, dgu8t over
 // ldt padded rows); dy is the row-major upstream gradient of the expert-order
 // rows (its rows urow(tm).. for tile row tm), W_down^T of expert e at
 // wdt + e * w_estride (bytes); the tile count comes from the plan.
-__global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
+__global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ wdt, const uint8_t* __restrict__ gu8,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, float* __restrict__ amax,
     uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n,
@@ -867,7 +900,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   // Its LDS range is disjoint from the main loop's ring and the staging
   // tiles; the main loop's first barrier publishes it.
   floatx2* lut = reinterpret_cast<floatx2*>(lds + kDgradLutOff);
-  {
+  if (tid < 256) {
 #pragma clang fp contract(off)
     const float gl = __builtin_amdgcn_cvt_f32_fp8(tid, 0) * (1.0f / scale[1]);
     const float sig = 1.0f / (1.0f + expf(-gl));
@@ -881,7 +914,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   const float inv3 = 1.0f / m3s, bnd3 = kE5M2Max * inv3;
   uint8_t* Gt = lds;
   uint8_t* Ut = lds + kTile * kEpiStride2;
-  float* red = reinterpret_cast<float*>(lds + 2 * kTile * kEpiStride2);  // 4 floats after both tiles
+  float* red = reinterpret_cast<float*>(lds + 2 * kTile * kEpiStride2);  // 8 floats after both tiles
   float m3 = 0.f;
   // Persistent: work-group pid runs tiles pid, pid + gridDim.x, ...  (Work-
   // groups started a quarter of a tile apart per XCD, so that the tiles'
@@ -901,13 +934,13 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     a_rows = P.rows(tm);
     wb += P.expert(tm) * w_estride;
   }
-  floatx16 acc[4][4];
+  floatx16 acc[4][2];
   // A = dy row-major (rows past the tile's last read as zero through the
   // range check); B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
-  MainLoop<true, 0, 0, false>::run(
+  MainLoop<true, 0, 0, false, 2, kStages, 0, false, false, 4>::run(
       lds, reinterpret_cast<const uint8_t*>(dy) + a_row * ldb, a_rows * ldb, [=](int r) { return r * (int)ldb; },
       kStage, wb + n0 * kStage, ldb * ip - n0 * kStage,
-      [=](int r) { return plain_col(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
+      [=](int r) { return plain_col_nb<2>(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
   // Row-order epilogue, in two passes of 128 tile rows (the rows of
   // stage_bf16_half<P>): dh staged in LDS as bf16, then each thread takes
   // 16-column chunks of one row, reading gu8 and writing dgu8 as whole K-slab
@@ -915,15 +948,20 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
   const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 64, 2 * I * ldt - m0 * 64);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
   uint8_t* DH = lds;
-  uint8_t* G2 = lds + 128 * kBf16Stride;
+  // the staging tiles of the token-contiguous copy (MoE only); their offset
+  // goes through an empty asm so that the compiler does not hoist per-lane
+  // addresses into them out of the tile loop (a register it had to spill)
+  int g2off = 128 * kBf16Stride;
+  asm volatile("" : "+s"(g2off));
+  uint8_t* G2 = lds + g2off;
   uint8_t* U2 = G2 + 128 * kEpiStride2;
 #pragma unroll
   for (int P = 0; P < 2; ++P) {
-    // gu8 words of this thread's 8 chunks, requested at once
-    intx4 wg[8], wu[8];
+    // gu8 words of this thread's 4 chunks, requested at once
+    intx4 wg[4], wu[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int item = 4 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
+    for (int k = 0; k < 4; ++k) {
+      const int item = 8 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
       const int c = 64 * slab + 16 * (lane & 3);
       const int row = half_tile_row(lr, P);
       const int64_t j = n0 + c;
@@ -933,12 +971,12 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     }
     if (P == 1) __syncthreads();  // pass 0's dgu8t copy has read the LDS
     // dh rounded to bf16 (train.py:1082)
-    if (P == 0) stage_bf16_half<0>(DH, acc, 1.0f);
-    else stage_bf16_half<1>(DH, acc, 1.0f);
+    if (P == 0) stage_bf16_half8<0>(DH, acc, 1.0f);
+    else stage_bf16_half8<1>(DH, acc, 1.0f);
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int item = 4 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
+    for (int k = 0; k < 4; ++k) {
+      const int item = 8 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
       const int c = 64 * slab + 16 * (lane & 3);
       const int64_t t = m0 + half_tile_row(lr, P);
       const intx4 h0 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c);
@@ -995,16 +1033,16 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
     // 64-127 tile rows 128 + 64P.. (rows past T hold zero codes)
     if (dgu8t) {
       const int64_t rp2 = slab_rows(2 * I);
-      lds_rows_store_slab_tr<64>(G2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, n0);
-      lds_rows_store_slab_tr<64>(G2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, n0);
-      lds_rows_store_slab_tr<64>(U2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, I + n0);
-      lds_rows_store_slab_tr<64>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, I + n0);
+      lds_rows_store_slab_tr<64, 8>(G2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, n0);
+      lds_rows_store_slab_tr<64, 8>(G2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, n0);
+      lds_rows_store_slab_tr<64, 8>(U2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, I + n0);
+      lds_rows_store_slab_tr<64, 8>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, I + n0);
     }
   }
   __syncthreads();  // the next tile's DMA overwrites the staging tiles
   }
   m3 *= 1.0f / scale[1];  // s_gu, read again rather than held across the tile loop
-  block_amax_atomic<4>(m3, red, amax + 3);
+  block_amax_atomic<8>(m3, red, amax + 3);
 }
 
 // ---------------------------------------------------------------------------
@@ -1015,7 +1053,7 @@ __global__ __launch_bounds__(256, 1) void down_dgrad_swiglu_kernel(
 // With a MoE plan: tile row tm of padded expert order writes its rows(tm)
 // valid rows to dxn rows urow(tm).. (expert order, unpadded); W8^T of
 // expert e at w8t + e * w_estride, its scale wscale[e].
-__global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
+__global__ __launch_bounds__(512, 1) void gateup_dgrad_kernel(
     const uint8_t* __restrict__ dgu8, const uint8_t* __restrict__ w8t, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, uint16_t* __restrict__ dxn,
     int64_t ldt, int tiles_m, int tiles_n, const int* __restrict__ plan, int64_t w_estride) {
@@ -1035,21 +1073,21 @@ __global__ __launch_bounds__(256, 1) void gateup_dgrad_kernel(
     uend = u0 + P.rows(tm);
   }
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-  floatx16 acc[4][4];
+  floatx16 acc[4][2];
   // K-slab operands: dgu8 [2I/64][ldt][64], w8t [2I/64][slab_rows(D)][64]
-  MainLoop<false, kFmtE5M2, kFmtE4M3, false>::run(
+  MainLoop<false, kFmtE5M2, kFmtE4M3, false, 2, kStages, 0, false, false, 4>::run(
       lds, dgu8 + m0 * kStage, K * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage),
-      w8t + n0 * kStage, K * dp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(dp * kStage),
-      (int)(K / kStage), acc);
+      w8t + n0 * kStage, K * dp - n0 * kStage, [=](int r) { return plain_col_nb<2>(r) * kStage; },
+      (int)(dp * kStage), (int)(K / kStage), acc);
   // the scales are read after the K loop, so that nothing is held across it
   const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
-  stage_bf16_half<0>(lds, acc, sab);
+  stage_bf16_half8<0>(lds, acc, sab);
   __syncthreads();
-  write_bf16_half(lds, 0, u0, n0, uend, D, D, nullptr, dxn);
+  write_bf16_half<512>(lds, 0, u0, n0, uend, D, D, nullptr, dxn);
   __syncthreads();
-  stage_bf16_half<1>(lds, acc, sab);
+  stage_bf16_half8<1>(lds, acc, sab);
   __syncthreads();
-  write_bf16_half(lds, 1, u0, n0, uend, D, D, nullptr, dxn);
+  write_bf16_half<512>(lds, 1, u0, n0, uend, D, D, nullptr, dxn);
 }
 
 // ---------------------------------------------------------------------------
@@ -1645,7 +1683,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
   int rc = prep(down_fwd_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(512), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)h8, (const uint8_t*)wd8, (const uint16_t*)res, T, D, I, scale, wscale + 1,
                      (uint16_t*)y, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
@@ -1668,7 +1706,7 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
   const int grid = ntiles < n_cu ? ntiles : n_cu;
   rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(grid), dim3(256), kDgradLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(grid), dim3(512), kDgradLds, (hipStream_t)stream,
                      (const uint16_t*)dy, (const uint16_t*)wdt, (const uint8_t*)gu8, T, D, I, scale, amax,
                      (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
@@ -1684,7 +1722,7 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
   int rc = prep(gateup_dgrad_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(512), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)dgu8, (const uint8_t*)w8t, T, D, I, scale, wscale, (uint16_t*)dxn, ldt,
                      tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
@@ -1832,7 +1870,7 @@ int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D
   const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(D, kTile);
   int rc = prep(down_fwd_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(down_fwd_kernel, dim3(tiles_m * tiles_n), dim3(512), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)h8, (const uint8_t*)wd8, (const uint16_t*)nullptr, R, D, I, scale, q_d,
                      (uint16_t*)out, ldp, tiles_m, tiles_n, plan, I * slab_rows(D));
   return status();
@@ -1852,7 +1890,7 @@ int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const voi
   const int ntiles = tiles_m * tiles_n;  // an upper bound: the kernel reads the plan's count
   rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kDgradLds,
+  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(512), kDgradLds,
                      (hipStream_t)stream, (const uint16_t*)dout, (const uint16_t*)wdt, (const uint8_t*)gu8, R, D, I,
                      scale, amax, (uint8_t*)dgu8, (uint8_t*)dgu8t, ldp, tiles_m, tiles_n, plan,
                      2 * D * slab_rows(I));
@@ -1867,7 +1905,7 @@ int sfp8_moe_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t E, int
   const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(D, kTile);
   int rc = prep(gateup_dgrad_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(gateup_dgrad_kernel, dim3(tiles_m * tiles_n), dim3(512), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)dgu8, (const uint8_t*)w8t, R, D, I, scale, q_gu, (uint16_t*)dx, ldp, tiles_m,
                      tiles_n, plan, 2 * I * slab_rows(D));
   return status();

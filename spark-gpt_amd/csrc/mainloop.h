@@ -114,8 +114,9 @@ SFP8_DEV void sched_interleave_valu() {
 // and would wait for all of it first; the stage waits and barriers already
 // order every read after its stage's DMA.
 template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0,
-          bool TR_A = false, bool TR_B = false>
+          bool TR_A = false, bool TR_B = false, int WN = 2>
 struct MainLoop {
+  static constexpr int kWaves = 2 * WN;
   static_assert(!(TR_A || TR_B) || (!PAIRED && NB == 4), "transposing reads: plain, 256 x 256");
   static constexpr bool kTr = TR_A || TR_B;
   using Rsrc = typename std::conditional<kTr, intx4, __amdgpu_buffer_rsrc_t>::type;
@@ -135,11 +136,13 @@ struct MainLoop {
   }
   static_assert(NB == 2 || NB == 4, "2 or 4 B blocks per wave");
   static_assert(STAGES >= 3, "at least three LDS stages");
-  static constexpr int kTileN = 64 * NB;                  // B rows per tile
+  static constexpr int kTileN = 32 * NB * WN;             // B rows per tile
   static constexpr int kStageB = kTileN * kStage;
   static constexpr int kLdsB = STAGES * kStageA;           // start of the B stages
   static constexpr int kLds = STAGES * (kStageA + kStageB);
-  static constexpr int kDma = 4 + NB;                      // DMA instructions per wave per stage
+  static constexpr int kDmaA = 16 / kWaves;                // A DMA instructions per wave per stage
+  static constexpr int kDmaB = kTileN / 16 / kWaves;
+  static constexpr int kDma = kDmaA + kDmaB;               // DMA instructions per wave per stage
   using Acc = floatx16[4][NB];
 
   // DMA instruction j of this wave's share of one stage: J < 4 are A blocks,
@@ -147,12 +150,12 @@ struct MainLoop {
   static SFP8_DEV void load_one(int j, uint8_t* lds, int buf, Rsrc ra,
                                 Rsrc rb, const uint32_t (&voff_a)[4], const uint32_t (&voff_b)[NB],
                                 int soff_a, int soff_b, int wave) {
-    if (j < 4) {
-      uint8_t* dst = lds + buf * kStageA + (64 * wave + 16 * j) * kStage;
+    if (j < kDmaA) {
+      uint8_t* dst = lds + buf * kStageA + ((kTile / kWaves) * wave + 16 * j) * kStage;
       dma16(dst, ra, voff_a[j], soff_a);
     } else {
-      uint8_t* dst = lds + kLdsB + buf * kStageB + (16 * NB * wave + 16 * (j - 4)) * kStage;
-      dma16(dst, rb, voff_b[j - 4], soff_b);
+      uint8_t* dst = lds + kLdsB + buf * kStageB + ((kTileN / kWaves) * wave + 16 * (j - kDmaA)) * kStage;
+      dma16(dst, rb, voff_b[j - kDmaA], soff_b);
     }
   }
 
@@ -341,6 +344,23 @@ struct MainLoop {
       __builtin_amdgcn_sched_barrier(0);
       return;
     }
+    if constexpr (BF16 && NB == 2) {
+      // bf16, 8 waves of 128 x 64: 16 MFMAs of 32 cycles; six fragments and
+      // four DMA issues alternate over 10 of them
+      mfma_then_reads<P + 0, 0, 1>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 1, 0, 1>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 2, 1, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 3, 1, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 4, 2, 3>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 5, 2, 3>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 6, 3, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 7, 3, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 8, 4, 5>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + 9, 5, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_range<P + 10, kMfma>(cur, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
     if constexpr (!BF16 && NB == 4) {
       // fp8, 256 x 256: fragments and DMA issues alternate over 10 MFMAs
       // (2-3 % faster than 4 MFMAs of reads followed by 4 of DMA)
@@ -355,6 +375,18 @@ struct MainLoop {
       mfma_then_reads<P + 8, 7, 8>(lds, cur, nxt, acc, rd_buf, aoff, boff);
       mfma_then_dma<P + 9, 7, 8>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
       mfma_range<P + 10, kMfma>(cur, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
+    if constexpr (!BF16 && NB == 2 && kDma == 4) {
+      // fp8, 8 waves of 128 x 64: 8 MFMAs of 64 cycles; two fragments after
+      // each of 3, then two DMA issues after each of 2
+      mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + 1, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_reads<P + 2, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 3, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_dma<P + 4, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_range<P + 5, kMfma>(cur, acc);
       __builtin_amdgcn_sched_barrier(0);
       return;
     }
@@ -394,11 +426,11 @@ struct MainLoop {
     const uint32_t chunk_tr =
         BF16 ? (uint32_t)((lane & 3) << 4) : (uint32_t)(((lane & 3) ^ (((lane >> 4) & 1) << 1)) << 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      voff_a[j] = (uint32_t)a_rowoff(64 * wave + 16 * j + (lane >> 2)) + (TR_A ? chunk_tr : chunk);
+    for (int j = 0; j < kDmaA; ++j)
+      voff_a[j] = (uint32_t)a_rowoff((kTile / kWaves) * wave + 16 * j + (lane >> 2)) + (TR_A ? chunk_tr : chunk);
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-      voff_b[j] = (uint32_t)b_rowoff(16 * NB * wave + 16 * j + (lane >> 2)) + (TR_B ? chunk_tr : chunk);
+    for (int j = 0; j < kDmaB; ++j)
+      voff_b[j] = (uint32_t)b_rowoff((kTileN / kWaves) * wave + 16 * j + (lane >> 2)) + (TR_B ? chunk_tr : chunk);
     // fragment read offsets (lane half g reads logical chunks 2g, 2g+1)
     const int fr = lane & 31, g = lane >> 5;
     const int sw = (fr >> 2) & 3;
