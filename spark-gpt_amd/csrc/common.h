@@ -314,14 +314,14 @@ __host__ __device__ inline int64_t slab_rows(int64_t R) { return (R + 255) / 256
 // block into 16 column runs of 16 tokens (two ds_read_b64_tr_b8), and the
 // four groups take consecutive 16-token blocks, so each wave store covers 16
 // whole 64-byte slab rows.  Work unit u (64-token block u % 4, 16-column
-// block u / 4) goes to wave u % 4.
-template <int NC16>
+// block u / 4) goes to wave u % NW (NW = waves in the work-group, 4 or 8).
+template <int NC16, int NW = 4>
 SFP8_DEV void lds_tile_store_slab_tr(const uint8_t* lds, int stride, uint8_t* out, int64_t rpad, int64_t t0,
                                      int64_t c0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, li = lane & 15;
 #pragma unroll 4
-  for (int p = 0; p < NC16; ++p) {
-    const int u = p * 4 + wave;
+  for (int p = 0; p < NC16 * 4 / NW; ++p) {
+    const int u = p * NW + wave;
     const int r = 64 * (u & 3) + 16 * q, c = 16 * (u >> 2);
     const uint8_t* src = lds + (r + (li >> 1)) * stride + c + 8 * (li & 1);
     const intx2 a = lds_read_tr8(src);

@@ -90,6 +90,14 @@ SFP8_DEV int plain_col_nb(int r) {
   return 32 * NB * wn + 16 * NB * ((rl >> 2) & 1) + 16 * (rl >> 5) + 4 * ((rl >> 3) & 3) + (rl & 3);
 }
 
+// Paired (gate/up) layout, 8 waves: rows 0..127 are gate, 128..255 up; wave
+// column wn (0..3) owns rows 32*wn.. of each half (one block); column (within
+// the 128-column half) 32*wn + 16*g + v.
+SFP8_DEV int paired_col8(int r) {
+  const int rl = r & 127;
+  return 32 * (rl >> 5) + 16 * ((rl >> 2) & 1) + 4 * ((rl >> 3) & 3) + (rl & 3);
+}
+
 // Paired (gate/up) layout: rows 0..127 are gate, 128..255 up; wave column wn
 // owns rows 64*wn.. of each half; column (within the 128-column half)
 // 64*wn + 32*g + 16*nb + v.
@@ -103,11 +111,11 @@ SFP8_DEV int paired_col(int r) {
 // dst + (c0 / 64 + p) * ldrows * 64 + (r0 + r) * 64.  Sixteen consecutive
 // threads read one contiguous LDS row (no bank conflicts for NP = 4); the
 // global writes are 256-byte runs of 4 rows per block.
-template <int NP>
+template <int NP, int NT = 256>
 SFP8_DEV void lds_rows_to_kslab(const uint8_t* lds, int nrows, int stride, uint8_t* dst, int64_t ldrows, int64_t r0,
                                 int64_t c0) {
   const int total = nrows * NP * 4;
-  for (int idx = threadIdx.x; idx < total; idx += 256) {
+  for (int idx = threadIdx.x; idx < total; idx += NT) {
     const int ch = idx & 3, pb = (idx >> 2) % NP, r = idx / (4 * NP);
     *reinterpret_cast<intx4*>(dst + (c0 / 64 + pb) * ldrows * 64 + (r0 + r) * 64 + ch * 16) =
         *reinterpret_cast<const intx4*>(lds + r * stride + pb * 64 + ch * 16);
@@ -138,7 +146,10 @@ constexpr int kEpiStride = 144;
 // With a MoE plan (grouped experts): tile row tm of padded expert order,
 // its expert's W8 at w8 + e * w_estride and weight scale wscale[e]; tile
 // rows past the plan's count exit.
-__global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
+// 8 waves (two per SIMD): wave (wm, wn) owns tile rows 128*wm.. and the gate
+// and up columns 32*wn.. (one 32-column block of each), so the serial
+// epilogue of one wave overlaps the other's on the same SIMD.
+__global__ __launch_bounds__(512, 1) void swiglu_fwd_kernel(
     const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, float* __restrict__ amax,
     uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int64_t ldt,
@@ -156,12 +167,12 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 128;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  floatx16 acc[4][4];
+  floatx16 acc[4][2];  // [tb][0] gate, [tb][1] up
   // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64]; one K stage of
   // the tile is 256 contiguous rows of A and two runs of 128 rows of B
-  MainLoop<false, kFmtE4M3, kFmtE4M3, true>::run(
+  MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, kStages, 0, false, false, 4>::run(
       lds, x8 + m0 * kStage, D * ldt - m0 * kStage, [=](int r) { return r * kStage; }, (int)(ldt * kStage), w8,
-      D * 2 * I, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
+      D * 2 * I, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col8(r)) * kStage; },
       (int)(2 * I * kStage), (int)(D / kStage), acc);
   // All scales are powers of two, so the dequantization factor commutes with
   // every rounding step: with gb, ub = bf16(acc) (unscaled),
@@ -182,14 +193,14 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   float* red = reinterpret_cast<float*>(lds + 3 * kTile * kEpiStride);
   float m_gu = 0.f, m_h = 0.f;
   const int fr = lane & 31, g = lane >> 5;
-  const int cb = 64 * wn + 32 * g;  // first of this lane's 32 columns
-  // g, u (bf16-rounded, unscaled) and h of unit (tb, nb, q): 4 columns
-  auto unit = [&](int tb, int nb, int q, float (&gb)[4], float (&ub)[4], float (&hb)[4]) {
+  const int cb = 32 * wn + 16 * g;  // first of this lane's 16 columns
+  // g, u (bf16-rounded, unscaled) and h of unit (tb, q): 4 columns
+  auto unit = [&](int tb, int q, float (&gb)[4], float (&ub)[4], float (&hb)[4]) {
     // g, u rounded to bf16 as in the bf16 path (train.py:1006-1007)
 #pragma unroll
     for (int e = 0; e < 4; e += 2) {
-      const uint32_t pg = pack2_bf16(acc[tb][nb][4 * q + e], acc[tb][nb][4 * q + e + 1]);
-      const uint32_t pu = pack2_bf16(acc[tb][nb + 2][4 * q + e], acc[tb][nb + 2][4 * q + e + 1]);
+      const uint32_t pg = pack2_bf16(acc[tb][0][4 * q + e], acc[tb][0][4 * q + e + 1]);
+      const uint32_t pu = pack2_bf16(acc[tb][1][4 * q + e], acc[tb][1][4 * q + e + 1]);
       gb[e] = __uint_as_float(pg << 16);
       gb[e + 1] = __uint_as_float(pg & 0xffff0000u);
       ub[e] = __uint_as_float(pu << 16);
@@ -204,14 +215,13 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int row = 128 * wm + 32 * tb + fr;  // token within the tile
-    uint32_t gw[8], uw[8], hw[8];
+    uint32_t gw[4], uw[4], hw[4];
     bool bad = false;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float gb[4], ub[4], hb[4];
-        unit(tb, nb, q, gb, ub, hb);
+        unit(tb, q, gb, ub, hb);
         // NaN-propagating maxima: inside the e4m3 range (after scaling) the
         // unclamped conversions are exact; otherwise the row block is redone
         float a = max3_nan(fabsf(gb[0]), fabsf(ub[0]), fabsf(gb[1]));
@@ -223,7 +233,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
         bad |= !(a <= bnd1) | !(b <= bnd2);
         m_gu = fmaxf(m_gu, a);  // a NaN here is redone by the exact path
         m_h = fmaxf(m_h, b);
-        const int k = 4 * nb + q;
+        const int k = q;
         gw[k] = pack4_e4m3_scaled_noclamp(gb[0], gb[1], gb[2], gb[3], inv1, 0u);
         uw[k] = pack4_e4m3_scaled_noclamp(ub[0], ub[1], ub[2], ub[3], inv1, 0u);
         hw[k] = pack4_e4m3_scaled_noclamp(hb[0], hb[1], hb[2], hb[3], inv2, 0u);
@@ -231,18 +241,17 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
     }
     if (__builtin_amdgcn_ballot_w64(bad)) {  // wave-uniform; NaN or out-of-range data only
       asm volatile("" ::: "memory");
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float gb[4], ub[4], hb[4];
-          unit(tb, nb, q, gb, ub, hb);
+          unit(tb, q, gb, ub, hb);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {  // amax over the non-NaN values
             m_gu = fmaxf(m_gu, fmaxf(fabsf(gb[e]), fabsf(ub[e])));
             m_h = fmaxf(m_h, fabsf(hb[e]));
           }
-          const int k = 4 * nb + q;
+          const int k = q;
           gw[k] = fix_nan4(pack4_e4m3_scaled(gb[0], gb[1], gb[2], gb[3], inv1, bnd1), gb[0], gb[1], gb[2], gb[3]);
           uw[k] = fix_nan4(pack4_e4m3_scaled(ub[0], ub[1], ub[2], ub[3], inv1, bnd1), ub[0], ub[1], ub[2], ub[3]);
           hw[k] = fix_nan4(pack4_e4m3_scaled(hb[0], hb[1], hb[2], hb[3], inv2, bnd2), hb[0], hb[1], hb[2], hb[3]);
@@ -250,11 +259,8 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
       }
     }
     store16(Gt + row * kEpiStride + cb, {gw[0], gw[1], gw[2], gw[3]});
-    store16(Gt + row * kEpiStride + cb + 16, {gw[4], gw[5], gw[6], gw[7]});
     store16(Ut + row * kEpiStride + cb, {uw[0], uw[1], uw[2], uw[3]});
-    store16(Ut + row * kEpiStride + cb + 16, {uw[4], uw[5], uw[6], uw[7]});
     store16(Ht + row * kEpiStride + cb, {hw[0], hw[1], hw[2], hw[3]});
-    store16(Ht + row * kEpiStride + cb + 16, {hw[4], hw[5], hw[6], hw[7]});
   }
   m_gu *= deq;
   m_h *= deq * deq;
@@ -262,17 +268,23 @@ __global__ __launch_bounds__(256, 1) void swiglu_fwd_kernel(
   // gu8 (gate and up halves) and h8 as 64-column K-slab blocks (every tile
   // row: rows past T are zero padding), then, when asked for, the
   // token-contiguous h8t
-  lds_rows_to_kslab<2>(Gt, kTile, kEpiStride, gu8, ldt, m0, n0);
-  lds_rows_to_kslab<2>(Ut, kTile, kEpiStride, gu8, ldt, m0, I + n0);
-  lds_rows_to_kslab<2>(Ht, kTile, kEpiStride, h8, ldt, m0, n0);
-  if (h8t) lds_tile_store_slab_tr<8>(Ht, kEpiStride, h8t, slab_rows(I), m0, n0);
+  lds_rows_to_kslab<2, 512>(Gt, kTile, kEpiStride, gu8, ldt, m0, n0);
+  lds_rows_to_kslab<2, 512>(Ut, kTile, kEpiStride, gu8, ldt, m0, I + n0);
+  lds_rows_to_kslab<2, 512>(Ht, kTile, kEpiStride, h8, ldt, m0, n0);
+  if (h8t) lds_tile_store_slab_tr<8, 8>(Ht, kEpiStride, h8t, slab_rows(I), m0, n0);
   m_gu = wave_max(m_gu);
   m_h = wave_max(m_h);
-  if (lane == 0) { red[wave] = m_gu; red[4 + wave] = m_h; }
+  if (lane == 0) { red[wave] = m_gu; red[8 + wave] = m_h; }
   __syncthreads();
   if (tid == 0) {
-    atomic_max_nonneg(amax + 1, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-    atomic_max_nonneg(amax + 2, fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+    float a1 = red[0], a2 = red[8];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) {
+      a1 = fmaxf(a1, red[w]);
+      a2 = fmaxf(a2, red[8 + w]);
+    }
+    atomic_max_nonneg(amax + 1, a1);
+    atomic_max_nonneg(amax + 2, a2);
   }
 }
 
@@ -1544,7 +1556,7 @@ __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __res
 
 }  // namespace sfp8
 
-static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 32 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
+static_assert(3 * sfp8::kTile * sfp8::kEpiStride + 64 <= sfp8::kMainLds, "swiglu epilogue tiles fit the main loop's LDS");
 static_assert(sfp8::kPipeLds <= 160 * 1024, "deferred-epilogue SwiGLU fits the 160 KiB LDS");
 static_assert(128 * sfp8::kBf16Stride <= sfp8::kMainLds, "bf16 epilogue staging fits the main loop's LDS");
 static_assert(3 * 128 * sfp8::kGuStride <= sfp8::kMainLds, "bf16 SwiGLU staging fits the main loop's LDS");
@@ -1667,7 +1679,7 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
   const int tiles_m = cdiv(T, kTile), tiles_n = (int)(I / 128);
   int rc = prep(swiglu_fwd_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(tiles_m * tiles_n), dim3(512), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)x8, (const uint8_t*)w8, T, D, I, scale, wscale, amax, (uint8_t*)gu8,
                      (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
@@ -1856,7 +1868,7 @@ int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, i
   const int tiles_m = (int)(ldp / kTile), tiles_n = (int)(I / 128);
   int rc = prep(swiglu_fwd_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(tiles_m * tiles_n), dim3(256), kMainLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(tiles_m * tiles_n), dim3(512), kMainLds, (hipStream_t)stream,
                      (const uint8_t*)x8, (const uint8_t*)w8, ldp, D, I, scale, q_gu, amax, (uint8_t*)gu8,
                      (uint8_t*)h8, (uint8_t*)h8t, ldp, tiles_m, tiles_n, plan, D * slab_rows(2 * I));
   return status();

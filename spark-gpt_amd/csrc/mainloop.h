@@ -60,13 +60,16 @@ SFP8_DEV intx4 make_rsrc4(const void* base, int64_t bytes) {
 // wave (wm, wn) = (wave & 1, wave >> 1) owns A rows 128*wm.. (4 blocks of 32)
 // and NB blocks of 32 B rows:
 //   plain:  B rows 32*NB*wn + 32*nb
-//   paired: gate/up halves of the B tile (rows [0, 32*NB) gate, the rest up);
-//           wave wn owns gate blocks 16*NB*wn + 32*nb (nb < NB/2) and the up
-//           blocks at the same offsets in the second half.
-template <bool PAIRED, int NB>
+//   paired: gate/up halves of the B tile (rows [0, 16*NB*WN) gate, the rest
+//           up); wave wn owns gate blocks 16*NB*wn + 32*nb (nb < NB/2) and
+//           the up blocks at the same offsets in the second half.
+// WN = wave columns (2: 4 waves, 4: 8 waves).
+template <bool PAIRED, int NB, int WN = 2>
 struct BLayout {
   static constexpr int kWaveStride = PAIRED ? 16 * NB : 32 * NB;
-  static constexpr int off(int nb) { return PAIRED ? (nb < NB / 2 ? 32 * nb : 32 * NB + 32 * (nb - NB / 2)) : 32 * nb; }
+  static constexpr int off(int nb) {
+    return PAIRED ? (nb < NB / 2 ? 32 * nb : 16 * NB * WN + 32 * (nb - NB / 2)) : 32 * nb;
+  }
 };
 
 // Interleave N_MFMA MFMAs with N_DS LDS reads (spread over all of them) and
@@ -216,7 +219,7 @@ struct MainLoop {
       if constexpr (TR_B) {
         f.b[I - 4] = read_tr_block<I - 4>(lds + kLdsB + buf * kStageB, boff);
       } else {
-        const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB>::off(I - 4) * kStage;
+        const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB, WN>::off(I - 4) * kStage;
         const intx4 lo = *reinterpret_cast<const intx4*>(p + boff[0]);
         const intx4 hi = *reinterpret_cast<const intx4*>(p + boff[1]);
         f.b[I - 4] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -438,7 +441,7 @@ struct MainLoop {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
-      boff[h] = (uint32_t)(kLdsB + (BLayout<PAIRED, NB>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+      boff[h] = (uint32_t)(kLdsB + (BLayout<PAIRED, NB, WN>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
     }
     if constexpr (kTr && BF16) {
       // bf16 transposing reads: 16-lane group G = lane / 16 (lane half G / 2,
