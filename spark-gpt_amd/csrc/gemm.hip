@@ -332,6 +332,7 @@ struct SwigluPipe {
   static constexpr int kUnits = 16;  // 4 pairs each: unit u = row block u/4, pairs 4*(u%4) ..
   static constexpr int kSt = 4;      // LDS ring stages
   static constexpr int kDma = ML::kDma;
+  static constexpr int kPre = 2;     // MFMAs of a stage issued before its wait
   static_assert(NK >= kSt && NK % kSt == 0, "whole rings of K stages: a tile's stage s sits in slot s % kSt");
 
   // units run in stage kt: [ubeg(kt), ubeg(kt+1))
@@ -447,6 +448,10 @@ struct SwigluPipe {
   template <int KT>
   static SFP8_DEV void stage(Ctx& c, int a_ss, int b_ss) {
     constexpr int cur = KT & 1, nxt = cur ^ 1;
+    // the first kPre MFMAs (register operands only) go ahead of the wait,
+    // so the matrix core stays busy while it blocks
+    ML::template mfma_range<0, kPre>(c.f[cur], c.acc);
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (kSt - 3)) : "memory");
     __builtin_amdgcn_sched_barrier(0);
     // the fences come before the stage's memory operations: an asm statement
@@ -462,12 +467,12 @@ struct SwigluPipe {
       ML::load_stage(c.lds, slot, c.nra, c.nrb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
     }
     ML::read_frags(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
-    ML::template mfma_range<0, ML::kMfma>(c.f[cur], c.acc);
+    ML::template mfma_range<kPre, ML::kMfma>(c.f[cur], c.acc);
     units<ubeg(KT), ubeg(KT + 1)>(c);
-    // 8 MFMAs, 12 LDS reads, 6 DMAs, the units' vector ALU work spread
-    // after every MFMA (about 90 instructions per unit)
-    constexpr int nv = (ubeg(KT + 1) - ubeg(KT)) * 96 / ML::kMfma;
-    sched_interleave_valu<ML::kMfma, nv, 2 * (4 + 2), kDma>();
+    // the other MFMAs, 12 LDS reads, 6 DMAs, the units' vector ALU work
+    // spread after every MFMA (about 90 instructions per unit)
+    constexpr int nv = (ubeg(KT + 1) - ubeg(KT)) * 96 / (ML::kMfma - kPre);
+    sched_interleave_valu<ML::kMfma - kPre, nv, 2 * (4 + 2), kDma>();
     pins<ubeg(KT), ubeg(KT + 1)>(c);
     stores<ubeg(KT), ubeg(KT + 1)>(c);
   }
