@@ -163,10 +163,11 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
  * order by a second kernel on the same stream. */
 int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_t M, int64_t N, int64_t ldt,
                     const float* sa, const float* sb, float* out, float* ws, int64_t ws_floats, void* stream);
-/* K splits sfp8_gemm_wgrad / _rows use for (M, N, ldt): the power of two
- * (each split a multiple of 128 tokens and at least 2048) that minimises
- * rounds of work-groups on 256 CUs x K stages per split + the partials'
- * traffic.  A size query: needs no GPU. */
+/* K splits sfp8_gemm_wgrad / _rows use for (M, N, ldt): the count from 1 to
+ * 64 (each split a multiple of 128 tokens and at least 2048, the last one
+ * taking the rest) that minimises rounds of work-groups on 256 CUs x the
+ * longest split's K stages + the partials' traffic; 5 for both gradients of
+ * the T=65536, D=1024, I=3072 block.  A size query: needs no GPU. */
 int64_t sfp8_wgrad_splits(int64_t M, int64_t N, int64_t ldt);
 /* Bytes of a K-slab of a [rows, k] matrix (k bytes per row; -1 if k is not
  * a multiple of 64). */
