@@ -397,6 +397,76 @@ struct SwigluPipe {
     c.hw[Q] = pack4_e4m3_scaled_noclamp(hb[0], hb[1], hb[2], hb[3], c.inv2, c.hw[Q]);
   }
 
+  // A unit's working values between its pieces.
+  struct UnitTmp {
+    float gb[4], ub[4], hb[4], ex[4], sg[4];
+  };
+
+  // Piece P of unit U: the arithmetic of unit_compute<U>, the same
+  // operations in the same order per value, cut into six parts that go one
+  // after each of the stage's MFMAs past the barrier and software-pipelined
+  // over the unit's four pairs (the exponent of a pair one piece before its
+  // reciprocal), so that each part holds at most two transcendental
+  // instructions (a quarter of the vector ALU's rate) beside independent
+  // others.  A wave issues in order: more vector work between two MFMAs
+  // than the first one's 64 cycles holds back the second.  Each part reads
+  // its inputs and publishes its results through empty asm statements, so
+  // the compiler keeps it in its slot.
+  template <int TB, int Q, int E>
+  static SFP8_DEV void unit_unpack(Ctx& c, UnitTmp& t) {
+    uint32_t p = c.E[TB][4 * Q + E];
+    asm volatile("" : "+v"(p));
+    t.gb[E] = __uint_as_float(p << 16);
+    t.ub[E] = __uint_as_float(p & 0xffff0000u);
+    t.ex[E] = __builtin_amdgcn_exp2f(t.gb[E] * c.c_exp);
+  }
+  template <int U, int P>
+  static SFP8_DEV void unit_piece(Ctx& c, UnitTmp& t) {
+    constexpr int TB = U / 4, Q = U % 4;
+    if constexpr (P == 0) {
+      unit_unpack<TB, Q, 0>(c, t);
+      unit_unpack<TB, Q, 1>(c, t);
+      asm volatile("" ::"v"(t.ex[0]), "v"(t.ex[1]));
+    } else if constexpr (P == 1) {
+      t.sg[0] = __builtin_amdgcn_rcpf(1.0f + t.ex[0]);
+      t.sg[1] = __builtin_amdgcn_rcpf(1.0f + t.ex[1]);
+      unit_unpack<TB, Q, 2>(c, t);
+      asm volatile("" ::"v"(t.sg[0]), "v"(t.sg[1]), "v"(t.ex[2]));
+    } else if constexpr (P == 2) {
+      unit_unpack<TB, Q, 3>(c, t);
+      t.sg[2] = __builtin_amdgcn_rcpf(1.0f + t.ex[2]);
+      t.hb[0] = t.gb[0] * t.sg[0] * t.ub[0];
+      t.hb[1] = t.gb[1] * t.sg[1] * t.ub[1];
+      asm volatile("" ::"v"(t.ex[3]), "v"(t.sg[2]), "v"(t.hb[0]), "v"(t.hb[1]));
+    } else if constexpr (P == 3) {
+      t.sg[3] = __builtin_amdgcn_rcpf(1.0f + t.ex[3]);
+      t.hb[2] = t.gb[2] * t.sg[2] * t.ub[2];
+      // NaN-propagating maximum of the gate and up magnitudes: inside the
+      // e4m3 range (after scaling) no clamp can act and no NaN needs
+      // patching, so the unclamped conversions are exact; otherwise the row
+      // block's block_store redoes them (wave-uniform, rare)
+      float a = max3_nan(fabsf(t.gb[0]), fabsf(t.ub[0]), fabsf(t.gb[1]));
+      a = max3_nan(a, fabsf(t.ub[1]), fabsf(t.gb[2]));
+      a = max3_nan(a, fabsf(t.ub[2]), fabsf(t.gb[3]));
+      a = __builtin_elementwise_maximum(a, fabsf(t.ub[3]));
+      c.bad |= !(a <= c.bnd1);
+      c.m_gu = fmaxf(c.m_gu, a);  // a NaN here is redone by the exact path
+      asm volatile("" ::"v"(t.sg[3]), "v"(t.hb[2]), "v"(c.m_gu));
+    } else if constexpr (P == 4) {
+      t.hb[3] = t.gb[3] * t.sg[3] * t.ub[3];
+      float b = max3_nan(fabsf(t.hb[0]), fabsf(t.hb[1]), fabsf(t.hb[2]));
+      b = __builtin_elementwise_maximum(b, fabsf(t.hb[3]));
+      c.bad |= !(b <= c.bnd2);
+      c.m_h = fmaxf(c.m_h, b);
+      c.gw[Q] = pack4_e4m3_scaled_noclamp(t.gb[0], t.gb[1], t.gb[2], t.gb[3], c.inv1, c.gw[Q]);
+      asm volatile("" ::"v"(c.m_h), "v"(c.gw[Q]));
+    } else {
+      c.uw[Q] = pack4_e4m3_scaled_noclamp(t.ub[0], t.ub[1], t.ub[2], t.ub[3], c.inv1, c.uw[Q]);
+      c.hw[Q] = pack4_e4m3_scaled_noclamp(t.hb[0], t.hb[1], t.hb[2], t.hb[3], c.inv2, c.hw[Q]);
+      asm volatile("" ::"v"(c.uw[Q]), "v"(c.hw[Q]));
+    }
+  }
+
   // After the last unit of row block TB: the exact conversions when a unit
   // of the block saw NaN or out-of-range data (wave-uniform, rare), the
   // three 16-byte global stores and the h bytes into the LDS tile.
@@ -454,27 +524,36 @@ struct SwigluPipe {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (kSt - 3)) : "memory");
     __builtin_amdgcn_sched_barrier(0);
-    // the fences come before the stage's memory operations: an asm statement
-    // with side effects stays ordered after every load issued before it, and
-    // the units' arithmetic after the fences
-    fences<ubeg(KT), ubeg(KT + 1)>(c);
-    constexpr int slot = (KT + kSt - 1) % kSt;
-    if constexpr (KT + kSt - 1 < NK) {
-      constexpr int ld = KT + kSt - 1;
-      ML::load_stage(c.lds, slot, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
-    } else {
-      const int ld = c.has_next ? KT + kSt - 1 - NK : NK - 1;
-      ML::load_stage(c.lds, slot, c.nra, c.nrb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
-    }
-    ML::read_frags(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
-    ML::template mfma_range<kPre, ML::kMfma>(c.f[cur], c.acc);
-    units<ubeg(KT), ubeg(KT + 1)>(c);
-    // the other MFMAs, 12 LDS reads, 6 DMAs, the units' vector ALU work
-    // spread after every MFMA (about 90 instructions per unit)
-    constexpr int nv = (ubeg(KT + 1) - ubeg(KT)) * 96 / (ML::kMfma - kPre);
-    sched_interleave_valu<ML::kMfma - kPre, nv, 2 * (4 + 2), kDma>();
-    pins<ubeg(KT), ubeg(KT + 1)>(c);
+    UnitTmp t;
+    slot<KT, 0>(c, t, a_ss, b_ss);
+    slot<KT, 1>(c, t, a_ss, b_ss);
+    slot<KT, 2>(c, t, a_ss, b_ss);
+    slot<KT, 3>(c, t, a_ss, b_ss);
+    slot<KT, 4>(c, t, a_ss, b_ss);
+    slot<KT, 5>(c, t, a_ss, b_ss);
     stores<ubeg(KT), ubeg(KT + 1)>(c);
+  }
+
+  template <int KT, int J>
+  static SFP8_DEV void slot(Ctx& c, UnitTmp& t, int a_ss, int b_ss) {
+    constexpr int cur = KT & 1, nxt = cur ^ 1;
+    ML::template mfma_range<kPre + J, kPre + J + 1>(c.f[cur], c.acc);
+    if constexpr (J < 2) {
+      constexpr int slot_ = (KT + kSt - 1) % kSt;
+#pragma unroll
+      for (int j = J * kDma / 2; j < (J + 1) * kDma / 2; ++j) {
+        if constexpr (KT + kSt - 1 < NK) {
+          constexpr int ld = KT + kSt - 1;
+          ML::load_one(j, c.lds, slot_, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
+        } else {
+          const int ld = c.has_next ? KT + kSt - 1 - NK : NK - 1;
+          ML::load_one(j, c.lds, slot_, c.nra, c.nrb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
+        }
+      }
+    }
+    ML::template read_frag<J < 2 ? 4 + J : J - 2>(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
+    unit_piece<KT, J>(c, t);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // An empty asm that "rewrites" a unit's inputs after the stage's barrier
