@@ -296,9 +296,10 @@ __global__ __launch_bounds__(512, 1) void swiglu_fwd_kernel(
 // consecutive columns for each of its 4 row blocks.  One work-group per CU
 // walks its tiles; after tile i's K loop the lane packs bf16(g), bf16(u) of
 // its 64 pairs into 64 registers (E), and the SwiGLU of tile i runs in 16
-// units of 4 pairs spread over the K stages of tile i+1, in the same
-// instruction stream as its MFMAs (the matrix pipe runs them while the vector
-// ALU does the epilogue).  The h bytes of a tile also go to one of two LDS
+// units of 4 pairs, one per K stage of tile i+1, in the same instruction
+// stream as its MFMAs (the matrix pipe runs them while the vector ALU does the
+// epilogue): each unit in six pieces, one after each MFMA past the stage's
+// barrier.  The h bytes of a tile also go to one of two LDS
 // tiles; its token-contiguous (K-slab) copy is written at the next tile
 // boundary with LDS transpose reads.  The last tile's epilogue runs alone.
 // NK = D / 64 K stages, fully unrolled so each unit has a fixed stage; the K
@@ -509,12 +510,12 @@ struct SwigluPipe {
     store16(c.hbuf + row * kPipeHStride + col, c.hw);
   }
 
-  // Stage KT: wait for stage KT+1, barrier, DMA of stage KT+3 (of the next
-  // tile past the last stage), fragments of stage KT+1, the MFMAs of stage
-  // KT with this stage's epilogue units, then the row-block stores the units
-  // completed.  Vector stores count in vmcnt too and may complete after
-  // later loads, so the wait allows only the kDma loads issued after stage
-  // KT+1's; stores still in flight can make it wait for those as well.
+  // Stage KT: the first kPre MFMAs, then the wait for stage KT+1 and the
+  // barrier, then six slots (slot below), then the row-block stores the
+  // stage's unit completed.  Vector stores count in vmcnt too and may
+  // complete after later loads, so the wait allows only the kDma loads
+  // issued after stage KT+1's; stores still in flight can make it wait for
+  // those as well.
   template <int KT>
   static SFP8_DEV void stage(Ctx& c, int a_ss, int b_ss) {
     constexpr int cur = KT & 1, nxt = cur ^ 1;
@@ -534,6 +535,11 @@ struct SwigluPipe {
     stores<ubeg(KT), ubeg(KT + 1)>(c);
   }
 
+  // Slot J of stage KT: one MFMA past the barrier, then (J < 2) half of the
+  // DMA of stage KT+3 (of the next tile past the last stage), one fragment
+  // of stage KT+1 (B blocks first: the next stage's first MFMAs use b[0],
+  // b[1] and a[0]) and piece J of the stage's epilogue unit; the scheduling
+  // barrier keeps the slot's work after its MFMA.
   template <int KT, int J>
   static SFP8_DEV void slot(Ctx& c, UnitTmp& t, int a_ss, int b_ss) {
     constexpr int cur = KT & 1, nxt = cur ^ 1;
@@ -556,37 +562,6 @@ struct SwigluPipe {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // An empty asm that "rewrites" a unit's inputs after the stage's barrier
-  // keeps the compiler from hoisting the unit's arithmetic into an earlier
-  // stage.
-  template <int U0, int U1>
-  static SFP8_DEV void fences(Ctx& c) {
-    if constexpr (U0 < U1) {
-      constexpr int TB = U0 / 4, Q = U0 % 4;
-      asm volatile("" : "+v"(c.E[TB][4 * Q]), "+v"(c.E[TB][4 * Q + 1]), "+v"(c.E[TB][4 * Q + 2]),
-                   "+v"(c.E[TB][4 * Q + 3]));
-      fences<U0 + 1, U1>(c);
-    }
-  }
-
-  // An empty asm that reads a unit's packed bytes keeps the compiler from
-  // sinking the unit's arithmetic into a later stage (next to its store).
-  template <int U0, int U1>
-  static SFP8_DEV void pins(Ctx& c) {
-    if constexpr (U0 < U1) {
-      constexpr int Q = U0 % 4;
-      asm volatile("" ::"v"(c.gw[Q]), "v"(c.uw[Q]), "v"(c.hw[Q]));
-      pins<U0 + 1, U1>(c);
-    }
-  }
-
-  template <int U0, int U1>
-  static SFP8_DEV void units(Ctx& c) {
-    if constexpr (U0 < U1) {
-      unit_compute<U0>(c);
-      units<U0 + 1, U1>(c);
-    }
-  }
   template <int U0, int U1>
   static SFP8_DEV void stores(Ctx& c) {
     if constexpr (U0 < U1) {
