@@ -1412,7 +1412,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // written.
 constexpr int kGuStride = 272;  // staging row: 128 bf16 columns (256 bytes) + 16
 
-__global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
+// 8 waves (two per SIMD): wave (wm, wn) owns tile rows 128*wm.. and one
+// 32-column block of gate and one of up, columns 32*wn.. of each half.
+__global__ __launch_bounds__(512, 1) void bf16_swiglu_fwd_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ rstd, uint16_t* __restrict__ gu, uint16_t* __restrict__ h, int tiles_m, int tiles_n,
     const int* __restrict__ plan, int64_t w_estride, int64_t ldxs) {
@@ -1430,16 +1432,16 @@ __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
   const int64_t n0 = (int64_t)tn * 128;
   const int64_t ldx = D * 2;  // bytes per x row = K bytes
   const int64_t wr = slab_rows(2 * I);
-  floatx16 acc[4][4];
+  floatx16 acc[4][2];  // [tb][0] gate, [tb][1] up
   // A: x row-major [T, D] (rows past the tile's last read as zero through
   // the range check), or with ldxs > 0 its row K-slab [2D/64][ldxs][64]
   // (zero padding rows): a K stage of the tile is then one 16 KiB block of
   // whole 128-byte lines instead of 256 half lines 2D bytes apart
   const bool xslab = ldxs > 0;
-  MainLoop<true, 0, 0, true>::run(
+  MainLoop<true, 0, 0, true, 2, kStages, 0, false, false, 4>::run(
       lds, reinterpret_cast<const uint8_t*>(x) + r0 * (xslab ? kStage : ldx),
       xslab ? ldx * ldxs - r0 * kStage : nrows * ldx, [=](int r) { return r * (xslab ? kStage : (int)ldx); },
-      xslab ? (int)(ldxs * kStage) : kStage, w, ldx * wr, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col(r & 127)) * kStage; },
+      xslab ? (int)(ldxs * kStage) : kStage, w, ldx * wr, [=](int r) { return ((r >> 7) * (int)I + (int)n0 + paired_col8(r)) * kStage; },
       (int)(wr * kStage), (int)(ldx / kStage), acc);
   // Epilogue in two passes of 128 tile rows: pass P takes the lanes' row
   // blocks tb = 2P, 2P+1 (tile row 128 wm + 64 P + 32 (tb & 1) + fr, staging
@@ -1447,7 +1449,7 @@ __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
   // then writes them as whole 256-byte row runs.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1, fr = lane & 31, g = lane >> 5;
-  const int cb = 64 * wn + 32 * g;  // first of this lane's 32 columns in the tile
+  const int cb = 32 * wn + 16 * g;  // first of this lane's 16 columns in the tile
   uint8_t* Gs = lds;
   uint8_t* Us = lds + 128 * kGuStride;
   uint8_t* Hs = lds + 2 * 128 * kGuStride;
@@ -1460,26 +1462,23 @@ __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
       const int tb = 2 * P + q;
       const int lr = 128 * wm + 32 * tb + fr;  // row within the tile
       const float rs = (rstd && lr < nrows) ? rstd[r0 + lr] : 1.0f;
-      uint32_t gw[16], uw[16], hw[16];
+      uint32_t gw[8], uw[8], hw[8];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int v = 0; v < 16; v += 2) {
-          const uint32_t pg = pack2_bf16(acc[tb][nb][v] * rs, acc[tb][nb][v + 1] * rs);
-          const uint32_t pu = pack2_bf16(acc[tb][nb + 2][v] * rs, acc[tb][nb + 2][v + 1] * rs);
-          const float g0 = __uint_as_float(pg << 16), g1 = __uint_as_float(pg & 0xffff0000u);
-          const float u0 = __uint_as_float(pu << 16), u1 = __uint_as_float(pu & 0xffff0000u);
-          const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * c_exp));
-          const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * c_exp));
-          const int k = 8 * nb + v / 2;
-          gw[k] = pg;
-          uw[k] = pu;
-          hw[k] = pack2_bf16(g0 * s0 * u0, g1 * s1 * u1);
-        }
+      for (int v = 0; v < 16; v += 2) {
+        const uint32_t pg = pack2_bf16(acc[tb][0][v] * rs, acc[tb][0][v + 1] * rs);
+        const uint32_t pu = pack2_bf16(acc[tb][1][v] * rs, acc[tb][1][v + 1] * rs);
+        const float g0 = __uint_as_float(pg << 16), g1 = __uint_as_float(pg & 0xffff0000u);
+        const float u0 = __uint_as_float(pu << 16), u1 = __uint_as_float(pu & 0xffff0000u);
+        const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g0 * c_exp));
+        const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g1 * c_exp));
+        const int k = v / 2;
+        gw[k] = pg;
+        uw[k] = pu;
+        hw[k] = pack2_bf16(g0 * s0 * u0, g1 * s1 * u1);
       }
       const int sr = 64 * wm + 32 * q + fr;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         store16(Gs + sr * kGuStride + 2 * cb + 16 * j, {gw[4 * j], gw[4 * j + 1], gw[4 * j + 2], gw[4 * j + 3]});
         store16(Us + sr * kGuStride + 2 * cb + 16 * j, {uw[4 * j], uw[4 * j + 1], uw[4 * j + 2], uw[4 * j + 3]});
         store16(Hs + sr * kGuStride + 2 * cb + 16 * j, {hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]});
@@ -1487,7 +1486,7 @@ __global__ __launch_bounds__(256, 1) void bf16_swiglu_fwd_kernel(
     }
     __syncthreads();
     // 128 rows x 16 pieces of 16 bytes per output: sixteen lanes per row
-    for (int idx = threadIdx.x; idx < 128 * 16; idx += 256) {
+    for (int idx = threadIdx.x; idx < 128 * 16; idx += 512) {
       const int sr = idx >> 4, c = idx & 15;
       const int lr = half_tile_row(sr, P);
       const int64_t col = n0 + 8 * c;
@@ -2087,7 +2086,7 @@ int bf16_swiglu_launch(const void* x, const void* w, int64_t T, int64_t D, int64
   const int tiles_n = cdiv(I, 128);
   int rc = prep(bf16_swiglu_fwd_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(bf16_swiglu_fwd_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), kMainLds, st,
+  hipLaunchKernelGGL(bf16_swiglu_fwd_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), kMainLds, st,
                      (const uint16_t*)x, (const uint8_t*)w, T, D, I, rstd, (uint16_t*)gu, (uint16_t*)h, tiles_m,
                      tiles_n, plan, plan ? 2 * D * slab_rows(2 * I) : 0, ldxs);
   (void)E;
