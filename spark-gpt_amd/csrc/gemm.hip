@@ -1508,7 +1508,8 @@ __global__ __launch_bounds__(512, 1) void bf16_swiglu_fwd_kernel(
 // With a MoE plan: A in padded expert order, tile row tm writes its rows(tm)
 // valid rows to out rows urow(tm).. (expert order); B of expert e at
 // b + e * b_estride (bytes).
-__global__ __launch_bounds__(256, 1) void bf16_gemm_kernel(
+// 8 waves (two per SIMD), each 128 x 64.
+__global__ __launch_bounds__(512, 1) void bf16_gemm_kernel(
     const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, int64_t T, int64_t N, int64_t Kb, int64_t lda,
     uint16_t* __restrict__ out, int tiles_m, int tiles_n, const int* __restrict__ plan, int64_t b_estride) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -1524,18 +1525,18 @@ __global__ __launch_bounds__(256, 1) void bf16_gemm_kernel(
     uend = u0 + P.rows(tm);
   }
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-  floatx16 acc[4][4];
-  MainLoop<true, 0, 0, false>::run(
+  floatx16 acc[4][2];
+  MainLoop<true, 0, 0, false, 2, kStages, 0, false, false, 4>::run(
       lds, a + m0 * kStage, Kb * lda - m0 * kStage, [=](int r) { return r * kStage; }, (int)(lda * kStage),
-      b + n0 * kStage, Kb * bp - n0 * kStage, [=](int r) { return plain_col(r) * kStage; }, (int)(bp * kStage),
+      b + n0 * kStage, Kb * bp - n0 * kStage, [=](int r) { return plain_col_nb<2>(r) * kStage; }, (int)(bp * kStage),
       (int)(Kb / kStage), acc);
-  stage_bf16_half<0>(lds, acc, 1.0f);
+  stage_bf16_half8<0>(lds, acc, 1.0f);
   __syncthreads();
-  write_bf16_half(lds, 0, u0, n0, uend, N, N, nullptr, out);
+  write_bf16_half<512>(lds, 0, u0, n0, uend, N, N, nullptr, out);
   __syncthreads();
-  stage_bf16_half<1>(lds, acc, 1.0f);
+  stage_bf16_half8<1>(lds, acc, 1.0f);
   __syncthreads();
-  write_bf16_half(lds, 1, u0, n0, uend, N, N, nullptr, out);
+  write_bf16_half<512>(lds, 1, u0, n0, uend, N, N, nullptr, out);
 }
 
 // The bf16 weight gradient's reduction: out[m, n] = bf16(sum over s
@@ -2098,7 +2099,7 @@ int bf16_gemm_launch(const void* a, const void* b, int64_t T, int64_t N, int64_t
   const int tiles_n = cdiv(N, kTile);
   int rc = prep(bf16_gemm_kernel, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(bf16_gemm_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), kMainLds, st,
+  hipLaunchKernelGGL(bf16_gemm_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(512), kMainLds, st,
                      (const uint8_t*)a, (const uint8_t*)b, T, N, 2 * K, lda, (uint16_t*)out, tiles_m, tiles_n, plan,
                      plan ? 2 * K * slab_rows(N) : 0);
   return status();
