@@ -116,10 +116,14 @@ SFP8_DEV void sched_interleave_valu() {
 // transposing read as possibly aliasing any LDS DMA it knows to be in flight
 // and would wait for all of it first; the stage waits and barriers already
 // order every read after its stage's DMA.
+// TB = A blocks of 32 rows per wave: 4 (two wave rows of 128) or 2 (four
+// wave rows of 64; only the fragment, DMA and MFMA pieces, not run()).
 template <bool BF16, int FMT_A, int FMT_B, bool PAIRED, int NB = 4, int STAGES = kStages, int PRE = 0,
-          bool TR_A = false, bool TR_B = false, int WN = 2>
+          bool TR_A = false, bool TR_B = false, int WN = 2, int TB = 4>
 struct MainLoop {
-  static constexpr int kWaves = 2 * WN;
+  static_assert(TB == 4 || TB == 2, "2 or 4 A blocks per wave");
+  static constexpr int kWM = 8 / TB;                        // wave rows
+  static constexpr int kWaves = kWM * WN;
   static_assert(!(TR_A || TR_B) || (!PAIRED && NB == 4), "transposing reads: plain, 256 x 256");
   static constexpr bool kTr = TR_A || TR_B;
   using Rsrc = typename std::conditional<kTr, intx4, __amdgpu_buffer_rsrc_t>::type;
@@ -146,7 +150,7 @@ struct MainLoop {
   static constexpr int kDmaA = 16 / kWaves;                // A DMA instructions per wave per stage
   static constexpr int kDmaB = kTileN / 16 / kWaves;
   static constexpr int kDma = kDmaA + kDmaB;               // DMA instructions per wave per stage
-  using Acc = floatx16[4][NB];
+  using Acc = floatx16[TB][NB];
 
   // DMA instruction j of this wave's share of one stage: J < 4 are A blocks,
   // the rest B blocks (16 rows = 1 KiB each).
@@ -173,11 +177,11 @@ struct MainLoop {
   // Fragments of one stage: per block 32 bytes per lane (lane half g holds
   // logical chunks 2g, 2g+1 in the low / high 16 bytes).
   struct Frag {
-    intx8 a[4];
+    intx8 a[TB];
     intx8 b[NB];
   };
 
-  // Fragment I of one stage (I < 4: A block I, else B block I - 4): two
+  // Fragment I of one stage (I < TB: A block I, else B block I - TB): two
   // 16-byte LDS reads.
   // Four transposing reads of one block of a TR operand tile: block k (32
   // columns) lives in 64-column slab k / 2; off[2 q + (k & 1)] addresses
@@ -206,7 +210,7 @@ struct MainLoop {
   template <int I>
   static SFP8_DEV void read_frag(const uint8_t* lds, int buf, const uint32_t (&aoff)[8], const uint32_t (&boff)[8],
                                  Frag& f) {
-    if constexpr (I < 4) {
+    if constexpr (I < TB) {
       if constexpr (TR_A) {
         f.a[I] = read_tr_block<I>(lds + buf * kStageA, aoff);
       } else {
@@ -217,31 +221,26 @@ struct MainLoop {
       }
     } else {
       if constexpr (TR_B) {
-        f.b[I - 4] = read_tr_block<I - 4>(lds + kLdsB + buf * kStageB, boff);
+        f.b[I - TB] = read_tr_block<I - TB>(lds + kLdsB + buf * kStageB, boff);
       } else {
-        const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB, WN>::off(I - 4) * kStage;
+        const uint8_t* p = lds + buf * kStageB + BLayout<PAIRED, NB, WN>::off(I - TB) * kStage;
         const intx4 lo = *reinterpret_cast<const intx4*>(p + boff[0]);
         const intx4 hi = *reinterpret_cast<const intx4*>(p + boff[1]);
-        f.b[I - 4] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        f.b[I - TB] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     }
   }
 
+  template <int I = 0>
   static SFP8_DEV void read_frags(const uint8_t* lds, int buf, const uint32_t (&aoff)[8], const uint32_t (&boff)[8],
                                   Frag& f) {
-    read_frag<0>(lds, buf, aoff, boff, f);
-    read_frag<1>(lds, buf, aoff, boff, f);
-    read_frag<2>(lds, buf, aoff, boff, f);
-    read_frag<3>(lds, buf, aoff, boff, f);
-    read_frag<4>(lds, buf, aoff, boff, f);
-    read_frag<5>(lds, buf, aoff, boff, f);
-    if constexpr (NB == 4) {
-      read_frag<6>(lds, buf, aoff, boff, f);
-      read_frag<7>(lds, buf, aoff, boff, f);
+    if constexpr (I < TB + NB) {
+      read_frag<I>(lds, buf, aoff, boff, f);
+      read_frags<I + 1>(lds, buf, aoff, boff, f);
     }
   }
 
-  static constexpr int kMfma = (BF16 ? 8 : 4) * NB;  // MFMAs per stage
+  static constexpr int kMfma = (BF16 ? 2 : 1) * TB * NB;  // MFMAs per stage
   // MFMAs of a stage issued before its barrier: they need only registers, and
   // keep the matrix pipe busy while the waves meet.
   static constexpr int kPre = PRE;
@@ -257,7 +256,7 @@ struct MainLoop {
         acc[tb][nb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[nb], f.a[tb], acc[tb][nb], FMT_B, FMT_A,
                                                                       0, 0, 0, 0);
       } else {
-        const int h = i / (4 * NB), tb = (i / NB) % 4, nb = i % NB;
+        const int h = i / (TB * NB), tb = (i / NB) % TB, nb = i % NB;
         const bf16x8 av = __builtin_bit_cast(
             bf16x8, h ? __builtin_shufflevector(f.a[tb], f.a[tb], 4, 5, 6, 7)
                       : __builtin_shufflevector(f.a[tb], f.a[tb], 0, 1, 2, 3));
@@ -413,6 +412,7 @@ struct MainLoop {
   template <class ARow, class BRow>
   static SFP8_DEV void run(uint8_t* lds, const uint8_t* a_base, int64_t a_bytes, ARow a_rowoff, int a_sstride,
                            const uint8_t* b_base, int64_t b_bytes, BRow b_rowoff, int b_sstride, int nk, Acc& acc) {
+    static_assert(TB == 4, "run() schedules four A blocks per wave");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
     const Rsrc ra = rsrc(a_base, a_bytes);
