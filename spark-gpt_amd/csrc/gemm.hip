@@ -309,6 +309,9 @@ constexpr int kPipeHStride = 80;                    // 64 h bytes + 16 per LDS r
 constexpr int kPipeHBytes = kTile * kPipeHStride;   // one h tile
 constexpr int kPipeRing = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4>::kLds;  // 96 KiB
 constexpr int kPipeLds = kPipeRing + 2 * kPipeHBytes + 64;
+// the pipe's waves: 8 of 64 x 64 (two row blocks each)
+constexpr int kPipeTB = 2;
+constexpr int kPipeThreads = kPipeTB == 4 ? 256 : 512;
 
 // B-tile row r of the 128-row paired tile -> (half, column within 64):
 // half = r / 64 (gate, up); column = 32*wn + 16*g + v for the lane layout.
@@ -317,27 +320,39 @@ SFP8_DEV int paired_col64(int r) {
   return 32 * wn + 16 * ((w >> 2) & 1) + 4 * (w >> 3) + (w & 3);
 }
 
-// The h tile's 256 rows of 64 bytes to 256 consecutive K-slab rows.
+// The h tile's 256 rows of 64 bytes to 256 consecutive K-slab rows (NT
+// threads, 16 bytes each per pass).
+template <int NT>
 SFP8_DEV void pipe_h8_rows(const uint8_t* hbuf, uint8_t* dst) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int idx = 256 * k + (int)threadIdx.x, r = idx >> 2, ch = idx & 3;
+  for (int k = 0; k < 1024 / NT; ++k) {
+    const int idx = NT * k + (int)threadIdx.x, r = idx >> 2, ch = idx & 3;
     *reinterpret_cast<intx4*>(dst + r * 64 + 16 * ch) =
         *reinterpret_cast<const intx4*>(hbuf + r * kPipeHStride + 16 * ch);
   }
 }
 
-template <int NK>
+// TB = row blocks of 32 per wave: 4 (4 waves of 128 x 64) or 2 (8 waves of
+// 64 x 64, two per SIMD: each wave's waits are covered by the other's
+// MFMAs).
+template <int NK, int TB>
 struct SwigluPipe {
-  using ML = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4>;
-  static constexpr int kUnits = 16;  // 4 pairs each: unit u = row block u/4, pairs 4*(u%4) ..
-  static constexpr int kSt = 4;      // LDS ring stages
+  using ML = MainLoop<false, kFmtE4M3, kFmtE4M3, true, 2, 4, 0, false, false, 2, TB>;
+  static constexpr int kWaves = ML::kWaves, kWM = ML::kWM;
+  static constexpr int kUnits = 4 * TB;  // 4 pairs each: unit u = row block u/4, pairs 4*(u%4) ..
+  static constexpr int kSt = 4;          // LDS ring stages
   static constexpr int kDma = ML::kDma;
-  static constexpr int kPre = 2;     // MFMAs of a stage issued before its wait
+  static constexpr int kPre = TB == 4 ? 2 : 1;  // MFMAs of a stage issued before its wait
+  static constexpr int kSpan = NK / kUnits;     // stages per unit
+  static constexpr int kSlots = ML::kMfma - kPre;  // MFMAs past the barrier, one slot each
+  static constexpr int kDmaSlots = TB == 4 ? 2 : kSlots;  // slots carrying the DMA
   static_assert(NK >= kSt && NK % kSt == 0, "whole rings of K stages: a tile's stage s sits in slot s % kSt");
+  static_assert(NK % kUnits == 0 && kSpan * kSlots == 6, "each unit's six pieces fill the slots of its stages");
 
-  // units run in stage kt: [ubeg(kt), ubeg(kt+1))
-  static constexpr int ubeg(int kt) { return (kt * kUnits + NK - 1) / NK; }
+  // A unit's working values between its pieces.
+  struct UnitTmp {
+    float gb[4], ub[4], hb[4], ex[4], sg[4];
+  };
 
   struct Ctx {
     // main loop; the last kSt - 1 stages of a tile load the first stages of
@@ -349,10 +364,11 @@ struct SwigluPipe {
     bool has_next;
     int wave;
     typename ML::Frag f[2];
-    floatx16 acc[4][2];
+    floatx16 acc[TB][2];
     // previous tile's epilogue
-    uint32_t E[4][16];
+    uint32_t E[TB][16];
     uint32_t gw[4], uw[4], hw[4];
+    UnitTmp ut;  // the current unit's working values (its pieces may span two stages)
     bool bad;  // a unit of the current row block saw NaN or out-of-range data
     float m_gu, m_h;
     bool prev;            // a previous tile exists
@@ -370,11 +386,11 @@ struct SwigluPipe {
   // One unit: 4 pairs of row block TB, packed into byte Q of gw/uw/hw.
   template <int U>
   static SFP8_DEV void unit_compute(Ctx& c) {
-    constexpr int TB = U / 4, Q = U % 4;
+    constexpr int RB = U / 4, Q = U % 4;
     float gb[4], ub[4], hb[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t p = c.E[TB][4 * Q + e];
+      const uint32_t p = c.E[RB][4 * Q + e];
       gb[e] = __uint_as_float(p << 16);
       ub[e] = __uint_as_float(p & 0xffff0000u);
       const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c.c_exp));
@@ -398,11 +414,6 @@ struct SwigluPipe {
     c.hw[Q] = pack4_e4m3_scaled_noclamp(hb[0], hb[1], hb[2], hb[3], c.inv2, c.hw[Q]);
   }
 
-  // A unit's working values between its pieces.
-  struct UnitTmp {
-    float gb[4], ub[4], hb[4], ex[4], sg[4];
-  };
-
   // Piece P of unit U: the arithmetic of unit_compute<U>, the same
   // operations in the same order per value, cut into six parts that go one
   // after each of the stage's MFMAs past the barrier and software-pipelined
@@ -413,9 +424,9 @@ struct SwigluPipe {
   // than the first one's 64 cycles holds back the second.  Each part reads
   // its inputs and publishes its results through empty asm statements, so
   // the compiler keeps it in its slot.
-  template <int TB, int Q, int E>
+  template <int RB, int Q, int E>
   static SFP8_DEV void unit_unpack(Ctx& c, UnitTmp& t) {
-    uint32_t p = c.E[TB][4 * Q + E];
+    uint32_t p = c.E[RB][4 * Q + E];
     asm volatile("" : "+v"(p));
     t.gb[E] = __uint_as_float(p << 16);
     t.ub[E] = __uint_as_float(p & 0xffff0000u);
@@ -423,18 +434,18 @@ struct SwigluPipe {
   }
   template <int U, int P>
   static SFP8_DEV void unit_piece(Ctx& c, UnitTmp& t) {
-    constexpr int TB = U / 4, Q = U % 4;
+    constexpr int RB = U / 4, Q = U % 4;
     if constexpr (P == 0) {
-      unit_unpack<TB, Q, 0>(c, t);
-      unit_unpack<TB, Q, 1>(c, t);
+      unit_unpack<RB, Q, 0>(c, t);
+      unit_unpack<RB, Q, 1>(c, t);
       asm volatile("" ::"v"(t.ex[0]), "v"(t.ex[1]));
     } else if constexpr (P == 1) {
       t.sg[0] = __builtin_amdgcn_rcpf(1.0f + t.ex[0]);
       t.sg[1] = __builtin_amdgcn_rcpf(1.0f + t.ex[1]);
-      unit_unpack<TB, Q, 2>(c, t);
+      unit_unpack<RB, Q, 2>(c, t);
       asm volatile("" ::"v"(t.sg[0]), "v"(t.sg[1]), "v"(t.ex[2]));
     } else if constexpr (P == 2) {
-      unit_unpack<TB, Q, 3>(c, t);
+      unit_unpack<RB, Q, 3>(c, t);
       t.sg[2] = __builtin_amdgcn_rcpf(1.0f + t.ex[2]);
       t.hb[0] = t.gb[0] * t.sg[0] * t.ub[0];
       t.hb[1] = t.gb[1] * t.sg[1] * t.ub[1];
@@ -471,9 +482,9 @@ struct SwigluPipe {
   // After the last unit of row block TB: the exact conversions when a unit
   // of the block saw NaN or out-of-range data (wave-uniform, rare), the
   // three 16-byte global stores and the h bytes into the LDS tile.
-  template <int TB>
+  template <int RB>
   static SFP8_DEV void block_store(Ctx& c) {
-    const int lane = threadIdx.x & 63, wm = c.wave & 1, wn = c.wave >> 1;
+    const int lane = threadIdx.x & 63, wm = c.wave % kWM, wn = c.wave / kWM;
     const int fr = lane & 31, g = lane >> 5;
     if (__builtin_amdgcn_ballot_w64(c.bad)) {
       asm volatile("" ::: "memory");
@@ -482,7 +493,7 @@ struct SwigluPipe {
         float gb[4], ub[4], hb[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t p = c.E[TB][4 * q + e];
+          const uint32_t p = c.E[RB][4 * q + e];
           gb[e] = __uint_as_float(p << 16);
           ub[e] = __uint_as_float(p & 0xffff0000u);
           const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gb[e] * c.c_exp));
@@ -497,7 +508,7 @@ struct SwigluPipe {
       }
     }
     c.bad = false;
-    const int row = 128 * wm + 32 * TB + fr;
+    const int row = 32 * TB * wm + 32 * RB + fr;
     const int col = 32 * wn + 16 * g;
     const int64_t t = c.pm0 + row;
     if (c.prev) {
@@ -525,14 +536,17 @@ struct SwigluPipe {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kDma * (kSt - 3)) : "memory");
     __builtin_amdgcn_sched_barrier(0);
-    UnitTmp t;
-    slot<KT, 0>(c, t, a_ss, b_ss);
-    slot<KT, 1>(c, t, a_ss, b_ss);
-    slot<KT, 2>(c, t, a_ss, b_ss);
-    slot<KT, 3>(c, t, a_ss, b_ss);
-    slot<KT, 4>(c, t, a_ss, b_ss);
-    slot<KT, 5>(c, t, a_ss, b_ss);
-    stores<ubeg(KT), ubeg(KT + 1)>(c);
+    slots<KT, 0>(c, c.ut, a_ss, b_ss);
+    // the stage that finishes a unit that finishes a row block stores it
+    constexpr int U = KT / kSpan;
+    if constexpr (KT % kSpan == kSpan - 1 && U % 4 == 3) block_store<U / 4>(c);
+  }
+  template <int KT, int J>
+  static SFP8_DEV void slots(Ctx& c, UnitTmp& t, int a_ss, int b_ss) {
+    if constexpr (J < kSlots) {
+      slot<KT, J>(c, t, a_ss, b_ss);
+      slots<KT, J + 1>(c, t, a_ss, b_ss);
+    }
   }
 
   // Slot J of stage KT: one MFMA past the barrier, then (J < 2) half of the
@@ -544,10 +558,10 @@ struct SwigluPipe {
   static SFP8_DEV void slot(Ctx& c, UnitTmp& t, int a_ss, int b_ss) {
     constexpr int cur = KT & 1, nxt = cur ^ 1;
     ML::template mfma_range<kPre + J, kPre + J + 1>(c.f[cur], c.acc);
-    if constexpr (J < 2) {
+    if constexpr (J < kDmaSlots) {
       constexpr int slot_ = (KT + kSt - 1) % kSt;
 #pragma unroll
-      for (int j = J * kDma / 2; j < (J + 1) * kDma / 2; ++j) {
+      for (int j = J * kDma / kDmaSlots; j < (J + 1) * kDma / kDmaSlots; ++j) {
         if constexpr (KT + kSt - 1 < NK) {
           constexpr int ld = KT + kSt - 1;
           ML::load_one(j, c.lds, slot_, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
@@ -557,18 +571,20 @@ struct SwigluPipe {
         }
       }
     }
-    ML::template read_frag<J < 2 ? 4 + J : J - 2>(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
-    unit_piece<KT, J>(c, t);
+    if constexpr (TB == 4) {
+      ML::template read_frag<J < 2 ? 4 + J : J - 2>(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
+    } else if constexpr (J == 0) {
+      // a[0] and b[0] first (the next stage's MFMA ahead of its wait), then
+      // b[1], then a[1]
+      ML::template read_frag<0>(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
+      ML::template read_frag<2>(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
+    } else {
+      ML::template read_frag<J == 1 ? 3 : 1>(c.lds, (KT + 1) % kSt, c.aoff, c.boff, c.f[nxt]);
+    }
+    unit_piece<KT / kSpan, (KT % kSpan) * kSlots + J>(c, t);
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  template <int U0, int U1>
-  static SFP8_DEV void stores(Ctx& c) {
-    if constexpr (U0 < U1) {
-      if constexpr (U0 % 4 == 3) block_store<U0 / 4>(c);
-      stores<U0 + 1, U1>(c);
-    }
-  }
   template <int KT>
   static SFP8_DEV void stages(Ctx& c, int a_ss, int b_ss) {
     if constexpr (KT < NK) {
@@ -603,13 +619,13 @@ struct SwigluPipe {
   }
 };
 
-template <int NK>
-__global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
+template <int NK, int TB>
+__global__ __launch_bounds__(TB == 4 ? 256 : 512, 1) void swiglu_pipe_kernel(
     const uint8_t* __restrict__ x8, const uint8_t* __restrict__ w8, int64_t T, int64_t D, int64_t I,
     const float* __restrict__ scale, const float* __restrict__ wscale, float* __restrict__ amax,
     uint8_t* __restrict__ gu8, uint8_t* __restrict__ h8, uint8_t* __restrict__ h8t, int64_t ldt, int tiles_m,
     int tiles_n, const int* __restrict__ plan, int64_t w_estride) {
-  using P = SwigluPipe<NK>;
+  using P = SwigluPipe<NK, TB>;
   using ML = typename P::ML;
   extern __shared__ __align__(16) uint8_t lds[];
   typename P::Ctx c;
@@ -642,23 +658,24 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   // the first tile's K loop runs the epilogue units with no previous tile:
   // on zeros they add nothing to the amax slots (and store nothing)
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
+  for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) c.E[tb][v] = 0u;
-  const int lane = threadIdx.x & 63, wm = c.wave & 1, wn = c.wave >> 1;
+  const int lane = threadIdx.x & 63, wm = c.wave % P::kWM, wn = c.wave / P::kWM;
   const int fr = lane & 31, g = lane >> 5;
   const uint32_t chunk = (uint32_t)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
   const int sw = (fr >> 2) & 3;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    c.aoff[h] = (uint32_t)((128 * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
+    c.aoff[h] = (uint32_t)((32 * TB * wm + fr) * kStage + (((2 * g + h) ^ sw) << 4));
     c.boff[h] = (uint32_t)(ML::kLdsB + (BLayout<true, 2>::kWaveStride * wn + fr) * kStage + (((2 * g + h) ^ sw) << 4));
   }
   const int64_t rpad = slab_rows(I);
   const int ntiles = tiles_m * tiles_n;
   const int a_ss = (int)(ldt * kStage), b_ss = (int)(2 * I * kStage);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) c.voff_a[j] = (uint32_t)((64 * c.wave + 16 * j + (lane >> 2)) * kStage) + chunk;
+  for (int j = 0; j < ML::kDmaA; ++j)
+    c.voff_a[j] = (uint32_t)(((kTile / P::kWaves) * c.wave + 16 * j + (lane >> 2)) * kStage) + chunk;
   // K-slab operands: x8 [D/64][ldt][64], w8 [D/64][2I][64] (with a plan:
   // tile row tm's expert e at w8 + e * w_estride, its scale wscale[e]); tile
   // origin (m0, n0) -> A and B descriptors, B lane offsets, weight scale
@@ -673,8 +690,8 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     rb = make_rsrc(w8 + e * w_estride, D * 2 * I);
     q = wscale[e];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int r = 32 * c.wave + 16 * j + (lane >> 2);
+    for (int j = 0; j < ML::kDmaB; ++j) {
+      const int r = (128 / P::kWaves) * c.wave + 16 * j + (lane >> 2);
       voff_b[j] = (uint32_t)(((r >> 6) * (int)I + (int)n0 + paired_col64(r)) * kStage) + chunk;
     }
   };
@@ -703,7 +720,7 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
       c.nvoff_b[1] = c.voff_b[1];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TB; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) c.acc[i][j] = floatx16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                                           0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -715,12 +732,12 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
     // token rows of 64 bytes, one contiguous block; the optional h8t
     // transposed)
     if (c.prev) {
-      pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
-      if (h8t) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
+      pipe_h8_rows<64 * P::kWaves>(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
+      if (h8t) lds_tile_store_slab_tr<4, P::kWaves>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
     }
     // this tile's g, u (bf16, unscaled) become the next epilogue's input
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) c.E[tb][v] = pack2_bf16(c.acc[tb][0][v], c.acc[tb][1][v]);
     c.prev = true;
@@ -743,20 +760,26 @@ __global__ __launch_bounds__(256, 1) void swiglu_pipe_kernel(
   if (c.prev) {
     P::template tail_units<0>(c);
     __syncthreads();
-    pipe_h8_rows(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
-    if (h8t) lds_tile_store_slab_tr<4>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
+    pipe_h8_rows<64 * P::kWaves>(c.hbuf, h8 + (c.pn0 >> 6) * ldt * 64 + c.pm0 * 64);
+    if (h8t) lds_tile_store_slab_tr<4, P::kWaves>(c.hbuf, kPipeHStride, h8t, rpad, c.pm0, c.pn0);
   }
   P::next_scales(c, 1.f);  // folds the last epilogue's maxima
   float* red = reinterpret_cast<float*>(lds + kPipeRing + 2 * kPipeHBytes);
   float mg = wave_max(c.mx_gu), mh = wave_max(c.mx_h);
   if (lane == 0) {
     red[c.wave] = mg;
-    red[4 + c.wave] = mh;
+    red[P::kWaves + c.wave] = mh;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    atomic_max_nonneg(amax + 1, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-    atomic_max_nonneg(amax + 2, fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7])));
+    float a1 = red[0], a2 = red[P::kWaves];
+#pragma unroll
+    for (int w = 1; w < P::kWaves; ++w) {
+      a1 = fmaxf(a1, red[w]);
+      a2 = fmaxf(a2, red[P::kWaves + w]);
+    }
+    atomic_max_nonneg(amax + 1, a1);
+    atomic_max_nonneg(amax + 2, a2);
   }
 }
 
@@ -1727,9 +1750,9 @@ int sfp8_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t T, int64
     int n_cu = 0;
     int rc = cu_count(&n_cu);
     if (rc) return rc;
-    rc = prep(swiglu_pipe_kernel<16>, kPipeLds);
+    rc = prep(swiglu_pipe_kernel<16, kPipeTB>, kPipeLds);
     if (rc) return rc;
-    hipLaunchKernelGGL(swiglu_pipe_kernel<16>, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kPipeLds,
+    hipLaunchKernelGGL((swiglu_pipe_kernel<16, kPipeTB>), dim3(ntiles < n_cu ? ntiles : n_cu), dim3(kPipeThreads), kPipeLds,
                        (hipStream_t)stream, (const uint8_t*)x8, (const uint8_t*)w8, T, D, I, scale, wscale, amax,
                        (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, ldt, tiles_m, tiles_n, (const int*)nullptr,
                        (int64_t)0);
@@ -1916,9 +1939,9 @@ int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, i
     int n_cu = 0;
     int rc = cu_count(&n_cu);
     if (rc) return rc;
-    rc = prep(swiglu_pipe_kernel<16>, kPipeLds);
+    rc = prep(swiglu_pipe_kernel<16, kPipeTB>, kPipeLds);
     if (rc) return rc;
-    hipLaunchKernelGGL(swiglu_pipe_kernel<16>, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(256), kPipeLds,
+    hipLaunchKernelGGL((swiglu_pipe_kernel<16, kPipeTB>), dim3(ntiles < n_cu ? ntiles : n_cu), dim3(kPipeThreads), kPipeLds,
                        (hipStream_t)stream, (const uint8_t*)x8, (const uint8_t*)w8, ldp, D, I, scale, q_gu, amax,
                        (uint8_t*)gu8, (uint8_t*)h8, (uint8_t*)h8t, ldp, tiles_m, tiles_n, plan,
                        D * slab_rows(2 * I));

@@ -309,7 +309,7 @@ struct MainLoop {
   // fragment and one DMA over 16 MFMAs of 32 cycles, NB = 2 issues the
   // fragments over 3 MFMAs and then the DMA over 3.
   static constexpr int kSchedPre = 2;
-  static_assert(kMfma >= kSchedPre + (4 + NB) / 2 + (4 + NB) / 2, "stage too short for the schedule");
+  static_assert(TB != 4 || kMfma >= kSchedPre + (4 + NB) / 2 + (4 + NB) / 2, "stage too short for the schedule");
   static SFP8_DEV void stage(uint8_t* lds, const Frag& cur, Frag& nxt, Acc& acc, int dma_buf, int ld, int rd_buf,
                              Rsrc ra, Rsrc rb, const uint32_t (&voff_a)[4],
                              const uint32_t (&voff_b)[NB], int a_sstride, int b_sstride, const uint32_t (&aoff)[8],
