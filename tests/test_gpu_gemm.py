@@ -208,6 +208,14 @@ def test_down_dgrad_swiglu_every_gate_code(dev, T, D, I):
     assert int(d.max()) <= 1 and float((d > 0).float().mean()) < 1e-3
     dt = u8(sg.ops.unslab(dgu8t, 2 * I))
     assert torch.equal(dt[:, :T], got.t())
+    # without the token-contiguous copy (at D = 1024 the persistent 256 x 128
+    # kernel with the deferred epilogue): the same bytes, NaN codes and
+    # exact-path blocks included, and the same amax
+    amax2 = torch.zeros(5, device=dev)
+    dgu8b, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), slab(gu8, dev), s.to(dev), amax2,
+                                        copy=False)
+    assert torch.equal(u8(dgu8b), u8(dgu8s))
+    assert torch.equal(amax2, amax)
 
 
 @pytest.mark.parametrize("T,D,I", SHAPES[:3] + SHAPES_DGRAD_PIPE[2:])
@@ -232,6 +240,11 @@ def test_down_dgrad_swiglu_random(dev, T, D, I):
     assert float(unpinned.float().mean()) < 1e-3
     assert int(d[~unpinned].max()) <= 1 and float((d > 0).float().mean()) < 0.02
     torch.testing.assert_close(amax[3].cpu(), ra3, rtol=1e-2, atol=0)
+    amax2 = torch.zeros(5, device=dev)
+    dgu8b, _ = sg.ops.down_dgrad_swiglu(dy.to(dev), slab(wd.t(), dev), slab(gu8, dev), s.to(dev), amax2,
+                                        copy=False)
+    assert torch.equal(u8(dgu8b), u8(dgu8s))
+    assert torch.equal(amax2, amax)
 
 
 @pytest.mark.parametrize("T,D,I", SHAPES)
