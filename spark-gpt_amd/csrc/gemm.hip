@@ -1206,6 +1206,9 @@ __global__ __launch_bounds__(512, 1) void gateup_dgrad_kernel(
 // reads (MainLoop TR_A / TR_B); the partials then always go to `out` as the
 // workspace, in the same order (with TRB the columns unpermuted:
 // splitk_reduce_kernel<true>).
+// NW = 4 waves (one per SIMD) of 128 x 128, or 8 (two per SIMD) of 128 x 64,
+// so that one wave's stage waits and barriers are covered by the other's
+// MFMAs; the accumulator order follows the wave shape (acc_order_rc).
 // Addressing of a transposed-read operand: row r of block r / 64 (fp8) or
 // r / 32 (bf16) at token t lies at base + block * bs + t * ts, and ext bytes
 // are readable from base (the rest reads as zero).  A row K-slab of [T, L]
@@ -1215,11 +1218,17 @@ struct TrOp {
   int64_t ts, bs, ext;
 };
 
-template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false>
-__global__ __launch_bounds__(256, 1) void wgrad_kernel(
+// Waves per work-group of the weight gradients (FP8 and bf16).
+constexpr int kWgradWaves = 8;
+constexpr int kBf16WgradWaves = 8;
+
+template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 1) void wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldt,
     int64_t kchunk, const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out,
     int tiles_m, int tiles_n, int splits, int partials, TrOp tra, TrOp trb) {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  constexpr int NB = NW == 8 ? 2 : 4, WN = NW / 2;  // B blocks of 32 per wave, wave columns
   extern __shared__ __align__(16) uint8_t lds[];
   int tm, tn, sp;
   split_tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, splits, tm, tn, sp);
@@ -1227,7 +1236,7 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  floatx16 acc[4][4];
+  floatx16 acc[4][NB];
   const int64_t kb = (int64_t)sp * kchunk;
   {
     // K-slab operands: slab (kb / 64) of A starts at (kb / 64) * rpa * 64.
@@ -1241,36 +1250,36 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
     const uint8_t* b0 = TRB ? bt + (n0 / kRows) * trb.bs + t0 * trb.ts : bt + (kb / kStage) * rpb * kStage + n0 * kStage;
     const uint8_t* a_end = TRA ? at + tra.ext : at + ldt * rpa;
     const uint8_t* b_end = TRB ? bt + trb.ext : bt + ldt * rpb;
-    MainLoop<BF16, FMT_A, FMT_B, false, 4, kStages, 0, TRA, TRB>::run(
+    MainLoop<BF16, FMT_A, FMT_B, false, NB, kStages, 0, TRA, TRB, WN>::run(
         lds, a0, a_end - a0, [=](int r) { return TRA ? (r / kRows) * abs_ + (r % kRows) * ats : r * kStage; },
         TRA ? kRows * ats : (int)(rpa * kStage), b0, b_end - b0,
-        [=](int r) { return TRB ? (r / kRows) * bbs + (r % kRows) * bts : plain_col(r) * kStage; },
+        [=](int r) { return TRB ? (r / kRows) * bbs + (r % kRows) * bts : plain_col_nb<NB>(r) * kStage; },
         TRB ? kRows * bts : (int)(rpb * kStage), (int)((kchunk < ldt - kb ? kchunk : ldt - kb) / kStage), acc);
   }
   if (BF16 || TRA || TRB || partials) {
     // accumulator order: [split][tile][wave][tb][nb][i][lane][4]
     float* frag = out + ((int64_t)sp * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
-                  wave * (kTile * kTile / 4);
+                  wave * (kTile * kTile / NW);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          reinterpret_cast<floatx4*>(frag + (tb * 4 + nb) * 1024 + i * 256)[lane] =
+          reinterpret_cast<floatx4*>(frag + (tb * NB + nb) * 1024 + i * 256)[lane] =
               floatx4{acc[tb][nb][4 * i], acc[tb][nb][4 * i + 1], acc[tb][nb][4 * i + 2], acc[tb][nb][4 * i + 3]};
     return;
   }
   const float deq = 1.0f / (sa[0] * sb[0]);
   float* dst = out;
   const int fr = lane & 31, g = lane >> 5;
-  const int cb = 128 * wn + 64 * g;
+  const int cb = 32 * NB * wn + 16 * NB * g;  // plain_col_nb<NB>
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int64_t m = m0 + 128 * wm + 32 * tb + fr;
     if (m >= M) continue;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       const int64_t n = n0 + cb + 16 * nb;
       floatx4* p = reinterpret_cast<floatx4*>(dst + m * N + n);
       // N % 4 == 0: each float4 is wholly inside the row or wholly past it
@@ -1297,11 +1306,13 @@ __global__ __launch_bounds__(256, 1) void wgrad_kernel(
 // ws[e][sp][tile], summed in split order by splitk_reduce_kernel.
 // BF16: bf16 operands, 2 bytes per padded row (`ldp` counts K bytes), and the
 // partials always go to ws, for bf16_wgrad_reduce_kernel to round.
-template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false>
-__global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
+template <bool BF16, int FMT_A, int FMT_B, bool TRA = false, bool TRB = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 1) void moe_wgrad_kernel(
     const uint8_t* __restrict__ at, const uint8_t* __restrict__ bt, int64_t M, int64_t N, int64_t ldp,
     const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ out, float* __restrict__ ws,
     const int* __restrict__ plan, int tiles_m, int tiles_n, int splits) {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves (as wgrad_kernel)");
+  constexpr int NB = NW == 8 ? 2 : 4, WN = NW / 2;
   extern __shared__ __align__(16) uint8_t lds[];
   const MoePlan P{plan};
   const int tiles = tiles_m * tiles_n;
@@ -1332,36 +1343,36 @@ __global__ __launch_bounds__(256, 1) void moe_wgrad_kernel(
   const uint8_t* a_end = TRA ? at + (M / kRows) * ldt_tok * kStage : at + ldp * rpa;
   const uint8_t* b_end = TRB ? bt + (N / kRows) * ldt_tok * kStage : bt + ldp * rpb;
   const int64_t a_bytes = nk > 0 ? a_end - a0 : 0, b_bytes = nk > 0 ? b_end - b0 : 0;
-  floatx16 acc[4][4];
-  MainLoop<BF16, FMT_A, FMT_B, false, 4, kStages, 0, TRA, TRB>::run(
+  floatx16 acc[4][NB];
+  MainLoop<BF16, FMT_A, FMT_B, false, NB, kStages, 0, TRA, TRB, WN>::run(
       lds, a0, a_bytes, [=](int r) { return TRA ? ((r / kRows) * ltok + (r % kRows)) * kStage : r * kStage; },
       TRA ? kRows * kStage : (int)(rpa * kStage), b0, b_bytes,
-      [=](int r) { return TRB ? ((r / kRows) * ltok + (r % kRows)) * kStage : plain_col(r) * kStage; },
+      [=](int r) { return TRB ? ((r / kRows) * ltok + (r % kRows)) * kStage : plain_col_nb<NB>(r) * kStage; },
       TRB ? kRows * kStage : (int)(rpb * kStage), (int)nk, acc);
   if (BF16 || TRA || TRB || splits > 1) {
     // accumulator order: [expert][split][tile][wave][tb][nb][i][lane][4]
     float* frag = ws + (((int64_t)e * splits + sp) * tiles_m * tiles_n + (int64_t)tm * tiles_n + tn) * (kTile * kTile) +
-                  wave * (kTile * kTile / 4);
+                  wave * (kTile * kTile / NW);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          reinterpret_cast<floatx4*>(frag + (tb * 4 + nb) * 1024 + i * 256)[lane] =
+          reinterpret_cast<floatx4*>(frag + (tb * NB + nb) * 1024 + i * 256)[lane] =
               floatx4{acc[tb][nb][4 * i], acc[tb][nb][4 * i + 1], acc[tb][nb][4 * i + 2], acc[tb][nb][4 * i + 3]};
     return;
   }
   const float deq = 1.0f / (sa[0] * sb[0]);
   float* dst = out + (int64_t)e * M * N;
   const int fr = lane & 31, g = lane >> 5;
-  const int cb = 128 * wn + 64 * g;
+  const int cb = 32 * NB * wn + 16 * NB * g;  // plain_col_nb<NB>
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int64_t m = m0 + 128 * wm + 32 * tb + fr;
     if (m >= M) continue;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       const int64_t n = n0 + cb + 16 * nb;
       floatx4* p = reinterpret_cast<floatx4*>(dst + m * N + n);
 #pragma unroll
@@ -1379,14 +1390,28 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(float* __restrict__ out,
   if (i < n) *reinterpret_cast<floatx4*>(out + i) = floatx4{0.f, 0.f, 0.f, 0.f};
 }
 
+// Tile row r and column c of the first value of float4 q (< 16384) of one
+// 256 x 256 partial tile of wgrad_kernel<.., NW> in accumulator order
+// [wave][tb][nb][i][lane][4] (NB = 4 or 2 blocks of 32 columns per wave;
+// wave (wm, wn) = (wave & 1, wave >> 1) owns rows 128 wm.. and columns
+// 32 NB wn..): B-tile rows permuted by plain_col_nb<NB> (accumulator v of
+// block nb, lane half g is column 32 NB wn + 16 NB g + 16 nb + v), or with
+// TR_B unpermuted (column 32 NB wn + 32 nb + 8 (v / 4) + 4 g + v % 4).
+template <int NW, bool TR_B>
+SFP8_DEV void acc_order_rc(int q, int& r, int& c) {
+  constexpr int NB = NW == 8 ? 2 : 4, NBB = NW == 8 ? 1 : 2;
+  const int lane = q & 63, i = (q >> 6) & 3, nb = (q >> 8) & (NB - 1), tb = (q >> (8 + NBB)) & 3;
+  const int wave = (q >> (10 + NBB)) & (NW - 1), g = lane >> 5;
+  r = 128 * (wave & 1) + 32 * tb + (lane & 31);
+  c = 32 * NB * (wave >> 1) + (TR_B ? 32 * nb + 8 * i + 4 * g : 16 * NB * g + 16 * nb + 4 * i);
+}
+
 // Split-K reduction of the accumulator-order partials of wgrad_kernel:
 // out[m, n] = (sum over s ascending of ws[s]) / (sa * sb).  Thread q owns the
 // q-th float4 of one split's partials; its (m, n) follows from the MFMA
-// accumulator layout (B-tile rows permuted by plain_col: accumulator v of
-// block nb, lane half g is column 128*wn + 64*g + 16*nb + v).
-// TR_B: partials of wgrad_kernel<.., true> (B tile unpermuted: accumulator
-// v of block nb, lane half g is column 128*wn + 32*nb + 8*(v/4) + 4*g + v%4).
-template <bool TR_B = false>
+// accumulator layout (acc_order_rc; TR_B: partials of wgrad_kernel<..,
+// true>).
+template <bool TR_B = false, int NW = 4>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits,
                                                             int64_t n4, int tiles_n, int64_t M, int64_t N,
                                                             const float* __restrict__ sa,
@@ -1399,13 +1424,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
   floatx4 acc = w4[q];
   for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
-  const int lane = (int)(q & 63), i = (int)(q >> 6) & 3, nb = (int)(q >> 8) & 3, tb = (int)(q >> 10) & 3;
-  const int wave = (int)(q >> 12) & 3;
+  int r, c;
+  acc_order_rc<NW, TR_B>((int)(q & 16383), r, c);
   const int64_t tile = q >> 14;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
-  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
-  const int64_t n = tn * kTile + 128 * (wave >> 1) +
-                    (TR_B ? 32 * nb + 8 * i + 4 * (lane >> 5) : 64 * (lane >> 5) + 16 * nb + 4 * i);
+  const int64_t m = tm * kTile + r, n = tn * kTile + c;
   if (m < M && n < N) {
     const float deq = 1.0f / (sa[0] * sb[0]);
     *reinterpret_cast<floatx4*>(out + m * N + n) = acc * deq;
@@ -1566,7 +1589,7 @@ __global__ __launch_bounds__(512, 1) void bf16_gemm_kernel(
 // ascending of ws[s]) (the bf16 result of _swiglu_wgrad_kernel,
 // train.py:1983-2026), partials in wgrad_kernel's accumulator order;
 // blockIdx.y = expert of a grouped gradient (out [E, M, N]).
-template <bool TR_B = false>
+template <bool TR_B = false, int NW = 4>
 __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __restrict__ ws, int splits, int64_t n4,
                                                                 int tiles_n, int64_t M, int64_t N,
                                                                 uint16_t* __restrict__ out) {
@@ -1577,13 +1600,11 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
   floatx4 acc = w4[q];
   for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
-  const int lane = (int)(q & 63), i = (int)(q >> 6) & 3, nb = (int)(q >> 8) & 3, tb = (int)(q >> 10) & 3;
-  const int wave = (int)(q >> 12) & 3;
+  int r, c;
+  acc_order_rc<NW, TR_B>((int)(q & 16383), r, c);
   const int64_t tile = q >> 14;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
-  const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + (lane & 31);
-  const int64_t n = tn * kTile + 128 * (wave >> 1) +
-                    (TR_B ? 32 * nb + 8 * i + 4 * (lane >> 5) : 64 * (lane >> 5) + 16 * nb + 4 * i);
+  const int64_t m = tm * kTile + r, n = tn * kTile + c;
   if (m < M && n < N)  // N % 4 == 0: the 4 values are wholly inside or past the row
     *reinterpret_cast<intx2*>(out + m * N + n) = intx2{(int)pack2_bf16(acc[0], acc[1]), (int)pack2_bf16(acc[2], acc[3])};
 }
@@ -1595,8 +1616,8 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
 // the Newton-Schulz staging matrix ([M, N] bf16, the parameter's layout);
 // grad[m, n] = d when grad is given.  splits == 0: d = 0 (no tokens).  TR_B:
 // the partials' columns are in the transposed-read B order, as for
-// splitk_reduce_kernel<true>.
-template <bool TR_B = false>
+// splitk_reduce_kernel<true>; NW: the partials of wgrad_kernel<.., NW>.
+template <bool TR_B = false, int NW = 4>
 __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __restrict__ ws, int splits, int64_t n4,
                                                               int tiles_n, int64_t M, int64_t N,
                                                               const float* __restrict__ sa,
@@ -1612,9 +1633,10 @@ __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __res
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  constexpr int NB = NW == 8 ? 2 : 4, NBB = NW == 8 ? 1 : 2;
   const int lane = threadIdx.x & 63, i = threadIdx.x >> 6;
   const int64_t b = blockIdx.x;
-  const int nb = (int)(b & 3), tb = (int)(b >> 2) & 3, wave = (int)(b >> 4) & 3;
+  const int nb = (int)(b & (NB - 1)), tb = (int)(b >> NBB) & 3, wave = (int)(b >> (NBB + 2)) & (NW - 1);
   const int64_t tile = b >> 6;
   const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
   // local column (0..31) of this thread's float4 in the block
@@ -1624,8 +1646,9 @@ __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __res
   const int r = threadIdx.x >> 3, c2 = 4 * (threadIdx.x & 7);
   const int64_t m = tm * kTile + 128 * (wave & 1) + 32 * tb + r;
   // local column -> output column: TR_B blocks are 32 contiguous columns,
-  // the plain layout's two 16-column halves lie 64 columns apart
-  const int64_t n = tn * kTile + 128 * (wave >> 1) + (TR_B ? 32 * nb + c2 : 16 * nb + (c2 < 16 ? c2 : 48 + c2));
+  // the plain layout's two 16-column halves lie 16 NB columns apart
+  const int64_t n =
+      tn * kTile + 32 * NB * (wave >> 1) + (TR_B ? 32 * nb + c2 : 16 * nb + (c2 < 16 ? c2 : 16 * NB - 16 + c2));
   if (m >= M || n >= N) return;
   const floatx4 d = blk[r][c2 >> 2];
   if (grad) *reinterpret_cast<floatx4*>(grad + m * N + n) = d;
@@ -1702,19 +1725,20 @@ inline int64_t wgrad_chunk(int64_t ldt, int64_t s) {
 }  // namespace
 
 namespace {
-// The split partials ws[split][tile] (one 256 x 256 fp32 tile each, in MFMA
-// fragment order) of the FP8 weight gradient; TRA / TRB: that operand is the
-// row K-slab of the token-major activation instead of a token-contiguous copy.
+// The split partials ws[split][tile] (one 256 x 256 fp32 tile each, in
+// accumulator order of wgrad_kernel<.., kWgradWaves>) of the FP8 weight
+// gradient; TRA / TRB: that operand is the row K-slab of the token-major
+// activation instead of a token-contiguous copy.
 template <bool TRA, bool TRB>
 int wgrad_partials(const void* a, const void* b, int64_t M, int64_t N, int64_t ldt, const float* sa, const float* sb,
                    float* ws, int splits, hipStream_t st) {
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  const int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>, kMainLds);
+  const int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB, kWgradWaves>, kMainLds);
   if (rc) return rc;
   // row K-slabs over ldt tokens
   const TrOp tra{kStage, ldt * kStage, (M / 64) * ldt * kStage}, trb{kStage, ldt * kStage, (N / 64) * ldt * kStage};
-  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB>), dim3((unsigned)wgrad_grid(tiles_m * tiles_n, splits)),
-                     dim3(256), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, wgrad_chunk(ldt, splits), sa,
+  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, TRA, TRB, kWgradWaves>),
+                     dim3((unsigned)wgrad_grid(tiles_m * tiles_n, splits)), dim3(64 * kWgradWaves), kMainLds, st, (const uint8_t*)a, (const uint8_t*)b, M, N, ldt, wgrad_chunk(ldt, splits), sa,
                      sb, ws, tiles_m, tiles_n, splits, 1, tra, trb);
   return status();
 }
@@ -1904,16 +1928,17 @@ int sfp8_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, int64_
     return status();
   }
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
+  int rc = prep(wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, false, kWgradWaves>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)wgrad_grid(tiles_m * tiles_n, (int)splits)), dim3(256),
-                     kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, wgrad_chunk(ldt, splits), sa,
-                     sb, splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1), TrOp{}, TrOp{});
+  hipLaunchKernelGGL((wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, false, kWgradWaves>),
+                     dim3((unsigned)wgrad_grid(tiles_m * tiles_n, (int)splits)), dim3(64 * kWgradWaves), kMainLds, st,
+                     (const uint8_t*)at, (const uint8_t*)bt, M, N, ldt, wgrad_chunk(ldt, splits), sa, sb,
+                     splits > 1 ? ws : out, tiles_m, tiles_n, (int)splits, (int)(splits > 1), TrOp{}, TrOp{});
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
-                     (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  hipLaunchKernelGGL((splitk_reduce_kernel<false, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0,
+                     st, ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
 
@@ -2035,16 +2060,17 @@ int sfp8_moe_gemm_wgrad(const void* at, int fmt_a, const void* bt, int fmt_b, in
   if (splits > 1 && (!ws || ws_floats < sfp8_moe_wgrad_workspace_floats(M, N, E))) return kErrWorkspaceTooSmall;
   hipStream_t st = (hipStream_t)stream;
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3>, kMainLds);
+  int rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, false, kWgradWaves>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3>), dim3((unsigned)(tiles_m * tiles_n * splits * E)),
-                     dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, ldp, sa, sb, out, ws, plan,
-                     tiles_m, tiles_n, (int)splits);
+  hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, false, kWgradWaves>),
+                     dim3((unsigned)(tiles_m * tiles_n * splits * E)), dim3(64 * kWgradWaves), kMainLds, st,
+                     (const uint8_t*)at, (const uint8_t*)bt, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
+                     (int)splits);
   rc = status();
   if (rc || splits == 1) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
-                     (int)splits, n4, tiles_n, M, N, sa, sb, out);
+  hipLaunchKernelGGL((splitk_reduce_kernel<false, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256), (unsigned)E),
+                     dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
 
@@ -2069,21 +2095,24 @@ int sfp8_moe_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b
   const dim3 grid((unsigned)(tiles_m * tiles_n * splits * E));
   int rc;
   if (a_rows && b_rows) {
-    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, true>, kMainLds);
+    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, true, kWgradWaves>, kMainLds);
     if (!rc)
-      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, true>), grid, dim3(256), kMainLds, st,
+      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, true, kWgradWaves>), grid,
+                         dim3(64 * kWgradWaves), kMainLds, st,
                          (const uint8_t*)a, (const uint8_t*)b, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
                          (int)splits);
   } else if (a_rows) {
-    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, false>, kMainLds);
+    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, false, kWgradWaves>, kMainLds);
     if (!rc)
-      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, false>), grid, dim3(256), kMainLds, st,
+      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, true, false, kWgradWaves>), grid,
+                         dim3(64 * kWgradWaves), kMainLds, st,
                          (const uint8_t*)a, (const uint8_t*)b, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
                          (int)splits);
   } else {
-    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, true>, kMainLds);
+    rc = prep(moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, true, kWgradWaves>, kMainLds);
     if (!rc)
-      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, true>), grid, dim3(256), kMainLds, st,
+      hipLaunchKernelGGL((moe_wgrad_kernel<false, kFmtE5M2, kFmtE4M3, false, true, kWgradWaves>), grid,
+                         dim3(64 * kWgradWaves), kMainLds, st,
                          (const uint8_t*)a, (const uint8_t*)b, M, N, ldp, sa, sb, out, ws, plan, tiles_m, tiles_n,
                          (int)splits);
   }
@@ -2092,11 +2121,11 @@ int sfp8_moe_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
   if (b_rows)
-    hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st,
-                       ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
+    hipLaunchKernelGGL((splitk_reduce_kernel<true, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256), (unsigned)E),
+                       dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
   else
-    hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st,
-                       ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
+    hipLaunchKernelGGL((splitk_reduce_kernel<false, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256), (unsigned)E),
+                       dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
 
@@ -2193,16 +2222,16 @@ int sfp8_bf16_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t N, i
   const int64_t splits = sfp8_bf16_wgrad_splits(M, N, ldt);
   if (!ws || ws_floats < sfp8_bf16_wgrad_workspace_floats(M, N, ldt)) return kErrWorkspaceTooSmall;
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(wgrad_kernel<true, 0, 0>, kMainLds);
+  int rc = prep(wgrad_kernel<true, 0, 0, false, false, kBf16WgradWaves>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((wgrad_kernel<true, 0, 0>), dim3((unsigned)(tiles_m * tiles_n * splits)), dim3(256), kMainLds,
-                     st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws,
-                     tiles_m, tiles_n, (int)splits, 1, TrOp{}, TrOp{});
+  hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, false, false, kBf16WgradWaves>), dim3((unsigned)(tiles_m * tiles_n * splits)),
+                     dim3(64 * kBf16WgradWaves), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldt,
+                     2 * ldt / splits, nullptr, nullptr, ws, tiles_m, tiles_n, (int)splits, 1, TrOp{}, TrOp{});
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
-                     (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  hipLaunchKernelGGL((bf16_wgrad_reduce_kernel<false, kBf16WgradWaves>), dim3((unsigned)((n4 + 255) / 256), 1), dim3(256),
+                     0, st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
 
@@ -2220,16 +2249,17 @@ int sfp8_bf16_moe_gemm_wgrad(const void* at, const void* bt, int64_t M, int64_t 
   if (!ws || ws_floats < sfp8_bf16_moe_wgrad_workspace_floats(M, N, E)) return kErrWorkspaceTooSmall;
   hipStream_t st = (hipStream_t)stream;
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(moe_wgrad_kernel<true, 0, 0>, kMainLds);
+  int rc = prep(moe_wgrad_kernel<true, 0, 0, false, false, kBf16WgradWaves>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((moe_wgrad_kernel<true, 0, 0>), dim3((unsigned)(tiles_m * tiles_n * splits * E)),
-                     dim3(256), kMainLds, st, (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldp, nullptr, nullptr,
-                     nullptr, ws, plan, tiles_m, tiles_n, (int)splits);
+  hipLaunchKernelGGL((moe_wgrad_kernel<true, 0, 0, false, false, kBf16WgradWaves>),
+                     dim3((unsigned)(tiles_m * tiles_n * splits * E)), dim3(64 * kBf16WgradWaves), kMainLds, st,
+                     (const uint8_t*)at, (const uint8_t*)bt, M, N, 2 * ldp, nullptr, nullptr, nullptr, ws, plan,
+                     tiles_m, tiles_n, (int)splits);
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0, st, ws,
-                     (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  hipLaunchKernelGGL((bf16_wgrad_reduce_kernel<false, kBf16WgradWaves>), dim3((unsigned)((n4 + 255) / 256), (unsigned)E),
+                     dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
 
@@ -2258,28 +2288,28 @@ int sfp8_bf16_gemm_wgrad_rows(const void* a, const void* x, int x_rows, int64_t 
   const dim3 grid((unsigned)(tiles_m * tiles_n * splits));
   int rc;
   if (x_rows) {
-    rc = prep(wgrad_kernel<true, 0, 0, true, true>, kMainLds);
+    rc = prep(wgrad_kernel<true, 0, 0, true, true, kBf16WgradWaves>, kMainLds);
     if (!rc)
-      hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, true, true>), grid, dim3(256), kMainLds, st, (const uint8_t*)a,
-                         (const uint8_t*)x, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws, tiles_m, tiles_n,
-                         (int)splits, 1, tra, trb);
+      hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, true, true, kBf16WgradWaves>), grid, dim3(64 * kBf16WgradWaves),
+                         kMainLds, st, (const uint8_t*)a, (const uint8_t*)x, M, N, 2 * ldt, 2 * ldt / splits, nullptr,
+                         nullptr, ws, tiles_m, tiles_n, (int)splits, 1, tra, trb);
   } else {
-    rc = prep(wgrad_kernel<true, 0, 0, true, false>, kMainLds);
+    rc = prep(wgrad_kernel<true, 0, 0, true, false, kBf16WgradWaves>, kMainLds);
     if (!rc)
-      hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, true, false>), grid, dim3(256), kMainLds, st, (const uint8_t*)a,
-                         (const uint8_t*)x, M, N, 2 * ldt, 2 * ldt / splits, nullptr, nullptr, ws, tiles_m, tiles_n,
-                         (int)splits, 1, tra, TrOp{});
+      hipLaunchKernelGGL((wgrad_kernel<true, 0, 0, true, false, kBf16WgradWaves>), grid, dim3(64 * kBf16WgradWaves),
+                         kMainLds, st, (const uint8_t*)a, (const uint8_t*)x, M, N, 2 * ldt, 2 * ldt / splits, nullptr,
+                         nullptr, ws, tiles_m, tiles_n, (int)splits, 1, tra, TrOp{});
   }
   if (rc) return rc;
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
   if (x_rows)
-    hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<true>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
-                       (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+    hipLaunchKernelGGL((bf16_wgrad_reduce_kernel<true, kBf16WgradWaves>), dim3((unsigned)((n4 + 255) / 256), 1),
+                       dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   else
-    hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
-                       (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+    hipLaunchKernelGGL((bf16_wgrad_reduce_kernel<false, kBf16WgradWaves>), dim3((unsigned)((n4 + 255) / 256), 1),
+                       dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
 
@@ -2293,17 +2323,17 @@ int sfp8_bf16_moe_gemm_wgrad_rows(const void* a, const void* bt, int64_t M, int6
   if (!ws || ws_floats < sfp8_bf16_moe_wgrad_workspace_floats(M, N, E)) return kErrWorkspaceTooSmall;
   hipStream_t st = (hipStream_t)stream;
   const int tiles_m = cdiv(M, kTile), tiles_n = cdiv(N, kTile);
-  int rc = prep(moe_wgrad_kernel<true, 0, 0, true, false>, kMainLds);
+  int rc = prep(moe_wgrad_kernel<true, 0, 0, true, false, kBf16WgradWaves>, kMainLds);
   if (rc) return rc;
-  hipLaunchKernelGGL((moe_wgrad_kernel<true, 0, 0, true, false>),
-                     dim3((unsigned)(tiles_m * tiles_n * splits * E)), dim3(256), kMainLds, st,
+  hipLaunchKernelGGL((moe_wgrad_kernel<true, 0, 0, true, false, kBf16WgradWaves>),
+                     dim3((unsigned)(tiles_m * tiles_n * splits * E)), dim3(64 * kBf16WgradWaves), kMainLds, st,
                      (const uint8_t*)a, (const uint8_t*)bt, M, N, 2 * ldp, nullptr, nullptr, nullptr, ws, plan,
                      tiles_m, tiles_n, (int)splits);
   rc = status();
   if (rc) return rc;
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
-  hipLaunchKernelGGL(bf16_wgrad_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), (unsigned)E), dim3(256), 0,
-                     st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
+  hipLaunchKernelGGL((bf16_wgrad_reduce_kernel<false, kBf16WgradWaves>), dim3((unsigned)((n4 + 255) / 256), (unsigned)E),
+                     dim3(256), 0, st, ws, (int)splits, n4, tiles_n, M, N, (uint16_t*)out);
   return status();
 }
 
@@ -2334,11 +2364,11 @@ int sfp8_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b, in
   const int tiles_n = cdiv(N, kTile);
   const int64_t n4 = (int64_t)cdiv(M, kTile) * tiles_n * kTile * kTile / 4;
   if (b_rows)
-    hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws, splits,
-                       n4, tiles_n, M, N, sa, sb, out);
+    hipLaunchKernelGGL((splitk_reduce_kernel<true, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0,
+                       st, ws, splits, n4, tiles_n, M, N, sa, sb, out);
   else
-    hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0, st, ws,
-                       splits, n4, tiles_n, M, N, sa, sb, out);
+    hipLaunchKernelGGL((splitk_reduce_kernel<false, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256), 1), dim3(256), 0,
+                       st, ws, splits, n4, tiles_n, M, N, sa, sb, out);
   return status();
 }
 
@@ -2367,11 +2397,11 @@ int sfp8_gemm_wgrad_momentum(const void* a, int fmt_a, int a_rows, const void* b
   }
   const int64_t n4 = (int64_t)tiles_m * tiles_n * kTile * kTile / 4;
   if (b_rows)
-    hipLaunchKernelGGL(splitk_momentum_kernel<true>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws, splits,
-                       n4, tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
+    hipLaunchKernelGGL((splitk_momentum_kernel<true, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                       ws, splits, n4, tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
   else
-    hipLaunchKernelGGL(splitk_momentum_kernel<false>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws, splits,
-                       n4, tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
+    hipLaunchKernelGGL((splitk_momentum_kernel<false, kWgradWaves>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                       ws, splits, n4, tiles_n, M, N, sa, sb, grad, v, (uint16_t*)u, w_v, 1.0f - w_u);
   return status();
 }
 

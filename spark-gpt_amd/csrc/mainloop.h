@@ -124,7 +124,7 @@ struct MainLoop {
   static_assert(TB == 4 || TB == 2, "2 or 4 A blocks per wave");
   static constexpr int kWM = 8 / TB;                        // wave rows
   static constexpr int kWaves = kWM * WN;
-  static_assert(!(TR_A || TR_B) || (!PAIRED && NB == 4), "transposing reads: plain, 256 x 256");
+  static_assert(!(TR_A || TR_B) || (!PAIRED && 32 * NB * WN == 256), "transposing reads: plain, 256 x 256");
   static constexpr bool kTr = TR_A || TR_B;
   using Rsrc = typename std::conditional<kTr, intx4, __amdgpu_buffer_rsrc_t>::type;
   static SFP8_DEV Rsrc rsrc(const void* base, int64_t bytes) {
@@ -449,14 +449,14 @@ struct MainLoop {
       // addresses token 16 (G / 2) + 4 q + j / 4 and columns 16 (G % 2) +
       // 4 (j % 4) .. + 3; the read returns to lane 16 G + 4 a + b tokens
       // 16 (G / 2) + 4 q .. + 3 of column 16 (G % 2) + 4 a + b.  Slabs of the
-      // wave's rows: 4 wm (A) or 4 wn (B).
+      // wave's rows: 4 wm (A) or NB wn (B).
       const int G = lane >> 4, j = lane & 15;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int tok = 16 * (G >> 1) + 4 * q + (j >> 2);
         const uint32_t cb = (uint32_t)(32 * (G & 1) + 8 * (j & 3));
         if constexpr (TR_A) aoff[q] = (uint32_t)((128 * wm + tok) * kStage) + cb;
-        if constexpr (TR_B) boff[q] = (uint32_t)((128 * wn + tok) * kStage) + cb;
+        if constexpr (TR_B) boff[q] = (uint32_t)((32 * NB * wn + tok) * kStage) + cb;
       }
     } else if constexpr (kTr) {
       // Transposing reads: 16-lane group G = lane / 16 (lane half g = G / 2,
@@ -464,7 +464,7 @@ struct MainLoop {
       // addresses tile row (token) 32 g + 8 q + b of the block's slab and the
       // 8 bytes 8 h.. of logical chunk 2 (k & 1) + G % 2 (at its TR swizzle
       // position); the read returns to lane i rows 32 g + 8 q .. + 7 of column
-      // 16 (G % 2) + i.  Slab of the wave's rows: 2 wm (A) or 2 wn (B).
+      // 16 (G % 2) + i.  Slab of the wave's rows: 2 wm (A) or NB wn / 2 (B).
       const int G = lane >> 4, li = lane & 15, bq = li >> 1, hb = li & 1, gh = G >> 1, gc = G & 1;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -473,7 +473,7 @@ struct MainLoop {
           const int rr = 32 * gh + 8 * q + bq;  // row within the 64-row slab
           const uint32_t cb = (uint32_t)((((2 * k1 + gc) ^ (((rr >> 2) & 1) << 1)) << 4) + 8 * hb);
           if constexpr (TR_A) aoff[2 * q + k1] = (uint32_t)((128 * wm + rr) * kStage) + cb;
-          if constexpr (TR_B) boff[2 * q + k1] = (uint32_t)((128 * wn + rr) * kStage) + cb;
+          if constexpr (TR_B) boff[2 * q + k1] = (uint32_t)((32 * NB * wn + rr) * kStage) + cb;
         }
       }
     }
