@@ -971,7 +971,37 @@ __global__ __launch_bounds__(512, 1) void down_fwd_kernel(
 // all in the epilogue, whose loads, LDS round trips and barriers a single
 // wave per SIMD left exposed.
 constexpr int kEpiStride2 = 272;
-constexpr int kDgradLutOff = 2 * kTile * kEpiStride2 + 32;  // after Gt, Ut and the 8 reduction slots
+// LDS: the SwiGLU backward's table at offset 0 (so that an entry's address
+// is its code times 8), then the main loop's ring, later the epilogue's
+// staging tiles and 8 reduction slots
+constexpr int kDgradLutBytes = 256 * 8;
+
+// dg, du of the 4 columns of group w of a 16-column chunk: dh from the
+// staged bf16 words h0 (columns 0-7) and h1 (8-15), the gate and up codes
+// from gw and uw, the two factors per gate code from the table at LDS
+// address 0 (entry b at 8 b: the kernel has no static LDS, so its dynamic
+// LDS begins at 0, and one shift of the selected byte is the address); the
+// reference's order (train.py:1083-1087).
+typedef __attribute__((address_space(3))) const floatx2* lds_floatx2_ptr;
+SFP8_DEV void dgrad_swiglu4(const intx4& h0, const intx4& h1, uint32_t gw, uint32_t uw, int w, float (&dg)[4],
+                            float (&du)[4]) {
+  const uint32_t hw0 = (uint32_t)(w < 2 ? h0[2 * w] : h1[2 * w - 4]);
+  const uint32_t hw1 = (uint32_t)(w < 2 ? h0[2 * w + 1] : h1[2 * w - 3]);
+  const float dhv[4] = {__uint_as_float(hw0 << 16), __uint_as_float(hw0 & 0xffff0000u), __uint_as_float(hw1 << 16),
+                        __uint_as_float(hw1 & 0xffff0000u)};
+  const floatx2 g01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, false);
+  const floatx2 g23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, true);
+  const floatx2 u01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(uw, 1.0f, false);
+  const floatx2 u23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(uw, 1.0f, true);
+  const float g8v[4] = {g01.x, g01.y, g23.x, g23.y}, u8v[4] = {u01.x, u01.y, u23.x, u23.y};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // (sig, sig * (1 + g * (1 - sig)))
+    const floatx2 f = *reinterpret_cast<lds_floatx2_ptr>((uintptr_t)(((gw >> (8 * e)) & 0xFFu) << 3));
+    dg[e] = (dhv[e] * u8v[e]) * f.y;
+    du[e] = (dhv[e] * g8v[e]) * f.x;
+  }
+}
 
 // With a MoE plan: tile rows are padded expert order (gu8, dgu8, dgu8t over
 // ldt padded rows); dy is the row-major upstream gradient of the expert-order
@@ -993,7 +1023,8 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
   // rounded in the reference's order (train.py:1083-1087, no contraction).
   // Its LDS range is disjoint from the main loop's ring and the staging
   // tiles; the main loop's first barrier publishes it.
-  floatx2* lut = reinterpret_cast<floatx2*>(lds + kDgradLutOff);
+  floatx2* lut = reinterpret_cast<floatx2*>(lds);
+  uint8_t* const base = lds + kDgradLutBytes;  // the ring and the staging tiles
   if (tid < 256) {
 #pragma clang fp contract(off)
     const float gl = __builtin_amdgcn_cvt_f32_fp8(tid, 0) * (1.0f / scale[1]);
@@ -1006,9 +1037,7 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
   //   dgu8 = e5m2(d*q3) = e5m2(d'*(s_gu*q3)),  amax3 = s_gu*max(|dg|,|du|).
   const float m3s = (1.0f / scale[1]) * scale[3];
   const float inv3 = 1.0f / m3s, bnd3 = kE5M2Max * inv3;
-  uint8_t* Gt = lds;
-  uint8_t* Ut = lds + kTile * kEpiStride2;
-  float* red = reinterpret_cast<float*>(lds + 2 * kTile * kEpiStride2);  // 8 floats after both tiles
+  float* red = reinterpret_cast<float*>(base + 2 * kTile * kEpiStride2);  // 8 floats after the staging tiles
   float m3 = 0.f;
   // Persistent: work-group pid runs tiles pid, pid + gridDim.x, ...  (Work-
   // groups started a quarter of a tile apart per XCD, so that the tiles'
@@ -1032,7 +1061,7 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
   // A = dy row-major (rows past the tile's last read as zero through the
   // range check); B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
   MainLoop<true, 0, 0, false, 2, kStages, 0, false, false, 4>::run(
-      lds, reinterpret_cast<const uint8_t*>(dy) + a_row * ldb, a_rows * ldb, [=](int r) { return r * (int)ldb; },
+      base, reinterpret_cast<const uint8_t*>(dy) + a_row * ldb, a_rows * ldb, [=](int r) { return r * (int)ldb; },
       kStage, wb + n0 * kStage, ldb * ip - n0 * kStage,
       [=](int r) { return plain_col_nb<2>(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
   // Row-order epilogue, in two passes of 128 tile rows (the rows of
@@ -1041,11 +1070,11 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
   // rows; with dgu8t the codes also go to LDS for the token-contiguous copy.
   const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu8 + m0 * 64, 2 * I * ldt - m0 * 64);
   const int cols = (int)((I - n0) < kTile ? (I - n0) : kTile);  // 128 or 256
-  uint8_t* DH = lds;
+  uint8_t* DH = base;
   // the staging tiles of the token-contiguous copy (MoE only); their offset
   // goes through an empty asm so that the compiler does not hoist per-lane
   // addresses into them out of the tile loop (a register it had to spill)
-  int g2off = 128 * kBf16Stride;
+  int g2off = kDgradLutBytes + 128 * kBf16Stride;
   asm volatile("" : "+s"(g2off));
   uint8_t* G2 = lds + g2off;
   uint8_t* U2 = G2 + 128 * kEpiStride2;
@@ -1075,42 +1104,44 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
       const int64_t t = m0 + half_tile_row(lr, P);
       const intx4 h0 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c);
       const intx4 h1 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c + 16);
+      // The 16 values' unclamped codes and their NaN-propagating maximum
+      // magnitude (the first maximum3 of each group of four takes the
+      // running maximum): when it is inside the e5m2 range (after scaling)
+      // no clamp can act and no NaN needs its code, so the codes are
+      // exact; otherwise (wave-uniform, NaN or out-of-range data only) the
+      // chunk is computed again with the clamps and NaN codes, and the amax
+      // over its non-NaN values.
       uint32_t pg[4], pu[4];
+      float mc = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t hw0 = (uint32_t)(w < 2 ? h0[2 * w] : h1[2 * w - 4]);
-        const uint32_t hw1 = (uint32_t)(w < 2 ? h0[2 * w + 1] : h1[2 * w - 3]);
-        const float dhv[4] = {__uint_as_float(hw0 << 16), __uint_as_float(hw0 & 0xffff0000u),
-                              __uint_as_float(hw1 << 16), __uint_as_float(hw1 & 0xffff0000u)};
-        const uint32_t gw = (uint32_t)wg[k][w];
-        const floatx2 g01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, false);
-        const floatx2 g23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(gw, 1.0f, true);
-        const floatx2 u01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[k][w], 1.0f, false);
-        const floatx2 u23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8((uint32_t)wu[k][w], 1.0f, true);
-        const float g8v[4] = {g01.x, g01.y, g23.x, g23.y}, u8v[4] = {u01.x, u01.y, u23.x, u23.y};
         float dg[4], du[4];
+        dgrad_swiglu4(h0, h1, (uint32_t)wg[k][w], (uint32_t)wu[k][w], w, dg, du);
+        mc = max3_nan(mc, fabsf(dg[0]), fabsf(du[0]));
+        mc = max3_nan(mc, fabsf(dg[1]), fabsf(du[1]));
+        mc = max3_nan(mc, fabsf(dg[2]), fabsf(du[2]));
+        mc = max3_nan(mc, fabsf(dg[3]), fabsf(du[3]));
+        // the unclamped packs overwrite both halves of their third argument:
+        // the dead dh words, rather than a copy of a live register
+        pg[w] = pack4_e5m2_scaled_noclamp(dg[0], dg[1], dg[2], dg[3], inv3,
+                                          (uint32_t)(w < 2 ? h0[2 * w] : h1[2 * w - 4]));
+        pu[w] = pack4_e5m2_scaled_noclamp(du[0], du[1], du[2], du[3], inv3,
+                                          (uint32_t)(w < 2 ? h0[2 * w + 1] : h1[2 * w - 3]));
+      }
+      if (__builtin_amdgcn_ballot_w64(!(mc <= bnd3))) {
+        asm volatile("" ::: "memory");
+        mc = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const floatx2 f = lut[(gw >> (8 * e)) & 0xFFu];  // (sig, sig * (1 + g * (1 - sig)))
-          dg[e] = (dhv[e] * u8v[e]) * f.y;
-          du[e] = (dhv[e] * g8v[e]) * f.x;
-        }
-        float mw = max3_nan(fabsf(dg[0]), fabsf(du[0]), fabsf(dg[1]));
-        mw = max3_nan(mw, fabsf(du[1]), fabsf(dg[2]));
-        mw = max3_nan(mw, fabsf(du[2]), fabsf(dg[3]));
-        mw = __builtin_elementwise_maximum(mw, fabsf(du[3]));
-        pg[w] = pack4_e5m2_scaled_noclamp(dg[0], dg[1], dg[2], dg[3], inv3, gw);
-        pu[w] = pack4_e5m2_scaled_noclamp(du[0], du[1], du[2], du[3], inv3, gw);
-        if (__builtin_amdgcn_ballot_w64(!(mw <= bnd3))) {  // wave-uniform; NaN or out-of-range data only
-          asm volatile("" ::: "memory");
+        for (int w = 0; w < 4; ++w) {
+          float dg[4], du[4];
+          dgrad_swiglu4(h0, h1, (uint32_t)wg[k][w], (uint32_t)wu[k][w], w, dg, du);
           pg[w] = fix_nan4(pack4_e5m2_scaled(dg[0], dg[1], dg[2], dg[3], inv3, bnd3), dg[0], dg[1], dg[2], dg[3]);
           pu[w] = fix_nan4(pack4_e5m2_scaled(du[0], du[1], du[2], du[3], inv3, bnd3), du[0], du[1], du[2], du[3]);
-          mw = 0.f;  // amax over the non-NaN values
 #pragma unroll
-          for (int e = 0; e < 4; ++e) mw = fmaxf(mw, fmaxf(fabsf(dg[e]), fabsf(du[e])));
+          for (int e = 0; e < 4; ++e) mc = fmaxf(mc, fmaxf(fabsf(dg[e]), fabsf(du[e])));
         }
-        m3 = fmaxf(m3, mw);
       }
+      m3 = fmaxf(m3, mc);
       if (dgu8t) {  // staged for the token-contiguous copy
         store16(G2 + lr * kEpiStride2 + c, pg);
         store16(U2 + lr * kEpiStride2 + c, pu);
@@ -1674,8 +1705,8 @@ using namespace sfp8;
 namespace {
 
 // epilogue tiles (2 x 256 x 272) + 4 amax floats, or the main loop's ring
-constexpr int kDgradEpiLds = kDgradLutOff + 256 * 8;
-constexpr int kDgradLds = kDgradEpiLds > kMainLds ? kDgradEpiLds : kMainLds;
+constexpr int kDgradEpiLds = 2 * kTile * kEpiStride2 + 32;
+constexpr int kDgradLds = kDgradLutBytes + (kDgradEpiLds > kMainLds ? kDgradEpiLds : kMainLds);
 
 template <typename K>
 int prep(K kernel, int lds_bytes) {
