@@ -1,11 +1,13 @@
 // Pipelined MFMA main loop for C = A * B^T with K-contiguous A and B rows
-// (gfx950, one 256-thread work-group = 4 waves, one wave per SIMD).
+// (gfx950).
 //
-// Tile: 256 A rows x 64*NB B rows; each wave owns 128 A rows x 32*NB B rows as
-// 4 x NB MFMA 32x32 accumulators (fp32, 64*NB registers per lane).  NB = 4
-// (256 x 256 tiles, one work-group per CU) or NB = 2 (256 x 128 tiles, small
-// enough in registers and LDS for two work-groups per CU, so one's epilogue
-// overlaps the other's MFMAs).
+// Tile: 256 A rows x 32*NB*WN B rows, one work-group of (8/TB) x WN waves;
+// each wave owns 32*TB A rows x 32*NB B rows as TB x NB MFMA 32x32
+// accumulators (fp32, 16*TB*NB registers per lane).  The GEMMs here use
+// 8 waves (two per SIMD) of 128 x 64 (TB = 4, NB = 2, WN = 4) per 256 x 256
+// tile, or of 64 x 64 (TB = 2, NB = 2, WN = 2) per 256 x 128 tile, so that
+// one wave's stage waits and barriers are covered by the other's MFMAs; 4
+// waves of 128 x 128 (NB = 4, WN = 2) remain available.
 //
 // K advances in 64-byte stages through a ring of STAGES LDS buffers, each A
 // (16 KiB) + B (64*NB*64 bytes); A stages first, then B stages.
@@ -56,9 +58,8 @@ SFP8_DEV intx4 make_rsrc4(const void* base, int64_t bytes) {
   return intx4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), n, 0x00020000};
 }
 
-// One work-group of 4 waves computes a 256 (A rows) x 64*NB (B rows) tile;
-// wave (wm, wn) = (wave & 1, wave >> 1) owns A rows 128*wm.. (4 blocks of 32)
-// and NB blocks of 32 B rows:
+// B rows of a wave column: wave (wm, wn) owns A rows 32*TB*wm.. (TB blocks
+// of 32) and NB blocks of 32 B rows:
 //   plain:  B rows 32*NB*wn + 32*nb
 //   paired: gate/up halves of the B tile (rows [0, 16*NB*WN) gate, the rest
 //           up); wave wn owns gate blocks 16*NB*wn + 32*nb (nb < NB/2) and
@@ -109,9 +110,10 @@ SFP8_DEV void sched_interleave_valu() {
 // gradient reduces over -- and each fragment is assembled from four
 // transposing reads (ds_read_b64_tr_b8: 8 tokens of one column per lane;
 // ds_read_b64_tr_b16: 4 tokens) in the same (lane half, K) order as the plain
-// reads, so the MFMAs see the same values.  Only for a plain (unpaired) B.
-// With TR_B the B tile is not permuted: accumulator v of block nb in lane
-// half g is column 32 nb + 8 (v / 4) + 4 g + v % 4 of the wave's 128.  These
+// reads, so the MFMAs see the same values.  Only for a plain (unpaired) B of
+// 256 rows.  With TR_B the B tile is not permuted: accumulator v of block nb
+// in lane half g is column 32 nb + 8 (v / 4) + 4 g + v % 4 of the wave's
+// 32 NB.  These
 // instantiations issue their DMA as inline asm: the compiler treats a
 // transposing read as possibly aliasing any LDS DMA it knows to be in flight
 // and would wait for all of it first; the stage waits and barriers already
