@@ -382,6 +382,20 @@ struct MainLoop {
       __builtin_amdgcn_sched_barrier(0);
       return;
     }
+    if constexpr (!BF16 && NB == 2 && kDma == 4 && TR_A && TR_B) {
+      // fp8, 8 waves of 128 x 64, both operands through transposing reads
+      // (four per fragment): two fragments and two DMA issues alternate over
+      // 5 MFMAs (2 % faster on the gate/up weight gradient than the order
+      // below, which the plain reads prefer)
+      mfma_then_reads<P + 0, 0, 2>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 1, 0, 2>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 2, 2, 4>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_then_dma<P + 3, 2, 4>(lds, cur, acc, dma_buf, ra, rb, voff_a, voff_b, sa, sb, wave);
+      mfma_then_reads<P + 4, 4, 6>(lds, cur, nxt, acc, rd_buf, aoff, boff);
+      mfma_range<P + 5, kMfma>(cur, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
     if constexpr (!BF16 && NB == 2 && kDma == 4) {
       // fp8, 8 waves of 128 x 64: 8 MFMAs of 64 cycles; two fragments after
       // each of 3, then two DMA issues after each of 2
