@@ -564,7 +564,8 @@ struct SwigluPipe {
       for (int j = J * kDma / kDmaSlots; j < (J + 1) * kDma / kDmaSlots; ++j) {
         if constexpr (KT + kSt - 1 < NK) {
           constexpr int ld = KT + kSt - 1;
-          ML::load_one(j, c.lds, slot_, c.ra, c.rb, c.voff_a, c.voff_b, ld * a_ss, ld * b_ss, c.wave);
+          ML::load_one(j, c.lds, slot_, c.ra, c.rb, c.voff_a, c.voff_b, stage_off<ld>(a_ss), stage_off<ld>(b_ss),
+                       c.wave);
         } else {
           const int ld = c.has_next ? KT + kSt - 1 - NK : NK - 1;
           ML::load_one(j, c.lds, slot_, c.nra, c.nrb, c.voff_a, c.nvoff_b, ld * a_ss, ld * b_ss, c.wave);
@@ -583,6 +584,15 @@ struct SwigluPipe {
     }
     unit_piece<KT / kSpan, (KT % kSpan) * kSlots + J>(c, t);
     __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Stage LD's byte offset LD * ss, computed where it is used (otherwise
+  // the products for all fixed stages stay live in scalar registers across
+  // the tile loop).
+  template <int LD>
+  static SFP8_DEV int stage_off(int ss) {
+    asm volatile("" : "+s"(ss));
+    return LD * ss;
   }
 
   template <int KT>
