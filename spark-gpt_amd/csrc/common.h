@@ -28,6 +28,11 @@ constexpr float kE5M2Max = 57344.0f;
 // fp8 format selectors (the f8f6f4 MFMA's operand format fields use the same codes)
 constexpr int kFmtE4M3 = 0;
 constexpr int kFmtE5M2 = 1;
+// Cache-policy operand of the buffer-load builtins: the nontemporal (nt) bit,
+// for data a kernel reads once (streamed through the caches without
+// displacing the lines other work-groups re-read).  Plain pointer loads of
+// such data use __builtin_nontemporal_load, which sets the same bit.
+constexpr int kNT = 2;
 
 // Library status codes (hipError_t values are passed through unchanged and are
 // all positive; ours are negative).

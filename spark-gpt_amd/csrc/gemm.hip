@@ -881,7 +881,7 @@ SFP8_DEV void load_res_half(__amdgpu_buffer_rsrc_t rres, int p, int64_t n0, int6
     const int idx = (int)threadIdx.x + NT * k;
     const int lr = idx >> 5, c = idx & 31;
     const uint32_t off = (uint32_t)((half_tile_row(lr, p) * D + n0 + 8 * c) * 2);
-    rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0);
+    rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, kNT);
   }
 }
 
@@ -1099,8 +1099,8 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
       const int row = half_tile_row(lr, P);
       const int64_t j = n0 + c;
       const uint32_t jo = j < I ? (uint32_t)((j >> 6) * ldt * 64 + row * 64 + (j & 63)) : 0x80000000u;
-      wg[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, 0);
-      wu[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)(I * ldt), 0, 0);
+      wg[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, kNT);
+      wu[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)(I * ldt), 0, kNT);
     }
     if (P == 1) __syncthreads();  // pass 0's dgu8t copy has read the LDS
     // dh rounded to bf16 (train.py:1082)
@@ -1463,8 +1463,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   ws += (int64_t)blockIdx.y * splits * n4 * 4;
   out += (int64_t)blockIdx.y * M * N;
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
-  floatx4 acc = w4[q];
-  for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  floatx4 acc = __builtin_nontemporal_load(w4 + q);
+  for (int s = 1; s < splits; ++s) acc += __builtin_nontemporal_load(w4 + (int64_t)s * n4 + q);
   int r, c;
   acc_order_rc<NW, TR_B>((int)(q & 16383), r, c);
   const int64_t tile = q >> 14;
@@ -1639,8 +1639,8 @@ __global__ __launch_bounds__(256) void bf16_wgrad_reduce_kernel(const float* __r
   ws += (int64_t)blockIdx.y * splits * n4 * 4;
   out += (int64_t)blockIdx.y * M * N;
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
-  floatx4 acc = w4[q];
-  for (int s = 1; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  floatx4 acc = __builtin_nontemporal_load(w4 + q);
+  for (int s = 1; s < splits; ++s) acc += __builtin_nontemporal_load(w4 + (int64_t)s * n4 + q);
   int r, c;
   acc_order_rc<NW, TR_B>((int)(q & 16383), r, c);
   const int64_t tile = q >> 14;
@@ -1673,7 +1673,7 @@ __global__ __launch_bounds__(256) void splitk_momentum_kernel(const float* __res
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const floatx4* w4 = reinterpret_cast<const floatx4*>(ws);
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) acc += w4[(int64_t)s * n4 + q];
+  for (int s = 0; s < splits; ++s) acc += __builtin_nontemporal_load(w4 + (int64_t)s * n4 + q);
   constexpr int NB = NW == 8 ? 2 : 4, NBB = NW == 8 ? 1 : 2;
   const int lane = threadIdx.x & 63, i = threadIdx.x >> 6;
   const int64_t b = blockIdx.x;

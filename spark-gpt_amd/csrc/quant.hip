@@ -71,7 +71,8 @@ __global__ __launch_bounds__(256) void quant_rowcol_kernel(
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t gr = r0 + rr + Cfg::kRowsPerPass * i;
-    v[i] = live && gr < R ? *reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8) : intx4{0, 0, 0, 0};
+    v[i] = live && gr < R ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(x + gr * C + c0 + c8 * 8))
+                           : intx4{0, 0, 0, 0};
   }
   float m = 0.0f;
   bool nan = false;
@@ -228,7 +229,7 @@ void norm_quant_kernel(
 #pragma unroll
       for (int c = 0; c < Cfg::CPL; ++c) {
         const int d = (c * Cfg::LPR + li) * 8;
-        v[q][c] = t < T ? *reinterpret_cast<const intx4*>(h + t * D + d) : intx4{0, 0, 0, 0};
+        v[q][c] = t < T ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(h + t * D + d)) : intx4{0, 0, 0, 0};
       }
     }
     // the batch's row sums first; then lane li of each row group evaluates
@@ -644,9 +645,9 @@ void norm_bwd_kernel(
       for (int c = 0; c < Cfg::CPL; ++c) {
         const int d = (c * Cfg::LPR + li) * 8;
         const intx4 z = {0, 0, 0, 0};
-        vh[q][c] = valid ? *reinterpret_cast<const intx4*>(h + t * D + d) : z;
-        vg[q][c] = valid ? *reinterpret_cast<const intx4*>(dxn + t * D + d) : z;
-        vd[q][c] = valid ? *reinterpret_cast<const intx4*>(dy + t * D + d) : z;
+        vh[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(h + t * D + d)) : z;
+        vg[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(dxn + t * D + d)) : z;
+        vd[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(dy + t * D + d)) : z;
       }
       rsv[q] = valid ? rstd[t] : 0.0f;
     }
