@@ -848,27 +848,30 @@ SFP8_DEV void stage_bf16_half8(uint8_t* lds, const floatx16 (&acc)[4][2], float 
 // Tile row held in staging row lr of pass p.
 SFP8_DEV int half_tile_row(int lr, int p) { return 128 * (lr >> 6) + 64 * p + (lr & 63); }
 
-// Writes one staged pass to out[t, n] (bf16, leading dimension ld), adding the
-// bf16 residual res[t, n] first when res is given: out = bf16(res + staged).
-// NT = threads of the work-group.
+// Byte offset of out[t, n] (bf16, leading dimension ld) from out + m0 * ld,
+// or 2^31 -- past the range of any descriptor, so the store is dropped --
+// for t >= T or n >= N.  A bit mask rather than a select keeps the stores
+// free of branches (one store instruction per chunk, a fixed count per
+// wave).  Tile rows t - m0 < 256, so the offset needs ld < 2^22.
+SFP8_DEV uint32_t bf16_out_off(int64_t t, int64_t n, int64_t m0, int64_t T, int64_t N, int64_t ld) {
+  const uint32_t in = 0u - (uint32_t)(t < T && n < N);
+  return ((uint32_t)(((t - m0) * ld + n) * 2) & in) | (~in & 0x80000000u);
+}
+
+// Writes one staged pass to out[t, n] (bf16, leading dimension ld) for rows
+// m0.. of the tile below T and columns below N.  NT = threads of the
+// work-group.
 template <int NT = 256>
 SFP8_DEV void write_bf16_half(const uint8_t* lds, int p, int64_t m0, int64_t n0, int64_t T, int64_t N,
-                              int64_t ld, const uint16_t* __restrict__ res, uint16_t* __restrict__ out) {
-  for (int idx = threadIdx.x; idx < 128 * 32; idx += NT) {
+                              int64_t ld, uint16_t* __restrict__ out) {
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + m0 * ld, (T - m0) * ld * 2);
+#pragma unroll
+  for (int k = 0; k < 4096 / NT; ++k) {
+    const int idx = (int)threadIdx.x + NT * k;
     const int lr = idx >> 5, c = idx & 31;
     const int64_t t = m0 + half_tile_row(lr, p), n = n0 + 8 * c;
-    if (t >= T || n >= N) continue;
-    intx4 o = *reinterpret_cast<const intx4*>(lds + lr * kBf16Stride + c * 16);
-    if (res) {
-      const intx4 r = *reinterpret_cast<const intx4*>(res + t * ld + n);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t a = (uint32_t)r[i], b = (uint32_t)o[i];
-        o[i] = (int)pack2_bf16(__uint_as_float(b << 16) + __uint_as_float(a << 16),
-                               __uint_as_float(b & 0xffff0000u) + __uint_as_float(a & 0xffff0000u));
-      }
-    }
-    *reinterpret_cast<intx4*>(out + t * ld + n) = o;
+    const intx4 o = *reinterpret_cast<const intx4*>(lds + lr * kBf16Stride + c * 16);
+    __builtin_amdgcn_raw_buffer_store_b128(o, ro, bf16_out_off(t, n, m0, T, N, ld), 0, 0);
   }
 }
 
@@ -885,16 +888,17 @@ SFP8_DEV void load_res_half(__amdgpu_buffer_rsrc_t rres, int p, int64_t n0, int6
   }
 }
 
-// write_bf16_half with the residual already in registers.
+// write_bf16_half after adding the bf16 residual, already in registers:
+// out = bf16(res + staged).
 template <int NT>
 SFP8_DEV void write_bf16_half_res(const uint8_t* lds, int p, int64_t m0, int64_t n0, int64_t T, int64_t D,
                                   const intx4 (&rv)[4096 / NT], uint16_t* __restrict__ out) {
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + m0 * D, (T - m0) * D * 2);
 #pragma unroll
   for (int k = 0; k < 4096 / NT; ++k) {
     const int idx = (int)threadIdx.x + NT * k;
     const int lr = idx >> 5, c = idx & 31;
     const int64_t t = m0 + half_tile_row(lr, p), n = n0 + 8 * c;
-    if (t >= T || n >= D) continue;
     intx4 o = *reinterpret_cast<const intx4*>(lds + lr * kBf16Stride + c * 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -902,7 +906,7 @@ SFP8_DEV void write_bf16_half_res(const uint8_t* lds, int p, int64_t m0, int64_t
       o[i] = (int)pack2_bf16(__uint_as_float(b << 16) + __uint_as_float(a << 16),
                              __uint_as_float(b & 0xffff0000u) + __uint_as_float(a & 0xffff0000u));
     }
-    *reinterpret_cast<intx4*>(out + t * D + n) = o;
+    __builtin_amdgcn_raw_buffer_store_b128(o, ro, bf16_out_off(t, n, m0, T, D, D), 0, 0);
   }
 }
 
@@ -944,11 +948,11 @@ __global__ __launch_bounds__(512, 1) void down_fwd_kernel(
     // expert rows, no residual: out rounded to bf16 (train.py:1377-1378 stores acc / (s2 q_d) as bf16)
     stage_bf16_half8<0>(lds, acc, deq);
     __syncthreads();
-    write_bf16_half<512>(lds, 0, u0, n0, u0 + urows, D, D, nullptr, y);
+    write_bf16_half<512>(lds, 0, u0, n0, u0 + urows, D, D, y);
     __syncthreads();
     stage_bf16_half8<1>(lds, acc, deq);
     __syncthreads();
-    write_bf16_half<512>(lds, 1, u0, n0, u0 + urows, D, D, nullptr, y);
+    write_bf16_half<512>(lds, 1, u0, n0, u0 + urows, D, D, y);
     return;
   }
   const __amdgpu_buffer_rsrc_t rres = make_rsrc(res + m0 * D, (T - m0) * D * 2);
@@ -1017,14 +1021,16 @@ SFP8_DEV void dgrad_swiglu4(const intx4& h0, const intx4& h1, uint32_t gw, uint3
 // ldt padded rows); dy is the row-major upstream gradient of the expert-order
 // rows (its rows urow(tm).. for tile row tm), W_down^T of expert e at
 // wdt + e * w_estride (bytes); the tile count comes from the plan.
+// TCOPY: dgu8t is written too (staged in LDS per pass).
+template <bool TCOPY>
 __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ wdt, const uint8_t* __restrict__ gu8,
     int64_t T, int64_t D, int64_t I, const float* __restrict__ scale, float* __restrict__ amax,
     uint8_t* __restrict__ dgu8, uint8_t* __restrict__ dgu8t, int64_t ldt, int tiles_m, int tiles_n,
     const int* __restrict__ plan, int64_t w_estride) {
+  using Loop = MainLoop<true, 0, 0, false, 2, kStages, 0, false, false, 4>;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
   const int64_t ldb = D * 2;  // bytes
   const int64_t ip = slab_rows(I);
   // The gate operand of the SwiGLU backward is an e4m3 code here, so its two
@@ -1054,26 +1060,41 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
   // 256 KiB store bursts would not coincide, measured 2 % slower.)
   if (plan) tiles_m = MoePlan{plan}.ntiles();
   const int ntiles = tiles_m * tiles_n;
+  // A = dy row-major (rows past the tile's last read as zero through the
+  // range check); B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
+  const auto arow = [=](int r) { return r * (int)ldb; };
+  const auto brow = [=](int r) { return plain_col_nb<2>(r) * kStage; };
+  const int nk = (int)(ldb / kStage);
+  // the operands of tile `tile`: dy rows m0.. (dense) or the expert rows
+  // urow(tm).. (MoE), and W_down^T (of the tile's expert) from column n0
+  struct Ops {
+    const uint8_t* a;
+    int64_t a_bytes;
+    const uint8_t* b;
+    int64_t b_bytes;
+  };
+  const auto ops_of = [=](int tm, int tn) {
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+    int64_t a_row = m0, a_rows = T - m0;
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(wdt);
+    if (plan) {
+      const MoePlan P{plan};
+      a_row = P.urow(tm);
+      a_rows = P.rows(tm);
+      wb += P.expert(tm) * w_estride;
+    }
+    return Ops{reinterpret_cast<const uint8_t*>(dy) + a_row * ldb, a_rows * ldb, wb + n0 * kStage,
+               ldb * ip - n0 * kStage};
+  };
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
   int tm, tn;
   tile_coords(tile, ntiles, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-  // dy rows of this tile: rows m0.. (dense) or the expert rows urow(tm).. (MoE)
-  int64_t a_row = m0, a_rows = T - m0;
-  const uint8_t* wb = reinterpret_cast<const uint8_t*>(wdt);
-  if (plan) {
-    const MoePlan P{plan};
-    a_row = P.urow(tm);
-    a_rows = P.rows(tm);
-    wb += P.expert(tm) * w_estride;
-  }
   floatx16 acc[4][2];
-  // A = dy row-major (rows past the tile's last read as zero through the
-  // range check); B = Wd^T as a bf16 K-slab [2D/64][slab_rows(I)][64] (bytes)
-  MainLoop<true, 0, 0, false, 2, kStages, 0, false, false, 4>::run(
-      base, reinterpret_cast<const uint8_t*>(dy) + a_row * ldb, a_rows * ldb, [=](int r) { return r * (int)ldb; },
-      kStage, wb + n0 * kStage, ldb * ip - n0 * kStage,
-      [=](int r) { return plain_col_nb<2>(r) * kStage; }, (int)(ip * kStage), (int)(ldb / kStage), acc);
+  {
+    const Ops o = ops_of(tm, tn);
+    Loop::run(base, o.a, o.a_bytes, arow, kStage, o.b, o.b_bytes, brow, (int)(ip * kStage), nk, acc);
+  }
   // Row-order epilogue, in two passes of 128 tile rows (the rows of
   // stage_bf16_half<P>): dh staged in LDS as bf16, then each thread takes
   // 16-column chunks of one row, reading gu8 and writing dgu8 as whole K-slab
@@ -1088,93 +1109,141 @@ __global__ __launch_bounds__(512, 1) void down_dgrad_swiglu_kernel(
   asm volatile("" : "+s"(g2off));
   uint8_t* G2 = lds + g2off;
   uint8_t* U2 = G2 + 128 * kEpiStride2;
-#pragma unroll
-  for (int P = 0; P < 2; ++P) {
-    // gu8 words of this thread's 4 chunks, requested at once
-    intx4 wg[4], wu[4];
+  // Byte offset from gu8 / dgu8 + m0 * 64 of tile row `row`, tile column c
+  // of the gate half (the up half lies I * ldt further, and I * ldt < 2^31):
+  // a column past I gets offset 2^31, beyond the descriptors' range in both
+  // halves, so its loads return zero and its stores are dropped -- every
+  // chunk issues its instructions, a fixed count per wave, with no branch
+  // around them (a bit mask rather than a select, which the compiler turned
+  // into one).
+  const auto gu_off = [=](int c, int row) {
+    const int64_t j = n0 + c;
+    const uint32_t in = 0u - (uint32_t)(j < I);  // all ones for a column inside I
+    return ((uint32_t)((j >> 6) * ldt * 64 + row * 64 + (j & 63)) & in) | (~in & 0x80000000u);
+  };
+  const __amdgpu_buffer_rsrc_t rdg = make_rsrc(dgu8 + m0 * 64, 2 * I * ldt - m0 * 64);
+  // gu8 words of this thread's 4 chunks of pass P, requested at once
+  intx4 wg[4], wu[4];
+  const auto gu_loads = [&](int P) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int item = 8 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
       const int c = 64 * slab + 16 * (lane & 3);
       const int row = half_tile_row(lr, P);
-      const int64_t j = n0 + c;
-      const uint32_t jo = j < I ? (uint32_t)((j >> 6) * ldt * 64 + row * 64 + (j & 63)) : 0x80000000u;
-      wg[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo, 0, kNT);
-      wu[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, jo + (uint32_t)(I * ldt), 0, kNT);
+      wg[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, gu_off(c, row), 0, kNT);
+      wu[k] = __builtin_amdgcn_raw_buffer_load_b128(rgu, gu_off(c, row) + (uint32_t)(I * ldt), 0, kNT);
     }
-    if (P == 1) __syncthreads();  // pass 0's dgu8t copy has read the LDS
-    // dh rounded to bf16 (train.py:1082)
-    if (P == 0) stage_bf16_half8<0>(DH, acc, 1.0f);
-    else stage_bf16_half8<1>(DH, acc, 1.0f);
-    __syncthreads();
+  };
+  // the codes of chunk k of pass P (dh from the staged tile, gate and up
+  // codes from wg[k], wu[k]); the running amax in m3
+  const auto swiglu_chunk = [&](int P, int k, uint32_t (&pg)[4], uint32_t (&pu)[4]) {
+    const int item = 8 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
+    const int c = 64 * slab + 16 * (lane & 3);
+    const intx4 h0 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c);
+    const intx4 h1 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c + 16);
+    // The 16 values' unclamped codes and their NaN-propagating maximum
+    // magnitude (the first maximum3 of each group of four takes the
+    // running maximum): when it is inside the e5m2 range (after scaling)
+    // no clamp can act and no NaN needs its code, so the codes are
+    // exact; otherwise (wave-uniform, NaN or out-of-range data only) the
+    // chunk is computed again with the clamps and NaN codes, and the amax
+    // over its non-NaN values.
+    float mc = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int item = 8 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
-      const int c = 64 * slab + 16 * (lane & 3);
-      const int64_t t = m0 + half_tile_row(lr, P);
-      const intx4 h0 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c);
-      const intx4 h1 = *reinterpret_cast<const intx4*>(DH + lr * kBf16Stride + 2 * c + 16);
-      // The 16 values' unclamped codes and their NaN-propagating maximum
-      // magnitude (the first maximum3 of each group of four takes the
-      // running maximum): when it is inside the e5m2 range (after scaling)
-      // no clamp can act and no NaN needs its code, so the codes are
-      // exact; otherwise (wave-uniform, NaN or out-of-range data only) the
-      // chunk is computed again with the clamps and NaN codes, and the amax
-      // over its non-NaN values.
-      uint32_t pg[4], pu[4];
-      float mc = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      float dg[4], du[4];
+      dgrad_swiglu4(h0, h1, (uint32_t)wg[k][w], (uint32_t)wu[k][w], w, dg, du);
+      mc = max3_nan(mc, fabsf(dg[0]), fabsf(du[0]));
+      mc = max3_nan(mc, fabsf(dg[1]), fabsf(du[1]));
+      mc = max3_nan(mc, fabsf(dg[2]), fabsf(du[2]));
+      mc = max3_nan(mc, fabsf(dg[3]), fabsf(du[3]));
+      // the unclamped packs overwrite both halves of their third argument:
+      // the dead dh words, rather than a copy of a live register
+      pg[w] = pack4_e5m2_scaled_noclamp(dg[0], dg[1], dg[2], dg[3], inv3,
+                                        (uint32_t)(w < 2 ? h0[2 * w] : h1[2 * w - 4]));
+      pu[w] = pack4_e5m2_scaled_noclamp(du[0], du[1], du[2], du[3], inv3,
+                                        (uint32_t)(w < 2 ? h0[2 * w + 1] : h1[2 * w - 3]));
+    }
+    if (__builtin_amdgcn_ballot_w64(!(mc <= bnd3))) {
+      asm volatile("" ::: "memory");
+      mc = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         float dg[4], du[4];
         dgrad_swiglu4(h0, h1, (uint32_t)wg[k][w], (uint32_t)wu[k][w], w, dg, du);
-        mc = max3_nan(mc, fabsf(dg[0]), fabsf(du[0]));
-        mc = max3_nan(mc, fabsf(dg[1]), fabsf(du[1]));
-        mc = max3_nan(mc, fabsf(dg[2]), fabsf(du[2]));
-        mc = max3_nan(mc, fabsf(dg[3]), fabsf(du[3]));
-        // the unclamped packs overwrite both halves of their third argument:
-        // the dead dh words, rather than a copy of a live register
-        pg[w] = pack4_e5m2_scaled_noclamp(dg[0], dg[1], dg[2], dg[3], inv3,
-                                          (uint32_t)(w < 2 ? h0[2 * w] : h1[2 * w - 4]));
-        pu[w] = pack4_e5m2_scaled_noclamp(du[0], du[1], du[2], du[3], inv3,
-                                          (uint32_t)(w < 2 ? h0[2 * w + 1] : h1[2 * w - 3]));
-      }
-      if (__builtin_amdgcn_ballot_w64(!(mc <= bnd3))) {
-        asm volatile("" ::: "memory");
-        mc = 0.f;
+        pg[w] = fix_nan4(pack4_e5m2_scaled(dg[0], dg[1], dg[2], dg[3], inv3, bnd3), dg[0], dg[1], dg[2], dg[3]);
+        pu[w] = fix_nan4(pack4_e5m2_scaled(du[0], du[1], du[2], du[3], inv3, bnd3), du[0], du[1], du[2], du[3]);
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          float dg[4], du[4];
-          dgrad_swiglu4(h0, h1, (uint32_t)wg[k][w], (uint32_t)wu[k][w], w, dg, du);
-          pg[w] = fix_nan4(pack4_e5m2_scaled(dg[0], dg[1], dg[2], dg[3], inv3, bnd3), dg[0], dg[1], dg[2], dg[3]);
-          pu[w] = fix_nan4(pack4_e5m2_scaled(du[0], du[1], du[2], du[3], inv3, bnd3), du[0], du[1], du[2], du[3]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mc = fmaxf(mc, fmaxf(fabsf(dg[e]), fabsf(du[e])));
-        }
-      }
-      m3 = fmaxf(m3, mc);
-      if (dgu8t) {  // staged for the token-contiguous copy
-        store16(G2 + lr * kEpiStride2 + c, pg);
-        store16(U2 + lr * kEpiStride2 + c, pu);
-      }
-      // dgu8 is a K-slab [2I/64][ldt][64]; four lanes write one 64-byte row
-      if (c < cols) {
-        const int64_t j = n0 + c;
-        store16(dgu8 + (j >> 6) * ldt * 64 + t * 64 + (j & 63), pg);
-        store16(dgu8 + ((I + j) >> 6) * ldt * 64 + t * 64 + (j & 63), pu);
+        for (int e = 0; e < 4; ++e) mc = fmaxf(mc, fmaxf(fabsf(dg[e]), fabsf(du[e])));
       }
     }
-    __syncthreads();
-    // the token-contiguous dgu8t: local rows 0-63 are tile rows 64P.., rows
-    // 64-127 tile rows 128 + 64P.. (rows past T hold zero codes)
-    if (dgu8t) {
+    m3 = fmaxf(m3, mc);
+    if constexpr (TCOPY) {  // staged for the token-contiguous copy
+      store16(G2 + lr * kEpiStride2 + c, pg);
+      store16(U2 + lr * kEpiStride2 + c, pu);
+    }
+  };
+  // dgu8 is a K-slab [2I/64][ldt][64]; four lanes write one 64-byte row
+  const auto store_chunk = [&](int P, int k, const uint32_t (&pg)[4], const uint32_t (&pu)[4]) {
+    const int item = 8 * k + wave, slab = item & 3, lr = 16 * (item >> 2) + (lane >> 2);
+    const int c = 64 * slab + 16 * (lane & 3);
+    const uint32_t o = gu_off(c, half_tile_row(lr, P));
+    __builtin_amdgcn_raw_buffer_store_b128(intx4{(int)pg[0], (int)pg[1], (int)pg[2], (int)pg[3]}, rdg, o, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(intx4{(int)pu[0], (int)pu[1], (int)pu[2], (int)pu[3]}, rdg,
+                                           o + (uint32_t)(I * ldt), 0, 0);
+  };
+  if constexpr (TCOPY) {
+#pragma unroll
+    for (int P = 0; P < 2; ++P) {
+      gu_loads(P);
+      if (P == 1) __syncthreads();  // pass 0's dgu8t copy has read the LDS
+      // dh rounded to bf16 (train.py:1082)
+      if (P == 0) stage_bf16_half8<0>(DH, acc, 1.0f);
+      else stage_bf16_half8<1>(DH, acc, 1.0f);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t pg[4], pu[4];
+        swiglu_chunk(P, k, pg, pu);
+        store_chunk(P, k, pg, pu);
+      }
+      __syncthreads();
+      // the token-contiguous dgu8t: local rows 0-63 are tile rows 64P.., rows
+      // 64-127 tile rows 128 + 64P.. (rows past T hold zero codes)
       const int64_t rp2 = slab_rows(2 * I);
       lds_rows_store_slab_tr<64, 8>(G2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, n0);
       lds_rows_store_slab_tr<64, 8>(G2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, n0);
       lds_rows_store_slab_tr<64, 8>(U2, cols, kEpiStride2, dgu8t, rp2, m0 + 64 * P, I + n0);
-      lds_rows_store_slab_tr<64, 8>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P, I + n0);
+      lds_rows_store_slab_tr<64, 8>(U2 + 64 * kEpiStride2, cols, kEpiStride2, dgu8t, rp2, m0 + 128 + 64 * P,
+                                    I + n0);
     }
+    __syncthreads();  // the next tile's DMA overwrites the staging tiles
+  } else {
+    // Each chunk is stored as soon as its codes are made, so that the stores
+    // drain while the rest is computed.  (Deferring the first pass's stores
+    // behind the second pass's gu8 requests, so that waiting for those
+    // leaves the stores in flight, measured 2 % slower.)  The second pass's
+    // gu8 words are requested before its staging.
+    uint32_t pg[4][4], pu[4][4];
+    gu_loads(0);
+    stage_bf16_half8<0>(DH, acc, 1.0f);  // dh rounded to bf16 (train.py:1082)
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      swiglu_chunk(0, k, pg[k], pu[k]);
+      store_chunk(0, k, pg[k], pu[k]);
+    }
+    gu_loads(1);
+    __syncthreads();  // every wave has read pass 0's staged rows
+    stage_bf16_half8<1>(DH, acc, 1.0f);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      swiglu_chunk(1, k, pg[k], pu[k]);
+      store_chunk(1, k, pg[k], pu[k]);
+    }
+    __syncthreads();  // the next tile's DMA overwrites the staging tile
   }
-  __syncthreads();  // the next tile's DMA overwrites the staging tiles
   }
   m3 *= 1.0f / scale[1];  // s_gu, read again rather than held across the tile loop
   block_amax_atomic<8>(m3, red, amax + 3);
@@ -1218,11 +1287,11 @@ __global__ __launch_bounds__(512, 1) void gateup_dgrad_kernel(
   const float sab = (1.0f / scale[3]) * (1.0f / wscale[0]);  // both powers of two
   stage_bf16_half8<0>(lds, acc, sab);
   __syncthreads();
-  write_bf16_half<512>(lds, 0, u0, n0, uend, D, D, nullptr, dxn);
+  write_bf16_half<512>(lds, 0, u0, n0, uend, D, D, dxn);
   __syncthreads();
   stage_bf16_half8<1>(lds, acc, sab);
   __syncthreads();
-  write_bf16_half<512>(lds, 1, u0, n0, uend, D, D, nullptr, dxn);
+  write_bf16_half<512>(lds, 1, u0, n0, uend, D, D, dxn);
 }
 
 // ---------------------------------------------------------------------------
@@ -1619,11 +1688,11 @@ __global__ __launch_bounds__(512, 1) void bf16_gemm_kernel(
       (int)(Kb / kStage), acc);
   stage_bf16_half8<0>(lds, acc, 1.0f);
   __syncthreads();
-  write_bf16_half<512>(lds, 0, u0, n0, uend, N, N, nullptr, out);
+  write_bf16_half<512>(lds, 0, u0, n0, uend, N, N, out);
   __syncthreads();
   stage_bf16_half8<1>(lds, acc, 1.0f);
   __syncthreads();
-  write_bf16_half<512>(lds, 1, u0, n0, uend, N, N, nullptr, out);
+  write_bf16_half<512>(lds, 1, u0, n0, uend, N, N, out);
 }
 
 // The bf16 weight gradient's reduction: out[m, n] = bf16(sum over s
@@ -1836,7 +1905,7 @@ int sfp8_gemm_down_fwd(const void* h8, const void* wd8, const void* res, int64_t
                        const float* scale, const float* wscale, void* y, int64_t ldt, void* stream) {
   if (!wd8 || !scale || !wscale || (T > 0 && (!h8 || !res || !y))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || I % (2 * kStage) || D % 16 || ldt < T || ldt % kTile) return kErrBadShape;
-  if (!fits32(ldt, I) || !fits32(slab_rows(D), I)) return kErrBadShape;
+  if (!fits32(ldt, I) || !fits32(slab_rows(D), I) || !fits32(kTile, 2 * D)) return kErrBadShape;
   if (!al16(h8) || !al16(wd8) || !al16(res) || !al16(y)) return kErrBadAlignment;
   if (T == 0) return kOk;
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
@@ -1863,9 +1932,10 @@ int sfp8_gemm_down_dgrad_swiglu(const void* dy, const void* wdt, const void* gu8
   int rc = cu_count(&n_cu);
   if (rc) return rc;
   const int grid = ntiles < n_cu ? ntiles : n_cu;
-  rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
+  const auto kern = dgu8t ? down_dgrad_swiglu_kernel<true> : down_dgrad_swiglu_kernel<false>;
+  rc = prep(kern, kDgradLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(grid), dim3(512), kDgradLds, (hipStream_t)stream,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(512), kDgradLds, (hipStream_t)stream,
                      (const uint16_t*)dy, (const uint16_t*)wdt, (const uint8_t*)gu8, T, D, I, scale, amax,
                      (uint8_t*)dgu8, (uint8_t*)dgu8t, ldt, tiles_m, tiles_n, (const int*)nullptr, (int64_t)0);
   return status();
@@ -1875,7 +1945,7 @@ int sfp8_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t T, int64_t
                            const float* scale, const float* wscale, void* dxn, int64_t ldt, void* stream) {
   if (!w8t || !scale || !wscale || (T > 0 && (!dgu8 || !dxn))) return kErrNullPointer;
   if (T < 0 || D <= 0 || I <= 0 || (2 * I) % (2 * kStage) || D % 16 || ldt < T || ldt % kTile) return kErrBadShape;
-  if (!fits32(ldt, 2 * I) || !fits32(slab_rows(D), 2 * I)) return kErrBadShape;
+  if (!fits32(ldt, 2 * I) || !fits32(slab_rows(D), 2 * I) || !fits32(kTile, 2 * D)) return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dxn)) return kErrBadAlignment;
   if (T == 0) return kOk;
   const int tiles_m = cdiv(T, kTile), tiles_n = cdiv(D, kTile);
@@ -2025,7 +2095,8 @@ int sfp8_moe_gemm_gateup_swiglu_fwd(const void* x8, const void* w8, int64_t E, i
 int sfp8_moe_gemm_down_fwd(const void* h8, const void* wd8, int64_t E, int64_t D, int64_t I, const int* plan,
                            int64_t ldp, const float* scale, const float* q_d, void* out, int64_t R, void* stream) {
   if (!h8 || !wd8 || !plan || !scale || !q_d || (R > 0 && !out)) return kErrNullPointer;
-  if (!moe_shape(E, D, I, ldp) || R < 0 || !fits32(ldp, I) || !fits32(slab_rows(D), I)) return kErrBadShape;
+  if (!moe_shape(E, D, I, ldp) || R < 0 || !fits32(ldp, I) || !fits32(slab_rows(D), I) || !fits32(kTile, 2 * D))
+    return kErrBadShape;
   if (!al16(h8) || !al16(wd8) || !al16(out)) return kErrBadAlignment;
   const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(D, kTile);
   int rc = prep(down_fwd_kernel, kMainLds);
@@ -2048,9 +2119,10 @@ int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const voi
   if (rc) return rc;
   const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(I, kTile);
   const int ntiles = tiles_m * tiles_n;  // an upper bound: the kernel reads the plan's count
-  rc = prep(down_dgrad_swiglu_kernel, kDgradLds);
+  const auto kern = dgu8t ? down_dgrad_swiglu_kernel<true> : down_dgrad_swiglu_kernel<false>;
+  rc = prep(kern, kDgradLds);
   if (rc) return rc;
-  hipLaunchKernelGGL(down_dgrad_swiglu_kernel, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(512), kDgradLds,
+  hipLaunchKernelGGL(kern, dim3(ntiles < n_cu ? ntiles : n_cu), dim3(512), kDgradLds,
                      (hipStream_t)stream, (const uint16_t*)dout, (const uint16_t*)wdt, (const uint8_t*)gu8, R, D, I,
                      scale, amax, (uint8_t*)dgu8, (uint8_t*)dgu8t, ldp, tiles_m, tiles_n, plan,
                      2 * D * slab_rows(I));
@@ -2060,7 +2132,9 @@ int sfp8_moe_gemm_down_dgrad_swiglu(const void* dout, const void* wdt, const voi
 int sfp8_moe_gemm_gateup_dgrad(const void* dgu8, const void* w8t, int64_t E, int64_t D, int64_t I, const int* plan,
                                int64_t ldp, const float* scale, const float* q_gu, void* dx, int64_t R, void* stream) {
   if (!dgu8 || !w8t || !plan || !scale || !q_gu || (R > 0 && !dx)) return kErrNullPointer;
-  if (!moe_shape(E, D, I, ldp) || R < 0 || !fits32(ldp, 2 * I) || !fits32(slab_rows(D), 2 * I)) return kErrBadShape;
+  if (!moe_shape(E, D, I, ldp) || R < 0 || !fits32(ldp, 2 * I) || !fits32(slab_rows(D), 2 * I) ||
+      !fits32(kTile, 2 * D))
+    return kErrBadShape;
   if (!al16(dgu8) || !al16(w8t) || !al16(dx)) return kErrBadAlignment;
   const int tiles_m = (int)(ldp / kTile), tiles_n = cdiv(D, kTile);
   int rc = prep(gateup_dgrad_kernel, kMainLds);
@@ -2225,7 +2299,7 @@ int sfp8_bf16_gemm(const void* a, const void* b, int64_t T, int64_t N, int64_t K
                    void* stream) {
   if (!b || (T > 0 && (!a || !out))) return kErrNullPointer;
   if (T < 0 || N <= 0 || N % 8 || K <= 0 || K % 32 || lda < T || lda % kTile) return kErrBadShape;
-  if (!fits32(lda, 2 * K) || !fits32(slab_rows(N), 2 * K)) return kErrBadShape;
+  if (!fits32(lda, 2 * K) || !fits32(slab_rows(N), 2 * K) || !fits32(kTile, 2 * N)) return kErrBadShape;
   if (!al16(a) || !al16(b) || !al16(out)) return kErrBadAlignment;
   if (T == 0) return kOk;
   return bf16_gemm_launch(a, b, T, N, K, lda, out, nullptr, cdiv(T, kTile), (hipStream_t)stream);
