@@ -379,7 +379,10 @@ struct SwigluPipe {
     float s0, s1, s2;  // scale[0], scale[1], scale[2]
     float mx_gu, mx_h;  // amax so far, dequantized
     int64_t T, I, ldt;
-    uint8_t* gu8;
+    // gu8 (the K-slab [2I/64][ldt][64]) and the previous tile's byte offsets
+    // in it: gate block (pn0/64, rows pm0..) and up block (I + pn0)/64
+    __amdgpu_buffer_rsrc_t rgu;
+    uint32_t so_g, so_u;
     uint8_t* h8;
   };
 
@@ -510,13 +513,16 @@ struct SwigluPipe {
     c.bad = false;
     const int row = 32 * TB * wm + 32 * RB + fr;
     const int col = 32 * wn + 16 * g;
-    const int64_t t = c.pm0 + row;
     if (c.prev) {
       // gu8 is a K-slab [2I/64][ldt][64], h8 one of [I/64][ldt][64]: the
       // tile's 64 gate, 64 up and 64 h columns are one block each (rows past
-      // T hold the zeros computed from x8's zero padding)
-      store16(c.gu8 + (c.pn0 >> 6) * c.ldt * 64 + t * 64 + col, c.gw);
-      store16(c.gu8 + ((c.I + c.pn0) >> 6) * c.ldt * 64 + t * 64 + col, c.uw);
+      // T hold the zeros computed from x8's zero padding); the block's
+      // origin is the store's scalar offset
+      const uint32_t vo = (uint32_t)(row * 64 + col);
+      __builtin_amdgcn_raw_buffer_store_b128(intx4{(int)c.gw[0], (int)c.gw[1], (int)c.gw[2], (int)c.gw[3]},
+                                             c.rgu, vo, (int)c.so_g, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(intx4{(int)c.uw[0], (int)c.uw[1], (int)c.uw[2], (int)c.uw[3]},
+                                             c.rgu, vo, (int)c.so_u, 0);
     }
     store16(c.hbuf + row * kPipeHStride + col, c.hw);
   }
@@ -656,7 +662,8 @@ __global__ __launch_bounds__(TB == 4 ? 256 : 512, 1) void swiglu_pipe_kernel(
   c.T = T;
   c.I = I;
   c.ldt = ldt;
-  c.gu8 = gu8;
+  c.rgu = make_rsrc(gu8, 2 * I * ldt);
+  c.so_g = c.so_u = 0u;
   c.h8 = h8;
   c.bad = false;
 #pragma unroll
@@ -753,6 +760,8 @@ __global__ __launch_bounds__(TB == 4 ? 256 : 512, 1) void swiglu_pipe_kernel(
     c.prev = true;
     c.pm0 = m0;
     c.pn0 = n0;
+    c.so_g = (uint32_t)((n0 >> 6) * ldt * 64 + m0 * 64);
+    c.so_u = (uint32_t)(((I + n0) >> 6) * ldt * 64 + m0 * 64);
     c.hbuf = lds + kPipeRing + (it & 1) * kPipeHBytes;
     // the previous epilogue is complete: its amax joins, and this tile's
     // weight scale sets the next epilogue's constants
