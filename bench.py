@@ -311,8 +311,9 @@ def block_work(T: int, D: int, I: int) -> dict:
     """FLOP (or algorithmic bytes) per launch of each kernel of one block."""
     return {
         "norm_quant": (None, T * (3.0 * D + 4)),
-        "weight_quant_gu": (None, 10.0 * 2 * I * D),
-        "weight_quant_down": (None, 11.0 * D * I),
+        # the post-step hook: scale roll + both weight quantizations (fp32
+        # masters read twice, e4m3 copies, W_gu^T e4m3, W_down^T bf16)
+        "post_step_quant": (None, 10.0 * 2 * I * D + 11.0 * D * I + 40.0),
         "gateup_swiglu_fwd": (4.0 * T * D * I, None),
         "down_fwd": (2.0 * T * D * I, None),
         "down_dgrad_swiglu_bf16": (2.0 * T * D * I, None),
@@ -320,7 +321,6 @@ def block_work(T: int, D: int, I: int) -> dict:
         "norm_bwd": (None, T * (9.0 * D + 4)),
         "wgrad_down": (2.0 * T * D * I, None),
         "wgrad_gateup": (4.0 * T * D * I, None),
-        "update_scales": (None, 40.0),
     }
 
 
@@ -422,7 +422,8 @@ def launch_name(sym: str, a, D: int, I: int) -> str:
     return {"sfp8_norm_quant": "norm_quant", "sfp8_gemm_gateup_swiglu_fwd": "gateup_swiglu_fwd",
             "sfp8_gemm_down_fwd": "down_fwd", "sfp8_gemm_down_dgrad_swiglu": "down_dgrad_swiglu_bf16",
             "sfp8_gemm_gateup_dgrad": "gateup_dgrad", "sfp8_norm_bwd": "norm_bwd",
-            "sfp8_update_scales": "update_scales", "sfp8_moe_plan": "moe_plan",
+            "sfp8_update_scales": "update_scales", "sfp8_block_weight_quant": "post_step_quant",
+            "sfp8_moe_plan": "moe_plan",
             "sfp8_moe_gemm_gateup_swiglu_fwd": "moe_gateup_swiglu_fwd", "sfp8_moe_gemm_down_fwd": "moe_down_fwd",
             "sfp8_moe_gemm_down_dgrad_swiglu": "moe_down_dgrad_swiglu_bf16",
             "sfp8_moe_gemm_gateup_dgrad": "moe_gateup_dgrad", "sfp8_moe_topk_sum": "moe_topk_sum"}.get(sym, sym)
@@ -709,10 +710,8 @@ def main() -> None:
             "elements": {"x": T * D, "gu": 2 * T * I, "h": T * I, "d_gu": 2 * T * I, "dy": T * D}}
         kern = {
             "norm_quant": lambda: ops.norm_quant(h, nwd, scale, amax, 1e-6, copy=False),
-            "weight_quant_gu": lambda: ops.weight_quant(mlp.gate_up_proj.weight.detach(), wscale[0:1], w8=True,
-                                                        w8t=True),
-            "weight_quant_down": lambda: ops.weight_quant(mlp.down_proj.weight.detach(), wscale[1:2], w8=True,
-                                                          bf16t=True),
+            "post_step_quant": lambda: ops.block_weight_quant(mlp.gate_up_proj.weight.detach(),
+                                                             mlp.down_proj.weight.detach()),
             "gateup_swiglu_fwd": lambda: ops.gateup_swiglu_fwd(x8, w8, scale, wscale, amax, T, I, copy=False),
             "down_fwd": lambda: ops.down_fwd(h8, wd8, h, scale, wscale),
             "down_dgrad_swiglu_bf16": lambda: ops.down_dgrad_swiglu(dy, wdt, gu8, scale, amax, copy=False),

@@ -111,6 +111,18 @@ int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partial
  * with amax > 0 gets scale = exp2(floor(log2(fmax/amax)) - 1); amax = 0. */
 int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream);
 
+/* The post-step hook of one dense block (fp8_update_scales followed by the
+ * two just-in-time weight quantizations, train.py:937-952, 1211-1212) in two
+ * launches instead of five: sfp8_update_scales of the block's 5 slots (skipped
+ * when scale and amax are both null), then
+ *   sfp8_weight_quant(w_gu, gu_rows, gu_cols, .., q_out + 0, w8, w8t, null) and
+ *   sfp8_weight_quant(w_down, d_rows, d_cols, .., q_out + 1, wd8, null, wdt),
+ * with the same outputs byte for byte.  partials: nparts_cap >= 1024 floats.
+ * gu_rows, gu_cols, d_cols % 64 == 0, d_rows % 32 == 0; every output given. */
+int sfp8_block_weight_quant(const float* w_gu, int64_t gu_rows, int64_t gu_cols, const float* w_down, int64_t d_rows,
+                            int64_t d_cols, float* partials, int64_t nparts_cap, float* q_out, void* w8, void* w8t,
+                            void* wd8, void* wdt, float* scale, float* amax, void* stream);
+
 /* ---- GEMMs -------------------------------------------------------------- */
 
 /* gate/up forward + SwiGLU epilogue, replaces _fp8_swiglu_fwd_kernel

@@ -26,6 +26,7 @@ SIGNATURES = {
     "sfp8_norm_quant": (_INT, [_P, _P, _I64, _I64, _F32, _P, _P, _P, _P, _I64, _P, _P]),
     "sfp8_weight_quant": (_INT, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P]),
     "sfp8_update_scales": (_INT, [_P, _P, _I64, _P]),
+    "sfp8_block_weight_quant": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sfp8_gemm_gateup_swiglu_fwd": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "sfp8_gemm_down_fwd": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "sfp8_gemm_down_dgrad_swiglu": (_INT, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),

@@ -453,16 +453,14 @@ constexpr int WQ_PARTS = 512;
 
 // Expert e = blockIdx.y of a batch (E matrices of n elements, partials
 // gridDim.x per expert); a dense weight is the batch of one.
-__global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restrict__ w, int64_t n,
-                                                           float* __restrict__ partials) {
+// Block b of nb: the max |w| over its grid-stride share of w[0, n), to partials[b].
+SFP8_DEV void weight_amax_block(const float* __restrict__ w, int64_t n, int b, int nb, float* __restrict__ partials) {
   __shared__ float red[4];
-  w += (int64_t)blockIdx.y * n;
-  partials += (int64_t)blockIdx.y * gridDim.x;
   float m = 0.0f;
   const int64_t n4 = n >> 2;
-  const int64_t step = (int64_t)gridDim.x * 256;
+  const int64_t step = (int64_t)nb * 256;
   const floatx4* w4 = reinterpret_cast<const floatx4*>(w);
-  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  int64_t i = (int64_t)b * 256 + threadIdx.x;
   // four independent loads in flight per trip
   for (; i + 3 * step < n4; i += 4 * step) {
     floatx4 v[4];
@@ -476,40 +474,34 @@ __global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restric
     const floatx4 v = w4[i];
     m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
   }
-  if (blockIdx.x == 0)
+  if (b == 0)
     for (int64_t i = (n4 << 2) + threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(w[i]));
   m = wave_max(m);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) red[wid] = m;
   __syncthreads();
-  if (threadIdx.x == 0) partials[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  if (threadIdx.x == 0) partials[b] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void weight_amax_kernel(const float* __restrict__ w, int64_t n,
+                                                           float* __restrict__ partials) {
+  weight_amax_block(w + (int64_t)blockIdx.y * n, n, blockIdx.x, gridDim.x,
+                    partials + (int64_t)blockIdx.y * gridDim.x);
 }
 
 constexpr int WQ_TILE = 64;
 
-__global__ __launch_bounds__(256) void weight_quant_kernel(
-    const float* __restrict__ w, int64_t R, int64_t C, const float* __restrict__ partials, int nparts,
-    float* __restrict__ q_out, uint8_t* __restrict__ w8, uint8_t* __restrict__ w8t,
-    uint16_t* __restrict__ wbt) {
+// Tile (bx, by) of one matrix: rows 64 bx.., columns 64 by.. (the tiles
+// cover rows and columns up to multiples of 256, so that the padding rows of
+// every K-slab output are written, as zeros).
+SFP8_DEV void weight_quant_tile(const float* __restrict__ w, int64_t R, int64_t C, const float* __restrict__ partials,
+                                int nparts, float* __restrict__ q_out, uint8_t* __restrict__ w8,
+                                uint8_t* __restrict__ w8t, uint16_t* __restrict__ wbt, int bx, int by) {
   __shared__ float red[4];
   __shared__ float qs;
   __shared__ __align__(16) uint8_t t8[WQ_TILE * (WQ_TILE + 8)];
   __shared__ __align__(16) uint16_t t16[WQ_TILE * (WQ_TILE + 2)];
-  {
-    // expert e = blockIdx.z of a batch: its matrix, partials, scale and the
-    // three K-slab copies (each a whole K-slab per expert)
-    const int64_t e = blockIdx.z;
-    const int64_t rp_ = (R + 255) / 256 * 256, cp_ = (C + 255) / 256 * 256;
-    w += e * R * C;
-    partials += e * nparts;
-    q_out += e;
-    if (w8) w8 += e * C * rp_;
-    if (w8t) w8t += e * R * cp_;
-    if (wbt) wbt += e * R * cp_;
-  }
-  // The grid covers rows and columns up to multiples of 256, so that the
-  // padding rows of every K-slab output are written (as zeros).
-  const int64_t r0 = (int64_t)blockIdx.x * WQ_TILE, c0 = (int64_t)blockIdx.y * WQ_TILE;
+  const int64_t r0 = (int64_t)bx * WQ_TILE, c0 = (int64_t)by * WQ_TILE;
   const int64_t rp = (R + 255) / 256 * 256, cp = (C + 255) / 256 * 256;
   // each thread: 4 consecutive columns of 4 rows (64x64 tile = 1024 quads);
   // the tile's loads are issued first, so their latency overlaps the fold
@@ -532,7 +524,7 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
     const float a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float q = pow2_scale(a, kE4M3Max, 0, true);
     qs = q;
-    if (blockIdx.x == 0 && blockIdx.y == 0) *q_out = q;
+    if (bx == 0 && by == 0) *q_out = q;
   }
   __syncthreads();
   const float q = qs;
@@ -576,6 +568,59 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(
           intx4{(int)src[0], (int)src[1], (int)src[2], (int)src[3]};
     }
   }
+}
+
+__global__ __launch_bounds__(256) void weight_quant_kernel(
+    const float* __restrict__ w, int64_t R, int64_t C, const float* __restrict__ partials, int nparts,
+    float* __restrict__ q_out, uint8_t* __restrict__ w8, uint8_t* __restrict__ w8t,
+    uint16_t* __restrict__ wbt) {
+  // expert e = blockIdx.z of a batch: its matrix, partials, scale and the
+  // three K-slab copies (each a whole K-slab per expert)
+  const int64_t e = blockIdx.z;
+  const int64_t rp = (R + 255) / 256 * 256, cp = (C + 255) / 256 * 256;
+  weight_quant_tile(w + e * R * C, R, C, partials + e * nparts, nparts, q_out + e, w8 ? w8 + e * C * rp : nullptr,
+                    w8t ? w8t + e * R * cp : nullptr, wbt ? wbt + e * R * cp : nullptr, blockIdx.x, blockIdx.y);
+}
+
+// --------------------------------------------------------------------------
+// The post-step quantization of one dense block in two launches instead of
+// five: the gate/up master W_gu [R0, C0] -> w8, w8t and the down master
+// W_down [R1, C1] -> wd8, wdt (bf16 K-slab of its transpose), with the
+// delayed-scale roll of the block's 5 slots done by the first launch's
+// block (0, 0) (the roll and the quantizations share no data).
+struct WeightPair {
+  const float* w[2];
+  int64_t R[2], C[2];
+  float* partials;  // WQ_PARTS per matrix
+  int nparts[2];
+  float* q_out;     // [q_gu, q_d]
+  uint8_t* w8[2];
+  uint8_t* w8t;     // W_gu's
+  uint16_t* wbt;    // W_down's
+  int tiles_r[2], tiles_c[2];
+  float* scale;     // the 5 slots to roll, or null
+  float* amax;
+};
+
+__global__ __launch_bounds__(256) void weight_amax_pair_kernel(WeightPair p) {
+  const int j = blockIdx.y;
+  if (j == 0 && blockIdx.x == 0 && p.scale && threadIdx.x < 5) {
+    const int slot = threadIdx.x;
+    const float a = p.amax[slot];
+    if (a > 0.0f) p.scale[slot] = pow2_scale(a, slot < 3 ? kE4M3Max : kE5M2Max, 1, false);
+    p.amax[slot] = 0.0f;
+  }
+  if ((int)blockIdx.x >= p.nparts[j]) return;  // work-group uniform
+  weight_amax_block(p.w[j], p.R[j] * p.C[j], blockIdx.x, p.nparts[j], p.partials + j * WQ_PARTS);
+}
+
+// 1-D grid: W_gu's tiles (row-major over tiles_r[0] x tiles_c[0]), then W_down's.
+__global__ __launch_bounds__(256) void weight_quant_pair_kernel(WeightPair p) {
+  int t = blockIdx.x;
+  const int j = t < p.tiles_r[0] * p.tiles_c[0] ? 0 : 1;
+  if (j) t -= p.tiles_r[0] * p.tiles_c[0];
+  weight_quant_tile(p.w[j], p.R[j], p.C[j], p.partials + j * WQ_PARTS, p.nparts[j], p.q_out + j, p.w8[j],
+                    j ? nullptr : p.w8t, j ? p.wbt : nullptr, t / p.tiles_c[j], t % p.tiles_c[j]);
 }
 
 // --------------------------------------------------------------------------
@@ -1108,6 +1153,46 @@ int sfp8_weight_quant(const float* w, int64_t rows, int64_t cols, float* partial
 int sfp8_weight_quant_experts(const float* w, int64_t E, int64_t rows, int64_t cols, float* partials,
                               int64_t nparts_cap, float* q_out, void* w8, void* w8t, void* wbf16t, void* stream) {
   return weight_quant_batch(w, E, rows, cols, partials, nparts_cap, q_out, w8, w8t, wbf16t, (hipStream_t)stream);
+}
+
+int sfp8_block_weight_quant(const float* w_gu, int64_t gu_rows, int64_t gu_cols, const float* w_down, int64_t d_rows,
+                            int64_t d_cols, float* partials, int64_t nparts_cap, float* q_out, void* w8, void* w8t,
+                            void* wd8, void* wdt, float* scale, float* amax, void* stream) {
+  if (!w_gu || !w_down || !partials || !q_out || !w8 || !w8t || !wd8 || !wdt || (!scale != !amax))
+    return kErrNullPointer;
+  if (gu_rows <= 0 || gu_cols <= 0 || d_rows <= 0 || d_cols <= 0 || gu_cols % 64 || gu_rows % 64 || d_cols % 64 ||
+      d_rows % 32)
+    return kErrBadShape;
+  if (nparts_cap < 2 * WQ_PARTS) return kErrWorkspaceTooSmall;
+  if (!aligned16(w_gu) || !aligned16(w_down)) return kErrBadAlignment;
+  WeightPair p{};
+  p.w[0] = w_gu;
+  p.w[1] = w_down;
+  p.R[0] = gu_rows;
+  p.C[0] = gu_cols;
+  p.R[1] = d_rows;
+  p.C[1] = d_cols;
+  p.partials = partials;
+  for (int j = 0; j < 2; ++j) {
+    int np = (int)((p.R[j] * p.C[j] / 4 + 255) / 256);
+    p.nparts[j] = np > WQ_PARTS ? WQ_PARTS : (np < 1 ? 1 : np);
+    p.tiles_r[j] = (int)((p.R[j] + 255) / 256 * 4);
+    p.tiles_c[j] = (int)((p.C[j] + 255) / 256 * 4);
+  }
+  const int64_t ntiles = (int64_t)p.tiles_r[0] * p.tiles_c[0] + (int64_t)p.tiles_r[1] * p.tiles_c[1];
+  if (ntiles > 0x7fffffff) return kErrBadShape;
+  p.q_out = q_out;
+  p.w8[0] = (uint8_t*)w8;
+  p.w8[1] = (uint8_t*)wd8;
+  p.w8t = (uint8_t*)w8t;
+  p.wbt = (uint16_t*)wdt;
+  p.scale = scale;
+  p.amax = amax;
+  const hipStream_t st = (hipStream_t)stream;
+  const int gx = p.nparts[0] > p.nparts[1] ? p.nparts[0] : p.nparts[1];
+  hipLaunchKernelGGL(weight_amax_pair_kernel, dim3(gx, 2), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(weight_quant_pair_kernel, dim3((unsigned)ntiles), dim3(256), 0, st, p);
+  return launch_status();
 }
 
 int sfp8_update_scales(float* scale, float* amax, int64_t nsets, void* stream) {

@@ -83,10 +83,11 @@ def fp8_update_scales(model: nn.Module) -> None:
         scale = getattr(m, "fp8_scale", None)
         amax = getattr(m, "fp8_amax", None)
         if isinstance(scale, torch.Tensor) and isinstance(amax, torch.Tensor) and scale.numel() == 5:
-            ops.update_scales(scale, amax)
             w_gu, w_down = _dense_weights(m)
-            if w_gu is not None:
-                torch_ops.refresh_weight_cache(w_gu, w_down)
+            # a dense block's re-quantization rolls the scales in its own launches
+            rolled = w_gu is not None and torch_ops.refresh_weight_cache(w_gu, w_down, scale, amax)
+            if not rolled:
+                ops.update_scales(scale, amax)
 
 
 def _dense_weights(m: nn.Module):

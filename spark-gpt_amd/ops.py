@@ -153,6 +153,37 @@ def weight_quant(w: torch.Tensor, q_out: torch.Tensor, *, w8: bool = True, w8t: 
     return o8, o8t, obt
 
 
+def block_weight_quant(w_gu: torch.Tensor, w_down: torch.Tensor, scale=None, amax=None):
+    """Both weight quantizations of a dense block in two launches:
+    (w8, w8t, wd8, wdt, wscale) as weight_quant(w_gu, w8=True, w8t=True) and
+    weight_quant(w_down, w8=True, bf16t=True) return them, wscale = [q_gu,
+    q_d]; with scale and amax, also the delayed-scale roll of those 5 slots
+    (update_scales), in the first launch."""
+    _cuda_contig("w_gu", w_gu, torch.float32, 2)
+    _cuda_contig("w_down", w_down, torch.float32, 2)
+    R0, C0 = w_gu.shape
+    R1, C1 = w_down.shape
+    _need(R0 % 64 == 0 and C0 % 64 == 0, "gate/up weight rows and columns must be multiples of 64")
+    _need(C1 % 64 == 0 and R1 % 32 == 0, "down weight columns must be a multiple of 64, rows of 32")
+    _need(w_down.device == w_gu.device, "weights on one device")
+    if scale is not None or amax is not None:
+        _need(scale is not None and amax is not None, "scale and amax go together")
+        _state(scale, amax)
+        _need(scale.numel() == 5 and amax.numel() == 5, "one 5-slot set")
+        _need(scale.device == w_gu.device and amax.device == w_gu.device, "scale/amax on the weights' device")
+    dev = w_gu.device
+    w8 = kslab_empty(R0, C0, E4M3, dev)
+    w8t = kslab_empty(C0, R0, E4M3, dev)
+    wd8 = kslab_empty(R1, C1, E4M3, dev)
+    wdt = kslab_empty(C1, R1, torch.bfloat16, dev)
+    wscale = torch.empty(2, dtype=torch.float32, device=dev)
+    parts = torch.empty(1024, dtype=torch.float32, device=dev)
+    _lib.call("sfp8_block_weight_quant", w_gu.data_ptr(), R0, C0, w_down.data_ptr(), R1, C1, parts.data_ptr(),
+              parts.numel(), wscale.data_ptr(), w8.data_ptr(), w8t.data_ptr(), wd8.data_ptr(), wdt.data_ptr(),
+              _lib.ptr(scale), _lib.ptr(amax), _lib.stream_of(w_gu))
+    return w8, w8t, wd8, wdt, wscale
+
+
 def update_scales(scale: torch.Tensor, amax: torch.Tensor) -> None:
     """In-place delayed-scale roll of one or more contiguous 5-slot sets."""
     _need(scale.is_cuda and amax.is_cuda, "scale/amax must be device tensors")

@@ -60,22 +60,22 @@ def _wkey(w_gu: Tensor, w_down: Tensor):
             tuple(w_down.shape))
 
 
-def quantize_weights(w_gu: Tensor, w_down: Tensor):
+def quantize_weights(w_gu: Tensor, w_down: Tensor, scale=None, amax=None):
     """(w8, w8t, wd8, wdt, wscale): e4m3 K-slabs of W_gu and its transpose,
     of W_down, the bf16 K-slab of W_down^T and the pow2 weight scales.
     Dense masters (2-D): wscale = [q_gu, q_d] (train.py:949-952, 1211-1213,
-    1224-1225).  Expert masters (3-D, [E, 2I, D] and [E, D, I]): every copy
-    stacked per expert and wscale [2, E] (train.py:1536-1540, 1561-1562,
-    1572-1573)."""
+    1224-1225), both in two launches, which also roll the block's 5 scale
+    slots when scale and amax are given (the post-step hook's update_scales).
+    Expert masters (3-D, [E, 2I, D] and [E, D, I]): every copy stacked per
+    expert and wscale [2, E] (train.py:1536-1540, 1561-1562, 1572-1573);
+    scale and amax must not be given for them."""
     if w_gu.dim() == 3:
+        assert scale is None and amax is None
         wscale = torch.empty(2, w_gu.shape[0], dtype=torch.float32, device=w_gu.device)
         w8, w8t, _ = ops.weight_quant_experts(_master(w_gu), wscale[0], w8=True, w8t=True)
         wd8, _, wdt = ops.weight_quant_experts(_master(w_down), wscale[1], w8=True, bf16t=True)
         return w8, w8t, wd8, wdt, wscale
-    wscale = torch.empty(2, dtype=torch.float32, device=w_gu.device)
-    w8, w8t, _ = ops.weight_quant(_master(w_gu), wscale[0:1], w8=True, w8t=True)
-    wd8, _, wdt = ops.weight_quant(_master(w_down), wscale[1:2], w8=True, bf16t=True)
-    return w8, w8t, wd8, wdt, wscale
+    return ops.block_weight_quant(_master(w_gu), _master(w_down), scale, amax)
 
 
 def _drop_entry(i: int, ref) -> None:
@@ -121,18 +121,22 @@ def op(name: str):
 
 
 @torch.no_grad()
-def refresh_weight_cache(w_gu: Tensor, w_down: Tensor) -> None:
+def refresh_weight_cache(w_gu: Tensor, w_down: Tensor, scale=None, amax=None) -> bool:
     """Re-quantize the cached copies of (w_gu, w_down), if there are any:
     called after the optimizer has written the masters (which it may do
-    without moving their version counters)."""
+    without moving their version counters).  With the block's 5-slot scale
+    and amax (dense masters only), the same launches also roll them; returns
+    whether they did (when nothing was re-quantized, the caller rolls)."""
     with _WLOCK:
         ent = _WCACHE.get(id(w_gu))
     if ent is None or ent[0]() is not w_gu:
-        return
+        return False
     if not FP8_WEIGHT_CACHE or not w_gu.is_cuda:
         _drop_entry(id(w_gu), ent[0])
-        return
-    _store(w_gu, w_down, quantize_weights(w_gu, w_down))
+        return False
+    roll = scale is not None and w_gu.dim() == 2
+    _store(w_gu, w_down, quantize_weights(w_gu, w_down, scale if roll else None, amax if roll else None))
+    return roll
 
 
 def clear_weight_cache() -> None:

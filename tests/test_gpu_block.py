@@ -199,14 +199,22 @@ def test_compiled_block_matches_eager(dev, backend):
 
 
 def _count_weight_quant(monkeypatch):
+    """Counts weight quantizations: one per weight_quant call, two per
+    block_weight_quant call (both masters of a block)."""
     calls = []
     real = sg.ops.weight_quant
+    real_pair = sg.ops.block_weight_quant
 
     def counted(*a, **k):
         calls.append(a[0].shape)
         return real(*a, **k)
 
+    def counted_pair(*a, **k):
+        calls.extend([a[0].shape, a[1].shape])
+        return real_pair(*a, **k)
+
     monkeypatch.setattr(sg.ops, "weight_quant", counted)
+    monkeypatch.setattr(sg.ops, "block_weight_quant", counted_pair)
     return calls
 
 

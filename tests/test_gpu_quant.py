@@ -228,3 +228,35 @@ def test_weight_scale_band(dev):
         sg.ops.weight_quant(w.to(dev), q, w8=True)
         _, rq = O.quantize_weight(w)
         assert q.item() == rq.item(), a
+
+
+@pytest.mark.parametrize("D,I", [(1024, 3072), (256, 1024), (192, 128)])
+def test_block_weight_quant_equals_two_calls(dev, D, I):
+    """The post-step hook's two-launch form (scale roll + both weight
+    quantizations) writes the same bytes as update_scales and the two
+    weight_quant calls, and every output against the reference recipe."""
+    g = torch.Generator().manual_seed(D + I)
+    w_gu = (torch.randn(2 * I, D, generator=g) * D ** -0.5).to(dev)
+    w_d = (torch.randn(D, I, generator=g) * I ** -0.5).to(dev)
+    amax = torch.tensor([3.0, 0.0, 1e-3, 70000.0, float("nan")])
+    scale0 = torch.tensor([1.0, 2.0, 4.0, 8.0, 16.0])
+    s1, a1 = scale0.to(dev), amax.to(dev)
+    s2, a2 = scale0.to(dev), amax.to(dev)
+    w8, w8t, wd8, wdt, ws = sg.ops.block_weight_quant(w_gu, w_d, s1, a1)
+    sg.ops.update_scales(s2, a2)
+    q = torch.empty(2, device=dev)
+    r8, r8t, _ = sg.ops.weight_quant(w_gu, q[0:1], w8=True, w8t=True)
+    rd8, _, rdt = sg.ops.weight_quant(w_d, q[1:2], w8=True, bf16t=True)
+    torch.cuda.synchronize()
+    for a, b in ((w8, r8), (w8t, r8t), (wd8, rd8), (wdt, rdt), (ws, q)):
+        assert torch.equal(a.view(torch.uint8).cpu(), b.view(torch.uint8).cpu())
+    same = (s1.cpu() == s2.cpu()) | (torch.isnan(s1.cpu()) & torch.isnan(s2.cpu()))
+    assert bool(same.all()) and torch.all(a1.cpu() == 0) and torch.all(a2.cpu() == 0)
+    q_ref_gu = O.quantize_weight(w_gu.cpu())[1]
+    q_ref_d = O.quantize_weight(w_d.cpu())[1]
+    assert ws[0].item() == q_ref_gu.item() and ws[1].item() == q_ref_d.item()
+    # without scale and amax nothing is rolled
+    s3, a3 = scale0.to(dev), amax.to(dev)
+    sg.ops.block_weight_quant(w_gu, w_d)
+    torch.cuda.synchronize()
+    assert torch.equal(s3.cpu(), scale0) and torch.equal(a3.cpu().nan_to_num(-1), amax.nan_to_num(-1))
