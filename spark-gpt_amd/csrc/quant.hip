@@ -187,6 +187,12 @@ struct NormCfg {
   static constexpr int PASSES = RT / (BW * RPW);
   static constexpr int LB = (BW == 8 ? 2 : 4) / CPL;  // row chunks per lane in one load batch
   static constexpr int PB_BWD = LB < PASSES ? (LB > 0 ? LB : 1) : PASSES;
+  // norm_bwd loads the next batch while it computes one (two register sets)
+  // at D = 2048 (3 % faster alone); at D = 4096 two sets do not fit the
+  // registers, and up to D = 1024 they need 2 waves per SIMD instead of 4,
+  // which measured 5 % slower in the block's step (as did the same for
+  // norm_quant's batches: no faster)
+  static constexpr bool PIPE_BWD = CPL == 4;
   static_assert(QPASSES % PB == 0 && PASSES % PB_BWD == 0, "whole load batches");
 };
 
@@ -676,12 +682,15 @@ void norm_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) { w[c][j] = a[j]; w[c][4 + j] = b[j]; acc[c][j] = 0.f; acc[c][4 + j] = 0.f; }
   }
-  // wave wid takes row passes wid, wid + BW, ...; PB_BWD passes' loads are
-  // issued before any of them is used
-#pragma unroll 1
-  for (int pb = 0; pb < Cfg::PASSES; pb += Cfg::PB_BWD) {
+  // wave wid takes row passes wid, wid + BW, ...; a batch is PB_BWD passes
+  // whose loads are issued together, and the next batch's loads are issued
+  // before this batch is computed (two register sets, so each wave keeps a
+  // batch of loads in flight while it computes)
+  struct Batch {
     intx4 vh[Cfg::PB_BWD][Cfg::CPL], vg[Cfg::PB_BWD][Cfg::CPL], vd[Cfg::PB_BWD][Cfg::CPL];
     float rsv[Cfg::PB_BWD];
+  };
+  const auto load_batch = [&](int pb, Batch& B) {
 #pragma unroll
     for (int q = 0; q < Cfg::PB_BWD; ++q) {
       const int64_t t = t0 + (wid + Cfg::BW * (pb + q)) * Cfg::RPW + sr;
@@ -690,24 +699,26 @@ void norm_bwd_kernel(
       for (int c = 0; c < Cfg::CPL; ++c) {
         const int d = (c * Cfg::LPR + li) * 8;
         const intx4 z = {0, 0, 0, 0};
-        vh[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(h + t * D + d)) : z;
-        vg[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(dxn + t * D + d)) : z;
-        vd[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(dy + t * D + d)) : z;
+        B.vh[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(h + t * D + d)) : z;
+        B.vg[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(dxn + t * D + d)) : z;
+        B.vd[q][c] = valid ? __builtin_nontemporal_load(reinterpret_cast<const intx4*>(dy + t * D + d)) : z;
       }
-      rsv[q] = valid ? rstd[t] : 0.0f;
+      B.rsv[q] = valid ? rstd[t] : 0.0f;
     }
+  };
+  const auto compute_batch = [&](int pb, const Batch& B) {
 #pragma unroll
     for (int q = 0; q < Cfg::PB_BWD; ++q) {
       const int r = (wid + Cfg::BW * (pb + q)) * Cfg::RPW + sr;
       const int64_t t = t0 + r;
       const bool valid = t < T;
-      const float rs = rsv[q];
+      const float rs = B.rsv[q];
       float S = 0.0f;
 #pragma unroll
       for (int c = 0; c < Cfg::CPL; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const uint32_t uh = (uint32_t)vh[q][c][j >> 1], ug = (uint32_t)vg[q][c][j >> 1];
+          const uint32_t uh = (uint32_t)B.vh[q][c][j >> 1], ug = (uint32_t)B.vg[q][c][j >> 1];
           const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
           const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
           S += (g * w[c][j]) * hf;
@@ -721,8 +732,8 @@ void norm_bwd_kernel(
         float o[8], dyf[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const uint32_t uh = (uint32_t)vh[q][c][j >> 1], ug = (uint32_t)vg[q][c][j >> 1];
-          const uint32_t ud = (uint32_t)vd[q][c][j >> 1];
+          const uint32_t uh = (uint32_t)B.vh[q][c][j >> 1], ug = (uint32_t)B.vg[q][c][j >> 1];
+          const uint32_t ud = (uint32_t)B.vd[q][c][j >> 1];
           const float hf = bf16_bits_to_f32((j & 1) ? (uh >> 16) : (uh & 0xffffu));
           const float g = bf16_bits_to_f32((j & 1) ? (ug >> 16) : (ug & 0xffffu));
           dyf[j] = bf16_bits_to_f32((j & 1) ? (ud >> 16) : (ud & 0xffffu));
@@ -744,6 +755,24 @@ void norm_bwd_kernel(
         // stores from the registers here, where the LDS is needed anyway)
         if (dy8 || dy8t) *reinterpret_cast<intx2*>(tile + r * Cfg::STRIDE + d) = intx2{(int)lo, (int)hi};
       }
+    }
+  };
+  if constexpr (Cfg::PIPE_BWD) {
+    Batch b0, b1;
+    load_batch(0, b0);
+#pragma unroll 1
+    for (int pb = 0; pb < Cfg::PASSES; pb += 2 * Cfg::PB_BWD) {
+      if (pb + Cfg::PB_BWD < Cfg::PASSES) load_batch(pb + Cfg::PB_BWD, b1);
+      compute_batch(pb, b0);
+      if (pb + 2 * Cfg::PB_BWD < Cfg::PASSES) load_batch(pb + 2 * Cfg::PB_BWD, b0);
+      if (pb + Cfg::PB_BWD < Cfg::PASSES) compute_batch(pb + Cfg::PB_BWD, b1);
+    }
+  } else {
+#pragma unroll 1
+    for (int pb = 0; pb < Cfg::PASSES; pb += Cfg::PB_BWD) {
+      Batch b;
+      load_batch(pb, b);
+      compute_batch(pb, b);
     }
   }
   if (dy8 || dy8t) {  // whole slab runs from the tile; rows past T hold zero codes
