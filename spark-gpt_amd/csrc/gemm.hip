@@ -41,17 +41,23 @@ SFP8_DEV void raster(int lid, int tiles_m, int tiles_n, int& tm, int& tn) {
 
 // Work-groups are dispatched round-robin over the 8 XCDs (pid % 8): the
 // logical index of work-group pid of nwg when each XCD (with its own L2)
-// takes a contiguous run of logical indices.  A bijection of [0, nwg).
-SFP8_DEV int xcd_run(int pid, int nwg) {
+// takes a contiguous run of logical indices (walked from its end with rev).
+// A bijection of [0, nwg).
+SFP8_DEV int xcd_run(int pid, int nwg, bool rev = false) {
   const int per = nwg >> 3, rem = nwg & 7;
-  const int xcd = pid & 7, local = pid >> 3;
+  const int xcd = pid & 7;
+  const int len = xcd < rem ? per + 1 : per;
+  const int local = rev ? len - 1 - (pid >> 3) : (pid >> 3);
   return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
 // Work-group -> tile mapping: XCD-contiguous runs of logical tiles, rastered
-// as above.
-SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, int& tn) {
-  raster(xcd_run(pid, nwg), tiles_m, tiles_n, tm, tn);
+// as above.  rev: each XCD walks its run backwards, so that a consumer of the
+// previous kernel's output (run in the same order, forwards) reads the most
+// recently written row blocks first, while they may still be in the memory-
+// side cache.
+SFP8_DEV void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, int& tn, bool rev = false) {
+  raster(xcd_run(pid, nwg, rev), tiles_m, tiles_n, tm, tn);
 }
 
 // Split-K mapping of a 1-D grid of tiles * splits work-groups.  Work-groups
@@ -1274,7 +1280,8 @@ __global__ __launch_bounds__(512, 1) void gateup_dgrad_kernel(
   const int64_t K = 2 * I;
   const int64_t dp = slab_rows(D);
   int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  // backwards: the dgrad wrote d_gu8 in forward order (0.304 -> 0.302 ms)
+  tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn, true);
   int64_t u0 = (int64_t)tm * kTile, uend = T;  // output rows of this tile
   if (plan) {
     const MoePlan P{plan};
