@@ -1604,6 +1604,9 @@ __global__ __launch_bounds__(512, 1) void bf16_swiglu_fwd_kernel(
   const int64_t n0 = (int64_t)tn * 128;
   const int64_t ldx = D * 2;  // bytes per x row = K bytes
   const int64_t wr = slab_rows(2 * I);
+  // the outputs from the tile's first row (gu [rows, 2I], h [rows, I], bf16)
+  const __amdgpu_buffer_rsrc_t rgu = make_rsrc(gu + r0 * 2 * I, nrows * 4 * I);
+  const __amdgpu_buffer_rsrc_t rho = make_rsrc(h + r0 * I, nrows * 2 * I);
   floatx16 acc[4][2];  // [tb][0] gate, [tb][1] up
   // A: x row-major [T, D] (rows past the tile's last read as zero through
   // the range check), or with ldxs > 0 its row K-slab [2D/64][ldxs][64]
@@ -1657,17 +1660,25 @@ __global__ __launch_bounds__(512, 1) void bf16_swiglu_fwd_kernel(
       }
     }
     __syncthreads();
-    // 128 rows x 16 pieces of 16 bytes per output: sixteen lanes per row
-    for (int idx = threadIdx.x; idx < 128 * 16; idx += 512) {
+    // 128 rows x 16 pieces of 16 bytes per output: sixteen lanes per row;
+    // buffer stores from the tile's first row, a piece past the valid rows or
+    // past I (I % 8 == 0: whole pieces) at offset 2^31 (beyond the range:
+    // dropped), so every thread issues the same stores without a branch
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = (int)threadIdx.x + 512 * k;
       const int sr = idx >> 4, c = idx & 15;
       const int lr = half_tile_row(sr, P);
       const int64_t col = n0 + 8 * c;
-      if (lr >= nrows || col >= I) continue;  // I % 8 == 0: whole pieces
-      const int64_t t = r0 + lr;
-      *reinterpret_cast<intx4*>(gu + t * 2 * I + col) = *reinterpret_cast<const intx4*>(Gs + sr * kGuStride + 16 * c);
-      *reinterpret_cast<intx4*>(gu + t * 2 * I + I + col) =
-          *reinterpret_cast<const intx4*>(Us + sr * kGuStride + 16 * c);
-      *reinterpret_cast<intx4*>(h + t * I + col) = *reinterpret_cast<const intx4*>(Hs + sr * kGuStride + 16 * c);
+      const uint32_t in = 0u - (uint32_t)(lr < nrows && col < I);
+      const uint32_t og = ((uint32_t)((lr * 2 * I + col) * 2) & in) | (~in & 0x80000000u);
+      const uint32_t oh = ((uint32_t)((lr * I + col) * 2) & in) | (~in & 0x80000000u);
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const intx4*>(Gs + sr * kGuStride + 16 * c), rgu,
+                                             og, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const intx4*>(Us + sr * kGuStride + 16 * c), rgu,
+                                             og + (uint32_t)(2 * I), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const intx4*>(Hs + sr * kGuStride + 16 * c), rho,
+                                             oh, 0, 0);
     }
   }
 }
@@ -2263,7 +2274,10 @@ int sfp8_moe_gemm_wgrad_rows(const void* a, int fmt_a, int a_rows, const void* b
 
 // ---- bf16 SwiGLU path (the default, non-FP8 path) ----
 namespace {
-inline bool bf16_shape(int64_t D, int64_t I) { return D > 0 && I > 0 && D % 64 == 0 && I % 64 == 0; }
+// (a tile's gu rows, 256 x 2I bf16, are addressed with 32-bit offsets)
+inline bool bf16_shape(int64_t D, int64_t I) {
+  return D > 0 && I > 0 && D % 64 == 0 && I % 64 == 0 && fits32(kTile, 4 * I);
+}
 
 int bf16_swiglu_launch(const void* x, const void* w, int64_t T, int64_t D, int64_t I, const float* rstd, void* gu,
                        void* h, const int* plan, int64_t E, int tiles_m, int64_t ldxs, hipStream_t st) {
