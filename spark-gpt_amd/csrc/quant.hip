@@ -975,6 +975,32 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ p
 // Row groups of the first colsum pass for nb partial rows.
 static inline int64_t colsum_groups(int64_t nb) { return nb < kColsumGroups ? nb : kColsumGroups; }
 
+// The same sums in one launch for up to kColsum1Rows partial rows (the
+// block's 1024 row blocks at 65536 tokens): work-group x owns 32 columns;
+// thread (g, c), g = 0..31, sums rows g, g + 32, ... in ascending order,
+// then thread c of group 0 adds the 32 group sums in the order g = 0..31.
+// The order depends only on nb.
+constexpr int kColsum1Rows = 2048;
+__global__ __launch_bounds__(1024) void colsum1_kernel(const float* __restrict__ part, int64_t nb, int64_t D,
+                                                       float* __restrict__ out) {
+  __shared__ float red[32][33];
+  const int c = threadIdx.x & 31, g = threadIdx.x >> 5;
+  const int64_t d = (int64_t)blockIdx.x * 32 + c;
+  float s = 0.0f;
+  if (d < D) {
+#pragma unroll 16
+    for (int64_t b = g; b < nb; b += 32) s += __builtin_nontemporal_load(part + b * D + d);
+  }
+  red[g][c] = s;
+  __syncthreads();
+  if (g == 0 && d < D) {
+    float t = red[0][c];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) t += red[i][c];
+    out[d] = t;
+  }
+}
+
 }  // namespace sfp8
 
 // ============================================================================
@@ -1024,6 +1050,24 @@ static inline int launch_status() {
 
 static inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 
+// d_norm_w = the column sums of the nb partial rows at part (group sums,
+// when two passes are needed, after them).
+static int colsum_launch(float* part, int64_t nb, int64_t D, float* dnw, hipStream_t st) {
+  if (nb <= kColsum1Rows) {
+    hipLaunchKernelGGL(colsum1_kernel, dim3((unsigned)((D + 31) / 32)), dim3(1024), 0, st, (const float*)part, nb, D,
+                       dnw);
+    return launch_status();
+  }
+  // partial rows: nb from the norm kernel, then the group sums after them
+  const int64_t G = colsum_groups(nb), rpg = (nb + G - 1) / G;
+  float* group_sums = part + nb * D;
+  const unsigned cblk = (unsigned)((D + 63) / 64);
+  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, (unsigned)G), dim3(256), 0, st, part, nb, rpg, D, group_sums);
+  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, 1), dim3(256), 0, st, (const float*)group_sums, G, G, D, dnw);
+  return launch_status();
+}
+
+
 template <typename K>
 static int allow_lds(K kernel, size_t bytes) {
   // dynamic LDS above 64 KiB must be opted into per kernel
@@ -1059,26 +1103,11 @@ static int launch_norm_bwd(const void* h, const float* rstd, const void* dxn, co
   hipLaunchKernelGGL(norm_bwd_kernel<D>, dim3(nblk), dim3(64 * Cfg::BW), lds, st, (const uint16_t*)h, rstd,
                      (const uint16_t*)dxn, (const uint16_t*)dy, nw, T, scale, amax, (uint16_t*)dh, part,
                      (uint8_t*)dy8, (uint8_t*)dy8t, ldt);
-  // partial rows: nblk from the norm kernel, then the group sums after them
-  const int64_t nb = (int64_t)nblk, G = colsum_groups(nb), rpg = (nb + G - 1) / G;
-  float* group_sums = part + nb * D;
-  const unsigned cblk = (unsigned)((D + 63) / 64);
-  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, (unsigned)G), dim3(256), 0, st, part, nb, rpg, (int64_t)D,
-                     group_sums);
-  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, 1), dim3(256), 0, st, (const float*)group_sums, G, G,
-                     (int64_t)D, dnw);
-  return launch_status();
+  const int rc2 = launch_status();
+  if (rc2) return rc2;
+  return colsum_launch(part, (int64_t)nblk, D, dnw, st);
 }
 
-static int colsum_launch(float* part, int64_t nb, int64_t D, float* dnw, hipStream_t st) {
-  // partial rows: nb from the norm kernel, then the group sums after them
-  const int64_t G = colsum_groups(nb), rpg = (nb + G - 1) / G;
-  float* group_sums = part + nb * D;
-  const unsigned cblk = (unsigned)((D + 63) / 64);
-  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, (unsigned)G), dim3(256), 0, st, part, nb, rpg, D, group_sums);
-  hipLaunchKernelGGL(colsum_kernel, dim3(cblk, 1), dim3(256), 0, st, (const float*)group_sums, G, G, D, dnw);
-  return launch_status();
-}
 
 static int launch_norm_bwd_wide(const void* h, const float* rstd, const void* dxn, const void* dy, const float* nw,
                                 int64_t T, int64_t D, const float* scale, float* amax, void* dh, float* dnw,
